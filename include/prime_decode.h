@@ -1,0 +1,94 @@
+/* C ABI of the MI355X (gfx950) SmolLM2 decode megakernel library `libprime_decode.so`.
+ *
+ * Every entry point takes plain device pointers and sizes; no torch types cross this boundary.
+ * Launches are asynchronous on `stream` (a hipStream_t, or NULL for the null stream); the return
+ * value is 0 or a status code (see prime_decode_status_string / decode360_status_string).
+ *
+ * Reference interfaces each entry replaces (paths under Mantissagithub/prime-kernels):
+ *   decode360, decode360_workspace_bytes, decode360_debug_bytes, decode360_status_string
+ *       prime_kernels/decode_megakernel_360m/csrc/block360_kernel.inc:849-938
+ *   mk_decode, mk_workspace_bytes, mk_status_string, mk_query
+ *       prime_kernels/decode_megakernel/csrc/megakernel.cu:833-927
+ * pk_decode / pk_workspace_bytes / pk_query are this library's superset of both (model choice,
+ * layer count, LM head with greedy ids and optional logits); they have no single counterpart.
+ */
+#ifndef PRIME_DECODE_H
+#define PRIME_DECODE_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes (block360.cu:42-51 keeps the same numbers). */
+#define PK_OK 0
+#define PK_ERR_BATCH 9101        /* batch outside the supported range */
+#define PK_ERR_MAX_SEQ 9102      /* max_seq_len / seq_lens outside the supported range */
+#define PK_ERR_NULL 9103         /* a required pointer is NULL */
+#define PK_ERR_COOP 9104         /* cooperative launch unsupported */
+#define PK_ERR_RESIDENCY 9105    /* workgroups cannot all be resident (LDS / CU count) */
+#define PK_ERR_ARCH 9106         /* device is not gfx950 */
+#define PK_ERR_ALIGN 9107        /* KV offsets/strides not multiples of 8 elements, or pointers not 16-B aligned */
+#define PK_ERR_SCRATCH 9108      /* workspace or debug buffer too small */
+#define PK_ERR_BLOCK 9109        /* block_size != 16, bt_stride too small, or bad layer index */
+#define PK_ERR_MODEL 9110        /* unknown model id or layer count */
+#define PK_ERR_DEBUG 9111        /* per-stage debug capture is not available in this build */
+
+/* Models. */
+#define PK_MODEL_SMOLLM2_360M 360
+#define PK_MODEL_SMOLLM2_135M 135
+
+/* Workspace bytes for `model` (zero-initialise it once; it carries the step epoch). */
+size_t pk_workspace_bytes(int model);
+
+/* One greedy decode step for B sequences (vLLM FLASH_ATTN metadata, paged KV [blocks, KVH, 16, 128]).
+ *   layers: device table [n_layers][6] of pointers (norm1, qkv, o, norm2, gate_up, down), bf16.
+ *   kv: device table [n_layers] of cache base pointers; K at k_off, V at v_off (elements).
+ *   out_hidden [B, H] bf16 receives the final-normed hidden state.
+ *   out_ids [B] int64 and/or out_logits [B, 49152] bf16 request the tied LM head (NULL: skipped).
+ *   layer_outputs [n_layers, B, H] bf16 is optional. */
+int pk_decode(void* stream, int model, int B, int n_layers, const void* input_ids, int ids_i64,
+              const void* embed, const void* final_norm, const void* positions, const void* seq_lens,
+              const void* block_table, int bt_stride, const void* slot_mapping, const void* layers,
+              void* const* kv, long long k_off, long long v_off, long long block_stride,
+              long long token_stride, long long head_stride, int block_size, const void* cos_sin,
+              int cs_fp32, void* out_hidden, void* layer_outputs, void* out_ids, void* out_logits,
+              void* scratch, size_t scratch_bytes, int max_seq_len);
+
+/* Device properties relevant to the launch (current device). Returns a status. */
+int pk_query(int* cu_count, int* coop, int* max_lds_per_block, int* is_gfx950, size_t* lds_bytes);
+
+/* Human-readable status (static storage). */
+const char* prime_decode_status_string(int status);
+
+/* ---- reference-compatible entry points -------------------------------------------------- */
+
+/* SmolLM2-360M, 32 layers, hidden state out (block360_kernel.inc:852-862, same argument list).
+ * `debug` must be NULL (per-stage capture: PK_ERR_DEBUG); `debug_layer_index` must be -1..31. */
+int decode360(void* stream, int B, const void* input_ids, const void* embed, const void* final_norm,
+              const void* positions, const void* seq_lens, const void* block_table, int bt_stride,
+              const void* slot_mapping, const void* layers, void* const* kv, long long k_off,
+              long long v_off, long long block_stride, long long token_stride, long long head_stride,
+              int block_size, const void* cos_sin, int cs_fp32, void* out_hidden, void* layer_outputs,
+              void* scratch, size_t scratch_bytes, void* debug, size_t debug_bytes, int max_seq_len,
+              int debug_layer_index);
+size_t decode360_workspace_bytes(void);   /* block360_kernel.inc:849 */
+size_t decode360_debug_bytes(void);       /* block360_kernel.inc:850; 0: capture unavailable */
+const char* decode360_status_string(int status);  /* block360_kernel.inc:925-938 */
+
+/* SmolLM2-135M, 30 layers (megakernel.cu:844-851, same argument list). */
+int mk_decode(void* stream, int B, const void* input_ids, int ids_i64, const void* positions,
+              const void* seq_lens, const void* block_table, int bt_stride, const void* slot_mapping,
+              const void* layers, const void* embed, const void* final_norm, void* const* kv_layers,
+              long long k_off, long long v_off, long long block_stride, long long token_stride,
+              long long head_stride, int block_size, const void* cos_sin, int cs_fp32,
+              void* out_hidden, void* scratch, size_t scratch_bytes, int max_seq_len);
+size_t mk_workspace_bytes(int B, int max_seq_len);  /* megakernel.cu:838-842 */
+const char* mk_status_string(int status);            /* megakernel.cu:914-927 */
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PRIME_DECODE_H */

@@ -1,0 +1,197 @@
+"""Host wrapper shared by the 360M and 135M decode kernels.
+
+Mirrors the reference wrapper prime_kernels/decode_megakernel_360m/__init__.py:60-234 (contract
+checks with the same ValueError messages, per-device runtime with module-owned workspace and
+output buffer, device pointer tables rebuilt only when a data_ptr changes and then updated in
+place) and calls the C ABI `pk_decode` (include/prime_decode.h) on the current HIP stream.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from prime_kernels_amd import _native
+
+BLOCK_SIZE = 16
+EPS = 1e-5
+VOCAB = 49152
+
+
+@dataclass(frozen=True)
+class Model:
+    name: str
+    model_id: int
+    hidden: int
+    inter: int
+    heads: int
+    kv_heads: int
+    layers: int
+    head_dim: int = 64
+    max_batch: int = 1
+    max_seq: int = 12288
+
+    @property
+    def qkv_rows(self) -> int:
+        return (self.heads + 2 * self.kv_heads) * self.head_dim
+
+    def shapes(self):
+        h, i = self.hidden, self.inter
+        return ((h,), (self.qkv_rows, h), (h, h), (h,), (2 * i, h), (h, i))
+
+
+class _Runtime:
+    """Per-device state (reference: decode_megakernel_360m/__init__.py:60-70)."""
+
+    def __init__(self, model: Model, device: torch.device):
+        lib = _native.library()
+        self.lib = lib
+        self.device = device
+        nbytes = lib.pk_workspace_bytes(model.model_id)
+        # zero once: exchange tags start invalid, the step epoch starts at 0
+        self.scratch = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        self.out = torch.empty((model.max_batch, model.hidden), dtype=torch.bfloat16, device=device)
+        self.ids = torch.empty((model.max_batch,), dtype=torch.int64, device=device)
+        self.layers_t = None
+        self.kv_t = None
+        self.table_key = None
+
+    def abort_word(self) -> int:
+        """Non-zero when a bounded wait inside the kernel gave up (a failed step)."""
+        return int(self.scratch[4:8].view(torch.int32).item())
+
+
+_runtimes: dict = {}
+
+
+def runtime(model: Model, device: torch.device) -> _Runtime:
+    key = (model.model_id, device)
+    if key not in _runtimes:
+        _runtimes[key] = _Runtime(model, device)
+    return _runtimes[key]
+
+
+def _check_tensor(tensor, name, *, dtype=None, device=None, shape=None):
+    if not isinstance(tensor, torch.Tensor) or not tensor.is_cuda:
+        raise ValueError(f"{name} must be a CUDA tensor")
+    if dtype is not None and tensor.dtype != dtype:
+        raise ValueError(f"{name} must have dtype {dtype}")
+    if device is not None and tensor.device != device:
+        raise ValueError(f"{name} must be on {device}")
+    if shape is not None and tuple(tensor.shape) != shape:
+        raise ValueError(f"{name} must have shape {shape}")
+
+
+def _tables(rt: _Runtime, layers, kv_caches):
+    """Device pointer tables (reference: decode_megakernel_360m/__init__.py:126-139)."""
+    key = (tuple(t.data_ptr() for layer in layers for t in layer), tuple(t.data_ptr() for t in kv_caches))
+    if key != rt.table_key:
+        layer_table = torch.tensor([[t.data_ptr() for t in layer] for layer in layers], dtype=torch.int64)
+        kv_table = torch.tensor([t.data_ptr() for t in kv_caches], dtype=torch.int64)
+        if rt.layers_t is None or rt.layers_t.shape != layer_table.shape:
+            rt.layers_t = layer_table.to(rt.device)
+            rt.kv_t = kv_table.to(rt.device)
+        else:
+            # in place, so graphs captured with these tables see the new pointers
+            rt.layers_t.copy_(layer_table)
+            rt.kv_t.copy_(kv_table)
+        rt.table_key = key
+    return rt.layers_t, rt.kv_t
+
+
+def decode_step(model: Model, *, input_ids, positions, seq_lens, block_table, slot_mapping, embed, layers,
+                final_norm, kv_caches, cos_sin_cache, eps, layer_outputs=None, debug=None,
+                debug_layer_index=-1, return_token_ids=False, logits_out=None, num_layers=None):
+    """One decode step; inputs follow vLLM FLASH_ATTN metadata (reference signature
+    decode_megakernel_360m/__init__.py:142-144).
+
+    Returns the final-normed hidden state [B, H] bf16 -- a view of a per-device buffer that the
+    next call overwrites.  With `return_token_ids=True` returns (hidden, ids[B] int64) where ids
+    are the greedy tokens of the tied LM head (also a reused buffer).  `logits_out` ([B, 49152]
+    bf16, caller-owned) receives the LM-head logits.  `num_layers` runs only the first N layers
+    (default: all), for tests on truncated models."""
+    nl = model.layers if num_layers is None else int(num_layers)
+    batch = input_ids.shape[0]
+    if not 1 <= batch <= model.max_batch:
+        raise ValueError(f"batch must be 1..{model.max_batch}, got {batch}")
+    if eps != EPS:
+        raise ValueError(f"the kernel is built for rms eps {EPS}, got {eps}")
+    if not 1 <= nl <= model.layers:
+        raise ValueError(f"num_layers must be 1..{model.layers}")
+    if len(layers) != nl or len(kv_caches) != nl:
+        raise ValueError(f"expected {nl} layers and KV caches")
+    if debug_layer_index < -1 or debug_layer_index >= model.layers:
+        raise ValueError(f"debug_layer_index must be -1 or a layer index 0..{model.layers - 1}")
+    if debug is not None:
+        raise ValueError("per-stage debug capture is not available in this build")
+
+    device = input_ids.device
+    _check_tensor(input_ids, "input_ids", device=device)
+    if input_ids.dtype not in (torch.int32, torch.int64) or input_ids.ndim != 1:
+        raise ValueError("input_ids must be a 1-D int32 or int64 tensor")
+    _check_tensor(positions, "positions", dtype=torch.int64, device=device, shape=(batch,))
+    _check_tensor(seq_lens, "seq_lens", dtype=torch.int32, device=device, shape=(batch,))
+    _check_tensor(slot_mapping, "slot_mapping", dtype=torch.int64, device=device, shape=(batch,))
+    if block_table.dtype != torch.int32 or block_table.device != device or block_table.ndim != 2 \
+            or block_table.shape[0] < batch:
+        raise ValueError("block_table must be int32 [B, width] on the input device")
+    if block_table.stride(1) != 1:
+        raise ValueError("block_table must have contiguous rows")
+    if not 1 <= block_table.shape[1] * BLOCK_SIZE <= model.max_seq:
+        raise ValueError(f"block_table context capacity must be 1..{model.max_seq}")
+    _check_tensor(embed, "embed", dtype=torch.bfloat16, device=device)
+    _check_tensor(final_norm, "final_norm", dtype=torch.bfloat16, device=device, shape=(model.hidden,))
+    if embed.ndim != 2 or embed.shape != (VOCAB, model.hidden) or not embed.is_contiguous():
+        raise ValueError(f"embed must be contiguous BF16 [{VOCAB}, {model.hidden}]")
+    for i, layer in enumerate(layers):
+        if len(layer) != 6:
+            raise ValueError(f"layer {i} must contain six weight tensors")
+        for name, tensor, shape in zip(("norm1", "qkv", "o", "norm2", "gate_up", "down"), layer, model.shapes()):
+            _check_tensor(tensor, f"layer {i} {name}", dtype=torch.bfloat16, device=device, shape=shape)
+            if not tensor.is_contiguous():
+                raise ValueError(f"layer {i} {name} must be contiguous")
+    kv0 = kv_caches[0]
+    _check_tensor(kv0, "kv_caches[0]", dtype=torch.bfloat16, device=device)
+    if kv0.ndim != 4 or kv0.shape[1] != model.kv_heads or kv0.shape[3] != 2 * model.head_dim or kv0.stride(3) != 1:
+        raise ValueError(f"KV caches must use vLLM FLASH_ATTN [blocks, {model.kv_heads}, 16, "
+                         f"{2 * model.head_dim}] K/V-packed layout")
+    if kv0.shape[2] != BLOCK_SIZE:
+        raise ValueError("the kernel requires KV block_size=16")
+    for i, kv in enumerate(kv_caches):
+        _check_tensor(kv, f"kv_caches[{i}]", dtype=torch.bfloat16, device=device, shape=tuple(kv0.shape))
+        if kv.stride() != kv0.stride():
+            raise ValueError("all KV caches must share strides")
+    _check_tensor(cos_sin_cache, "cos_sin_cache", device=device)
+    if cos_sin_cache.dtype not in (torch.bfloat16, torch.float32) or cos_sin_cache.ndim != 2 \
+            or cos_sin_cache.shape[1] != model.head_dim or not cos_sin_cache.is_contiguous():
+        raise ValueError(f"cos_sin_cache must be contiguous BF16 or FP32 [max_position, {model.head_dim}]")
+    if layer_outputs is not None:
+        _check_tensor(layer_outputs, "layer_outputs", dtype=torch.bfloat16, device=device,
+                      shape=(nl, batch, model.hidden))
+        if not layer_outputs.is_contiguous():
+            raise ValueError("layer_outputs must be contiguous")
+    if logits_out is not None:
+        _check_tensor(logits_out, "logits_out", dtype=torch.bfloat16, device=device, shape=(batch, VOCAB))
+        if not logits_out.is_contiguous():
+            raise ValueError("logits_out must be contiguous")
+
+    rt = runtime(model, device)
+    layers_t, kv_t = _tables(rt, layers, kv_caches)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    want_ids = return_token_ids or logits_out is not None
+    rc = rt.lib.pk_decode(
+        stream, model.model_id, batch, nl, input_ids.data_ptr(), int(input_ids.dtype == torch.int64),
+        embed.data_ptr(), final_norm.data_ptr(), positions.data_ptr(), seq_lens.data_ptr(),
+        block_table.data_ptr(), block_table.stride(0), slot_mapping.data_ptr(), layers_t.data_ptr(),
+        kv_t.data_ptr(), 0, model.head_dim, kv0.stride(0), kv0.stride(2), kv0.stride(1), BLOCK_SIZE,
+        cos_sin_cache.data_ptr(), int(cos_sin_cache.dtype == torch.float32), rt.out.data_ptr(),
+        layer_outputs.data_ptr() if layer_outputs is not None else None,
+        rt.ids.data_ptr() if want_ids else None,
+        logits_out.data_ptr() if logits_out is not None else None,
+        rt.scratch.data_ptr(), rt.scratch.numel(), block_table.shape[1] * BLOCK_SIZE)
+    if rc != 0:
+        raise RuntimeError(f"{model.name} failed: {_native.status_string(rc)}")
+    if return_token_ids:
+        return rt.out[:batch], rt.ids[:batch]
+    return rt.out[:batch]

@@ -1,0 +1,56 @@
+"""ctypes binding of the C ABI in include/prime_decode.h (libprime_decode.so).
+
+This is the only place Python crosses into native code.  There is no fallback: if the library
+is missing the import-time call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libprime_decode.so"
+
+MODEL_360M = 360
+MODEL_135M = 135
+
+_lib = None
+
+vp, ci, ll, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_size_t
+
+# symbol -> (restype, argtypes); the list every test checks against include/prime_decode.h
+SIGNATURES = {
+    "pk_workspace_bytes": (sz, [ci]),
+    "pk_decode": (ci, [vp, ci, ci, ci, vp, ci, vp, vp, vp, vp, vp, ci, vp, vp, vp,
+                       ll, ll, ll, ll, ll, ci, vp, ci, vp, vp, vp, vp, vp, sz, ci]),
+    "pk_query": (ci, [ctypes.POINTER(ci), ctypes.POINTER(ci), ctypes.POINTER(ci), ctypes.POINTER(ci),
+                      ctypes.POINTER(sz)]),
+    "prime_decode_status_string": (ctypes.c_char_p, [ci]),
+    "decode360": (ci, [vp, ci, vp, vp, vp, vp, vp, vp, ci, vp, vp, vp, ll, ll, ll, ll, ll, ci, vp, ci,
+                       vp, vp, vp, sz, vp, sz, ci, ci]),
+    "decode360_workspace_bytes": (sz, []),
+    "decode360_debug_bytes": (sz, []),
+    "decode360_status_string": (ctypes.c_char_p, [ci]),
+    "mk_decode": (ci, [vp, ci, vp, ci, vp, vp, vp, ci, vp, vp, vp, vp, vp, ll, ll, ll, ll, ll, ci, vp,
+                       ci, vp, vp, sz, ci]),
+    "mk_workspace_bytes": (sz, [ci, ci]),
+    "mk_status_string": (ctypes.c_char_p, [ci]),
+}
+
+
+def library() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.is_file():
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m prime_kernels_amd.build`")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def status_string(rc: int) -> str:
+    return library().prime_decode_status_string(rc).decode()
