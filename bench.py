@@ -1,0 +1,153 @@
+"""Decode throughput of SmolLM2-360M (bf16, batch 1, 1024-token context) on one MI355X.
+
+One step = one greedy decode step of the full model (32 layers + tied LM head + argmax), i.e. one
+launch of the persistent megakernel.  The KV cache holds a synthetic 1024-token context
+(N(0,1) bf16), weights are seeded random-init (N(0,0.02) bf16): BASELINE config 3.  W untimed
+warmup steps, then exactly K timed steps starting at position 1024 (context 1025 .. 1024+K),
+bracketed by synchronisation and HIP events on the launch stream.
+
+Prints one JSON line with the metric, the HBM roofline of the kernel (algorithmic bytes per step
+from the reference's own accounting) and a CPU baseline (the oracle's eager step on host cores).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+CONTEXT = 1024
+W_LAYER_360M = 19_664_640
+E_LMHEAD_360M = 94_371_840
+KV_TOKEN_360M = 40_960
+HIDDEN_BYTES = 1_920
+
+
+def step_bytes(S: int, layers: int = 32) -> int:
+    """Algorithmic bytes of one step attending S tokens (S counts the new one)."""
+    return layers * W_LAYER_360M + E_LMHEAD_360M + HIDDEN_BYTES + KV_TOKEN_360M * S + KV_TOKEN_360M + HIDDEN_BYTES
+
+
+def cpu_baseline(seconds: float = 15.0) -> dict:
+    """The oracle's eager bf16 step (oracle/smollm2.py) on this host's cores, full 360M model,
+    1024-token synthetic context; a bounded sample of steps (about `seconds` of CPU work)."""
+    import torch
+    from oracle import smollm2 as O
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    geom = O.SMOLLM2_360M
+    w = O.make_weights(geom, 7)
+    kv = O.make_paged_kv(geom, 1, CONTEXT + 64, seed=11)
+    cos_sin = O.rope_cos_sin(CONTEXT + 64)
+    O.decode_step(w, [5], [CONTEXT], kv, cos_sin)  # untimed warmup
+    times = []
+    t_end = time.perf_counter() + seconds
+    k = 1
+    while time.perf_counter() < t_end and k < 60:
+        t0 = time.perf_counter()
+        O.decode_step(w, [5 + k], [CONTEXT + k], kv, cos_sin)
+        times.append(time.perf_counter() - t0)
+        k += 1
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{len(times)} greedy steps of the full 360M model at context {CONTEXT + 1}..{CONTEXT + len(times)} "
+                      f"(median step {med * 1e3:.1f} ms, torch {torch.__version__} CPU eager bf16, "
+                      f"os.cpu_count()={os.cpu_count()})"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: every box in this setup has one MI355X and the decode "
+              f"path shards by data parallelism with no exchange (see DESIGN.md); --gpus {args.gpus} is not run.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import prime_kernels_amd as pk
+    from prime_kernels_amd import workload as WL
+    from prime_kernels_amd._decode import StepLauncher
+
+    mod = pk.load("decode_megakernel_360m")
+    model = mod.MODEL
+    dev = torch.device("cuda:0")
+    K, W = args.steps, args.warmup
+    embed, final_norm, layers = WL.random_weights(model, 1234, dev)
+    kv = WL.PagedKV(model, 1, CONTEXT + max(K, W) + 16, device=dev, seed=5, fill="randn")
+    cos_sin = WL.rope_table(CONTEXT + max(K, W) + 16, device=dev)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream(dev)
+    warm = StepLauncher(model, embed=embed, layers=layers, final_norm=final_norm, kv_caches=kv.caches,
+                        block_table=kv.block_table, cos_sin_cache=cos_sin, first_id=17, start_pos=CONTEXT, steps=max(W, 1))
+    for k in range(W):
+        warm.launch(k, stream.cuda_stream)
+    timed = StepLauncher(model, embed=embed, layers=layers, final_norm=final_norm, kv_caches=kv.caches,
+                         block_table=kv.block_table, cos_sin_cache=cos_sin, first_id=17, start_pos=CONTEXT, steps=K)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for k in range(K):
+        timed.launch(k, stream.cuda_stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1)
+    abort = timed.rt.abort_word()
+    if abort:
+        raise RuntimeError("kernel reported an abandoned wait (abort word set)")
+    ids = timed.ids.cpu()
+    if not bool(((ids >= 0) & (ids < 49152)).all()):
+        raise RuntimeError("greedy ids out of range")
+
+    total_bytes = sum(step_bytes(CONTEXT + 1 + k) for k in range(K))
+    ms_per_step = ms / K
+    achieved = total_bytes / (ms * 1e-3) / 1e9
+    traffic = None
+    tfile = ROOT / "profiles" / "decode360_ctx1024_traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+    line = {
+        "metric": "decode tok/s, SmolLM2-360M bf16 bs=1 ctx=1024; % of HBM roofline",
+        "value": round(K / (ms * 1e-3), 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded random-init weights N(0,0.02) bf16, KV context N(0,1) bf16, greedy ids fed back on device)",
+        "config": {"workload": "smollm2-360m greedy decode, batch 1, 1024-token context, K steps at context 1025..1024+K",
+                   "batch": 1, "context": CONTEXT, "layers": 32, "lm_head": "tied, fused argmax",
+                   "launch": "one cooperative kernel per step, 256 workgroups"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "bytes_per_step": round(total_bytes / K)},
+        "host_wall_ms_per_step": round(wall * 1e3 / K, 5),
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

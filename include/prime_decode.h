@@ -59,6 +59,10 @@ int pk_decode(void* stream, int model, int B, int n_layers, const void* input_id
 /* Device properties relevant to the launch (current device). Returns a status. */
 int pk_query(int* cu_count, int* coop, int* max_lds_per_block, int* is_gfx950, size_t* lds_bytes);
 
+/* Diagnostics: record per-phase wall-clock timestamps (100 MHz) of subsequent launches into
+ * `buf` ([256][n_layers*16 + 4] uint64, device memory); NULL disables. No reference counterpart. */
+void pk_set_trace(void* buf);
+
 /* Human-readable status (static storage). */
 const char* prime_decode_status_string(int status);
 

@@ -195,3 +195,49 @@ def decode_step(model: Model, *, input_ids, positions, seq_lens, block_table, sl
     if return_token_ids:
         return rt.out[:batch], rt.ids[:batch]
     return rt.out[:batch]
+
+
+class StepLauncher:
+    """Pre-validated, allocation-free launcher for a run of greedy decode steps (batch 1).
+
+    All per-step metadata lives in device arrays prepared once: step k reads its input id from
+    ids[k] and writes the greedy id to ids[k+1], so consecutive steps chain on the device with no
+    host synchronisation (the way graph-replayed serving steps run, decode_backend.after.py:276-277).
+    """
+
+    def __init__(self, model: Model, *, embed, layers, final_norm, kv_caches, block_table, cos_sin_cache,
+                 first_id: int, start_pos: int, steps: int, logits: bool = False):
+        dev = embed.device
+        self.model = model
+        self.rt = runtime(model, dev)
+        self.lib = self.rt.lib
+        self.layers_t, self.kv_t = _tables(self.rt, layers, kv_caches)
+        self.keep = (embed, layers, final_norm, kv_caches, block_table, cos_sin_cache)
+        kv0 = kv_caches[0]
+        self.kv_strides = (0, model.head_dim, kv0.stride(0), kv0.stride(2), kv0.stride(1))
+        pos = torch.arange(start_pos, start_pos + steps, dtype=torch.int64)
+        bt = block_table[0].cpu().to(torch.int64)
+        self.positions = pos.to(dev)
+        self.seq_lens = (pos + 1).to(torch.int32).to(dev)
+        self.slots = (bt[pos // 16] * 16 + pos % 16).to(dev)
+        self.ids = torch.zeros(steps + 1, dtype=torch.int64, device=dev)
+        self.ids[0] = first_id
+        self.logits = torch.empty((1, VOCAB), dtype=torch.bfloat16, device=dev) if logits else None
+        self.steps = steps
+        self.max_seq = block_table.shape[1] * BLOCK_SIZE
+        if start_pos + steps > self.max_seq:
+            raise ValueError("block table too small for the requested steps")
+
+    def launch(self, k: int, stream: int) -> None:
+        m, rt = self.model, self.rt
+        embed, layers, final_norm, kv_caches, block_table, cos_sin = self.keep
+        rc = self.lib.pk_decode(
+            stream, m.model_id, 1, len(layers), self.ids.data_ptr() + 8 * k, 1, embed.data_ptr(),
+            final_norm.data_ptr(), self.positions.data_ptr() + 8 * k, self.seq_lens.data_ptr() + 4 * k,
+            block_table.data_ptr(), block_table.stride(0), self.slots.data_ptr() + 8 * k,
+            self.layers_t.data_ptr(), self.kv_t.data_ptr(), *self.kv_strides, BLOCK_SIZE,
+            cos_sin.data_ptr(), int(cos_sin.dtype == torch.float32), rt.out.data_ptr(), None,
+            self.ids.data_ptr() + 8 * (k + 1), self.logits.data_ptr() if self.logits is not None else None,
+            rt.scratch.data_ptr(), rt.scratch.numel(), self.max_seq)
+        if rc != 0:
+            raise RuntimeError(f"{m.name} failed: {_native.status_string(rc)}")

@@ -26,6 +26,7 @@ SIGNATURES = {
     "pk_query": (ci, [ctypes.POINTER(ci), ctypes.POINTER(ci), ctypes.POINTER(ci), ctypes.POINTER(ci),
                       ctypes.POINTER(sz)]),
     "prime_decode_status_string": (ctypes.c_char_p, [ci]),
+    "pk_set_trace": (None, [vp]),
     "decode360": (ci, [vp, ci, vp, vp, vp, vp, vp, vp, ci, vp, vp, vp, ll, ll, ll, ll, ll, ci, vp, ci,
                        vp, vp, vp, sz, vp, sz, ci, ci]),
     "decode360_workspace_bytes": (sz, []),

@@ -33,6 +33,8 @@
 
 namespace pk {
 
+static unsigned long long* g_trace = nullptr;
+
 // ------------------------------------------------------------------------------------------------
 // Geometry and launch constants
 // ------------------------------------------------------------------------------------------------
@@ -100,6 +102,7 @@ struct Params {
   int n_layers;
   int lm_head;                 // 1: run the LM head + argmax
   int ids_i64;
+  unsigned long long* trace;   // optional per-phase timestamps (diagnostics)
 };
 
 // Exchange-buffer layout (32-bit words).
@@ -179,6 +182,15 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Diagnostic timestamps: TR_EVENTS per layer per workgroup, plus TR_TAIL at the end.
+constexpr int TR_EVENTS = 16;
+constexpr int TR_TAIL = 4;
+__device__ __forceinline__ void trace_at(const Params& p, int layer, int ev, int n_layers) {
+  if (p.trace)
+    p.trace[size_t(blockIdx.x) * (size_t(n_layers) * TR_EVENTS + TR_TAIL) + size_t(layer) * TR_EVENTS + ev] =
+        wall_clock64();
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -377,8 +389,10 @@ __device__ void producer(const Params& p, const Plan<G>& P, Smem<G>& sm) {
       if (pos >= uint32_t(DEPTH) * PKT) st_lds(&sm.filled, pos - uint32_t(DEPTH) * PKT);
     }
   };
-  for (int l = 0; l < p.n_layers && !dead; ++l)
+  for (int l = 0; l < p.n_layers && !dead; ++l) {
     for (int kind = 0; kind < SEGS_PER_LAYER && !dead; ++kind) issue_segment(kind, l, 0);
+    if (lane == 0) trace_at(p, l, 15, p.n_layers);
+  }
   for (int j = 0; j < P.n_lm && !dead; ++j) issue_segment(6, 0, j);
   wait_vmcnt<0>();
   st_lds(&sm.filled, pos);
@@ -621,6 +635,7 @@ __device__ void attention(Consumer<G>& C, int l, uint32_t seg) {
     C.poll_vec(W::qkv(l, b) + G::H + G::KVH * 64 + size_t(g) * 64, 64, sm.xs + 256);
   }
   C.cbar();
+  if (C.ct == 0) trace_at(p, l, 3, p.n_layers);
   // RoPE, HF rounding: bf16(bf16(x*cos) + bf16(rotate_half(x)*sin)) (modeling_llama.py:138-160)
   const int nrot = P.leader ? 256 : 192;
   for (int i = C.ct; i < nrot; i += NCT) {
@@ -737,6 +752,7 @@ __device__ void attention(Consumer<G>& C, int l, uint32_t seg) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) sm.opart[(C.cw * 3 + h) * 64 + lane * 8 + e] = acc[h][e];
   C.cbar();
+  if (C.ct == 0) trace_at(p, l, 4, p.n_layers);
   C.release(C.pos);  // K/V chunk no longer needed
   const int t = C.ct;
   float o_own = 0.f;
@@ -791,6 +807,7 @@ __device__ void attention(Consumer<G>& C, int l, uint32_t seg) {
       M = Mn;
     }
     C.put16(W::attn(l, b) + size_t(g * 3 + h) * 64 + d, O / Ls);
+    if (t == 0) trace_at(p, l, 5, p.n_layers);
   }
   // append the new token's K (rotated) and V at slot_mapping[b]; slot < 0 skips
   const long long slot = p.slot_mapping[b];
@@ -810,6 +827,9 @@ __device__ void consumer(const Params& p, const Plan<G>& P, Smem<G>& sm, uint32_
   using W = WS<G>;
   const int lane = C.lane;
   const int b = 0;
+  auto tr = [&](int l, int ev) { if (C.ct == 0) trace_at(p, l, ev, p.n_layers); };
+  if (C.ct == 0 && p.trace)
+    p.trace[size_t(blockIdx.x) * (size_t(p.n_layers) * TR_EVENTS + TR_TAIL) + size_t(p.n_layers) * TR_EVENTS] = wall_clock64();
 
   for (int l = 0; l < p.n_layers; ++l) {
     const LayerW Lw = p.layers[l];
@@ -818,6 +838,7 @@ __device__ void consumer(const Params& p, const Plan<G>& P, Smem<G>& sm, uint32_
       const uint32_t seg = C.next_seg(seg_bytes(P, 0, 0));
       const int nrows = P.q1 - P.q0;
       C.wait_filled(seg + pad_pkt(seg_bytes(P, 0, 0)));
+      tr(l, 0);
       uint4 w[Rows<G>::QKV][XRegs<G::H>::CPL];
       int rows[Rows<G>::QKV];
       const int nr = pull<G, G::H, Rows<G>::QKV>(C, seg, nrows, w, rows);
@@ -831,6 +852,7 @@ __device__ void consumer(const Params& p, const Plan<G>& P, Smem<G>& sm, uint32_
         C.poll_vec(W::x(l - 1, b), G::H, sm.xs);
       }
       C.cbar();
+      tr(l, 1);
       for (int i = C.ct; i < G::H; i += NCT) sm.xkeep[i] = sm.xs[i];
       const float rs = rms_scale(C.sumsq(sm.xs, G::H), G::H);
       XRegs<G::H> xr;
@@ -839,6 +861,7 @@ __device__ void consumer(const Params& p, const Plan<G>& P, Smem<G>& sm, uint32_
       dots<G::H, Rows<G>::QKV>(w, xr, nr, lane, out);
       if (lane == 0)
         for (int r = 0; r < nr; ++r) C.put16(W::qkv(l, b) + P.q0 + rows[r], rnd(out[r]));
+      tr(l, 2);
     }
     // ---------------- P2: attention ----------------
     {
@@ -854,8 +877,10 @@ __device__ void consumer(const Params& p, const Plan<G>& P, Smem<G>& sm, uint32_
       int rows[Rows<G>::O];
       const int nr = pull<G, G::H, Rows<G>::O>(C, seg, nrows, w, rows);
       C.release(C.pos);
+      tr(l, 6);
       C.poll_vec(W::attn(l, b), G::H, sm.xs);
       C.cbar();
+      tr(l, 7);
       XRegs<G::H> xr;
       load_x<G::H>(xr, sm.xs, lane);
       float out[Rows<G>::O];
@@ -865,6 +890,7 @@ __device__ void consumer(const Params& p, const Plan<G>& P, Smem<G>& sm, uint32_
           const int row = P.o0 + rows[r];
           C.put16(W::h1(l, b) + row, sm.xkeep[row] + rnd(out[r]));
         }
+      tr(l, 8);
     }
     // ---------------- P4: RMSNorm(h1) + gate/up + SwiGLU ----------------
     {
@@ -878,8 +904,10 @@ __device__ void consumer(const Params& p, const Plan<G>& P, Smem<G>& sm, uint32_
       const int nr = pull<G, G::H, Rows<G>::ACT>(C, segg, na, wg, rows);
       pull<G, G::H, Rows<G>::ACT>(C, segu, na, wu, rows);
       C.release(C.pos);
+      tr(l, 9);
       C.poll_vec(W::h1(l, b), G::H, sm.xs);
       C.cbar();
+      tr(l, 10);
       for (int i = C.ct; i < G::H; i += NCT) sm.h1keep[i] = sm.xs[i];
       const float rs = rms_scale(C.sumsq(sm.xs, G::H), G::H);
       XRegs<G::H> xr;
@@ -893,6 +921,7 @@ __device__ void consumer(const Params& p, const Plan<G>& P, Smem<G>& sm, uint32_
           const float silu = rnd(gv / (1.0f + expf(-gv)));
           C.put16(W::act(l, b) + P.a0 + rows[r], silu * uv);
         }
+      tr(l, 11);
     }
     // ---------------- P5: down + residual ----------------
     {
@@ -903,8 +932,10 @@ __device__ void consumer(const Params& p, const Plan<G>& P, Smem<G>& sm, uint32_
       int rows[Rows<G>::DOWN];
       const int nr = pull<G, G::I, Rows<G>::DOWN>(C, seg, nrows, w, rows);
       C.release(C.pos);
+      tr(l, 12);
       C.poll_vec(W::act(l, b), G::I, sm.xs);
       C.cbar();
+      tr(l, 13);
       XRegs<G::I> xr;
       load_x<G::I>(xr, sm.xs, lane);
       float out[Rows<G>::DOWN];
@@ -916,6 +947,7 @@ __device__ void consumer(const Params& p, const Plan<G>& P, Smem<G>& sm, uint32_
           C.put16(W::x(l, b) + row, y);
           if (p.layer_outputs) p.layer_outputs[(size_t(l) * p.B + b) * G::H + row] = uint16_t(f2bf(y));
         }
+      tr(l, 14);
     }
   }
   // ---------------- final RMSNorm + LM head + argmax ----------------
@@ -954,6 +986,8 @@ __device__ void consumer(const Params& p, const Plan<G>& P, Smem<G>& sm, uint32_
   }
   if (lane == 0) { sm.lm_val[C.cw] = best; sm.lm_idx[C.cw] = best_i; }
   C.cbar();
+  if (C.ct == 0 && p.trace)
+    p.trace[size_t(blockIdx.x) * (size_t(p.n_layers) * TR_EVENTS + TR_TAIL) + size_t(p.n_layers) * TR_EVENTS + 1] = wall_clock64();
   if (C.ct == 0) {
     float bv = sm.lm_val[0];
     int bi = sm.lm_idx[0];
@@ -1114,6 +1148,7 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
   p.B = B;
   p.n_layers = n_layers;
   p.lm_head = (out_ids || out_logits) ? 1 : 0;
+  p.trace = g_trace;
   return launch<G>(p, reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -1122,6 +1157,10 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
 // ------------------------------------------------------------------------------------------------
 // C ABI
 // ------------------------------------------------------------------------------------------------
+
+// Diagnostics: per-phase wall-clock timestamps for the next launches (NULL disables).
+// Layout: [256 workgroups][n_layers * 16 + 4] uint64.
+extern "C" void pk_set_trace(void* buf) { pk::g_trace = reinterpret_cast<unsigned long long*>(buf); }
 
 extern "C" size_t pk_workspace_bytes(int model) {
   if (model == PK_MODEL_SMOLLM2_360M) return pk::WS<pk::G360>::TOTAL * 4;
