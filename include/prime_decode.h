@@ -42,6 +42,14 @@ extern "C" {
 /* Workspace bytes for `model` (zero-initialise it once; it carries the step epoch). */
 size_t pk_workspace_bytes(int model);
 
+/* Allocate a zeroed workspace on the current device: kind 0 ordinary device memory, 1 fine-grained
+ * (lower cross-XCD latency for the exchange words).  NULL on failure.  No reference counterpart:
+ * the reference's wrapper allocates its scratch with torch (decode_megakernel_360m/__init__.py:63). */
+void* pk_workspace_alloc(size_t bytes, int kind);
+int pk_workspace_free(void* ptr);
+/* Synchronous copy of n header words of a workspace to the host (0 epoch, 1 abort, 2 abort site). */
+int pk_workspace_read(const void* ws, size_t word, unsigned* out, int n);
+
 /* One greedy decode step for B sequences (vLLM FLASH_ATTN metadata, paged KV [blocks, KVH, 16, 128]).
  *   layers: device table [n_layers][6] of pointers (norm1, qkv, o, norm2, gate_up, down), bf16.
  *   kv: device table [n_layers] of cache base pointers; K at k_off, V at v_off (elements).

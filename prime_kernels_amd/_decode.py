@@ -8,6 +8,8 @@ place) and calls the C ABI `pk_decode` (include/prime_decode.h) on the current H
 
 from __future__ import annotations
 
+import ctypes
+import os
 from dataclasses import dataclass
 
 import torch
@@ -42,24 +44,40 @@ class Model:
 
 
 class _Runtime:
-    """Per-device state (reference: decode_megakernel_360m/__init__.py:60-70)."""
+    """Per-device state (reference: decode_megakernel_360m/__init__.py:60-70).
+
+    The workspace (exchange words + step epoch) is module-owned and lives for the process; it is
+    fine-grained device memory unless PK_WORKSPACE=coarse."""
 
     def __init__(self, model: Model, device: torch.device):
         lib = _native.library()
         self.lib = lib
         self.device = device
         nbytes = lib.pk_workspace_bytes(model.model_id)
-        # zero once: exchange tags start invalid, the step epoch starts at 0
-        self.scratch = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        kind = 0 if os.environ.get("PK_WORKSPACE", "fine") == "coarse" else 1
+        with torch.cuda.device(device):
+            ptr = lib.pk_workspace_alloc(nbytes, kind)
+        if not ptr:
+            raise RuntimeError(f"could not allocate a {nbytes}-byte decode workspace on {device}")
+        self.scratch_ptr = ptr
+        self.scratch_bytes = nbytes
         self.out = torch.empty((model.max_batch, model.hidden), dtype=torch.bfloat16, device=device)
         self.ids = torch.empty((model.max_batch,), dtype=torch.int64, device=device)
         self.layers_t = None
         self.kv_t = None
         self.table_key = None
 
+    def header(self, n: int = 3) -> list:
+        buf = (ctypes.c_uint * n)()
+        with torch.cuda.device(self.device):
+            rc = self.lib.pk_workspace_read(self.scratch_ptr, 0, buf, n)
+        if rc != 0:
+            raise RuntimeError(f"workspace read failed: {_native.status_string(rc)}")
+        return list(buf)
+
     def abort_word(self) -> int:
         """Non-zero when a bounded wait inside the kernel gave up (a failed step)."""
-        return int(self.scratch[4:8].view(torch.int32).item())
+        return self.header(2)[1]
 
 
 _runtimes: dict = {}
@@ -189,7 +207,7 @@ def decode_step(model: Model, *, input_ids, positions, seq_lens, block_table, sl
         layer_outputs.data_ptr() if layer_outputs is not None else None,
         rt.ids.data_ptr() if want_ids else None,
         logits_out.data_ptr() if logits_out is not None else None,
-        rt.scratch.data_ptr(), rt.scratch.numel(), block_table.shape[1] * BLOCK_SIZE)
+        rt.scratch_ptr, rt.scratch_bytes, block_table.shape[1] * BLOCK_SIZE)
     if rc != 0:
         raise RuntimeError(f"{model.name} failed: {_native.status_string(rc)}")
     if return_token_ids:
@@ -238,6 +256,6 @@ class StepLauncher:
             self.layers_t.data_ptr(), self.kv_t.data_ptr(), *self.kv_strides, BLOCK_SIZE,
             cos_sin.data_ptr(), int(cos_sin.dtype == torch.float32), rt.out.data_ptr(), None,
             self.ids.data_ptr() + 8 * (k + 1), self.logits.data_ptr() if self.logits is not None else None,
-            rt.scratch.data_ptr(), rt.scratch.numel(), self.max_seq)
+            rt.scratch_ptr, rt.scratch_bytes, self.max_seq)
         if rc != 0:
             raise RuntimeError(f"{m.name} failed: {_native.status_string(rc)}")

@@ -21,6 +21,9 @@ vp, ci, ll, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_size
 # symbol -> (restype, argtypes); the list every test checks against include/prime_decode.h
 SIGNATURES = {
     "pk_workspace_bytes": (sz, [ci]),
+    "pk_workspace_alloc": (vp, [sz, ci]),
+    "pk_workspace_free": (ci, [vp]),
+    "pk_workspace_read": (ci, [vp, sz, ctypes.POINTER(ctypes.c_uint), ci]),
     "pk_decode": (ci, [vp, ci, ci, ci, vp, ci, vp, vp, vp, vp, vp, ci, vp, vp, vp,
                        ll, ll, ll, ll, ll, ci, vp, ci, vp, vp, vp, vp, vp, sz, ci]),
     "pk_query": (ci, [ctypes.POINTER(ci), ctypes.POINTER(ci), ctypes.POINTER(ci), ctypes.POINTER(ci),

@@ -50,14 +50,15 @@ using G360 = Geom<960, 15, 5, 2560, 32>;   // decode_megakernel_360m/__init__.py
 using G135 = Geom<576, 9, 3, 1536, 30>;    // decode_megakernel/__init__.py:37-43
 
 constexpr int NWG = 256;                 // persistent workgroups (one per CU)
+constexpr int NPW = 4;                   // producer waves per workgroup (LDS-DMA issue is per-wave bound)
 constexpr int NCW = 4;                   // consumer waves per workgroup
 constexpr int NCT = 64 * NCW;            // consumer threads
-constexpr int WG_THREADS = 64 * (1 + NCW);
+constexpr int WG_THREADS = 64 * (NPW + NCW);
 constexpr uint32_t RING = 128u * 1024u;  // LDS ring bytes (power of two)
 constexpr uint32_t PKT = 1024;           // one LDS-DMA instruction: 64 lanes x 16 B
-constexpr int DEPTH = 48;                // packets in flight per workgroup
+constexpr int DEPTH = 16;                // packets in flight per producer wave
 constexpr int TC_MAX = 256;              // max cached tokens per attention chunk (64 KB of K/V)
-constexpr int TC_TARGET = 128;           // preferred tokens per chunk
+constexpr int TC_TARGET = 64;            // preferred tokens per chunk
 constexpr int LM_ROWS = 16;              // LM-head rows per ring segment
 constexpr int MAX_B = 16;                // exchange-buffer slots per layer
 constexpr int REC_WORDS = 3 * 66;        // attention partial: 3 heads x (m, l, o[64]), 64-bit words
@@ -124,29 +125,62 @@ struct WS {
 };
 
 // ------------------------------------------------------------------------------------------------
-// Scalar helpers
+// Scalar and cross-lane helpers
 // ------------------------------------------------------------------------------------------------
 
 __device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
+__device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 
-// fp32 -> bf16 bits, round to nearest even (NaN stays NaN).
-__device__ __forceinline__ uint32_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+// fp32 -> bf16, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+__device__ __forceinline__ float rnd(float f) { return float((__bf16)f); }
+// Two fp32 -> packed bf16 pair {lo = a, hi = b}, one instruction.
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  const bf16x2 v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
 }
-__device__ __forceinline__ float rnd(float f) { return bf2f(f2bf(f)); }
+// acc + a.lo*b.lo + a.hi*b.hi over packed bf16 pairs (v_dot2_f32_bf16).
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), acc, false);
+}
 
+// DPP move: lanes whose source is outside the row, or that the row/bank masks disable, get `old`.
+template <int CTRL, int RM = 0xf, int BM = 0xf>
+__device__ __forceinline__ float dpp(float old, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                               __builtin_bit_cast(int, v), CTRL, RM, BM, false));
+}
+__device__ __forceinline__ float lane63(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+// Wave64 sum / max through DPP row shifts and row broadcasts; the result is uniform.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  v += dpp<0x111>(0.f, v);            // row_shr:1
+  v += dpp<0x112>(0.f, v);            // row_shr:2
+  v += dpp<0x114, 0xf, 0xe>(0.f, v);  // row_shr:4, banks 1-3
+  v += dpp<0x118, 0xf, 0xc>(0.f, v);  // row_shr:8, banks 2-3
+  v += dpp<0x142, 0xa>(0.f, v);       // row_bcast:15 into rows 1, 3
+  v += dpp<0x143, 0xc>(0.f, v);       // row_bcast:31 into rows 2, 3
+  return lane63(v);
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
+  v = fmaxf(v, dpp<0x111>(v, v));
+  v = fmaxf(v, dpp<0x112>(v, v));
+  v = fmaxf(v, dpp<0x114, 0xf, 0xe>(v, v));
+  v = fmaxf(v, dpp<0x118, 0xf, 0xc>(v, v));
+  v = fmaxf(v, dpp<0x142, 0xa>(v, v));
+  v = fmaxf(v, dpp<0x143, 0xc>(v, v));
+  return lane63(v);
+}
+// Sum over each aligned group of 8 lanes; every lane of the group gets the group sum.
+__device__ __forceinline__ float group8_sum(float v) {
+  v += dpp<0xb1>(0.f, v);                  // quad_perm [1,0,3,2]
+  v += dpp<0x4e>(0.f, v);                  // quad_perm [2,3,0,1]
+  float t = dpp<0x104, 0xf, 0x5>(0.f, v);  // row_shl:4 into banks 0, 2
+  t = dpp<0x114, 0xf, 0xa>(t, v);          // row_shr:4 into banks 1, 3
+  return v + t;
 }
 
 // Device-scope (coherent across XCDs) accesses for exchange words.
@@ -161,6 +195,14 @@ __device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
 }
 __device__ __forceinline__ void st_dev64(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+// 16-byte device-scope load (sc1); each 32-bit word is read atomically.
+__device__ __forceinline__ u32x4 ld_dev128(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, int(byte_off), 0, 16);
 }
 
 // LDS words shared between the waves of one workgroup.
@@ -183,9 +225,10 @@ __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
 // Diagnostic timestamps: TR_EVENTS per layer per workgroup, plus TR_TAIL at the end.
-constexpr int TR_EVENTS = 16;
+constexpr int TR_EVENTS = 40;
 constexpr int TR_TAIL = 4;
 __device__ __forceinline__ void trace_at(const Params& p, int layer, int ev, int n_layers) {
   if (p.trace)
@@ -203,39 +246,29 @@ template <class G>
 struct Plan {
   int wg;
   int q0, q1;   // QKV rows
-  int o0, o1;   // O rows
+  int o0, o1;   // O rows (only workgroups without an attention chunk, when those are at least half)
   int a0, a1;   // act indices (gate rows a0..a1-1, up rows I+a0..)
   int d0, d1;   // down rows
   int v0, v1;   // LM-head rows
   int n_lm;     // LM segments
   // attention (batch 1)
   int att;      // 1: this workgroup owns an attention chunk
+  int natt;     // workgroups with a chunk (0 .. natt-1)
   int g, c, C, t0, t1;   // kv head, chunk, chunks, cached token range [t0, t1)
   int S, pos;   // tokens attended (incl. new) and the new token's position
   int leader;   // owns the new token, merges the chunk partials and appends K/V
 
-  __device__ void init(const Params& p, int wg_) {
+  __device__ __forceinline__ void init(const Params& p, int wg_) {
     wg = wg_;
-    q0 = split_lo(G::QKV, NWG, wg); q1 = split_lo(G::QKV, NWG, wg + 1);
-    o0 = split_lo(G::H, NWG, wg);   o1 = split_lo(G::H, NWG, wg + 1);
-    a0 = split_lo(G::I, NWG, wg);   a1 = split_lo(G::I, NWG, wg + 1);
-    d0 = split_lo(G::H, NWG, wg);   d1 = split_lo(G::H, NWG, wg + 1);
-    if (p.lm_head) {
-      v0 = split_lo(G::V, NWG, wg); v1 = split_lo(G::V, NWG, wg + 1);
-    } else {
-      v0 = v1 = 0;
-    }
-    n_lm = (v1 - v0 + LM_ROWS - 1) / LM_ROWS;
     S = max(p.seq_lens[0], 1);
     pos = int(max(p.positions[0], (int64_t)0));
     const int old = S - 1;
     int C0 = old <= 0 ? 1 : (old + TC_TARGET - 1) / TC_TARGET;
-    const int cmax = NWG / G::KVH;
-    C0 = min(C0, cmax);
-    int tc = old <= 0 ? 16 : ((old + C0 - 1) / C0 + 15) / 16 * 16;
+    C0 = min(C0, NWG / G::KVH);
+    const int tc = old <= 0 ? 16 : ((old + C0 - 1) / C0 + 15) / 16 * 16;
     C = old <= 0 ? 1 : (old + tc - 1) / tc;
-    const int items = G::KVH * C;
-    att = wg < items;
+    natt = G::KVH * C;
+    att = wg < natt;
     g = c = t0 = t1 = leader = 0;
     if (att) {
       g = wg / C;
@@ -244,23 +277,60 @@ struct Plan {
       t1 = min((c + 1) * tc, old);
       leader = c == C - 1;
     }
+    // QKV and O rows go to the workgroups without an attention chunk when those are at least
+    // half: attention workgroups also stream their KV chunk, and their P2 precedes P3.
+    if (natt <= NWG / 2) {
+      const int nw = NWG - natt, i = wg - natt;
+      q0 = att ? 0 : split_lo(G::QKV, nw, i);
+      q1 = att ? 0 : split_lo(G::QKV, nw, i + 1);
+      o0 = att ? 0 : split_lo(G::H, nw, i);
+      o1 = att ? 0 : split_lo(G::H, nw, i + 1);
+    } else {
+      q0 = split_lo(G::QKV, NWG, wg); q1 = split_lo(G::QKV, NWG, wg + 1);
+      o0 = split_lo(G::H, NWG, wg); o1 = split_lo(G::H, NWG, wg + 1);
+    }
+    a0 = split_lo(G::I, NWG, wg);   a1 = split_lo(G::I, NWG, wg + 1);
+    d0 = split_lo(G::H, NWG, wg);   d1 = split_lo(G::H, NWG, wg + 1);
+    if (p.lm_head) {
+      v0 = split_lo(G::V, NWG, wg); v1 = split_lo(G::V, NWG, wg + 1);
+    } else {
+      v0 = v1 = 0;
+    }
+    n_lm = (v1 - v0 + LM_ROWS - 1) / LM_ROWS;
   }
 };
 
-// Byte sizes of the segments a workgroup streams, in stream order.
-// Per layer: 0 QKV rows, 1 KV chunk, 2 O rows, 3 gate rows, 4 up rows, 5 down rows;
-// then n_lm LM-head segments.
-constexpr int SEGS_PER_LAYER = 6;
+// Most rows any wave computes per phase (balanced split, then round-robin over the NCW waves).
+template <class G>
+struct Rows {
+  static constexpr int per_wave(int rows_per_wg) { return (rows_per_wg + NCW - 1) / NCW; }
+  static constexpr int QKV = per_wave((G::QKV + NWG / 2 - 1) / (NWG / 2));
+  static constexpr int O = per_wave((G::H + NWG / 2 - 1) / (NWG / 2));
+  static constexpr int ACT = per_wave((G::I + NWG - 1) / NWG);
+  static constexpr int DOWN = per_wave((G::H + NWG - 1) / NWG);
+  static constexpr int LM = LM_ROWS / NCW;
+};
+
+// Segments a workgroup streams, in stream order.  Per layer: norm1 weights, QKV rows, the
+// rotary cos/sin row (attention workgroups), the KV chunk, O rows, norm2 weights, gate rows,
+// up rows, down rows; after the last layer: the final-norm weights and the LM-head segments.
+// Small vectors go through the ring too, so no consumer ever waits on a global load for them.
+enum SegKind { S_NORM1, S_QKV, S_CS, S_KV, S_O, S_NORM2, S_GATE, S_UP, S_DOWN, SEGS_PER_LAYER };
+constexpr int S_FNORM = 100, S_LM = 101;
 
 template <class G>
-__device__ __forceinline__ uint32_t seg_bytes(const Plan<G>& P, int kind, int lm_index) {
+__device__ __forceinline__ uint32_t seg_bytes(const Plan<G>& P, int kind, int lm_index, int cs_fp32) {
   switch (kind) {
-    case 0: return uint32_t(P.q1 - P.q0) * G::H * 2;
-    case 1: return P.att ? uint32_t(P.t1 - P.t0) * 256u : 0u;
-    case 2: return uint32_t(P.o1 - P.o0) * G::H * 2;
-    case 3:
-    case 4: return uint32_t(P.a1 - P.a0) * G::H * 2;
-    case 5: return uint32_t(P.d1 - P.d0) * G::I * 2;
+    case S_NORM1: return P.q1 > P.q0 ? G::H * 2 : 0u;
+    case S_NORM2:
+    case S_FNORM: return G::H * 2;
+    case S_QKV: return uint32_t(P.q1 - P.q0) * G::H * 2;
+    case S_CS: return P.att ? (cs_fp32 ? 256u : 128u) : 0u;
+    case S_KV: return P.att ? uint32_t(P.t1 - P.t0) * 256u : 0u;
+    case S_O: return uint32_t(P.o1 - P.o0) * G::H * 2;
+    case S_GATE:
+    case S_UP: return uint32_t(P.a1 - P.a0) * G::H * 2;
+    case S_DOWN: return uint32_t(P.d1 - P.d0) * G::I * 2;
     default: {
       const int r0 = P.v0 + lm_index * LM_ROWS;
       const int r1 = min(r0 + LM_ROWS, P.v1);
@@ -271,6 +341,11 @@ __device__ __forceinline__ uint32_t seg_bytes(const Plan<G>& P, int kind, int lm
 
 __device__ __forceinline__ uint32_t pad_pkt(uint32_t b) { return (b + PKT - 1) & ~(PKT - 1); }
 
+// Ring byte offset (within a KV segment) of 16-byte piece `part` of K (v=0) or V (v=1) of token j.
+__device__ __forceinline__ uint32_t kv_slot(int j, int v, int part) {
+  return uint32_t(j) * 256u + uint32_t(v) * 128u + uint32_t((part + j) & 7) * 16u;
+}
+
 // ------------------------------------------------------------------------------------------------
 // Shared memory layout
 // ------------------------------------------------------------------------------------------------
@@ -278,21 +353,30 @@ __device__ __forceinline__ uint32_t pad_pkt(uint32_t b) { return (b + PKT - 1) &
 template <class G>
 struct Smem {
   static constexpr int XS = G::I > G::H ? G::I : G::H;
+  // Attention inputs and scores share storage with the phase-input vector: attention starts after
+  // a consumer barrier that follows the last xs read of P1, and every xs write after attention
+  // follows the attention barrier, after which only wml/wo (separate) are read.
+  struct Attn {
+    float qkvw[NCW][5 * 64];     // per-wave attention inputs (3 q heads, k_new, v_new; pre-RoPE)
+    float sc[3][TC_MAX + 4];     // per-head scores
+    uint16_t pb[3][TC_MAX + 4];  // per-head probabilities (bf16), pairs read as 32-bit words
+  };
   uint8_t ring[RING];
-  float xs[XS];              // current phase input (bf16 values as fp32)
-  float xkeep[G::H];         // layer input x (residual for O)
-  float h1keep[G::H];        // h1 (residual for down)
-  float red[64];
-  float qrot[3 * 64];
-  float knew[64];
-  float vnew[64];
-  float sc[3 * (TC_MAX + 1)];
-  float opart[NCW * 3 * 64];
-  float ml[8];
+  union {
+    float xs[XS];                // current phase input (bf16 values as fp32)
+    Attn at;
+  };
+  float xkeep[G::H];             // layer input x (residual for O)
+  float h1keep[G::H];            // h1 (residual for down)
+  float red[NCW];
+  float wml[NCW][2][3];          // per-wave softmax max / sum per head
+  float wo[NCW][3][64];          // per-wave P.V partial per head
+  LayerW lw[G::L];               // layer pointer table (read by the producers from LDS)
+  const void* kvp[G::L];         // per-layer KV cache base
   int32_t blk[TC_MAX / 16 + 2];
   float lm_val[NCW];
   int32_t lm_idx[NCW];
-  uint32_t filled;
+  uint32_t front[NPW];           // per producer wave: stream bytes below which its packets landed
   uint32_t consumed[NCW];
   uint32_t cbar;
 };
@@ -305,7 +389,7 @@ struct Spin {
   uint32_t n = 0;
   uint32_t* abort_word;
   int where;
-  __device__ Spin(uint32_t* ws, int w) : abort_word(ws + HDR_ABORT), where(w) {}
+  __device__ __forceinline__ Spin(uint32_t* ws, int w) : abort_word(ws + HDR_ABORT), where(w) {}
   // Returns false when the wait must be abandoned.
   __device__ __forceinline__ bool again() {
     ++n;
@@ -326,76 +410,101 @@ struct Spin {
 // Producer wave
 // ------------------------------------------------------------------------------------------------
 
+// NPW producer waves share the stream: global packet n (1 KB of the stream, ring slot n mod
+// RING/PKT) is issued by wave n % NPW.  Each wave keeps at most DEPTH of its packets in flight and
+// publishes front[w] = start of its oldest packet that may still be in flight; consumers take the
+// minimum over the waves.  Nothing here waits on a compiler-visible vector-memory load: the
+// pointer tables and block ids come from LDS, so the only vmcnt waits are the explicit ones.
 template <class G>
-__device__ void producer(const Params& p, const Plan<G>& P, Smem<G>& sm) {
+__device__ __forceinline__ void producer(const Params& p, const Plan<G>& P, Smem<G>& sm) {
+  const int pw = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const uint32_t ring_base = uint32_t(reinterpret_cast<uintptr_t>(sm.ring));
-  // Block ids of this workgroup's attention chunk (same for every layer).
-  if (P.att) {
+  // Block ids of this workgroup's attention chunk (the same for every layer).
+  if (pw == 0 && P.att) {
     const int nb = (P.t1 > P.t0) ? ((P.t1 - 1) / 16 - P.t0 / 16 + 1) : 0;
     for (int i = lane; i < nb; i += 64) sm.blk[i] = p.block_table[P.t0 / 16 + i];
   }
   wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();  // consumers may read blk[] after this
 
-  uint32_t pos = 0;
+  uint32_t n = 0;  // global packet index at the start of the current segment
   Spin spin(p.ws, 1);
   bool dead = false;
-  auto ring_space = [&]() -> bool {
-    uint32_t cmin = ld_lds(&sm.consumed[0]);
+  auto cmin = [&]() -> uint32_t {
+    uint32_t c = ld_lds(&sm.consumed[0]);
 #pragma unroll
-    for (int w = 1; w < NCW; ++w) cmin = min(cmin, ld_lds(&sm.consumed[w]));
-    return pos + PKT <= cmin + RING;
+    for (int w = 1; w < NCW; ++w) c = min(c, ld_lds(&sm.consumed[w]));
+    return c;
+  };
+  auto publish = [&](uint32_t first_pending_packet) {
+    if (lane == 0) st_lds(&sm.front[pw], first_pending_packet * PKT);
   };
   auto issue_segment = [&](int kind, int layer, int lm_index) {
-    const uint32_t bytes = seg_bytes(P, kind, lm_index);
+    const uint32_t bytes = seg_bytes(P, kind, lm_index, p.cs_fp32);
     const uint32_t npk = pad_pkt(bytes) / PKT;
+    if (npk == 0) return;
     const uint8_t* base = nullptr;
-    if (kind != 1) {
-      const LayerW* Lw = p.layers + layer;
+    const uint8_t* cache = nullptr;
+    if (kind == S_KV) {
+      cache = reinterpret_cast<const uint8_t*>(sm.kvp[layer]);
+    } else if (kind == S_FNORM) {
+      base = reinterpret_cast<const uint8_t*>(p.final_norm);
+    } else if (kind == S_LM) {
+      base = reinterpret_cast<const uint8_t*>(p.embed) + size_t(P.v0 + lm_index * LM_ROWS) * G::H * 2;
+    } else if (kind == S_CS) {
+      base = reinterpret_cast<const uint8_t*>(p.cos_sin) + size_t(P.pos) * 64 * (p.cs_fp32 ? 4 : 2);
+    } else {
+      const LayerW& Lw = sm.lw[layer];
       switch (kind) {
-        case 0: base = reinterpret_cast<const uint8_t*>(Lw->qkv) + size_t(P.q0) * G::H * 2; break;
-        case 2: base = reinterpret_cast<const uint8_t*>(Lw->o) + size_t(P.o0) * G::H * 2; break;
-        case 3: base = reinterpret_cast<const uint8_t*>(Lw->gate_up) + size_t(P.a0) * G::H * 2; break;
-        case 4: base = reinterpret_cast<const uint8_t*>(Lw->gate_up) + size_t(G::I + P.a0) * G::H * 2; break;
-        case 5: base = reinterpret_cast<const uint8_t*>(Lw->down) + size_t(P.d0) * G::I * 2; break;
-        default: base = reinterpret_cast<const uint8_t*>(p.embed) + size_t(P.v0 + lm_index * LM_ROWS) * G::H * 2; break;
+        case S_NORM1: base = reinterpret_cast<const uint8_t*>(Lw.norm1); break;
+        case S_QKV: base = reinterpret_cast<const uint8_t*>(Lw.qkv) + size_t(P.q0) * G::H * 2; break;
+        case S_O: base = reinterpret_cast<const uint8_t*>(Lw.o) + size_t(P.o0) * G::H * 2; break;
+        case S_NORM2: base = reinterpret_cast<const uint8_t*>(Lw.norm2); break;
+        case S_GATE: base = reinterpret_cast<const uint8_t*>(Lw.gate_up) + size_t(P.a0) * G::H * 2; break;
+        case S_UP: base = reinterpret_cast<const uint8_t*>(Lw.gate_up) + size_t(G::I + P.a0) * G::H * 2; break;
+        default: base = reinterpret_cast<const uint8_t*>(Lw.down) + size_t(P.d0) * G::I * 2; break;
       }
     }
-    const uint8_t* cache = kind == 1 ? reinterpret_cast<const uint8_t*>(p.kv[layer]) : nullptr;
-    for (uint32_t k = 0; k < npk; ++k) {
-      while (!ring_space()) {
+    for (uint32_t i = (uint32_t(pw) + NPW - n % NPW) % NPW; i < npk && !dead; i += NPW) {
+      const uint32_t gn = n + i;
+      if ((gn + 1) * PKT > cmin() + RING) {
         wait_vmcnt<0>();
-        st_lds(&sm.filled, pos);
-        if (!spin.again()) { dead = true; return; }
+        publish(gn);
+        while ((gn + 1) * PKT > cmin() + RING)
+          if (!spin.again()) { dead = true; break; }
+        if (dead) break;
       }
-      const uint32_t off = k * PKT + uint32_t(lane) * 16u;
+      const uint32_t off = i * PKT + uint32_t(lane) * 16u;
       const uint8_t* src;
-      if (kind == 1) {
-        // 4 tokens per packet; per token 8 lanes of K (128 B) then 8 lanes of V.
-        const int t = P.t0 + int(k) * 4 + (lane >> 4);
+      if (kind == S_KV) {
+        // 4 tokens per packet, 256 B each: 8 K slots then 8 V slots of 16 B.  Slot s of chunk
+        // token j holds piece (s - j) mod 8, so 8 consecutive tokens read with one piece index hit
+        // 8 different LDS banks (kv_slot).
+        const int jt = int(i) * 4 + (lane >> 4);
+        const int t = P.t0 + jt;
         const int piece = (lane >> 3) & 1;
-        const int part = lane & 7;
-        const int blk = sm.blk[t / 16 - P.t0 / 16];
+        const int part = ((lane & 7) - jt) & 7;
+        const int blk = off < bytes ? sm.blk[t / 16 - P.t0 / 16] : 0;
         const long long e = (long long)blk * p.block_stride + (long long)(t & 15) * p.token_stride +
                             (long long)P.g * p.head_stride + (piece ? p.v_off : p.k_off) + part * 8;
         src = cache + e * 2;
       } else {
         src = base + off;
       }
-      if (off < bytes) dma16(src, __builtin_amdgcn_readfirstlane(ring_base + (pos & (RING - 1))));
-      pos += PKT;
+      if (off < bytes) dma16(src, __builtin_amdgcn_readfirstlane(ring_base + ((gn * PKT) & (RING - 1))));
       wait_vmcnt<DEPTH>();
-      if (pos >= uint32_t(DEPTH) * PKT) st_lds(&sm.filled, pos - uint32_t(DEPTH) * PKT);
+      // of this wave's packets gn, gn-NPW, ..., the last DEPTH may still be in flight
+      if (gn >= uint32_t(DEPTH - 1) * NPW) publish(gn - uint32_t(DEPTH - 1) * NPW);
     }
+    n += npk;
   };
-  for (int l = 0; l < p.n_layers && !dead; ++l) {
+  for (int l = 0; l < p.n_layers && !dead; ++l)
     for (int kind = 0; kind < SEGS_PER_LAYER && !dead; ++kind) issue_segment(kind, l, 0);
-    if (lane == 0) trace_at(p, l, 15, p.n_layers);
-  }
-  for (int j = 0; j < P.n_lm && !dead; ++j) issue_segment(6, 0, j);
+  if (!dead) issue_segment(S_FNORM, 0, 0);
+  for (int j = 0; j < P.n_lm && !dead; ++j) issue_segment(S_LM, 0, j);
   wait_vmcnt<0>();
-  st_lds(&sm.filled, pos);
+  publish(dead ? 0x3fffffu : n);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -410,129 +519,248 @@ struct Consumer {
   int cw, lane, ct;          // consumer wave, lane, consumer thread id
   uint32_t pos = 0;          // stream cursor (mirrors the producer)
   uint32_t bar_gen = 0;
-  uint32_t epoch, tag16, tag32;
+  uint32_t tag16, tag32;
   bool dead = false;
 
-  __device__ Consumer(const Params& p_, const Plan<G>& P_, Smem<G>& sm_, uint32_t ep)
+  __device__ __forceinline__ Consumer(const Params& p_, const Plan<G>& P_, Smem<G>& sm_, uint32_t ep)
       : p(p_), P(P_), sm(sm_) {
-    cw = (threadIdx.x >> 6) - 1;
+    cw = (threadIdx.x >> 6) - NPW;
     lane = threadIdx.x & 63;
     ct = cw * 64 + lane;
-    epoch = ep;
     tag32 = ep;
     tag16 = ((ep - 1u) % 65535u) + 1u;
   }
 
+  // Makes the lane ids opaque at a phase boundary, so per-lane addresses are recomputed inside the
+  // layer loop instead of being hoisted out of it and kept live in registers.
+  __device__ __forceinline__ void refresh() { asm volatile("" : "+v"(lane), "+v"(ct)); }
+
   // Claims the next segment of the stream; returns its start position.
-  __device__ uint32_t next_seg(uint32_t bytes) {
+  __device__ __forceinline__ uint32_t next_seg(uint32_t bytes) {
     const uint32_t s = pos;
     pos += pad_pkt(bytes);
     return s;
   }
-  __device__ void wait_filled(uint32_t end) {
+  __device__ __forceinline__ uint32_t filled() const {
+    uint32_t f = ld_lds(&sm.front[0]);
+#pragma unroll
+    for (int w = 1; w < NPW; ++w) f = min(f, ld_lds(&sm.front[w]));
+    return f;
+  }
+  __device__ __forceinline__ void wait_filled(uint32_t end) {
     if (dead) return;
     Spin spin(p.ws, 2);
-    while (ld_lds(&sm.filled) < end)
+    while (filled() < end)
       if (!spin.again()) { dead = true; return; }
   }
-  __device__ void release(uint32_t end) {
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): ring reads of this wave have returned
+  __device__ __forceinline__ void release(uint32_t end) {
+    wait_lgkm0();  // ring reads of this wave have returned
     if (lane == 0) st_lds(&sm.consumed[cw], end);
   }
-  // Barrier over the NCW consumer waves.
-  __device__ void cbar() {
+  // Barrier over the NCW consumer waves (LDS counter; the producer never joins).
+  __device__ __forceinline__ void cbar() {
     bar_gen += NCW;
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     if (lane == 0) __hip_atomic_fetch_add(&sm.cbar, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     Spin spin(p.ws, 3);
     while (ld_lds(&sm.cbar) < bar_gen)
       if (!spin.again()) { dead = true; break; }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   }
-
   __device__ __forceinline__ uint4 ring16(uint32_t at) const {
     return *reinterpret_cast<const uint4*>(sm.ring + (at & (RING - 1)));
   }
+  __device__ __forceinline__ uint32_t ring4(uint32_t at) const {
+    return *reinterpret_cast<const uint32_t*>(sm.ring + (at & (RING - 1)));
+  }
+  __device__ __forceinline__ uint32_t w16(float v) const { return (tag16 << 16) | f2bf(v); }
+  __device__ __forceinline__ bool ok4(u32x4 v) const {
+    return (v.x >> 16) == tag16 && (v.y >> 16) == tag16 && (v.z >> 16) == tag16 && (v.w >> 16) == tag16;
+  }
 
-  // Poll `n` tagged bf16 words at ws+off into sm.xs (as fp32); every consumer thread takes
-  // 4-word groups.  Returns the wave-partial sum of squares (for RMSNorm) in every lane.
-  __device__ void poll_vec(size_t off, int n, float* dst) {
-    const uint32_t* src = p.ws + off;
-    __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, 0x7fffffff, 0x00020000);
-    for (int i = ct * 4; i < n; i += NCT * 4) {
-      Spin spin(p.ws, 4);
-      while (true) {
-        const uint32_t rem = uint32_t(n - i);
-        uint32_t w0, w1, w2, w3;
-        if (rem >= 4) {
-          typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-          u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, i * 4, 0, 16);
-          w0 = v.x; w1 = v.y; w2 = v.z; w3 = v.w;
-        } else {
-          w0 = ld_dev(src + i);
-          w1 = rem > 1 ? ld_dev(src + i + 1) : (tag16 << 16);
-          w2 = rem > 2 ? ld_dev(src + i + 2) : (tag16 << 16);
-          w3 = tag16 << 16;
+  // Poll `n` (multiple of 4) tagged bf16 words at ws+off, split over all consumer threads; writes
+  // the values (fp32) to dst[] (and keep[] when given).  Every load of a thread is in flight at
+  // once; only groups whose tags are stale are polled again.  Returns this wave's sum of squares.
+  template <int MAXG>
+  __device__ __forceinline__ float poll_split(size_t off, int n, float* dst, float* keep) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(p.ws + off);
+    u32x4 v[MAXG];
+    uint32_t pend = 0;
+#pragma unroll
+    for (int g = 0; g < MAXG; ++g) {
+      const int i = (ct + g * NCT) * 4;
+      if (i < n) { v[g] = ld_dev128(r, uint32_t(i) * 4u); pend |= 1u << g; }
+    }
+    float ss = 0.f;
+    Spin spin(p.ws, 4);
+    while (true) {
+#pragma unroll
+      for (int g = 0; g < MAXG; ++g) {
+        if ((pend >> g) & 1u) {
+          if (ok4(v[g])) {
+            const int i = (ct + g * NCT) * 4;
+            const float f0 = bf_lo(v[g].x), f1 = bf_lo(v[g].y), f2 = bf_lo(v[g].z), f3 = bf_lo(v[g].w);
+            *reinterpret_cast<float4*>(dst + i) = make_float4(f0, f1, f2, f3);
+            if (keep) *reinterpret_cast<float4*>(keep + i) = make_float4(f0, f1, f2, f3);
+            ss += f0 * f0 + f1 * f1 + f2 * f2 + f3 * f3;
+            pend &= ~(1u << g);
+          }
         }
-        if ((w0 >> 16) == tag16 && (w1 >> 16) == tag16 && (w2 >> 16) == tag16 && (w3 >> 16) == tag16) {
-          dst[i] = bf2f(w0 & 0xffffu);
-          if (rem > 1) dst[i + 1] = bf2f(w1 & 0xffffu);
-          if (rem > 2) dst[i + 2] = bf2f(w2 & 0xffffu);
-          if (rem > 3) dst[i + 3] = bf2f(w3 & 0xffffu);
-          break;
-        }
-        if (dead || !spin.again()) { dead = true; break; }
       }
+      if (!pend) break;
+      if (dead || !spin.again()) { dead = true; break; }
+#pragma unroll
+      for (int g = 0; g < MAXG; ++g)
+        if ((pend >> g) & 1u) v[g] = ld_dev128(r, uint32_t((ct + g * NCT) * 4) * 4u);
+    }
+    return wave_sum(ss);
+  }
+
+  // Poll three regions of tagged words (each a multiple of 4 words, total <= 512) with this wave
+  // alone (no barrier); values -> dst[0 .. n0 + n1 + n2).  Both loads of a lane are in flight at once.
+  __device__ __forceinline__ void poll_wave3(size_t off0, int n0, size_t off1, int n1, size_t off2, int n2,
+                                             float* dst) {
+    const __amdgpu_buffer_rsrc_t r0 = rsrc(p.ws + off0), r1 = rsrc(p.ws + off1), r2 = rsrc(p.ws + off2);
+    auto load = [&](int i) -> u32x4 {
+      if (i < n0) return ld_dev128(r0, uint32_t(i) * 4u);
+      if (i < n0 + n1) return ld_dev128(r1, uint32_t(i - n0) * 4u);
+      return ld_dev128(r2, uint32_t(i - n0 - n1) * 4u);
+    };
+    const int n = n0 + n1 + n2;
+    const int i0 = lane * 4, i1 = (lane + 64) * 4;
+    u32x4 v0, v1;
+    uint32_t pend = 0;
+    if (i0 < n) { v0 = load(i0); pend |= 1u; }
+    if (i1 < n) { v1 = load(i1); pend |= 2u; }
+    Spin spin(p.ws, 7);
+    while (true) {
+      if ((pend & 1u) && ok4(v0)) {
+        *reinterpret_cast<float4*>(dst + i0) = make_float4(bf_lo(v0.x), bf_lo(v0.y), bf_lo(v0.z), bf_lo(v0.w));
+        pend &= ~1u;
+      }
+      if ((pend & 2u) && ok4(v1)) {
+        *reinterpret_cast<float4*>(dst + i1) = make_float4(bf_lo(v1.x), bf_lo(v1.y), bf_lo(v1.z), bf_lo(v1.w));
+        pend &= ~2u;
+      }
+      if (!pend) break;
+      if (dead || !spin.again()) { dead = true; break; }
+      if (pend & 1u) v0 = load(i0);
+      if (pend & 2u) v1 = load(i1);
     }
   }
 
-  // Sum of squares of dst[0..n) (fixed order), broadcast to all consumer lanes.  Ends with cbar.
-  __device__ float sumsq(const float* v, int n) {
-    float s = 0.f;
-    for (int i = ct; i < n; i += NCT) s += v[i] * v[i];
-    s = wave_sum(s);
-    if (lane == 0) sm.red[cw] = s;
+  // Sum of the per-wave values in red[] after a barrier (fixed order: deterministic).
+  __device__ __forceinline__ float block_total(float wave_value) {
+    if (lane == 0) sm.red[cw] = wave_value;
     cbar();
     float t = 0.f;
 #pragma unroll
     for (int w = 0; w < NCW; ++w) t += sm.red[w];
     return t;
   }
-
-  __device__ __forceinline__ void put16(size_t off, float v) {
-    st_dev(p.ws + off, (tag16 << 16) | f2bf(v));
-  }
 };
 
-// x values (fp32) for the 16-byte chunks a lane owns: chunk j = lane + 64*c.
+// A lane owns the 16-byte chunks j = lane + 64*c of every row (K bf16 per row).
 template <int K>
-struct XRegs {
+struct Chunks {
   static constexpr int CH = K / 8;
   static constexpr int CPL = (CH + 63) / 64;
-  float v[CPL][8];
 };
 
-// Dot products of `nr` rows (held as 16-byte chunks per lane) with x; returns the wave-reduced
-// sums in lane-independent registers.
+// Rows cw + NCW*r (r < MAXR, row < nrows) of a ring segment -> registers.
+template <class G, int K, int MAXR>
+__device__ __forceinline__ void pull(const Consumer<G>& C, uint32_t seg_start, int nrows,
+                                     uint4 (&w)[MAXR][Chunks<K>::CPL]) {
+#pragma unroll
+  for (int r = 0; r < MAXR; ++r) {
+    const int row = C.cw + NCW * r;
+#pragma unroll
+    for (int c = 0; c < Chunks<K>::CPL; ++c) {
+      const int ch = C.lane + 64 * c;
+      w[r][c] = (row < nrows && ch < Chunks<K>::CH)
+                    ? C.ring16(seg_start + uint32_t(row) * K * 2 + uint32_t(ch) * 16)
+                    : make_uint4(0, 0, 0, 0);
+    }
+  }
+}
+
+// Norm-weight chunks of a lane, from the ring segment that carries them.
+template <class G, int K>
+__device__ __forceinline__ void load_normw(const Consumer<G>& C, uint4 (&nw)[Chunks<K>::CPL], uint32_t seg) {
+#pragma unroll
+  for (int c = 0; c < Chunks<K>::CPL; ++c) {
+    const int ch = C.lane + 64 * c;
+    nw[c] = ch < Chunks<K>::CH ? C.ring16(seg + uint32_t(ch) * 16u) : make_uint4(0, 0, 0, 0);
+  }
+}
+
+// x chunks of a lane from LDS as packed bf16 pairs: plain (the values are bf16 already), or
+// RMS-normalised with LlamaRMSNorm rounding y = bf16(w * bf16(x * rs)) (modeling_llama.py:62-67).
+template <int K, bool NORM>
+__device__ __forceinline__ void load_x(uint4 (&x)[Chunks<K>::CPL], const float* xs,
+                                       const uint4 (&nw)[Chunks<K>::CPL], float rs, int lane) {
+#pragma unroll
+  for (int c = 0; c < Chunks<K>::CPL; ++c) {
+    const int ch = lane + 64 * c;
+    if (ch < Chunks<K>::CH) {
+      const float4 a = *reinterpret_cast<const float4*>(xs + ch * 8);
+      const float4 b = *reinterpret_cast<const float4*>(xs + ch * 8 + 4);
+      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      uint32_t o[4];
+      if (NORM) {
+        const uint32_t u[4] = {nw[c].x, nw[c].y, nw[c].z, nw[c].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t t = pack2(v[2 * e] * rs, v[2 * e + 1] * rs);
+          o[e] = pack2(bf_lo(u[e]) * bf_lo(t), bf_hi(u[e]) * bf_hi(t));
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = pack2(v[2 * e], v[2 * e + 1]);
+      }
+      x[c] = make_uint4(o[0], o[1], o[2], o[3]);
+    } else {
+      x[c] = make_uint4(0, 0, 0, 0);
+    }
+  }
+}
+
+// out[r] = row r . x (fp32 accumulation of bf16 pair products), wave-reduced, uniform.
 template <int K, int MAXR>
-__device__ __forceinline__ void dots(const uint4 (&w)[MAXR][XRegs<K>::CPL], const XRegs<K>& x, int nr,
-                                     int lane, float (&out)[MAXR]) {
-  constexpr int CPL = XRegs<K>::CPL;
-  constexpr int CH = XRegs<K>::CH;
+__device__ __forceinline__ void dots(const uint4 (&w)[MAXR][Chunks<K>::CPL], const uint4 (&x)[Chunks<K>::CPL],
+                                     float (&out)[MAXR]) {
 #pragma unroll
   for (int r = 0; r < MAXR; ++r) {
     float acc = 0.f;
-    if (r < nr) {
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        if (lane + 64 * c < CH) {
-          const uint32_t u[4] = {w[r][c].x, w[r][c].y, w[r][c].z, w[r][c].w};
+    for (int c = 0; c < Chunks<K>::CPL; ++c) {
+      acc = dot2(w[r][c].x, x[c].x, acc);
+      acc = dot2(w[r][c].y, x[c].y, acc);
+      acc = dot2(w[r][c].z, x[c].z, acc);
+      acc = dot2(w[r][c].w, x[c].w, acc);
+    }
+    out[r] = acc;
+  }
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            acc = fmaf(bf2f(u[e] & 0xffffu), x.v[c][2 * e], acc);
-            acc = fmaf(__uint_as_float(u[e] & 0xffff0000u), x.v[c][2 * e + 1], acc);
-          }
+  for (int r = 0; r < MAXR; ++r) out[r] = wave_sum(out[r]);
+}
+
+// out[r] = row (cw + NCW*r) of a ring segment . x, reading the weights straight from LDS.
+template <class G, int K, int MAXR>
+__device__ __forceinline__ void dots_ring(const Consumer<G>& C, uint32_t seg, int nrows,
+                                          const uint4 (&x)[Chunks<K>::CPL], float (&out)[MAXR]) {
+#pragma unroll
+  for (int r = 0; r < MAXR; ++r) {
+    const int row = C.cw + NCW * r;
+    float acc = 0.f;
+    if (row < nrows) {
+#pragma unroll
+      for (int c = 0; c < Chunks<K>::CPL; ++c) {
+        const int ch = C.lane + 64 * c;
+        if (ch < Chunks<K>::CH) {
+          const uint4 w = C.ring16(seg + uint32_t(row) * K * 2 + uint32_t(ch) * 16);
+          acc = dot2(w.x, x[c].x, acc);
+          acc = dot2(w.y, x[c].y, acc);
+          acc = dot2(w.z, x[c].z, acc);
+          acc = dot2(w.w, x[c].w, acc);
         }
       }
     }
@@ -542,59 +770,14 @@ __device__ __forceinline__ void dots(const uint4 (&w)[MAXR][XRegs<K>::CPL], cons
   for (int r = 0; r < MAXR; ++r) out[r] = wave_sum(out[r]);
 }
 
-// Loads rows [first + cw + NCW*i] of a segment (row length K elements) into registers.
-template <class G, int K, int MAXR>
-__device__ __forceinline__ int pull(Consumer<G>& C, uint32_t seg_start, int nrows,
-                                    uint4 (&w)[MAXR][XRegs<K>::CPL], int (&rows)[MAXR]) {
-  constexpr int CPL = XRegs<K>::CPL;
-  constexpr int CH = XRegs<K>::CH;
-  int nr = 0;
+// Value of row `lane` (lanes < MAXR), for one store instruction per wave.
+template <int MAXR>
+__device__ __forceinline__ float pick(const float (&out)[MAXR], int lane) {
+  float v = out[0];
 #pragma unroll
-  for (int r = 0; r < MAXR; ++r) {
-    const int row = C.cw + NCW * r;
-    rows[r] = row;
-    if (row < nrows) {
-      nr = r + 1;
-#pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        const int ch = C.lane + 64 * c;
-        if (ch < CH) w[r][c] = C.ring16(seg_start + uint32_t(row) * K * 2 + uint32_t(ch) * 16);
-      }
-    }
-  }
-  return nr;
-}
-
-// Normalised x registers: xr = bf16(w * bf16(x * rs)) per element (LlamaRMSNorm rounding).
-template <int K>
-__device__ __forceinline__ void load_x(XRegs<K>& xr, const float* xs, int lane) {
-  constexpr int CH = XRegs<K>::CH;
-#pragma unroll
-  for (int c = 0; c < XRegs<K>::CPL; ++c) {
-    const int ch = lane + 64 * c;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) xr.v[c][e] = ch < CH ? xs[ch * 8 + e] : 0.f;
-  }
-}
-template <int K>
-__device__ __forceinline__ void load_x_norm(XRegs<K>& xr, const float* xs, const uint16_t* w, float rs, int lane) {
-  constexpr int CH = XRegs<K>::CH;
-#pragma unroll
-  for (int c = 0; c < XRegs<K>::CPL; ++c) {
-    const int ch = lane + 64 * c;
-    if (ch < CH) {
-      const uint4 wv = *reinterpret_cast<const uint4*>(w + ch * 8);
-      const uint32_t u[4] = {wv.x, wv.y, wv.z, wv.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        xr.v[c][2 * e] = rnd(bf2f(u[e] & 0xffffu) * rnd(xs[ch * 8 + 2 * e] * rs));
-        xr.v[c][2 * e + 1] = rnd(__uint_as_float(u[e] & 0xffff0000u) * rnd(xs[ch * 8 + 2 * e + 1] * rs));
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xr.v[c][e] = 0.f;
-    }
-  }
+  for (int r = 1; r < MAXR; ++r)
+    if (lane == r) v = out[r];
+  return v;
 }
 
 __device__ __forceinline__ float rms_scale(float sumsq, int n) {
@@ -602,392 +785,450 @@ __device__ __forceinline__ float rms_scale(float sumsq, int n) {
   return 1.0f / sqrtf(mean + 1e-5f);
 }
 
-// ---- phase bodies ------------------------------------------------------------------------------
+// ------------------------------------------------------------------------------------------------
+// P2: attention for one chunk (batch 1).  The chunk's tokens (cached ones, plus the new one for the
+// leader) are split over the 4 consumer waves in even-aligned ranges; each wave handles all 3 query
+// heads of KV head g for its tokens: RoPE on the queries (and the new key), scores with bf16 dot2,
+// a per-wave softmax partial, and P.V with bf16 probabilities (HF rounds the probabilities to bf16
+// before P.V, modeling_llama.py:207-208).  One barrier merges the waves; wave h < 3 then owns head
+// 3g+h: it writes the chunk's partial record (non-leader) or merges all chunks of KV head g by
+// log-sum-exp (leader).  The leader's wave 3 appends the new K/V (block360_kernel.inc:124-135).
+// ------------------------------------------------------------------------------------------------
 
-// Rows per wave for each GEMV phase (ceil over the balanced split, then over NCW waves).
 template <class G>
-struct Rows {
-  static constexpr int QKV = ((G::QKV + NWG - 1) / NWG + NCW - 1) / NCW;
-  static constexpr int O = ((G::H + NWG - 1) / NWG + NCW - 1) / NCW;
-  static constexpr int ACT = ((G::I + NWG - 1) / NWG + NCW - 1) / NCW;
-  static constexpr int DOWN = ((G::H + NWG - 1) / NWG + NCW - 1) / NCW;
-};
-
-// P2 for one attention chunk (batch 1): RoPE on q (and the new k), scores over the ring-resident
-// cached K plus the new token, fp32 softmax partial (m, l, o), then either a partial record
-// (non-leader) or the log-sum-exp merge of all chunks of this KV head (leader), which also
-// appends the new K/V to the paged cache (block360_kernel.inc:124-135).
-template <class G>
-__device__ void attention(Consumer<G>& C, int l, uint32_t seg) {
+__device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, uint32_t seg) {
   const Params& p = C.p;
   const Plan<G>& P = C.P;
   Smem<G>& sm = C.sm;
   using W = WS<G>;
-  const int b = 0, g = P.g, lane = C.lane;
+  const int b = 0, g = P.g, lane = C.lane, w = C.cw;
   const int T_old = P.t1 - P.t0;
   const int T = T_old + (P.leader ? 1 : 0);
-  constexpr int SCS = TC_MAX + 1;
+  // this wave's tokens [j0, j1): even-aligned split; the new token (index T_old) is the last one
+  auto edge = [&](int k) { return k >= NCW ? T : ((T * k) / NCW) & ~1; };
+  const int j0 = edge(w), j1 = edge(w + 1);
+  const bool has_new = P.leader && j1 == T && T > j0;
+  if (P.q1 > P.q0) C.cbar();  // P1 of this workgroup read xs, which shares storage with sm.at
+  float* in = sm.at.qkvw[w];
+  const size_t qkv = W::qkv(l, b);
 
-  C.wait_filled(C.pos);
-  C.poll_vec(W::qkv(l, b) + size_t(g) * 192, 192, sm.xs);
-  if (P.leader) {
-    C.poll_vec(W::qkv(l, b) + G::H + size_t(g) * 64, 64, sm.xs + 192);
-    C.poll_vec(W::qkv(l, b) + G::H + G::KVH * 64 + size_t(g) * 64, 64, sm.xs + 256);
-  }
-  C.cbar();
-  if (C.ct == 0) trace_at(p, l, 3, p.n_layers);
-  // RoPE, HF rounding: bf16(bf16(x*cos) + bf16(rotate_half(x)*sin)) (modeling_llama.py:138-160)
-  const int nrot = P.leader ? 256 : 192;
-  for (int i = C.ct; i < nrot; i += NCT) {
-    const int d = i & 63, base = i - d, f = d & 31;
-    float c, s;
+  // rotary cos/sin of this step's position, from the ring segment that carries the table row
+  auto cs_at = [&](int f, float& c, float& s) {
     if (p.cs_fp32) {
-      const float* row = reinterpret_cast<const float*>(p.cos_sin) + size_t(P.pos) * 64;
-      c = row[f];
-      s = row[32 + f];
+      c = __uint_as_float(C.ring4(segc + uint32_t(f) * 4u));
+      s = __uint_as_float(C.ring4(segc + 128u + uint32_t(f) * 4u));
     } else {
-      const uint16_t* row = reinterpret_cast<const uint16_t*>(p.cos_sin) + size_t(P.pos) * 64;
-      c = bf2f(row[f]);
-      s = bf2f(row[32 + f]);
+      c = bf2f(*reinterpret_cast<const uint16_t*>(sm.ring + ((segc + uint32_t(f) * 2u) & (RING - 1))));
+      s = bf2f(*reinterpret_cast<const uint16_t*>(sm.ring + ((segc + 64u + uint32_t(f) * 2u) & (RING - 1))));
     }
-    const float x = sm.xs[i];
-    const float rot = d < 32 ? -sm.xs[base + d + 32] : sm.xs[base + d - 32];
-    const float r = rnd(rnd(x * c) + rnd(rot * s));
-    if (i < 192) sm.qrot[i] = r;
-    else sm.knew[d] = r;
-  }
-  if (P.leader)
-    for (int i = C.ct; i < 64; i += NCT) sm.vnew[i] = sm.xs[256 + i];
-  C.cbar();
+  };
+  // RoPE with HF rounding: bf16(bf16(x*cos) + bf16(rotate_half(x)*sin)) (modeling_llama.py:138-160)
+  auto rope = [&](const float* head, int d, float c, float s) {
+    const float x = head[d];
+    const float rot = d < 32 ? -head[d + 32] : head[d - 32];
+    return rnd(rnd(x * c) + rnd(rot * s));
+  };
 
-  // scores: 8 lanes per token (8 dims each), 32 tokens per pass over the 4 consumer waves
-  const int grp = C.cw * 8 + (lane >> 3);
-  const int part = lane & 7;
-  float q[3][8];
+  const int part = lane & 7, grp = lane >> 3;
+  // queries of the 3 heads -> in[0, 192); the new key -> in[192, 256) and value -> in[256, 320)
+  const bool need_kv = has_new || (P.leader && w == NCW - 1);
+  C.poll_wave3(qkv + size_t(g) * 192, 192, qkv + G::H + size_t(g) * 64, need_kv ? 64 : 0,
+               qkv + G::H + G::KVH * 64 + size_t(g) * 64, need_kv ? 64 : 0, in);
+  C.wait_filled(C.pos);  // cos/sin row and KV chunk are in the ring
+  float cs8[8], sn8[8];
 #pragma unroll
-  for (int h = 0; h < 3; ++h)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) q[h][e] = sm.qrot[h * 64 + part * 8 + e];
-  for (int j0 = 0; j0 < T; j0 += 32) {
-    const int j = j0 + grp;
-    float k8[8];
-    if (j < T_old) {
-      const uint4 kv = C.ring16(seg + uint32_t(j) * 256u + uint32_t(part) * 16u);
-      const uint32_t u[4] = {kv.x, kv.y, kv.z, kv.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) { k8[2 * e] = bf2f(u[e] & 0xffffu); k8[2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u); }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) k8[e] = j < T ? sm.knew[part * 8 + e] : 0.f;
-    }
-    float dd[3];
-#pragma unroll
-    for (int h = 0; h < 3; ++h) {
-      float a = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) a = fmaf(q[h][e], k8[e], a);
-      a += __shfl_xor(a, 1);
-      a += __shfl_xor(a, 2);
-      a += __shfl_xor(a, 4);
-      dd[h] = a;
-    }
-    if (part == 0 && j < T)
-#pragma unroll
-      for (int h = 0; h < 3; ++h) sm.sc[h * SCS + j] = rnd(dd[h]) * 0.125f;
-  }
-  C.cbar();
-  // per-head max and exp-sum (wave h handles head h)
-  if (C.cw < 3) {
-    const int h = C.cw;
-    float m = -INFINITY;
-    for (int j = lane; j < T; j += 64) m = fmaxf(m, sm.sc[h * SCS + j]);
-    m = wave_max(m);
-    float s = 0.f;
-    for (int j = lane; j < T; j += 64) {
-      const float e = expf(sm.sc[h * SCS + j] - m);
-      sm.sc[h * SCS + j] = e;
-      s += e;
-    }
-    s = wave_sum(s);
-    if (lane == 0) { sm.ml[h] = m; sm.ml[4 + h] = s; }
-  }
-  C.cbar();
-  // PV: acc[h][e] over this lane group's tokens
-  float acc[3][8];
-#pragma unroll
-  for (int h = 0; h < 3; ++h)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
-  for (int j = grp; j < T; j += 32) {
-    float v8[8];
-    if (j < T_old) {
-      const uint4 vv = C.ring16(seg + uint32_t(j) * 256u + 128u + uint32_t(part) * 16u);
-      const uint32_t u[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) { v8[2 * e] = bf2f(u[e] & 0xffffu); v8[2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u); }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v8[e] = sm.vnew[part * 8 + e];
-    }
-#pragma unroll
-    for (int h = 0; h < 3; ++h) {
-      const float pj = sm.sc[h * SCS + j];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(pj, v8[e], acc[h][e]);
+  for (int e = 0; e < 8; ++e) cs_at((part * 8 + e) & 31, cs8[e], sn8[e]);
+  wait_lgkm0();
+  if (w == 0 && lane == 0) trace_at(p, l, 3, p.n_layers);
+  if (P.leader && w == NCW - 1) {
+    // KV append: rotated new K and new V at slot_mapping[b]; slot < 0 skips
+    const long long slot = p.slot_mapping[b];
+    if (slot >= 0) {
+      float c, s;
+      cs_at(lane & 31, c, s);
+      uint16_t* cache = reinterpret_cast<uint16_t*>(p.kv[l]);
+      const long long e = (slot / 16) * p.block_stride + (slot % 16) * p.token_stride + (long long)g * p.head_stride;
+      cache[e + p.k_off + lane] = uint16_t(f2bf(rope(in + 192, lane, c, s)));
+      cache[e + p.v_off + lane] = uint16_t(f2bf(in[256 + lane]));
     }
   }
+  // rotated queries (dims part*8 .. part*8+7 of each head) and new key, packed bf16 pairs
+  uint32_t q[3][4], kn[4];
 #pragma unroll
-  for (int h = 0; h < 3; ++h)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float a = acc[h][e];
-      a += __shfl_xor(a, 8);
-      a += __shfl_xor(a, 16);
-      a += __shfl_xor(a, 32);
-      acc[h][e] = a;
-    }
-  if (lane < 8)
+  for (int e2 = 0; e2 < 4; ++e2) {
+    const int d = part * 8 + 2 * e2;
 #pragma unroll
     for (int h = 0; h < 3; ++h)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sm.opart[(C.cw * 3 + h) * 64 + lane * 8 + e] = acc[h][e];
-  C.cbar();
-  if (C.ct == 0) trace_at(p, l, 4, p.n_layers);
-  C.release(C.pos);  // K/V chunk no longer needed
-  const int t = C.ct;
-  float o_own = 0.f;
-  if (t < 192) {
-    const int h = t >> 6, d = t & 63;
-#pragma unroll
-    for (int w = 0; w < NCW; ++w) o_own += sm.opart[(w * 3 + h) * 64 + d];
+      q[h][e2] = pack2(rope(in + h * 64, d, cs8[2 * e2], sn8[2 * e2]),
+                       rope(in + h * 64, d + 1, cs8[2 * e2 + 1], sn8[2 * e2 + 1]));
+    kn[e2] = has_new ? pack2(rope(in + 192, d, cs8[2 * e2], sn8[2 * e2]),
+                             rope(in + 192, d + 1, cs8[2 * e2 + 1], sn8[2 * e2 + 1]))
+                     : 0u;
   }
-  uint64_t* rec_base = reinterpret_cast<uint64_t*>(p.ws + W::rec(l, 0));
-  if (!P.leader) {
-    uint64_t* rec = rec_base + size_t(P.wg) * REC_WORDS;
-    const uint64_t tg = uint64_t(C.tag32) << 32;
-    if (t < 192) {
-      const int h = t >> 6, d = t & 63;
-      st_dev64(rec + h * 66 + 2 + d, tg | __float_as_uint(o_own));
-    } else if (t < 198) {
-      const int h = (t - 192) >> 1, k = (t - 192) & 1;
-      st_dev64(rec + h * 66 + k, tg | __float_as_uint(sm.ml[k * 4 + h]));
+  if (w == 0 && lane == 0) trace_at(p, l, 16, p.n_layers);
+  // scores: 8 lanes per token (8 dims each), 8 tokens per pass; s = bf16(q.k) * 1/8 (exact scale)
+  for (int jb = j0; jb < j1; jb += 8) {
+    const int j = jb + grp;
+    const uint4 k = j < T_old ? C.ring16(seg + kv_slot(j, 0, part)) : make_uint4(kn[0], kn[1], kn[2], kn[3]);
+    float s3[3];
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      float a = dot2(q[h][0], k.x, 0.f);
+      a = dot2(q[h][1], k.y, a);
+      a = dot2(q[h][2], k.z, a);
+      a = dot2(q[h][3], k.w, a);
+      s3[h] = group8_sum(a);
     }
+    if (part == 0 && j < j1)
+#pragma unroll
+      for (int h = 0; h < 3; ++h) sm.at.sc[h][j] = rnd(s3[h]) * 0.125f;
+  }
+  wait_lgkm0();
+  if (w == 0 && lane == 0) trace_at(p, l, 17, p.n_layers);
+  // softmax partial of this wave's tokens: m = max s, p = exp(s - m) (bf16 for P.V), l = sum exp
+  float m3[3], l3[3];
+#pragma unroll
+  for (int h = 0; h < 3; ++h) {
+    float m = -INFINITY;
+    for (int j = j0 + lane; j < j1; j += 64) m = fmaxf(m, sm.at.sc[h][j]);
+    m = wave_max(m);
+    float ls = 0.f;
+    for (int j = j0 + lane; j < j1; j += 64) {
+      const float e = expf(sm.at.sc[h][j] - m);
+      sm.at.pb[h][j] = uint16_t(f2bf(e));
+      ls += e;
+    }
+    m3[h] = m;
+    l3[h] = wave_sum(ls);
+  }
+  wait_lgkm0();
+  if (w == 0 && lane == 0) trace_at(p, l, 18, p.n_layers);
+  // P.V: lane = (half, d2) owns dims 2*d2, 2*d2+1; token pairs alternate between the halves
+  const int half = lane >> 5, d2 = lane & 31;
+  const int jo1 = min(j1, T_old);
+  const int npairs = jo1 > j0 ? (jo1 - j0) / 2 : 0;
+  const uint32_t voff = uint32_t(d2 & 3) * 4u;
+  float acc[3][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
+#pragma unroll 4
+  for (int k = half; k < npairs; k += 2) {
+    const int j = j0 + 2 * k;
+    const uint32_t va = C.ring4(seg + kv_slot(j, 1, d2 >> 2) + voff);
+    const uint32_t vb = C.ring4(seg + kv_slot(j + 1, 1, d2 >> 2) + voff);
+    const uint32_t lo = __builtin_amdgcn_perm(vb, va, 0x05040100u);  // {v_j[2d2], v_j+1[2d2]}
+    const uint32_t hi = __builtin_amdgcn_perm(vb, va, 0x07060302u);  // {v_j[2d2+1], v_j+1[2d2+1]}
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      const uint32_t pp = *reinterpret_cast<const uint32_t*>(&sm.at.pb[h][j]);
+      acc[h][0] = dot2(pp, lo, acc[h][0]);
+      acc[h][1] = dot2(pp, hi, acc[h][1]);
+    }
+  }
+  if (half == 0) {
+    if (jo1 > j0 && ((jo1 - j0) & 1)) {  // odd cached token at the end of the range
+      const int j = jo1 - 1;
+      const uint32_t v = C.ring4(seg + kv_slot(j, 1, d2 >> 2) + voff);
+#pragma unroll
+      for (int h = 0; h < 3; ++h) {
+        const float pj = bf2f(sm.at.pb[h][j]);
+        acc[h][0] = fmaf(pj, bf_lo(v), acc[h][0]);
+        acc[h][1] = fmaf(pj, bf_hi(v), acc[h][1]);
+      }
+    }
+    if (has_new) {
+#pragma unroll
+      for (int h = 0; h < 3; ++h) {
+        const float pj = bf2f(sm.at.pb[h][T_old]);
+        acc[h][0] = fmaf(pj, in[256 + 2 * d2], acc[h][0]);
+        acc[h][1] = fmaf(pj, in[256 + 2 * d2 + 1], acc[h][1]);
+      }
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < 3; ++h) {
+    acc[h][0] += __shfl_xor(acc[h][0], 32);
+    acc[h][1] += __shfl_xor(acc[h][1], 32);
+  }
+  C.release(C.pos);  // this wave no longer reads the K/V chunk
+  if (lane < 32)
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      sm.wo[w][h][2 * d2] = acc[h][0];
+      sm.wo[w][h][2 * d2 + 1] = acc[h][1];
+    }
+  if (lane == 0)
+#pragma unroll
+    for (int h = 0; h < 3; ++h) { sm.wml[w][0][h] = m3[h]; sm.wml[w][1][h] = l3[h]; }
+  C.cbar();
+  if (w == 0 && lane == 0) trace_at(p, l, 19, p.n_layers);
+  if (w >= 3) return;
+  // wave w: head h = 3g + w.  Merge the 4 wave partials (fixed order) into the chunk partial.
+  const int hh = w, d = lane;
+  float M = -INFINITY, Ls = 0.f, O = 0.f;
+  auto merge = [&](float mc, float lc, float oc) {
+    const float Mn = fmaxf(M, mc);
+    const float sa = M == -INFINITY ? 0.f : expf(M - Mn);
+    const float sb = mc == -INFINITY ? 0.f : expf(mc - Mn);
+    Ls = Ls * sa + lc * sb;
+    O = O * sa + oc * sb;
+    M = Mn;
+  };
+#pragma unroll
+  for (int v = 0; v < NCW; ++v) merge(sm.wml[v][0][hh], sm.wml[v][1][hh], sm.wo[v][hh][d]);
+  if (w == 0 && lane == 0) trace_at(p, l, 4, p.n_layers);
+  uint64_t* rec_base = reinterpret_cast<uint64_t*>(p.ws + W::rec(l, 0));
+  const uint64_t tg = uint64_t(C.tag32) << 32;
+  if (!P.leader) {
+    uint64_t* rec = rec_base + size_t(P.wg) * REC_WORDS + hh * 66;
+    st_dev64(rec + 2 + d, tg | __float_as_uint(O));
+    if (lane == 0) st_dev64(rec, tg | __float_as_uint(M));
+    if (lane == 1) st_dev64(rec + 1, tg | __float_as_uint(Ls));
     return;
   }
-  // leader: online log-sum-exp merge in chunk order 0..C-1 (this chunk is C-1)
-  if (t < 192) {
-    const int h = t >> 6, d = t & 63;
-    float M = -INFINITY, Ls = 0.f, O = 0.f;
-    for (int c = 0; c < P.C; ++c) {
-      float mc, lc, oc;
-      if (c == P.C - 1) {
-        mc = sm.ml[h];
-        lc = sm.ml[4 + h];
-        oc = o_own;
-      } else {
-        const uint64_t* rec = rec_base + size_t(g * P.C + c) * REC_WORDS + h * 66;
-        uint64_t w0, w1, w2;
-        Spin spin(p.ws, 5);
-        while (true) {
-          w0 = ld_dev64(rec);
-          w1 = ld_dev64(rec + 1);
-          w2 = ld_dev64(rec + 2 + d);
-          if (uint32_t(w0 >> 32) == C.tag32 && uint32_t(w1 >> 32) == C.tag32 && uint32_t(w2 >> 32) == C.tag32) break;
-          if (C.dead || !spin.again()) { C.dead = true; break; }
-        }
-        mc = __uint_as_float(uint32_t(w0));
-        lc = __uint_as_float(uint32_t(w1));
-        oc = __uint_as_float(uint32_t(w2));
+  // leader: online log-sum-exp merge over chunks 0..C-1 in order (this chunk is C-1)
+  const float m_own = M, l_own = Ls, o_own = O;
+  M = -INFINITY;
+  Ls = 0.f;
+  O = 0.f;
+  constexpr int MB = 4;  // chunk records polled at once
+  for (int c0 = 0; c0 < P.C - 1; c0 += MB) {
+    const int nc = min(MB, P.C - 1 - c0);
+    uint64_t rm[MB], rl[MB], ro[MB];
+    uint32_t pend = 0;
+#pragma unroll
+    for (int k = 0; k < MB; ++k) {
+      if (k < nc) {
+        const uint64_t* rec = rec_base + size_t(g * P.C + c0 + k) * REC_WORDS + hh * 66;
+        rm[k] = ld_dev64(rec);
+        rl[k] = ld_dev64(rec + 1);
+        ro[k] = ld_dev64(rec + 2 + d);
+        pend |= 1u << k;
       }
-      const float Mn = fmaxf(M, mc);
-      const float a = M == -INFINITY ? 0.f : expf(M - Mn);
-      const float bsc = mc == -INFINITY ? 0.f : expf(mc - Mn);
-      Ls = Ls * a + lc * bsc;
-      O = O * a + oc * bsc;
-      M = Mn;
     }
-    C.put16(W::attn(l, b) + size_t(g * 3 + h) * 64 + d, O / Ls);
-    if (t == 0) trace_at(p, l, 5, p.n_layers);
+    Spin spin(p.ws, 5);
+    while (true) {
+#pragma unroll
+      for (int k = 0; k < MB; ++k)
+        if (((pend >> k) & 1u) && uint32_t(rm[k] >> 32) == C.tag32 && uint32_t(rl[k] >> 32) == C.tag32 &&
+            uint32_t(ro[k] >> 32) == C.tag32)
+          pend &= ~(1u << k);
+      if (!pend) break;
+      if (C.dead || !spin.again()) { C.dead = true; break; }
+#pragma unroll
+      for (int k = 0; k < MB; ++k) {
+        if ((pend >> k) & 1u) {
+          const uint64_t* rec = rec_base + size_t(g * P.C + c0 + k) * REC_WORDS + hh * 66;
+          rm[k] = ld_dev64(rec);
+          rl[k] = ld_dev64(rec + 1);
+          ro[k] = ld_dev64(rec + 2 + d);
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < MB; ++k)
+      if (k < nc)
+        merge(__uint_as_float(uint32_t(rm[k])), __uint_as_float(uint32_t(rl[k])), __uint_as_float(uint32_t(ro[k])));
   }
-  // append the new token's K (rotated) and V at slot_mapping[b]; slot < 0 skips
-  const long long slot = p.slot_mapping[b];
-  if (slot >= 0 && t < 128) {
-    uint16_t* cache = reinterpret_cast<uint16_t*>(p.kv[l]);
-    const long long blk = slot / 16, off = slot % 16;
-    const long long e = blk * p.block_stride + off * p.token_stride + (long long)g * p.head_stride +
-                        (t < 64 ? p.k_off : p.v_off) + (t & 63);
-    cache[e] = uint16_t(f2bf(t < 64 ? sm.knew[t] : sm.vnew[t - 64]));
-  }
+  if (w == 0 && lane == 0) trace_at(p, l, 20, p.n_layers);
+  merge(m_own, l_own, o_own);
+  st_dev(p.ws + W::attn(l, b) + size_t(g * 3 + hh) * 64 + d, C.w16(O / Ls));
+  if (w == 0 && lane == 0) trace_at(p, l, 5, p.n_layers);
 }
 
+// ------------------------------------------------------------------------------------------------
+// Consumer main loop
+// ------------------------------------------------------------------------------------------------
+
 template <class G>
-__device__ void consumer(const Params& p, const Plan<G>& P, Smem<G>& sm, uint32_t epoch) {
+__device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem<G>& sm, uint32_t epoch) {
   Consumer<G> C(p, P, sm, epoch);
   __builtin_amdgcn_s_barrier();  // pairs with the producer's barrier (blk[] ready)
   using W = WS<G>;
-  const int lane = C.lane;
+  using R = Rows<G>;
+  constexpr int GH = (G::H + NCT * 4 - 1) / (NCT * 4);   // poll groups per thread, H words
+  constexpr int GI = (G::I + NCT * 4 - 1) / (NCT * 4);   // ... I words
   const int b = 0;
   auto tr = [&](int l, int ev) { if (C.ct == 0) trace_at(p, l, ev, p.n_layers); };
   if (C.ct == 0 && p.trace)
-    p.trace[size_t(blockIdx.x) * (size_t(p.n_layers) * TR_EVENTS + TR_TAIL) + size_t(p.n_layers) * TR_EVENTS] = wall_clock64();
+    p.trace[size_t(blockIdx.x) * (size_t(p.n_layers) * TR_EVENTS + TR_TAIL) + size_t(p.n_layers) * TR_EVENTS] =
+        wall_clock64();
 
   for (int l = 0; l < p.n_layers; ++l) {
-    const LayerW Lw = p.layers[l];
     // ---------------- P1: RMSNorm(x) + QKV ----------------
-    {
-      const uint32_t seg = C.next_seg(seg_bytes(P, 0, 0));
-      const int nrows = P.q1 - P.q0;
-      C.wait_filled(seg + pad_pkt(seg_bytes(P, 0, 0)));
+    C.refresh();
+    if (P.q1 > P.q0) {
+      const uint32_t segn = C.next_seg(seg_bytes(P, S_NORM1, 0, p.cs_fp32));
+      const uint32_t seg = C.next_seg(seg_bytes(P, S_QKV, 0, p.cs_fp32));
+      C.wait_filled(C.pos);
       tr(l, 0);
-      uint4 w[Rows<G>::QKV][XRegs<G::H>::CPL];
-      int rows[Rows<G>::QKV];
-      const int nr = pull<G, G::H, Rows<G>::QKV>(C, seg, nrows, w, rows);
-      C.release(C.pos);
+      uint4 nw[Chunks<G::H>::CPL];
+      load_normw<G, G::H>(C, nw, segn);
+      float ss;
       if (l == 0) {
         const long long id = p.ids_i64 ? reinterpret_cast<const int64_t*>(p.input_ids)[b]
                                        : reinterpret_cast<const int32_t*>(p.input_ids)[b];
         const uint16_t* e = p.embed + size_t(id) * G::H;
-        for (int i = C.ct; i < G::H; i += NCT) sm.xs[i] = bf2f(e[i]);
+        float s = 0.f;
+        for (int i = C.ct; i < G::H; i += NCT) {
+          const float v = bf2f(e[i]);
+          sm.xs[i] = v;
+          sm.xkeep[i] = v;
+          s += v * v;
+        }
+        ss = wave_sum(s);
       } else {
-        C.poll_vec(W::x(l - 1, b), G::H, sm.xs);
+        ss = C.template poll_split<GH>(W::x(l - 1, b), G::H, sm.xs, sm.xkeep);
       }
-      C.cbar();
+      const float rs = rms_scale(C.block_total(ss), G::H);
       tr(l, 1);
-      for (int i = C.ct; i < G::H; i += NCT) sm.xkeep[i] = sm.xs[i];
-      const float rs = rms_scale(C.sumsq(sm.xs, G::H), G::H);
-      XRegs<G::H> xr;
-      load_x_norm<G::H>(xr, sm.xs, Lw.norm1, rs, lane);
-      float out[Rows<G>::QKV];
-      dots<G::H, Rows<G>::QKV>(w, xr, nr, lane, out);
-      if (lane == 0)
-        for (int r = 0; r < nr; ++r) C.put16(W::qkv(l, b) + P.q0 + rows[r], rnd(out[r]));
+      uint4 x[Chunks<G::H>::CPL];
+      load_x<G::H, true>(x, sm.xs, nw, rs, C.lane);
+      tr(l, 21);
+      float out[R::QKV];
+      dots_ring<G, G::H, R::QKV>(C, seg, P.q1 - P.q0, x, out);
+      C.release(C.pos);
+      tr(l, 22);
+      const int row = C.cw + NCW * C.lane;
+      if (C.lane < R::QKV && row < P.q1 - P.q0) st_dev(p.ws + W::qkv(l, b) + P.q0 + row, C.w16(pick(out, C.lane)));
       tr(l, 2);
     }
     // ---------------- P2: attention ----------------
+    C.refresh();
     {
-      const uint32_t seg = C.next_seg(seg_bytes(P, 1, 0));
-      if (P.att) attention(C, l, seg);
+      const uint32_t segc = C.next_seg(seg_bytes(P, S_CS, 0, p.cs_fp32));
+      const uint32_t seg = C.next_seg(seg_bytes(P, S_KV, 0, p.cs_fp32));
+      if (P.att) attention(C, l, segc, seg);
     }
     // ---------------- P3: O + residual ----------------
+    C.refresh();
     {
-      const uint32_t seg = C.next_seg(seg_bytes(P, 2, 0));
+      const uint32_t seg = C.next_seg(seg_bytes(P, S_O, 0, p.cs_fp32));
       const int nrows = P.o1 - P.o0;
-      C.wait_filled(C.pos);
-      uint4 w[Rows<G>::O][XRegs<G::H>::CPL];
-      int rows[Rows<G>::O];
-      const int nr = pull<G, G::H, Rows<G>::O>(C, seg, nrows, w, rows);
-      C.release(C.pos);
-      tr(l, 6);
-      C.poll_vec(W::attn(l, b), G::H, sm.xs);
-      C.cbar();
-      tr(l, 7);
-      XRegs<G::H> xr;
-      load_x<G::H>(xr, sm.xs, lane);
-      float out[Rows<G>::O];
-      dots<G::H, Rows<G>::O>(w, xr, nr, lane, out);
-      if (lane == 0)
-        for (int r = 0; r < nr; ++r) {
-          const int row = P.o0 + rows[r];
-          C.put16(W::h1(l, b) + row, sm.xkeep[row] + rnd(out[r]));
+      if (nrows > 0) {
+        C.wait_filled(C.pos);
+        tr(l, 6);
+        C.template poll_split<GH>(W::attn(l, b), G::H, sm.xs, nullptr);
+        C.cbar();
+        tr(l, 7);
+        uint4 x[Chunks<G::H>::CPL];
+        const uint4 none[Chunks<G::H>::CPL] = {};
+        load_x<G::H, false>(x, sm.xs, none, 1.f, C.lane);
+        float out[R::O];
+        dots_ring<G, G::H, R::O>(C, seg, nrows, x, out);
+        C.release(C.pos);
+        const int row = C.cw + NCW * C.lane;
+        if (C.lane < R::O && row < nrows) {
+          const int r = P.o0 + row;
+          st_dev(p.ws + W::h1(l, b) + r, C.w16(sm.xkeep[r] + rnd(pick(out, C.lane))));
         }
-      tr(l, 8);
+        tr(l, 8);
+      } else {
+        C.release(C.pos);
+      }
     }
     // ---------------- P4: RMSNorm(h1) + gate/up + SwiGLU ----------------
+    C.refresh();
     {
-      const uint32_t segg = C.next_seg(seg_bytes(P, 3, 0));
-      const uint32_t segu = C.next_seg(seg_bytes(P, 4, 0));
+      const uint32_t segn = C.next_seg(seg_bytes(P, S_NORM2, 0, p.cs_fp32));
+      const uint32_t segg = C.next_seg(seg_bytes(P, S_GATE, 0, p.cs_fp32));
+      const uint32_t segu = C.next_seg(seg_bytes(P, S_UP, 0, p.cs_fp32));
       const int na = P.a1 - P.a0;
       C.wait_filled(C.pos);
-      uint4 wg[Rows<G>::ACT][XRegs<G::H>::CPL];
-      uint4 wu[Rows<G>::ACT][XRegs<G::H>::CPL];
-      int rows[Rows<G>::ACT];
-      const int nr = pull<G, G::H, Rows<G>::ACT>(C, segg, na, wg, rows);
-      pull<G, G::H, Rows<G>::ACT>(C, segu, na, wu, rows);
-      C.release(C.pos);
+      uint4 nw[Chunks<G::H>::CPL];
+      load_normw<G, G::H>(C, nw, segn);
       tr(l, 9);
-      C.poll_vec(W::h1(l, b), G::H, sm.xs);
-      C.cbar();
+      const float ss = C.template poll_split<GH>(W::h1(l, b), G::H, sm.xs, sm.h1keep);
+      const float rs = rms_scale(C.block_total(ss), G::H);
       tr(l, 10);
-      for (int i = C.ct; i < G::H; i += NCT) sm.h1keep[i] = sm.xs[i];
-      const float rs = rms_scale(C.sumsq(sm.xs, G::H), G::H);
-      XRegs<G::H> xr;
-      load_x_norm<G::H>(xr, sm.xs, Lw.norm2, rs, lane);
-      float og[Rows<G>::ACT], ou[Rows<G>::ACT];
-      dots<G::H, Rows<G>::ACT>(wg, xr, nr, lane, og);
-      dots<G::H, Rows<G>::ACT>(wu, xr, nr, lane, ou);
-      if (lane == 0)
-        for (int r = 0; r < nr; ++r) {
-          const float gv = rnd(og[r]), uv = rnd(ou[r]);
-          const float silu = rnd(gv / (1.0f + expf(-gv)));
-          C.put16(W::act(l, b) + P.a0 + rows[r], silu * uv);
-        }
+      uint4 x[Chunks<G::H>::CPL];
+      load_x<G::H, true>(x, sm.xs, nw, rs, C.lane);
+      float og[R::ACT], ou[R::ACT];
+      dots_ring<G, G::H, R::ACT>(C, segg, na, x, og);
+      dots_ring<G, G::H, R::ACT>(C, segu, na, x, ou);
+      C.release(C.pos);
+      const int row = C.cw + NCW * C.lane;
+      if (C.lane < R::ACT && row < na) {
+        const float gv = rnd(pick(og, C.lane)), uv = rnd(pick(ou, C.lane));
+        const float silu = rnd(gv / (1.0f + expf(-gv)));
+        st_dev(p.ws + W::act(l, b) + P.a0 + row, C.w16(silu * uv));
+      }
       tr(l, 11);
     }
     // ---------------- P5: down + residual ----------------
+    C.refresh();
     {
-      const uint32_t seg = C.next_seg(seg_bytes(P, 5, 0));
+      const uint32_t seg = C.next_seg(seg_bytes(P, S_DOWN, 0, p.cs_fp32));
       const int nrows = P.d1 - P.d0;
       C.wait_filled(C.pos);
-      uint4 w[Rows<G>::DOWN][XRegs<G::I>::CPL];
-      int rows[Rows<G>::DOWN];
-      const int nr = pull<G, G::I, Rows<G>::DOWN>(C, seg, nrows, w, rows);
-      C.release(C.pos);
       tr(l, 12);
-      C.poll_vec(W::act(l, b), G::I, sm.xs);
+      C.template poll_split<GI>(W::act(l, b), G::I, sm.xs, nullptr);
       C.cbar();
       tr(l, 13);
-      XRegs<G::I> xr;
-      load_x<G::I>(xr, sm.xs, lane);
-      float out[Rows<G>::DOWN];
-      dots<G::I, Rows<G>::DOWN>(w, xr, nr, lane, out);
-      if (lane == 0)
-        for (int r = 0; r < nr; ++r) {
-          const int row = P.d0 + rows[r];
-          const float y = rnd(sm.h1keep[row] + rnd(out[r]));
-          C.put16(W::x(l, b) + row, y);
-          if (p.layer_outputs) p.layer_outputs[(size_t(l) * p.B + b) * G::H + row] = uint16_t(f2bf(y));
-        }
+      uint4 x[Chunks<G::I>::CPL];
+      const uint4 none[Chunks<G::I>::CPL] = {};
+      load_x<G::I, false>(x, sm.xs, none, 1.f, C.lane);
+      float out[R::DOWN];
+      dots_ring<G, G::I, R::DOWN>(C, seg, nrows, x, out);
+      C.release(C.pos);
+      const int row = C.cw + NCW * C.lane;
+      if (C.lane < R::DOWN && row < nrows) {
+        const int r = P.d0 + row;
+        const float y = rnd(sm.h1keep[r] + rnd(pick(out, C.lane)));
+        st_dev(p.ws + W::x(l, b) + r, C.w16(y));
+        if (p.layer_outputs) p.layer_outputs[(size_t(l) * p.B + b) * G::H + r] = uint16_t(f2bf(y));
+      }
       tr(l, 14);
     }
   }
   // ---------------- final RMSNorm + LM head + argmax ----------------
-  C.poll_vec(W::x(p.n_layers - 1, b), G::H, sm.xs);
-  C.cbar();
-  const float rs = rms_scale(C.sumsq(sm.xs, G::H), G::H);
-  XRegs<G::H> xr;
-  load_x_norm<G::H>(xr, sm.xs, p.final_norm, rs, lane);
+  const uint32_t segf = C.next_seg(seg_bytes(P, S_FNORM, 0, p.cs_fp32));
+  C.wait_filled(C.pos);
+  uint4 nw[Chunks<G::H>::CPL];
+  load_normw<G, G::H>(C, nw, segf);
+  C.release(C.pos);
+  const float ss = C.template poll_split<GH>(W::x(p.n_layers - 1, b), G::H, sm.xs, nullptr);
+  const float rs = rms_scale(C.block_total(ss), G::H);
+  uint4 x[Chunks<G::H>::CPL];
+  load_x<G::H, true>(x, sm.xs, nw, rs, C.lane);
   if (P.wg == 0) {
     // final-normed hidden state (the reference's out_hidden, block360_kernel.inc:810-815)
-    for (int i = C.ct; i < G::H; i += NCT)
-      p.out_hidden[size_t(b) * G::H + i] =
-          uint16_t(f2bf(rnd(bf2f(p.final_norm[i]) * rnd(sm.xs[i] * rs))));
+#pragma unroll
+    for (int c = 0; c < Chunks<G::H>::CPL; ++c) {
+      const int ch = C.lane + 64 * c;
+      if (C.cw == 0 && ch < Chunks<G::H>::CH)
+        *reinterpret_cast<uint4*>(p.out_hidden + size_t(b) * G::H + ch * 8) = x[c];
+    }
   }
   if (!p.lm_head) return;
   float best = -INFINITY;
   int best_i = 0x7fffffff;
   for (int j = 0; j < P.n_lm; ++j) {
-    const uint32_t seg = C.next_seg(seg_bytes(P, 6, j));
+    const uint32_t seg = C.next_seg(seg_bytes(P, S_LM, j, p.cs_fp32));
     const int r0 = P.v0 + j * LM_ROWS;
     const int nrows = min(LM_ROWS, P.v1 - r0);
     C.wait_filled(C.pos);
-    constexpr int MR = LM_ROWS / NCW;
-    uint4 w[MR][XRegs<G::H>::CPL];
-    int rows[MR];
-    const int nr = pull<G, G::H, MR>(C, seg, nrows, w, rows);
+    float out[R::LM];
+    dots_ring<G, G::H, R::LM>(C, seg, nrows, x, out);
     C.release(C.pos);
-    float out[MR];
-    dots<G::H, MR>(w, xr, nr, lane, out);
-    for (int r = 0; r < nr; ++r) {
-      const float v = rnd(out[r]);
-      const int idx = r0 + rows[r];
-      if (lane == 0 && p.out_logits) p.out_logits[size_t(b) * G::V + idx] = uint16_t(f2bf(v));
-      if (v > best || (v == best && idx < best_i)) { best = v; best_i = idx; }
+#pragma unroll
+    for (int r = 0; r < R::LM; ++r) {
+      const int row = C.cw + NCW * r;
+      if (row < nrows) {
+        const float v = rnd(out[r]);
+        const int idx = r0 + row;
+        if (v > best || (v == best && idx < best_i)) { best = v; best_i = idx; }
+      }
+    }
+    if (p.out_logits) {
+      const int row = C.cw + NCW * C.lane;
+      if (C.lane < R::LM && row < nrows)
+        p.out_logits[size_t(b) * G::V + r0 + row] = uint16_t(f2bf(pick(out, C.lane)));
     }
   }
-  if (lane == 0) { sm.lm_val[C.cw] = best; sm.lm_idx[C.cw] = best_i; }
+  if (C.lane == 0) { sm.lm_val[C.cw] = best; sm.lm_idx[C.cw] = best_i; }
   C.cbar();
   if (C.ct == 0 && p.trace)
-    p.trace[size_t(blockIdx.x) * (size_t(p.n_layers) * TR_EVENTS + TR_TAIL) + size_t(p.n_layers) * TR_EVENTS + 1] = wall_clock64();
+    p.trace[size_t(blockIdx.x) * (size_t(p.n_layers) * TR_EVENTS + TR_TAIL) + size_t(p.n_layers) * TR_EVENTS + 1] =
+        wall_clock64();
   if (C.ct == 0) {
     float bv = sm.lm_val[0];
     int bi = sm.lm_idx[0];
@@ -1003,11 +1244,10 @@ __device__ void consumer(const Params& p, const Plan<G>& P, Smem<G>& sm, uint32_
   for (int q = C.ct; q < NWG; q += NCT) {
     const uint64_t* src = reinterpret_cast<const uint64_t*>(p.ws + W::lm(b, q));
     Spin spin(p.ws, 6);
-    uint64_t r;
-    while (true) {
-      r = ld_dev64(src);
-      if (uint32_t(r >> 32) == C.tag32) break;
+    uint64_t r = ld_dev64(src);
+    while (uint32_t(r >> 32) != C.tag32) {
       if (C.dead || !spin.again()) { C.dead = true; break; }
+      r = ld_dev64(src);
     }
     const float v = bf2f(uint32_t(r) & 0xffffu);
     const int i = int((uint32_t(r) >> 16) & 0xffffu);
@@ -1019,7 +1259,7 @@ __device__ void consumer(const Params& p, const Plan<G>& P, Smem<G>& sm, uint32_
     const int oi = __shfl_xor(bi, o);
     if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
   }
-  if (lane == 0) { sm.lm_val[C.cw] = bv; sm.lm_idx[C.cw] = bi; }
+  if (C.lane == 0) { sm.lm_val[C.cw] = bv; sm.lm_idx[C.cw] = bi; }
   C.cbar();
   if (C.ct == 0) {
     bv = sm.lm_val[0];
@@ -1039,16 +1279,21 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel(Params p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
   Smem<G>& sm = *reinterpret_cast<Smem<G>*>(smem_raw);
   if (threadIdx.x == 0) {
-    sm.filled = 0;
+    for (int w = 0; w < NPW; ++w) sm.front[w] = 0;
     for (int w = 0; w < NCW; ++w) sm.consumed[w] = 0;
     sm.cbar = 0;
+  }
+  // pointer tables into LDS, so the producers never wait on a vector-memory load of their own
+  for (int i = threadIdx.x; i < p.n_layers; i += WG_THREADS) {
+    sm.lw[i] = p.layers[i];
+    sm.kvp[i] = p.kv[i];
   }
   __syncthreads();
   Plan<G> P;
   P.init(p, blockIdx.x);
   uint32_t epoch = ld_dev(p.ws + HDR_EPOCH) + 1u;
   if (epoch == 0) epoch = 1;
-  if (threadIdx.x < 64) producer<G>(p, P, sm);
+  if (threadIdx.x < 64 * NPW) producer<G>(p, P, sm);
   else consumer<G>(p, P, sm, epoch);
   __syncthreads();
   if (blockIdx.x == 0 && threadIdx.x == 0) st_dev(p.ws + HDR_EPOCH, epoch);
@@ -1056,6 +1301,8 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel(Params p) {
 
 template <class G>
 constexpr size_t lds_bytes() { return sizeof(Smem<G>); }
+static_assert(sizeof(Smem<G360>) <= 160 * 1024, "LDS budget of one gfx950 workgroup");
+static_assert(sizeof(Smem<G135>) <= 160 * 1024, "LDS budget of one gfx950 workgroup");
 
 struct DeviceInfo {
   int ok = 0, status = 0, cus = 0, coop = 0, max_lds = 0, gfx950 = 0;
@@ -1079,16 +1326,37 @@ static DeviceInfo query_device() {
   return d;
 }
 
+// Per-device launch state: properties are queried and the LDS attribute set once per device.
+template <class G>
+struct LaunchCache {
+  static constexpr int MAX_DEV = 64;
+  int ready[MAX_DEV] = {};
+  int status[MAX_DEV] = {};
+};
+
 template <class G>
 static int launch(const Params& p, hipStream_t stream) {
-  const DeviceInfo d = query_device();
-  if (!d.ok) return d.status;
-  if (!d.gfx950) return PK_ERR_ARCH;
-  if (!d.coop) return PK_ERR_COOP;
-  if (d.cus < NWG || size_t(d.max_lds) < lds_bytes<G>()) return PK_ERR_RESIDENCY;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<G>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes<G>()));
+  static LaunchCache<G> cache;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= LaunchCache<G>::MAX_DEV) return PK_ERR_RESIDENCY;
+  if (!cache.ready[dev]) {
+    const DeviceInfo d = query_device();
+    int st = 0;
+    if (!d.ok) st = d.status;
+    else if (!d.gfx950) st = PK_ERR_ARCH;
+    else if (!d.coop) st = PK_ERR_COOP;
+    else if (d.cus < NWG || size_t(d.max_lds) < lds_bytes<G>()) st = PK_ERR_RESIDENCY;
+    else {
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<G>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes<G>()));
+      if (e != hipSuccess) st = e;
+    }
+    cache.status[dev] = st;
+    cache.ready[dev] = 1;
+  }
+  if (cache.status[dev]) return cache.status[dev];
   Params q = p;
   void* args[] = {&q};
   e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(decode_kernel<G>), dim3(NWG),
@@ -1161,6 +1429,25 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
 // Diagnostics: per-phase wall-clock timestamps for the next launches (NULL disables).
 // Layout: [256 workgroups][n_layers * 16 + 4] uint64.
 extern "C" void pk_set_trace(void* buf) { pk::g_trace = reinterpret_cast<unsigned long long*>(buf); }
+
+// Workspace in fine-grained device memory (lower cross-XCD round trip for the exchange words).
+// Zero-initialised.  kind 0: ordinary (coarse-grained) device memory, 1: fine-grained.
+extern "C" void* pk_workspace_alloc(size_t bytes, int kind) {
+  void* ptr = nullptr;
+  hipError_t e = kind == 1 ? hipExtMallocWithFlags(&ptr, bytes, hipDeviceMallocFinegrained) : hipMalloc(&ptr, bytes);
+  if (e != hipSuccess) return nullptr;
+  if (hipMemset(ptr, 0, bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+    (void)hipFree(ptr);
+    return nullptr;
+  }
+  return ptr;
+}
+extern "C" int pk_workspace_free(void* ptr) { return hipFree(ptr); }
+// Copy n 32-bit words of a workspace (header words: 0 epoch, 1 abort flag, 2 abort site) to host.
+extern "C" int pk_workspace_read(const void* ws, size_t word, unsigned* out, int n) {
+  const hipError_t e = hipMemcpy(out, reinterpret_cast<const unsigned*>(ws) + word, size_t(n) * 4, hipMemcpyDeviceToHost);
+  return e;
+}
 
 extern "C" size_t pk_workspace_bytes(int model) {
   if (model == PK_MODEL_SMOLLM2_360M) return pk::WS<pk::G360>::TOTAL * 4;
