@@ -1,0 +1,124 @@
+"""Shared helpers for the GPU parity tests: identical inputs for the HIP kernel and the CPU oracle.
+
+Weights and paged KV caches are built on the CPU (seeded), the oracle (oracle/smollm2.py) runs on
+those CPU tensors, and the kernel runs on GPU copies of the very same bits.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from oracle import smollm2 as O
+
+BF16 = torch.bfloat16
+LOGIT_ATOL = 2e-2      # north-star tolerance on bf16 logits (max abs err)
+COS_MIN = 0.9999       # north-star cosine similarity on logits
+
+
+def module_for(geom: O.Geometry):
+    import prime_kernels_amd as pk
+
+    return pk.load("decode_megakernel_360m" if geom.hidden == 960 else "decode_megakernel")
+
+
+class Case:
+    """One decode step's inputs, on CPU (oracle) and GPU (kernel)."""
+
+    def __init__(self, geom: O.Geometry, w: O.Weights, kv: O.PagedKV, max_pos: int, dev="cuda:0"):
+        self.geom, self.w, self.kv = geom, w, kv
+        self.cos_sin = O.rope_cos_sin(max_pos, geom.head_dim, geom.theta)
+        self.dev = torch.device(dev)
+        self.wd = w.to(self.dev)
+        self.kvd = [c.to(self.dev) for c in kv.caches]
+        self.btd = kv.block_table.to(self.dev)
+        self.csd = self.cos_sin.to(self.dev)
+        self.mod = module_for(geom)
+
+    def sync_kv_from_oracle(self) -> None:
+        for g, c in zip(self.kvd, self.kv.caches):
+            g.copy_(c)
+
+    def kernel_step(self, ids, positions, seq_lens=None, slot_mapping=None, *, logits=True, layer_outputs=False,
+                    ids_dtype=torch.int64, cs_fp32=False):
+        B = len(ids)
+        dev = self.dev
+        pos = torch.tensor(positions, dtype=torch.int64, device=dev)
+        sl = torch.tensor(seq_lens if seq_lens is not None else [p + 1 for p in positions], dtype=torch.int32, device=dev)
+        if slot_mapping is None:
+            slot_mapping = [self.kv.slot(b, int(sl[b]) - 1) for b in range(B)]
+        slots = torch.tensor(slot_mapping, dtype=torch.int64, device=dev)
+        lg = torch.empty((B, self.geom.vocab), dtype=BF16, device=dev) if logits else None
+        lo = torch.empty((self.geom.layers, B, self.geom.hidden), dtype=BF16, device=dev) if layer_outputs else None
+        cs = self.csd.float().contiguous() if cs_fp32 else self.csd
+        hid, out_ids = self.mod.decode_step(
+            input_ids=torch.tensor(ids, dtype=ids_dtype, device=dev), positions=pos, seq_lens=sl,
+            block_table=self.btd, slot_mapping=slots, embed=self.wd.embed, layers=self.wd.layers,
+            final_norm=self.wd.final_norm, kv_caches=self.kvd, cos_sin_cache=cs, eps=1e-5,
+            num_layers=self.geom.layers, return_token_ids=True, logits_out=lg, layer_outputs=lo)
+        torch.cuda.synchronize()
+        rt = self.mod.workspace(dev)
+        assert rt.abort_word() == 0, "kernel abandoned a bounded wait"
+        res = {"hidden": hid.clone().cpu(), "ids": out_ids.clone().cpu()}
+        if logits:
+            res["logits"] = lg.cpu()
+        if layer_outputs:
+            res["layer_outputs"] = lo.cpu()
+        return res
+
+    def oracle_step(self, ids, positions, seq_lens=None, slot_mapping=None, layer_outputs=False):
+        return O.decode_step(self.w, ids, positions, self.kv, self.cos_sin, seq_lens=seq_lens,
+                             slot_mapping=slot_mapping, layer_outputs=layer_outputs)
+
+
+def compare_logits(k: torch.Tensor, r: torch.Tensor) -> dict:
+    kf, rf = k.float(), r.float()
+    err = (kf - rf).abs().max().item()
+    cos = torch.nn.functional.cosine_similarity(kf.flatten(), rf.flatten(), dim=0).item()
+    return {"max_abs": err, "cos": cos}
+
+
+def greedy_ok(kernel_id: int, ref_logits: torch.Tensor, tol: float = LOGIT_ATOL) -> bool:
+    """Greedy id matches the oracle's argmax, or the oracle itself has a near-tie (top-1 minus the
+    kernel's pick within the logit tolerance), which bf16-tolerance parity cannot resolve."""
+    ref = ref_logits.float()
+    best = int(torch.argmax(ref))
+    if kernel_id == best:
+        return True
+    return (ref[best] - ref[kernel_id]).item() <= tol
+
+
+def random_kv_case(geom: O.Geometry, seed: int, contexts, *, max_pos: int | None = None, norm_jitter=0.05,
+                   fill_seed: int | None = None, extra_blocks: int = 0) -> Case:
+    w = O.make_weights(geom, seed, norm_jitter=norm_jitter)
+    cap = max(contexts) + 16
+    kv = O.make_paged_kv(geom, len(contexts), cap, seed=fill_seed if fill_seed is not None else seed + 3,
+                         extra_blocks=extra_blocks)
+    return Case(geom, w, kv, max_pos or cap + 16)
+
+
+def assert_step_parity(kres: dict, rres: dict, label: str = "") -> dict:
+    out = {}
+    for b in range(kres["hidden"].shape[0]):
+        c = compare_logits(kres["logits"][b], rres["logits"][b])
+        assert c["max_abs"] <= LOGIT_ATOL, f"{label} b={b} logits max abs err {c['max_abs']}"
+        assert c["cos"] >= COS_MIN, f"{label} b={b} logits cosine {c['cos']}"
+        h = compare_logits(kres["hidden"][b], rres["hidden"][b])
+        assert h["cos"] >= COS_MIN, f"{label} b={b} hidden cosine {h['cos']}"
+        assert greedy_ok(int(kres["ids"][b]), rres["logits"][b]), \
+            f"{label} b={b} greedy id {int(kres['ids'][b])} vs oracle {int(rres['ids'][b])}"
+        out[b] = c
+    return out
+
+
+def ulp_distance(a: torch.Tensor, b: torch.Tensor) -> int:
+    return O.max_ulp(a, b)
+
+
+def finite(t: torch.Tensor) -> bool:
+    return bool(torch.isfinite(t.float()).all())
+
+
+__all__ = ["Case", "compare_logits", "greedy_ok", "random_kv_case", "assert_step_parity", "LOGIT_ATOL",
+           "COS_MIN", "math"]

@@ -1,0 +1,127 @@
+"""CPU-side checks of the package: registry surface, manifest, the C ABI library's exports and its
+argument validation (which returns before any GPU call), and the wrapper's contract errors."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import prime_kernels_amd as pk
+from prime_kernels_amd import _native, _spec
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "prime_decode.h"
+
+
+def test_registry_surface():
+    assert pk.KERNELS == ("decode_megakernel_360m", "decode_megakernel")
+    s = pk.spec("decode_megakernel_360m")
+    assert s.module == "prime_kernels_amd.decode_megakernel_360m"
+    assert [str(a) for a in s.archs] == ["gfx950"] and s.ops == "prime_decode"
+    assert s.supports("gfx950:sramecc+:xnack-") and not s.supports("gfx942:sramecc+:xnack-")
+    with pytest.raises(KeyError):
+        pk.spec("flash_moe")
+    st = pk.status()
+    assert set(st) == set(pk.KERNELS)
+    if not torch.cuda.is_available():
+        assert all("HIP device" in v or "not compiled" in v for v in st.values())
+        with pytest.raises(RuntimeError):
+            pk.load("decode_megakernel_360m")
+
+
+def test_arch_parse():
+    assert str(_spec.Arch.parse("gfx950")) == "gfx950"
+    with pytest.raises(ValueError):
+        _spec.Arch.parse("8.9")
+
+
+def _header_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b([a-z_0-9]+)\s*\(", text)) - {"defined"})
+
+
+def test_library_exports_every_header_symbol():
+    lib = _native.library()
+    names = _header_functions()
+    assert "decode360" in names and "mk_decode" in names and "pk_decode" in names
+    for name in names:
+        assert hasattr(lib, name), f"libprime_decode.so does not export {name}"
+    assert set(names) <= set(_native.SIGNATURES), "ctypes signatures missing for a header function"
+
+
+def test_status_strings_and_sizes():
+    lib = _native.library()
+    want = {9101: "batch_out_of_range", 9103: "null_device_pointer", 9104: "cooperative_launch_unsupported",
+            9106: "kernel_requires_gfx950", 9107: "kv_offsets_or_pointers_not_16_byte_aligned",
+            9108: "scratch_or_debug_buffer_too_small", 9109: "block_size_or_stride_invalid"}
+    for code, s in want.items():
+        assert lib.decode360_status_string(code).decode() == s
+        assert lib.mk_status_string(code).decode() == s
+    assert lib.decode360_workspace_bytes() == lib.pk_workspace_bytes(360) > 0
+    assert lib.mk_workspace_bytes(1, 1024) == lib.pk_workspace_bytes(135) > 0
+    assert lib.pk_workspace_bytes(7) == 0
+    assert lib.decode360_debug_bytes() == 0
+
+
+def _args(**over):
+    """A pk_decode argument list with plausible (fake, never dereferenced) pointers."""
+    a = dict(stream=None, model=360, B=1, n_layers=32, input_ids=16, ids_i64=1, embed=16, final_norm=16,
+             positions=16, seq_lens=16, block_table=16, bt_stride=64, slot_mapping=16, layers=16, kv=16,
+             k_off=0, v_off=64, block_stride=10240, token_stride=128, head_stride=2048, block_size=16,
+             cos_sin=16, cs_fp32=0, out_hidden=16, layer_outputs=None, out_ids=None, out_logits=None,
+             scratch=16, scratch_bytes=1 << 40, max_seq_len=1024)
+    a.update(over)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(B=0), 9101), (dict(B=2), 9101), (dict(n_layers=0), 9110), (dict(n_layers=33), 9110),
+    (dict(model=7), 9110), (dict(max_seq_len=0), 9102), (dict(max_seq_len=1 << 20), 9102),
+    (dict(embed=None), 9103), (dict(scratch=None), 9103), (dict(scratch_bytes=1024), 9108),
+    (dict(block_size=32), 9109), (dict(bt_stride=1), 9109), (dict(k_off=4), 9107),
+    (dict(embed=24), 9107), (dict(out_logits=8), 9107),
+])
+def test_pk_decode_rejects_bad_arguments_without_gpu(over, code):
+    lib = _native.library()
+    assert lib.pk_decode(*_args(**over)) == code
+
+
+def test_reference_abi_validation():
+    lib = _native.library()
+    vp = 16
+    base = [None, 1, vp, vp, vp, vp, vp, vp, 64, vp, vp, vp, 0, 64, 10240, 128, 2048, 16, vp, 0, vp, None, vp,
+            1 << 40, None, 0, 1024, -1]
+    bad = list(base); bad[1] = 3
+    assert lib.decode360(*bad) == 9101
+    bad = list(base); bad[-1] = 40
+    assert lib.decode360(*bad) == 9109
+    bad = list(base); bad[24] = vp
+    assert lib.decode360(*bad) == 9111
+    mk = [None, 5, vp, 1, vp, vp, vp, 64, vp, vp, vp, vp, vp, 0, 64, 10240, 128, 2048, 16, vp, 0, vp, vp, 1 << 40, 1024]
+    assert lib.mk_decode(*mk) == 9101
+
+
+def test_wrapper_contract_errors_on_cpu_tensors():
+    from prime_kernels_amd import decode_megakernel_360m as m
+    z = torch.zeros(1, dtype=torch.int64)
+    kw = dict(input_ids=z, positions=z, seq_lens=z.int(), block_table=torch.zeros(1, 4, dtype=torch.int32),
+              slot_mapping=z, embed=torch.zeros(1), layers=[()] * 32, final_norm=torch.zeros(960),
+              kv_caches=[torch.zeros(1)] * 32, cos_sin_cache=torch.zeros(4, 64), eps=1e-5)
+    with pytest.raises(ValueError, match="CUDA tensor"):
+        m.decode_step(**kw)
+    with pytest.raises(ValueError, match="rms eps"):
+        m.decode_step(**dict(kw, eps=1e-6))
+    with pytest.raises(ValueError, match="batch"):
+        m.decode_step(**dict(kw, input_ids=torch.zeros(2, dtype=torch.int64)))
+    with pytest.raises(ValueError, match="layers"):
+        m.decode_step(**dict(kw, layers=[()] * 3))
+
+
+def test_manifest_lists_built_sources():
+    for name in pk.KERNELS:
+        s = pk.spec(name)
+        assert all(src.is_file() for src in s.sources)
+        assert (pk.LIB_DIR / s.library).is_file(), "run __graft_entry__.build() first"
