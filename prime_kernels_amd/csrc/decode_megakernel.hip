@@ -11,8 +11,9 @@
 // Phases per layer (the reference's eight grid barriers per layer, block360_kernel.inc:96-803,
 // become data-flow edges):
 //   P1 RMSNorm(x) + QKV GEMV             -> qkv (pre-RoPE, bf16)
-//   P2 RoPE + GQA attention partials over a KV chunk; chunk leaders merge (log-sum-exp)
-//                                         -> attn (bf16)
+//   P2 RoPE + GQA attention over KV chunks: chunk softmax statistics are exchanged so every
+//      probability is rounded with the global max and sum, as HF does; chunk leaders add the
+//      fp32 partial sums of p.v                  -> attn (bf16)
 //   P3 O GEMV + residual                  -> h1
 //   P4 RMSNorm(h1) + gate/up GEMV + SwiGLU -> act
 //   P5 down GEMV + residual               -> x (layer output)
@@ -61,7 +62,8 @@ constexpr int TC_MAX = 256;              // max cached tokens per attention chun
 constexpr int TC_TARGET = 64;            // preferred tokens per chunk
 constexpr int LM_ROWS = 16;              // LM-head rows per ring segment
 constexpr int MAX_B = 16;                // exchange-buffer slots per layer
-constexpr int REC_WORDS = 3 * 66;        // attention partial: 3 heads x (m, l, o[64]), 64-bit words
+constexpr int REC_WORDS = 3 * 64;        // attention partial: 3 heads x sum(p.v)[64], 64-bit words
+constexpr int STAT_WORDS = 6;            // chunk softmax statistics: 3 heads x (max, sum), 64-bit words
 constexpr uint32_t SPIN_LIMIT = 1u << 22;
 constexpr int kMaxSeq = 12288;          // tokens per sequence (block_table capacity)
 
@@ -113,7 +115,9 @@ struct WS {
   static constexpr size_t LAYER = PER_B * MAX_B;
   static constexpr size_t REC0 = HDR_WORDS + LAYER * G::L;
   static constexpr size_t REC_LAYER = size_t(NWG) * REC_WORDS * 2;
-  static constexpr size_t LM0 = REC0 + REC_LAYER * G::L;
+  static constexpr size_t STAT0 = REC0 + REC_LAYER * G::L;
+  static constexpr size_t STAT_LAYER = size_t(NWG) * STAT_WORDS * 2;
+  static constexpr size_t LM0 = STAT0 + STAT_LAYER * G::L;
   static constexpr size_t TOTAL = LM0 + size_t(MAX_B) * NWG * 2;
   __device__ static size_t qkv(int l, int b) { return HDR_WORDS + l * LAYER + b * PER_B; }
   __device__ static size_t attn(int l, int b) { return qkv(l, b) + G::QKV; }
@@ -121,6 +125,7 @@ struct WS {
   __device__ static size_t act(int l, int b) { return h1(l, b) + G::H; }
   __device__ static size_t x(int l, int b) { return act(l, b) + G::I; }
   __device__ static size_t rec(int l, int item) { return REC0 + l * REC_LAYER + size_t(item) * REC_WORDS * 2; }
+  __device__ static size_t stat(int l, size_t item) { return STAT0 + l * STAT_LAYER + item * STAT_WORDS * 2; }
   __device__ static size_t lm(int b, int wg) { return LM0 + (size_t(b) * NWG + wg) * 2; }
 };
 
@@ -789,10 +794,12 @@ __device__ __forceinline__ float rms_scale(float sumsq, int n) {
 // P2: attention for one chunk (batch 1).  The chunk's tokens (cached ones, plus the new one for the
 // leader) are split over the 4 consumer waves in even-aligned ranges; each wave handles all 3 query
 // heads of KV head g for its tokens: RoPE on the queries (and the new key), scores with bf16 dot2,
-// a per-wave softmax partial, and P.V with bf16 probabilities (HF rounds the probabilities to bf16
-// before P.V, modeling_llama.py:207-208).  One barrier merges the waves; wave h < 3 then owns head
-// 3g+h: it writes the chunk's partial record (non-leader) or merges all chunks of KV head g by
-// log-sum-exp (leader).  The leader's wave 3 appends the new K/V (block360_kernel.inc:124-135).
+// the chunk's softmax max and sum of exp, exchanged between the C chunks of KV head g, so each
+// probability is bf16(exp(s - M) / L) with the max M and sum L over all tokens, exactly the values
+// HF rounds to bf16 before P.V (softmax in fp32, then .to(bf16): modeling_llama.py:207-208).  Then
+// P.V with bf16 dot2; one barrier adds the waves' fp32 partials; wave h < 3 owns head 3g+h: it
+// writes the chunk's partial record (non-leader), or adds all chunks of KV head g in chunk order
+// and rounds once (leader).  The leader's wave 3 appends the new K/V (block360_kernel.inc:124-135).
 // ------------------------------------------------------------------------------------------------
 
 template <class G>
@@ -885,24 +892,93 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   }
   wait_lgkm0();
   if (w == 0 && lane == 0) trace_at(p, l, 17, p.n_layers);
-  // softmax partial of this wave's tokens: m = max s, p = exp(s - m) (bf16 for P.V), l = sum exp
-  float m3[3], l3[3];
+  // chunk softmax statistics per head: max and sum of exp over this wave's tokens, then over the
+  // chunk (all waves), then over all chunks of KV head g (one exchange of 3 x (max, sum) records)
 #pragma unroll
   for (int h = 0; h < 3; ++h) {
     float m = -INFINITY;
     for (int j = j0 + lane; j < j1; j += 64) m = fmaxf(m, sm.at.sc[h][j]);
     m = wave_max(m);
     float ls = 0.f;
-    for (int j = j0 + lane; j < j1; j += 64) {
-      const float e = expf(sm.at.sc[h][j] - m);
-      sm.at.pb[h][j] = uint16_t(f2bf(e));
-      ls += e;
+    for (int j = j0 + lane; j < j1; j += 64) ls += expf(sm.at.sc[h][j] - m);
+    ls = wave_sum(ls);
+    if (lane == 0) { sm.wml[w][0][h] = m; sm.wml[w][1][h] = ls; }
+  }
+  C.cbar();
+  float Mh[3], Lh[3];
+#pragma unroll
+  for (int h = 0; h < 3; ++h) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < NCW; ++v) m = fmaxf(m, sm.wml[v][0][h]);
+    float ls = 0.f;
+#pragma unroll
+    for (int v = 0; v < NCW; ++v) {
+      const float mv = sm.wml[v][0][h];
+      ls += mv == -INFINITY ? 0.f : sm.wml[v][1][h] * expf(mv - m);
     }
-    m3[h] = m;
-    l3[h] = wave_sum(ls);
+    Mh[h] = m;
+    Lh[h] = ls;
+  }
+  const uint64_t tg = uint64_t(C.tag32) << 32;
+  if (P.C > 1) {
+    uint64_t* stat_base = reinterpret_cast<uint64_t*>(p.ws + W::stat(l, size_t(g) * P.C));
+    if (w == 0 && lane < 6) {
+      const int h = lane >> 1;
+      const float v = (lane & 1) ? (h == 0 ? Lh[0] : h == 1 ? Lh[1] : Lh[2]) : (h == 0 ? Mh[0] : h == 1 ? Mh[1] : Mh[2]);
+      st_dev64(stat_base + size_t(P.c) * STAT_WORDS + lane, tg | __float_as_uint(v));
+    }
+    // lane k polls chunk k (and k + 64): 3 x 16 bytes = (m, l) of the 3 heads
+    const __amdgpu_buffer_rsrc_t r = rsrc(stat_base);
+    u32x4 s[2][3];
+    uint32_t pend = 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int k = lane + 64 * i;
+      if (k < P.C) {
+#pragma unroll
+        for (int h = 0; h < 3; ++h) s[i][h] = ld_dev128(r, uint32_t(k * STAT_WORDS + 2 * h) * 8u);
+        pend |= 1u << i;
+      }
+    }
+    auto fresh = [&](const u32x4& v) { return v.y == C.tag32 && v.w == C.tag32; };
+    Spin spin(p.ws, 6);
+    while (true) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        if (((pend >> i) & 1u) && fresh(s[i][0]) && fresh(s[i][1]) && fresh(s[i][2])) pend &= ~(1u << i);
+      if (!pend) break;
+      if (C.dead || !spin.again()) { C.dead = true; break; }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        if ((pend >> i) & 1u)
+#pragma unroll
+          for (int h = 0; h < 3; ++h) s[i][h] = ld_dev128(r, uint32_t((lane + 64 * i) * STAT_WORDS + 2 * h) * 8u);
+    }
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      float m = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        if (lane + 64 * i < P.C) m = fmaxf(m, __uint_as_float(s[i][h].x));
+      m = wave_max(m);
+      float ls = 0.f;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        if (lane + 64 * i < P.C) ls += __uint_as_float(s[i][h].z) * expf(__uint_as_float(s[i][h].x) - m);
+      Mh[h] = m;
+      Lh[h] = wave_sum(ls);
+    }
+  }
+  if (w == 0 && lane == 0) trace_at(p, l, 18, p.n_layers);
+  // probabilities with the softmax's global max and sum, rounded to bf16 before P.V as HF does
+  // (softmax in fp32, then .to(bf16): modeling_llama.py:207-208)
+#pragma unroll
+  for (int h = 0; h < 3; ++h) {
+    const float inv = 1.0f / Lh[h];
+    for (int j = j0 + lane; j < j1; j += 64) sm.at.pb[h][j] = uint16_t(f2bf(expf(sm.at.sc[h][j] - Mh[h]) * inv));
   }
   wait_lgkm0();
-  if (w == 0 && lane == 0) trace_at(p, l, 18, p.n_layers);
   // P.V: lane = (half, d2) owns dims 2*d2, 2*d2+1; token pairs alternate between the halves
   const int half = lane >> 5, d2 = lane & 31;
   const int jo1 = min(j1, T_old);
@@ -955,82 +1031,52 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
       sm.wo[w][h][2 * d2] = acc[h][0];
       sm.wo[w][h][2 * d2 + 1] = acc[h][1];
     }
-  if (lane == 0)
-#pragma unroll
-    for (int h = 0; h < 3; ++h) { sm.wml[w][0][h] = m3[h]; sm.wml[w][1][h] = l3[h]; }
   C.cbar();
   if (w == 0 && lane == 0) trace_at(p, l, 19, p.n_layers);
   if (w >= 3) return;
-  // wave w: head h = 3g + w.  Merge the 4 wave partials (fixed order) into the chunk partial.
+  // wave w: head h = 3g + w.  The chunk's partial sum of p.v (fixed wave order), fp32.
   const int hh = w, d = lane;
-  float M = -INFINITY, Ls = 0.f, O = 0.f;
-  auto merge = [&](float mc, float lc, float oc) {
-    const float Mn = fmaxf(M, mc);
-    const float sa = M == -INFINITY ? 0.f : expf(M - Mn);
-    const float sb = mc == -INFINITY ? 0.f : expf(mc - Mn);
-    Ls = Ls * sa + lc * sb;
-    O = O * sa + oc * sb;
-    M = Mn;
-  };
+  float O = 0.f;
 #pragma unroll
-  for (int v = 0; v < NCW; ++v) merge(sm.wml[v][0][hh], sm.wml[v][1][hh], sm.wo[v][hh][d]);
+  for (int v = 0; v < NCW; ++v) O += sm.wo[v][hh][d];
   if (w == 0 && lane == 0) trace_at(p, l, 4, p.n_layers);
   uint64_t* rec_base = reinterpret_cast<uint64_t*>(p.ws + W::rec(l, 0));
-  const uint64_t tg = uint64_t(C.tag32) << 32;
   if (!P.leader) {
-    uint64_t* rec = rec_base + size_t(P.wg) * REC_WORDS + hh * 66;
-    st_dev64(rec + 2 + d, tg | __float_as_uint(O));
-    if (lane == 0) st_dev64(rec, tg | __float_as_uint(M));
-    if (lane == 1) st_dev64(rec + 1, tg | __float_as_uint(Ls));
+    st_dev64(rec_base + size_t(P.wg) * REC_WORDS + hh * 64 + d, tg | __float_as_uint(O));
     return;
   }
-  // leader: online log-sum-exp merge over chunks 0..C-1 in order (this chunk is C-1)
-  const float m_own = M, l_own = Ls, o_own = O;
-  M = -INFINITY;
-  Ls = 0.f;
+  // leader: sum the chunk partials 0..C-1 in chunk order (this chunk is C-1), round once
+  const float o_own = O;
   O = 0.f;
-  constexpr int MB = 4;  // chunk records polled at once
+  constexpr int MB = 8;  // chunk records polled at once
   for (int c0 = 0; c0 < P.C - 1; c0 += MB) {
     const int nc = min(MB, P.C - 1 - c0);
-    uint64_t rm[MB], rl[MB], ro[MB];
+    uint64_t ro[MB];
     uint32_t pend = 0;
 #pragma unroll
-    for (int k = 0; k < MB; ++k) {
+    for (int k = 0; k < MB; ++k)
       if (k < nc) {
-        const uint64_t* rec = rec_base + size_t(g * P.C + c0 + k) * REC_WORDS + hh * 66;
-        rm[k] = ld_dev64(rec);
-        rl[k] = ld_dev64(rec + 1);
-        ro[k] = ld_dev64(rec + 2 + d);
+        ro[k] = ld_dev64(rec_base + size_t(g * P.C + c0 + k) * REC_WORDS + hh * 64 + d);
         pend |= 1u << k;
       }
-    }
     Spin spin(p.ws, 5);
     while (true) {
 #pragma unroll
       for (int k = 0; k < MB; ++k)
-        if (((pend >> k) & 1u) && uint32_t(rm[k] >> 32) == C.tag32 && uint32_t(rl[k] >> 32) == C.tag32 &&
-            uint32_t(ro[k] >> 32) == C.tag32)
-          pend &= ~(1u << k);
+        if (((pend >> k) & 1u) && uint32_t(ro[k] >> 32) == C.tag32) pend &= ~(1u << k);
       if (!pend) break;
       if (C.dead || !spin.again()) { C.dead = true; break; }
 #pragma unroll
-      for (int k = 0; k < MB; ++k) {
-        if ((pend >> k) & 1u) {
-          const uint64_t* rec = rec_base + size_t(g * P.C + c0 + k) * REC_WORDS + hh * 66;
-          rm[k] = ld_dev64(rec);
-          rl[k] = ld_dev64(rec + 1);
-          ro[k] = ld_dev64(rec + 2 + d);
-        }
-      }
+      for (int k = 0; k < MB; ++k)
+        if ((pend >> k) & 1u) ro[k] = ld_dev64(rec_base + size_t(g * P.C + c0 + k) * REC_WORDS + hh * 64 + d);
     }
 #pragma unroll
     for (int k = 0; k < MB; ++k)
-      if (k < nc)
-        merge(__uint_as_float(uint32_t(rm[k])), __uint_as_float(uint32_t(rl[k])), __uint_as_float(uint32_t(ro[k])));
+      if (k < nc) O += __uint_as_float(uint32_t(ro[k]));
   }
   if (w == 0 && lane == 0) trace_at(p, l, 20, p.n_layers);
-  merge(m_own, l_own, o_own);
-  st_dev(p.ws + W::attn(l, b) + size_t(g * 3 + hh) * 64 + d, C.w16(O / Ls));
+  O += o_own;
+  st_dev(p.ws + W::attn(l, b) + size_t(g * 3 + hh) * 64 + d, C.w16(O));
   if (w == 0 && lane == 0) trace_at(p, l, 5, p.n_layers);
 }
 

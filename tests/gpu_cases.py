@@ -71,6 +71,43 @@ class Case:
         return O.decode_step(self.w, ids, positions, self.kv, self.cos_sin, seq_lens=seq_lens,
                              slot_mapping=slot_mapping, layer_outputs=layer_outputs)
 
+    def eager_gpu_step(self, ids, positions, layer_outputs=False):
+        """The oracle's eager algorithm on GPU tensors (PyTorch's GPU BLAS and kernels): a second
+        implementation of the same rounding points, differing only in accumulation order.  Its
+        distance from the CPU oracle is the noise floor a correct kernel cannot beat at full
+        depth, where random-init layers amplify last-bit differences.  Call before oracle_step
+        of the same step (it reads the CPU caches, which oracle_step appends to)."""
+        kvg = O.PagedKV([c.to(self.dev) for c in self.kv.caches], self.btd, self.kv.block_size)
+        wg = O.Weights(self.geom, self.wd.embed, self.wd.final_norm, self.wd.layers)
+        r = O.decode_step(wg, ids, positions, kvg, self.csd, layer_outputs=layer_outputs)
+        return {k: (v.cpu() if torch.is_tensor(v) else v) for k, v in r.items()}
+
+    TF_ROW = 0  # embedding row that carries a teacher-forced hidden state
+
+    def teacher_forced_layer(self, li: int, x_in: torch.Tensor, position: int, *, logits=False):
+        """Layer `li` alone through the kernel (num_layers=1, that layer's weights and cache) with
+        the hidden state `x_in` [H] as its input, placed in row TF_ROW of a copy of the embedding.
+        Returns the layer output [H] (and the final-norm hidden state and logits if asked; the
+        embedding is tied, so logit TF_ROW is x_in's own and is not comparable)."""
+        if not hasattr(self, "_embed_tf"):
+            self._embed_tf = self.wd.embed.clone()
+        self._embed_tf[self.TF_ROW] = x_in.to(self.dev, BF16)
+        dev = self.dev
+        lo = torch.empty((1, 1, self.geom.hidden), dtype=BF16, device=dev)
+        lg = torch.empty((1, self.geom.vocab), dtype=BF16, device=dev) if logits else None
+        hid, ids = self.mod.decode_step(
+            input_ids=torch.tensor([self.TF_ROW], device=dev), positions=torch.tensor([position], device=dev),
+            seq_lens=torch.tensor([position + 1], dtype=torch.int32, device=dev), block_table=self.btd,
+            slot_mapping=torch.tensor([self.kv.slot(0, position)], device=dev), embed=self._embed_tf,
+            layers=[self.wd.layers[li]], final_norm=self.wd.final_norm, kv_caches=[self.kvd[li]],
+            cos_sin_cache=self.csd, eps=1e-5, num_layers=1, return_token_ids=True, logits_out=lg,
+            layer_outputs=lo)
+        torch.cuda.synchronize()
+        res = {"out": lo[0, 0].cpu(), "hidden": hid[0].cpu(), "ids": ids.cpu()}
+        if logits:
+            res["logits"] = lg[0].cpu()
+        return res
+
 
 def compare_logits(k: torch.Tensor, r: torch.Tensor) -> dict:
     kf, rf = k.float(), r.float()
@@ -112,6 +149,31 @@ def assert_step_parity(kres: dict, rres: dict, label: str = "") -> dict:
     return out
 
 
+FLOOR_FACTOR = 2.0     # full depth: kernel error may be at most this multiple of the eager-vs-eager floor
+
+
+def assert_within_floor(kres: dict, rres: dict, floor: dict, label: str = "") -> dict:
+    """Full-depth parity of a free-running step.  The north-star bound (LOGIT_ATOL, COS_MIN) is
+    unreachable there even for PyTorch eager on the GPU against PyTorch eager on the CPU: 30+
+    random-init layers amplify last-bit accumulation-order differences (GPU eager vs oracle at
+    SmolLM2-360M ctx 1024 measures about 0.07 max abs, cosine 0.9996).  The bar is therefore the
+    larger of the north-star bound and FLOOR_FACTOR times that measured floor; the per-layer
+    teacher-forced tests hold every layer to the north-star bound itself."""
+    c = compare_logits(kres["logits"][0], rres["logits"][0])
+    f = compare_logits(floor["logits"][0], rres["logits"][0])
+    atol = max(LOGIT_ATOL, FLOOR_FACTOR * f["max_abs"])
+    cos_min = min(COS_MIN, 1.0 - FLOOR_FACTOR * (1.0 - f["cos"]))
+    assert c["max_abs"] <= atol, f"{label} logits max abs err {c['max_abs']} > {atol} (floor {f})"
+    assert c["cos"] >= cos_min, f"{label} logits cosine {c['cos']} < {cos_min} (floor {f})"
+    assert greedy_ok(int(kres["ids"][0]), rres["logits"][0], tol=atol), \
+        f"{label} greedy id {int(kres['ids'][0])} vs oracle {int(rres['ids'][0])}"
+    return {"kernel": c, "eager_gpu_floor": f}
+
+
+def identical_fraction(a: torch.Tensor, b: torch.Tensor) -> float:
+    return float((a.to(BF16).view(torch.int16) == b.to(BF16).view(torch.int16)).float().mean().item())
+
+
 def ulp_distance(a: torch.Tensor, b: torch.Tensor) -> int:
     return O.max_ulp(a, b)
 
@@ -120,5 +182,5 @@ def finite(t: torch.Tensor) -> bool:
     return bool(torch.isfinite(t.float()).all())
 
 
-__all__ = ["Case", "compare_logits", "greedy_ok", "random_kv_case", "assert_step_parity", "LOGIT_ATOL",
-           "COS_MIN", "math"]
+__all__ = ["Case", "compare_logits", "greedy_ok", "random_kv_case", "assert_step_parity", "assert_within_floor",
+           "identical_fraction", "LOGIT_ATOL", "COS_MIN", "FLOOR_FACTOR", "math"]
