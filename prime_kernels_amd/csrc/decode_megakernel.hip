@@ -670,23 +670,6 @@ struct Chunks {
   static constexpr int CPL = (CH + 63) / 64;
 };
 
-// Rows cw + NCW*r (r < MAXR, row < nrows) of a ring segment -> registers.
-template <class G, int K, int MAXR>
-__device__ __forceinline__ void pull(const Consumer<G>& C, uint32_t seg_start, int nrows,
-                                     uint4 (&w)[MAXR][Chunks<K>::CPL]) {
-#pragma unroll
-  for (int r = 0; r < MAXR; ++r) {
-    const int row = C.cw + NCW * r;
-#pragma unroll
-    for (int c = 0; c < Chunks<K>::CPL; ++c) {
-      const int ch = C.lane + 64 * c;
-      w[r][c] = (row < nrows && ch < Chunks<K>::CH)
-                    ? C.ring16(seg_start + uint32_t(row) * K * 2 + uint32_t(ch) * 16)
-                    : make_uint4(0, 0, 0, 0);
-    }
-  }
-}
-
 // Norm-weight chunks of a lane, from the ring segment that carries them.
 template <class G, int K>
 __device__ __forceinline__ void load_normw(const Consumer<G>& C, uint4 (&nw)[Chunks<K>::CPL], uint32_t seg) {
@@ -728,15 +711,34 @@ __device__ __forceinline__ void load_x(uint4 (&x)[Chunks<K>::CPL], const float* 
   }
 }
 
-// out[r] = row r . x (fp32 accumulation of bf16 pair products), wave-reduced, uniform.
-template <int K, int MAXR>
-__device__ __forceinline__ void dots(const uint4 (&w)[MAXR][Chunks<K>::CPL], const uint4 (&x)[Chunks<K>::CPL],
-                                     float (&out)[MAXR]) {
+// out[r] = row (cw + NCW*r) of a ring segment . x, reading the weights straight from LDS.  The
+// reads are unconditional (ring addresses wrap, so rows past `nrows` read stale ring bytes whose
+// results are never stored), so all of a wave's LDS reads issue back to back before one wait; the
+// chunks past the row end (K/8 not a multiple of 64) are zeroed, since their lanes join the sum.
+template <class G, int K, int MAXR>
+__device__ __forceinline__ void dots_ring(const Consumer<G>& C, uint32_t seg, int nrows,
+                                          const uint4 (&x)[Chunks<K>::CPL], float (&out)[MAXR]) {
+  (void)nrows;
+  constexpr int CPL = Chunks<K>::CPL, CH = Chunks<K>::CH;
+  uint4 w[MAXR][CPL];
+#pragma unroll
+  for (int r = 0; r < MAXR; ++r) {
+    const uint32_t row = uint32_t(C.cw + NCW * r);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c)
+      w[r][c] = C.ring16(seg + row * uint32_t(K * 2) + uint32_t(C.lane + 64 * c) * 16u);
+  }
+  if (CH % 64 != 0) {
+    const bool tail_ok = C.lane + 64 * (CPL - 1) < CH;
+#pragma unroll
+    for (int r = 0; r < MAXR; ++r)
+      if (!tail_ok) w[r][CPL - 1] = make_uint4(0, 0, 0, 0);
+  }
 #pragma unroll
   for (int r = 0; r < MAXR; ++r) {
     float acc = 0.f;
 #pragma unroll
-    for (int c = 0; c < Chunks<K>::CPL; ++c) {
+    for (int c = 0; c < CPL; ++c) {
       acc = dot2(w[r][c].x, x[c].x, acc);
       acc = dot2(w[r][c].y, x[c].y, acc);
       acc = dot2(w[r][c].z, x[c].z, acc);
@@ -748,40 +750,19 @@ __device__ __forceinline__ void dots(const uint4 (&w)[MAXR][Chunks<K>::CPL], con
   for (int r = 0; r < MAXR; ++r) out[r] = wave_sum(out[r]);
 }
 
-// out[r] = row (cw + NCW*r) of a ring segment . x, reading the weights straight from LDS.
-template <class G, int K, int MAXR>
-__device__ __forceinline__ void dots_ring(const Consumer<G>& C, uint32_t seg, int nrows,
-                                          const uint4 (&x)[Chunks<K>::CPL], float (&out)[MAXR]) {
-#pragma unroll
-  for (int r = 0; r < MAXR; ++r) {
-    const int row = C.cw + NCW * r;
-    float acc = 0.f;
-    if (row < nrows) {
-#pragma unroll
-      for (int c = 0; c < Chunks<K>::CPL; ++c) {
-        const int ch = C.lane + 64 * c;
-        if (ch < Chunks<K>::CH) {
-          const uint4 w = C.ring16(seg + uint32_t(row) * K * 2 + uint32_t(ch) * 16);
-          acc = dot2(w.x, x[c].x, acc);
-          acc = dot2(w.y, x[c].y, acc);
-          acc = dot2(w.z, x[c].z, acc);
-          acc = dot2(w.w, x[c].w, acc);
-        }
-      }
-    }
-    out[r] = acc;
-  }
-#pragma unroll
-  for (int r = 0; r < MAXR; ++r) out[r] = wave_sum(out[r]);
-}
-
-// Value of row `lane` (lanes < MAXR), for one store instruction per wave.
+// Lane r (r < MAXR) gets out[r] (wave-uniform values), for one store instruction per wave.  The
+// lane id is made opaque at every step: a plain select chain on it is recognised as an indexed
+// read of the array, which the compiler then places in scratch memory (a global-memory round
+// trip on the critical path).
 template <int MAXR>
 __device__ __forceinline__ float pick(const float (&out)[MAXR], int lane) {
   float v = out[0];
 #pragma unroll
-  for (int r = 1; r < MAXR; ++r)
-    if (lane == r) v = out[r];
+  for (int r = 1; r < MAXR; ++r) {
+    int lr = lane;
+    asm volatile("" : "+v"(lr));
+    v = lr == r ? out[r] : v;
+  }
   return v;
 }
 
