@@ -43,9 +43,12 @@ extern "C" {
 size_t pk_workspace_bytes(int model);
 
 /* Allocate a zeroed workspace on the current device: kind 0 ordinary device memory, 1 fine-grained
- * (lower cross-XCD latency for the exchange words).  NULL on failure.  No reference counterpart:
- * the reference's wrapper allocates its scratch with torch (decode_megakernel_360m/__init__.py:63). */
+ * (lower cross-XCD latency for the exchange words), 2 uncached.  NULL on failure.  No reference
+ * counterpart: the reference's wrapper allocates its scratch with torch
+ * (decode_megakernel_360m/__init__.py:63). */
 void* pk_workspace_alloc(size_t bytes, int kind);
+/* Free a workspace; an uncached one (kind 2) is only forgotten and stays allocated until the
+ * process ends, because uncached memory a kernel has read must not be reused. */
 int pk_workspace_free(void* ptr);
 /* Synchronous copy of n header words of a workspace to the host (0 epoch, 1 abort, 2 abort site). */
 int pk_workspace_read(const void* ws, size_t word, unsigned* out, int n);
@@ -68,7 +71,7 @@ int pk_decode(void* stream, int model, int B, int n_layers, const void* input_id
 int pk_query(int* cu_count, int* coop, int* max_lds_per_block, int* is_gfx950, size_t* lds_bytes);
 
 /* Diagnostics: record per-phase wall-clock timestamps (100 MHz) of subsequent launches into
- * `buf` ([256][n_layers*16 + 4] uint64, device memory); NULL disables. No reference counterpart. */
+ * `buf` ([256][n_layers*40 + 4] uint64, device memory); NULL disables. No reference counterpart. */
 void pk_set_trace(void* buf);
 
 /* Human-readable status (static storage). */

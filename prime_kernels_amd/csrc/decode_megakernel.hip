@@ -27,6 +27,9 @@
 // the end of every step.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+#include <vector>
+
 #include <cstddef>
 #include <cstdint>
 
@@ -51,13 +54,19 @@ using G360 = Geom<960, 15, 5, 2560, 32>;   // decode_megakernel_360m/__init__.py
 using G135 = Geom<576, 9, 3, 1536, 30>;    // decode_megakernel/__init__.py:37-43
 
 constexpr int NWG = 256;                 // persistent workgroups (one per CU)
-constexpr int NPW = 4;                   // producer waves per workgroup (LDS-DMA issue is per-wave bound)
+#ifndef PK_PRODUCER_WAVES
+#define PK_PRODUCER_WAVES 4
+#endif
+#ifndef PK_DMA_DEPTH
+#define PK_DMA_DEPTH 16
+#endif
+constexpr int NPW = PK_PRODUCER_WAVES;   // producer waves per workgroup (LDS-DMA issue is per-wave bound)
 constexpr int NCW = 4;                   // consumer waves per workgroup
 constexpr int NCT = 64 * NCW;            // consumer threads
 constexpr int WG_THREADS = 64 * (NPW + NCW);
 constexpr uint32_t RING = 128u * 1024u;  // LDS ring bytes (power of two)
 constexpr uint32_t PKT = 1024;           // one LDS-DMA instruction: 64 lanes x 16 B
-constexpr int DEPTH = 16;                // packets in flight per producer wave
+constexpr int DEPTH = PK_DMA_DEPTH;      // packets in flight per producer wave
 constexpr int TC_MAX = 256;              // max cached tokens per attention chunk (64 KB of K/V)
 constexpr int TC_TARGET = 64;            // preferred tokens per chunk
 constexpr int LM_ROWS = 16;              // LM-head rows per ring segment
@@ -1459,17 +1468,37 @@ extern "C" void pk_set_trace(void* buf) { pk::g_trace = reinterpret_cast<unsigne
 
 // Workspace in fine-grained device memory (lower cross-XCD round trip for the exchange words).
 // Zero-initialised.  kind 0: ordinary (coarse-grained) device memory, 1: fine-grained.
+// Uncached allocations are never returned to the allocator: memory of this kind that a kernel has
+// read must stay allocated until the process ends (later allocations placed in freed uncached
+// memory have been seen to hold wrong values), so pk_workspace_free only forgets them.
+static std::mutex g_uncached_mu;
+static std::vector<void*> g_uncached;
+
 extern "C" void* pk_workspace_alloc(size_t bytes, int kind) {
   void* ptr = nullptr;
-  hipError_t e = kind == 1 ? hipExtMallocWithFlags(&ptr, bytes, hipDeviceMallocFinegrained) : hipMalloc(&ptr, bytes);
+  hipError_t e;
+  if (kind == 1) e = hipExtMallocWithFlags(&ptr, bytes, hipDeviceMallocFinegrained);
+  else if (kind == 2) e = hipExtMallocWithFlags(&ptr, bytes, hipDeviceMallocUncached);
+  else e = hipMalloc(&ptr, bytes);
   if (e != hipSuccess) return nullptr;
   if (hipMemset(ptr, 0, bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
-    (void)hipFree(ptr);
+    if (kind != 2) (void)hipFree(ptr);
     return nullptr;
+  }
+  if (kind == 2) {
+    std::lock_guard<std::mutex> lk(g_uncached_mu);
+    g_uncached.push_back(ptr);
   }
   return ptr;
 }
-extern "C" int pk_workspace_free(void* ptr) { return hipFree(ptr); }
+extern "C" int pk_workspace_free(void* ptr) {
+  {
+    std::lock_guard<std::mutex> lk(g_uncached_mu);
+    for (void* q : g_uncached)
+      if (q == ptr) return PK_OK;  // retained until the process ends
+  }
+  return hipFree(ptr);
+}
 // Copy n 32-bit words of a workspace (header words: 0 epoch, 1 abort flag, 2 abort site) to host.
 extern "C" int pk_workspace_read(const void* ws, size_t word, unsigned* out, int n) {
   const hipError_t e = hipMemcpy(out, reinterpret_cast<const unsigned*>(ws) + word, size_t(n) * 4, hipMemcpyDeviceToHost);
