@@ -34,12 +34,17 @@ extern "C" {
 #define PK_ERR_BLOCK 9109        /* block_size != 16, bt_stride too small, or bad layer index */
 #define PK_ERR_MODEL 9110        /* unknown model id or layer count */
 #define PK_ERR_DEBUG 9111        /* per-stage debug capture is not available in this build */
+#define PK_ERR_CAPTURE 9112      /* a workspace's first use (its zero fill) happened under stream capture */
 
 /* Models. */
 #define PK_MODEL_SMOLLM2_360M 360
 #define PK_MODEL_SMOLLM2_135M 135
 
-/* Workspace bytes for `model` (zero-initialise it once; it carries the step epoch). */
+/* Workspace bytes for `model`.  The workspace carries the step epoch and tagged exchange words, so
+ * it must start zeroed: pk_workspace_alloc returns a zeroed one, and any other buffer passed as
+ * `scratch` is zero-filled on the launch stream the first time it is seen on a device (refused
+ * with PK_ERR_CAPTURE if that first use is under stream capture).  A workspace stays dedicated
+ * to the library until pk_workspace_forget / pk_workspace_free. */
 size_t pk_workspace_bytes(int model);
 
 /* Allocate a zeroed workspace on the current device: kind 0 ordinary device memory, 1 fine-grained
@@ -50,6 +55,8 @@ void* pk_workspace_alloc(size_t bytes, int kind);
 /* Free a workspace; an uncached one (kind 2) is only forgotten and stays allocated until the
  * process ends, because uncached memory a kernel has read must not be reused. */
 int pk_workspace_free(void* ptr);
+/* The caller is reusing `ptr` for other data: it is zero-filled again at its next use. */
+int pk_workspace_forget(const void* ptr);
 /* Synchronous copy of n header words of a workspace to the host (0 epoch, 1 abort, 2 abort site). */
 int pk_workspace_read(const void* ws, size_t word, unsigned* out, int n);
 

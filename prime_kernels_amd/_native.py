@@ -23,6 +23,7 @@ SIGNATURES = {
     "pk_workspace_bytes": (sz, [ci]),
     "pk_workspace_alloc": (vp, [sz, ci]),
     "pk_workspace_free": (ci, [vp]),
+    "pk_workspace_forget": (ci, [vp]),
     "pk_workspace_read": (ci, [vp, sz, ctypes.POINTER(ctypes.c_uint), ci]),
     "pk_decode": (ci, [vp, ci, ci, ci, vp, ci, vp, vp, vp, vp, vp, ci, vp, vp, vp,
                        ll, ll, ll, ll, ll, ci, vp, ci, vp, vp, vp, vp, vp, sz, ci]),

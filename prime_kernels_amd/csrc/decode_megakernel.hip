@@ -1370,6 +1370,67 @@ struct LaunchCache {
   int status[MAX_DEV] = {};
 };
 
+// ------------------------------------------------------------------------------------------------
+// Workspace registry.  A step tells its exchange words apart from older contents only by their
+// tags, so a workspace must start zeroed.  Buffers from pk_workspace_alloc are zeroed there; a
+// buffer a caller passes in (the reference ABI takes plain scratch memory) is zero-filled on the
+// launch stream the first time it is seen on a device, by a fill kernel (graph-safe, no memset
+// node).  A first sight under stream capture is refused: the fill would be replayed with every
+// step and reset the epoch.  The library cannot see a caller reuse the memory for other data
+// between calls, so a workspace stays dedicated to it until pk_workspace_forget / _free.
+// ------------------------------------------------------------------------------------------------
+struct WsEntry {
+  int dev;
+  const void* ptr;
+  size_t bytes;
+};
+static std::mutex g_ws_mu;
+static std::vector<WsEntry> g_ws;
+
+__global__ void __launch_bounds__(256) zero_fill(uint4* p, size_t n) {
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+static void ws_register(int dev, const void* ptr, size_t bytes) {
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  for (WsEntry& w : g_ws)
+    if (w.dev == dev && w.ptr == ptr) {
+      w.bytes = bytes > w.bytes ? bytes : w.bytes;
+      return;
+    }
+  g_ws.push_back(WsEntry{dev, ptr, bytes});
+}
+
+static void ws_forget(const void* ptr) {
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  for (size_t i = 0; i < g_ws.size();)
+    if (g_ws[i].ptr == ptr) g_ws.erase(g_ws.begin() + long(i));
+    else ++i;
+}
+
+static int ensure_workspace(void* ws, size_t bytes, hipStream_t stream) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    for (const WsEntry& w : g_ws)
+      if (w.dev == dev && w.ptr == ws && w.bytes >= bytes) return PK_OK;
+  }
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  e = hipStreamIsCapturing(stream, &cs);
+  if (e != hipSuccess) return e;
+  if (cs != hipStreamCaptureStatusNone) return PK_ERR_CAPTURE;
+  const size_t n16 = bytes / 16;
+  const size_t blocks = (n16 + 255) / 256 < 2048 ? (n16 + 255) / 256 : 2048;
+  hipLaunchKernelGGL(zero_fill, dim3(unsigned(blocks)), dim3(256), 0, stream, reinterpret_cast<uint4*>(ws), n16);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  ws_register(dev, ws, bytes);
+  return PK_OK;
+}
+
 template <class G>
 static int launch(const Params& p, hipStream_t stream) {
   static LaunchCache<G> cache;
@@ -1453,6 +1514,9 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
   p.n_layers = n_layers;
   p.lm_head = (out_ids || out_logits) ? 1 : 0;
   p.trace = g_trace;
+  static_assert((WS<G>::TOTAL * 4) % 16 == 0, "workspace is zero-filled in 16-byte units");
+  const int st = ensure_workspace(scratch, WS<G>::TOTAL * 4, reinterpret_cast<hipStream_t>(stream));
+  if (st != PK_OK) return st;
   return launch<G>(p, reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -1489,9 +1553,16 @@ extern "C" void* pk_workspace_alloc(size_t bytes, int kind) {
     std::lock_guard<std::mutex> lk(g_uncached_mu);
     g_uncached.push_back(ptr);
   }
+  int dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess) pk::ws_register(dev, ptr, bytes);
   return ptr;
 }
+extern "C" int pk_workspace_forget(const void* ptr) {
+  pk::ws_forget(ptr);
+  return PK_OK;
+}
 extern "C" int pk_workspace_free(void* ptr) {
+  pk::ws_forget(ptr);
   {
     std::lock_guard<std::mutex> lk(g_uncached_mu);
     for (void* q : g_uncached)
@@ -1559,6 +1630,7 @@ extern "C" const char* prime_decode_status_string(int status) {
     case PK_ERR_BLOCK: return "block_size_or_stride_invalid";
     case PK_ERR_MODEL: return "unknown_model_or_layer_count";
     case PK_ERR_DEBUG: return "debug_capture_unavailable";
+    case PK_ERR_CAPTURE: return "workspace_first_use_under_stream_capture";
     default: return hipGetErrorString(static_cast<hipError_t>(status));
   }
 }

@@ -56,7 +56,8 @@ def test_status_strings_and_sizes():
     lib = _native.library()
     want = {9101: "batch_out_of_range", 9103: "null_device_pointer", 9104: "cooperative_launch_unsupported",
             9106: "kernel_requires_gfx950", 9107: "kv_offsets_or_pointers_not_16_byte_aligned",
-            9108: "scratch_or_debug_buffer_too_small", 9109: "block_size_or_stride_invalid"}
+            9108: "scratch_or_debug_buffer_too_small", 9109: "block_size_or_stride_invalid",
+            9112: "workspace_first_use_under_stream_capture"}
     for code, s in want.items():
         assert lib.decode360_status_string(code).decode() == s
         assert lib.mk_status_string(code).decode() == s

@@ -289,3 +289,57 @@ def test_reference_abi_decode360_matches_pk_decode():
     assert rc == 0, _native.status_string(rc)
     torch.cuda.synchronize()
     assert torch.equal(out.cpu(), k["hidden"])
+
+
+def _decode360_args(case, out, scratch, scratch_bytes, ids32, pos, sl, slot, layers_t, kv_t):
+    kv0 = case.kvd[0]
+    return (torch.cuda.current_stream().cuda_stream, 1, ids32.data_ptr(), case.wd.embed.data_ptr(),
+            case.wd.final_norm.data_ptr(), pos.data_ptr(), sl.data_ptr(), case.btd.data_ptr(), case.btd.stride(0),
+            slot.data_ptr(), layers_t.data_ptr(), kv_t.data_ptr(), 0, 64, kv0.stride(0), kv0.stride(2),
+            kv0.stride(1), 16, case.csd.data_ptr(), 0, out.data_ptr(), None, scratch, scratch_bytes, None, 0,
+            case.btd.shape[1] * 16, -1)
+
+
+def test_reference_abi_uninitialised_scratch():
+    """The reference ABI takes plain scratch memory (its harness passes torch.empty,
+    bench_r30_r34.py:168): a caller buffer full of garbage -- here words whose 16-bit tags look
+    current -- is zero-filled on first sight, so the result equals a clean workspace's; a buffer
+    seen for the first time under stream capture is refused (9112) instead."""
+    _need_gpu()
+    from prime_kernels_amd import _native
+    geom = O.SMOLLM2_360M
+    case = GC.random_kv_case(geom, 23, [300], norm_jitter=0.0)
+    lib = _native.library()
+    layers_t = torch.tensor([[t.data_ptr() for t in layer] for layer in case.wd.layers], dtype=torch.int64,
+                            device=case.dev)
+    kv_t = torch.tensor([c.data_ptr() for c in case.kvd], dtype=torch.int64, device=case.dev)
+    ids32 = torch.tensor([77], dtype=torch.int32, device=case.dev)
+    pos = torch.tensor([299], dtype=torch.int64, device=case.dev)
+    sl = torch.tensor([300], dtype=torch.int32, device=case.dev)
+    slot = torch.tensor([case.kv.slot(0, 299)], dtype=torch.int64, device=case.dev)
+    nbytes = lib.decode360_workspace_bytes()
+    clean = torch.empty((1, 960), dtype=BF16, device=case.dev)
+    rt = case.mod.workspace(case.dev)
+    rc = lib.decode360(*_decode360_args(case, clean, rt.scratch_ptr, rt.scratch_bytes, ids32, pos, sl, slot,
+                                        layers_t, kv_t))
+    assert rc == 0, _native.status_string(rc)
+    torch.cuda.synchronize()
+    garbage = torch.randint(0, 1 << 16, (nbytes // 4,), dtype=torch.int32, device=case.dev) | (1 << 16)
+    for trial in range(2):
+        case.sync_kv_from_oracle()
+        out = torch.empty((1, 960), dtype=BF16, device=case.dev)
+        rc = lib.decode360(*_decode360_args(case, out, garbage.data_ptr(), nbytes, ids32, pos, sl, slot,
+                                            layers_t, kv_t))
+        assert rc == 0, _native.status_string(rc)
+        torch.cuda.synchronize()
+        assert torch.equal(out, clean), f"trial {trial}"
+    assert lib.pk_workspace_forget(garbage.data_ptr()) == 0
+    # first sight under capture: refused before anything is launched
+    fresh = torch.zeros(nbytes // 4, dtype=torch.int32, device=case.dev)
+    out = torch.empty((1, 960), dtype=BF16, device=case.dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = lib.decode360(*_decode360_args(case, out, fresh.data_ptr(), nbytes, ids32, pos, sl, slot,
+                                            layers_t, kv_t))
+    assert rc == 9112, rc
+    assert _native.status_string(rc) == "workspace_first_use_under_stream_capture"
