@@ -43,6 +43,11 @@ class Model:
         return ((h,), (self.qkv_rows, h), (h, h), (h,), (2 * i, h), (h, i))
 
 
+SMOLLM2_360M = Model("decode_megakernel_360m", 360, hidden=960, inter=2560, heads=15, kv_heads=5, layers=32)
+SMOLLM2_135M = Model("decode_megakernel", 135, hidden=576, inter=1536, heads=9, kv_heads=3, layers=30)
+MODELS = {m.model_id: m for m in (SMOLLM2_360M, SMOLLM2_135M)}
+
+
 class _Runtime:
     """Per-device state (reference: decode_megakernel_360m/__init__.py:60-70).
 

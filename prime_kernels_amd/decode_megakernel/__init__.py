@@ -4,9 +4,10 @@ Drop-in for prime_kernels.decode_megakernel (reference __init__.py:134-205): sam
 `decode_step(**kw)` contract, plus the 360M wrapper's optional arguments and extensions.
 """
 
-from prime_kernels_amd._decode import Model, decode_step as _decode_step, runtime
+from prime_kernels_amd import _ops  # registers torch.ops.prime_decode.*
+from prime_kernels_amd._decode import SMOLLM2_135M, decode_step as _decode_step, runtime
 
-MODEL = Model("decode_megakernel", 135, hidden=576, inter=1536, heads=9, kv_heads=3, layers=30)
+MODEL = SMOLLM2_135M
 
 MAX_BATCH = MODEL.max_batch
 MAX_SEQ = MODEL.max_seq
@@ -25,3 +26,8 @@ def decode_step(**kw):
 
 def workspace(device):
     return runtime(MODEL, device)
+
+
+MODEL_ID = MODEL.model_id
+decode_step_op = _ops.decode_step      # torch.ops.prime_decode.decode_step(MODEL_ID, ...)
+decode_logits_op = _ops.decode_logits  # torch.ops.prime_decode.decode_logits(MODEL_ID, ..., logits)

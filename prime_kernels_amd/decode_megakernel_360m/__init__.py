@@ -7,9 +7,10 @@ Extensions: `return_token_ids=True` (greedy ids from the fused tied LM head), `l
 `num_layers=`.  Batch 1; KV block size 16; contexts up to 12288 tokens.
 """
 
-from prime_kernels_amd._decode import Model, decode_step as _decode_step, runtime
+from prime_kernels_amd import _ops  # registers torch.ops.prime_decode.*
+from prime_kernels_amd._decode import SMOLLM2_360M, decode_step as _decode_step, runtime
 
-MODEL = Model("decode_megakernel_360m", 360, hidden=960, inter=2560, heads=15, kv_heads=5, layers=32)
+MODEL = SMOLLM2_360M
 
 MAX_BATCH = MODEL.max_batch
 MAX_SEQ = MODEL.max_seq
@@ -29,3 +30,8 @@ def decode_step(**kw):
 def workspace(device):
     """The per-device runtime (workspace, output buffers) -- for diagnostics."""
     return runtime(MODEL, device)
+
+
+MODEL_ID = MODEL.model_id
+decode_step_op = _ops.decode_step      # torch.ops.prime_decode.decode_step(MODEL_ID, ...)
+decode_logits_op = _ops.decode_logits  # torch.ops.prime_decode.decode_logits(MODEL_ID, ..., logits)

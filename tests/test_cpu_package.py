@@ -126,3 +126,30 @@ def test_manifest_lists_built_sources():
         s = pk.spec(name)
         assert all(src.is_file() for src in s.sources)
         assert (pk.LIB_DIR / s.library).is_file(), "run __graft_entry__.build() first"
+
+
+def test_torch_ops_schema_and_fake_kernels():
+    """torch.ops.prime_decode.* exist with their schemas (KV caches and logits marked mutated)
+    and the fake kernels give the output shapes without running anything."""
+    import torch
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    import prime_kernels_amd.decode_megakernel_360m  # noqa: F401  (registers the ops)
+    s = str(torch.ops.prime_decode.decode_step.default._schema)
+    assert "Tensor(a9!)[] kv_caches" in s and s.endswith("-> (Tensor, Tensor)")
+    s = str(torch.ops.prime_decode.decode_logits.default._schema)
+    assert "Tensor(a12!) logits" in s
+    shapes = ((960,), (1600, 960), (960, 960), (960,), (5120, 960), (960, 2560))
+    with FakeTensorMode():
+        ids = torch.empty(1, dtype=torch.int64)
+        lw = [torch.empty(sh, dtype=torch.bfloat16) for _ in range(2) for sh in shapes]
+        kv = [torch.empty(8, 5, 16, 128, dtype=torch.bfloat16) for _ in range(2)]
+        args = (360, ids, ids, ids.int(), torch.empty(1, 4, dtype=torch.int32), ids,
+                torch.empty(49152, 960, dtype=torch.bfloat16), lw, torch.empty(960, dtype=torch.bfloat16), kv,
+                torch.empty(80, 64, dtype=torch.bfloat16), 1e-5)
+        h, i = torch.ops.prime_decode.decode_step(*args)
+        assert h.shape == (1, 960) and h.dtype == torch.bfloat16 and i.shape == (1,) and i.dtype == torch.int64
+        i2 = torch.ops.prime_decode.decode_logits(*args, torch.empty(1, 49152, dtype=torch.bfloat16))
+        assert i2.shape == (1,)
+        with pytest.raises(ValueError):
+            torch.ops.prime_decode.decode_step(360, *args[1:7], lw[:5], *args[8:])

@@ -343,3 +343,27 @@ def test_reference_abi_uninitialised_scratch():
                                             layers_t, kv_t))
     assert rc == 9112, rc
     assert _native.status_string(rc) == "workspace_first_use_under_stream_capture"
+
+
+def test_torch_op_matches_decode_step():
+    """torch.ops.prime_decode.decode_step / decode_logits give the same hidden state, ids and
+    logits as decode_step(**kw), as fresh tensors."""
+    _need_gpu()
+    geom = O.with_layers(O.SMOLLM2_360M, 2)
+    case = GC.random_kv_case(geom, 31, [150])
+    k = case.kernel_step([321], [149])
+    case.sync_kv_from_oracle()
+    d = case.dev
+    args = (case.mod.MODEL_ID, torch.tensor([321], device=d), torch.tensor([149], device=d),
+            torch.tensor([150], dtype=torch.int32, device=d), case.btd,
+            torch.tensor([case.kv.slot(0, 149)], device=d), case.wd.embed,
+            [t for layer in case.wd.layers for t in layer], case.wd.final_norm, case.kvd, case.csd, 1e-5)
+    h, ids = torch.ops.prime_decode.decode_step(*args)
+    lg = torch.empty((1, geom.vocab), dtype=BF16, device=d)
+    case.sync_kv_from_oracle()
+    ids2 = torch.ops.prime_decode.decode_logits(*args, lg)
+    torch.cuda.synchronize()
+    assert torch.equal(h.cpu(), k["hidden"]) and torch.equal(ids.cpu(), k["ids"]) and torch.equal(ids2.cpu(), k["ids"])
+    assert torch.equal(lg.cpu(), k["logits"])
+    h.add_(1)  # a fresh tensor: the module's buffer is untouched
+    assert torch.equal(case.mod.workspace(d).out[:1].cpu(), k["hidden"])
