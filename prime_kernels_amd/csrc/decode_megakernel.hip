@@ -60,6 +60,9 @@ constexpr int NWG = 256;                 // persistent workgroups (one per CU)
 #ifndef PK_DMA_DEPTH
 #define PK_DMA_DEPTH 16
 #endif
+#ifndef PK_POLL_SLEEP
+#define PK_POLL_SLEEP 1                  // s_sleep units (64 clocks) between polls of an exchange
+#endif
 constexpr int NPW = PK_PRODUCER_WAVES;   // producer waves per workgroup (LDS-DMA issue is per-wave bound)
 constexpr int NCW = 4;                   // consumer waves per workgroup
 constexpr int NCT = 64 * NCW;            // consumer threads
@@ -270,12 +273,14 @@ struct Plan {
   int natt;     // workgroups with a chunk (0 .. natt-1)
   int g, c, C, t0, t1;   // kv head, chunk, chunks, cached token range [t0, t1)
   int S, pos;   // tokens attended (incl. new) and the new token's position
+  long long slot;  // KV slot of the new token (slot_mapping[0]; < 0: no append)
   int leader;   // owns the new token, merges the chunk partials and appends K/V
 
   __device__ __forceinline__ void init(const Params& p, int wg_) {
     wg = wg_;
     S = max(p.seq_lens[0], 1);
     pos = int(max(p.positions[0], (int64_t)0));
+    slot = p.slot_mapping[0];
     const int old = S - 1;
     int C0 = old <= 0 ? 1 : (old + TC_TARGET - 1) / TC_TARGET;
     C0 = min(C0, NWG / G::KVH);
@@ -415,7 +420,7 @@ struct Spin {
         return false;
       }
     }
-    __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_s_sleep(PK_POLL_SLEEP);
     return true;
   }
 };
@@ -809,58 +814,81 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   float* in = sm.at.qkvw[w];
   const size_t qkv = W::qkv(l, b);
 
-  // rotary cos/sin of this step's position, from the ring segment that carries the table row
-  auto cs_at = [&](int f, float& c, float& s) {
-    if (p.cs_fp32) {
-      c = __uint_as_float(C.ring4(segc + uint32_t(f) * 4u));
-      s = __uint_as_float(C.ring4(segc + 128u + uint32_t(f) * 4u));
-    } else {
-      c = bf2f(*reinterpret_cast<const uint16_t*>(sm.ring + ((segc + uint32_t(f) * 2u) & (RING - 1))));
-      s = bf2f(*reinterpret_cast<const uint16_t*>(sm.ring + ((segc + 64u + uint32_t(f) * 2u) & (RING - 1))));
-    }
-  };
-  // RoPE with HF rounding: bf16(bf16(x*cos) + bf16(rotate_half(x)*sin)) (modeling_llama.py:138-160)
-  auto rope = [&](const float* head, int d, float c, float s) {
-    const float x = head[d];
-    const float rot = d < 32 ? -head[d + 32] : head[d - 32];
-    return rnd(rnd(x * c) + rnd(rot * s));
-  };
-
   const int part = lane & 7, grp = lane >> 3;
-  // queries of the 3 heads -> in[0, 192); the new key -> in[192, 256) and value -> in[256, 320)
-  const bool need_kv = has_new || (P.leader && w == NCW - 1);
-  C.poll_wave3(qkv + size_t(g) * 192, 192, qkv + G::H + size_t(g) * 64, need_kv ? 64 : 0,
-               qkv + G::H + G::KVH * 64 + size_t(g) * 64, need_kv ? 64 : 0, in);
+  // queries of the 3 heads -> in[0, 192); the new key -> in[192, 256) and value -> in[256, 320).
+  // The wave with the new token is the leader's last wave (edge(3) < T), which also appends K/V.
+  C.poll_wave3(qkv + size_t(g) * 192, 192, qkv + G::H + size_t(g) * 64, has_new ? 64 : 0,
+               qkv + G::H + G::KVH * 64 + size_t(g) * 64, has_new ? 64 : 0, in);
   C.wait_filled(C.pos);  // cos/sin row and KV chunk are in the ring
+  // cos/sin of dims 8*part .. 8*part+7 (mod 32): contiguous in the table row of this position
   float cs8[8], sn8[8];
+  {
+    const uint32_t f0 = uint32_t(part & 3) * 8u;
+    if (p.cs_fp32) {
+      const uint4 c0 = C.ring16(segc + f0 * 4u), c1 = C.ring16(segc + f0 * 4u + 16u);
+      const uint4 s0 = C.ring16(segc + 128u + f0 * 4u), s1 = C.ring16(segc + 128u + f0 * 4u + 16u);
+      const uint32_t cu[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+      const uint32_t su[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
-  for (int e = 0; e < 8; ++e) cs_at((part * 8 + e) & 31, cs8[e], sn8[e]);
-  wait_lgkm0();
-  if (w == 0 && lane == 0) trace_at(p, l, 3, p.n_layers);
-  if (P.leader && w == NCW - 1) {
-    // KV append: rotated new K and new V at slot_mapping[b]; slot < 0 skips
-    const long long slot = p.slot_mapping[b];
-    if (slot >= 0) {
-      float c, s;
-      cs_at(lane & 31, c, s);
-      uint16_t* cache = reinterpret_cast<uint16_t*>(p.kv[l]);
-      const long long e = (slot / 16) * p.block_stride + (slot % 16) * p.token_stride + (long long)g * p.head_stride;
-      cache[e + p.k_off + lane] = uint16_t(f2bf(rope(in + 192, lane, c, s)));
-      cache[e + p.v_off + lane] = uint16_t(f2bf(in[256 + lane]));
+      for (int e = 0; e < 8; ++e) { cs8[e] = __uint_as_float(cu[e]); sn8[e] = __uint_as_float(su[e]); }
+    } else {
+      const uint4 c = C.ring16(segc + f0 * 2u), sn = C.ring16(segc + 64u + f0 * 2u);
+      const uint32_t cu[4] = {c.x, c.y, c.z, c.w}, su[4] = {sn.x, sn.y, sn.z, sn.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        cs8[2 * e] = bf_lo(cu[e]); cs8[2 * e + 1] = bf_hi(cu[e]);
+        sn8[2 * e] = bf_lo(su[e]); sn8[2 * e + 1] = bf_hi(su[e]);
+      }
     }
   }
-  // rotated queries (dims part*8 .. part*8+7 of each head) and new key, packed bf16 pairs
-  uint32_t q[3][4], kn[4];
+  // RoPE with HF rounding, bf16(bf16(x*cos) + bf16(rotate_half(x)*sin)) (modeling_llama.py:138-160):
+  // this lane's dims 8*part..+7 of a head and their rotation partners 8*(part^4)..+7, as float4s;
+  // rotate_half negates the partner for the first half (dims < 32).
+  const float sgn = part < 4 ? -1.f : 1.f;
+  auto rope8 = [&](const float* head, uint32_t (&out)[4]) {
+    const float4 a0 = *reinterpret_cast<const float4*>(head + part * 8);
+    const float4 a1 = *reinterpret_cast<const float4*>(head + part * 8 + 4);
+    const float4 b0 = *reinterpret_cast<const float4*>(head + (part ^ 4) * 8);
+    const float4 b1 = *reinterpret_cast<const float4*>(head + (part ^ 4) * 8 + 4);
+    const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const float y[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    float r[8];
 #pragma unroll
-  for (int e2 = 0; e2 < 4; ++e2) {
-    const int d = part * 8 + 2 * e2;
+    for (int e = 0; e < 8; ++e) r[e] = rnd(rnd(x[e] * cs8[e]) + rnd((sgn * y[e]) * sn8[e]));
 #pragma unroll
-    for (int h = 0; h < 3; ++h)
-      q[h][e2] = pack2(rope(in + h * 64, d, cs8[2 * e2], sn8[2 * e2]),
-                       rope(in + h * 64, d + 1, cs8[2 * e2 + 1], sn8[2 * e2 + 1]));
-    kn[e2] = has_new ? pack2(rope(in + 192, d, cs8[2 * e2], sn8[2 * e2]),
-                             rope(in + 192, d + 1, cs8[2 * e2 + 1], sn8[2 * e2 + 1]))
-                     : 0u;
+    for (int e = 0; e < 4; ++e) out[e] = pack2(r[2 * e], r[2 * e + 1]);
+  };
+  wait_lgkm0();
+  if (w == 0 && lane == 0) trace_at(p, l, 3, p.n_layers);
+  // rotated queries and (for the wave with the new token) the rotated new key, packed bf16 pairs
+  uint32_t q[3][4], kn[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int h = 0; h < 3; ++h) rope8(in + h * 64, q[h]);
+  if (has_new) rope8(in + 192, kn);
+  if (has_new && P.slot >= 0 && grp < 2) {
+    // KV append at slot_mapping[b] (block360_kernel.inc:124-135; slot < 0 skips): lanes 0-7 store
+    // the rotated new K, lanes 8-15 the new V, 8 dims (16 bytes) per lane
+    uint16_t* cache = reinterpret_cast<uint16_t*>(const_cast<void*>(sm.kvp[l]));
+    const long long e = (P.slot / 16) * p.block_stride + (P.slot % 16) * p.token_stride +
+                        (long long)g * p.head_stride + (grp ? p.v_off : p.k_off) + part * 8;
+    uint32_t val[4];
+    if (grp == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) val[i] = kn[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) val[i] = pack2(in[256 + part * 8 + 2 * i], in[256 + part * 8 + 2 * i + 1]);
+    }
+    uint16_t* dst = cache + e;
+    if ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+      *reinterpret_cast<uint4*>(dst) = make_uint4(val[0], val[1], val[2], val[3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dst[2 * i] = uint16_t(val[i] & 0xffffu);
+        dst[2 * i + 1] = uint16_t(val[i] >> 16);
+      }
+    }
   }
   if (w == 0 && lane == 0) trace_at(p, l, 16, p.n_layers);
   // scores: 8 lanes per token (8 dims each), 8 tokens per pass; s = bf16(q.k) * 1/8 (exact scale)
@@ -883,32 +911,44 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   wait_lgkm0();
   if (w == 0 && lane == 0) trace_at(p, l, 17, p.n_layers);
   // chunk softmax statistics per head: max and sum of exp over this wave's tokens, then over the
-  // chunk (all waves), then over all chunks of KV head g (one exchange of 3 x (max, sum) records)
+  // chunk (all waves), then over all chunks of KV head g (one exchange of 3 x (max, sum) records).
+  // A wave holds at most 128 tokens (chunks are at most TC_MAX + 1), so 2 scores per lane and head.
+  static_assert(TC_MAX + 1 - ((3 * (TC_MAX + 1) / NCW) & ~1) <= 128 && (TC_MAX + 1) / NCW + 2 <= 128,
+                "per-wave token ranges fit two per lane");
+  float sv[3][2];
+#pragma unroll
+  for (int h = 0; h < 3; ++h)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int j = j0 + lane + 64 * i;
+      sv[h][i] = j < j1 ? sm.at.sc[h][j] : -INFINITY;
+    }
 #pragma unroll
   for (int h = 0; h < 3; ++h) {
-    float m = -INFINITY;
-    for (int j = j0 + lane; j < j1; j += 64) m = fmaxf(m, sm.at.sc[h][j]);
-    m = wave_max(m);
+    const float m = wave_max(fmaxf(sv[h][0], sv[h][1]));
     float ls = 0.f;
-    for (int j = j0 + lane; j < j1; j += 64) ls += expf(sm.at.sc[h][j] - m);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) ls += sv[h][i] == -INFINITY ? 0.f : expf(sv[h][i] - m);
     ls = wave_sum(ls);
     if (lane == 0) { sm.wml[w][0][h] = m; sm.wml[w][1][h] = ls; }
   }
   C.cbar();
+  // lane 4h + v holds wave v's (max, sum) of head h; max and rescaled sum over each quad of lanes
+  float mq = -INFINITY, lq = 0.f;
+  if (lane < 4 * 3) {
+    mq = sm.wml[lane & 3][0][lane >> 2];
+    lq = sm.wml[lane & 3][1][lane >> 2];
+  }
+  float mx = fmaxf(mq, dpp<0xb1>(mq, mq));  // quad_perm [1,0,3,2]
+  mx = fmaxf(mx, dpp<0x4e>(mx, mx));         // quad_perm [2,3,0,1]
+  float ex = mq == -INFINITY ? 0.f : lq * expf(mq - mx);
+  ex += dpp<0xb1>(0.f, ex);
+  ex += dpp<0x4e>(0.f, ex);
   float Mh[3], Lh[3];
 #pragma unroll
   for (int h = 0; h < 3; ++h) {
-    float m = -INFINITY;
-#pragma unroll
-    for (int v = 0; v < NCW; ++v) m = fmaxf(m, sm.wml[v][0][h]);
-    float ls = 0.f;
-#pragma unroll
-    for (int v = 0; v < NCW; ++v) {
-      const float mv = sm.wml[v][0][h];
-      ls += mv == -INFINITY ? 0.f : sm.wml[v][1][h] * expf(mv - m);
-    }
-    Mh[h] = m;
-    Lh[h] = ls;
+    Mh[h] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx), 4 * h));
+    Lh[h] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), 4 * h));
   }
   const uint64_t tg = uint64_t(C.tag32) << 32;
   if (P.C > 1) {
@@ -966,7 +1006,11 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
 #pragma unroll
   for (int h = 0; h < 3; ++h) {
     const float inv = 1.0f / Lh[h];
-    for (int j = j0 + lane; j < j1; j += 64) sm.at.pb[h][j] = uint16_t(f2bf(expf(sm.at.sc[h][j] - Mh[h]) * inv));
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int j = j0 + lane + 64 * i;
+      if (j < j1) sm.at.pb[h][j] = uint16_t(f2bf(expf(sv[h][i] - Mh[h]) * inv));
+    }
   }
   wait_lgkm0();
   // P.V: lane = (half, d2) owns dims 2*d2, 2*d2+1; token pairs alternate between the halves
