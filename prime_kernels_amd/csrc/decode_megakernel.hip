@@ -120,22 +120,31 @@ struct Params {
   unsigned long long* trace;   // optional per-phase timestamps (diagnostics)
 };
 
-// Exchange-buffer layout (32-bit words).
+// Exchange-buffer layout (32-bit words).  The per-layer vectors (qkv, attn, h1, act, x) of tagged
+// bf16 words are stored line-interleaved: 64-byte line k of vector (kind, layer, b) is line slot
+// (b * XLINES + k) * XSLOTS + layer * NKIND + kind, so the consecutive lines of one vector are
+// XSLOTS * 64 bytes apart (10 KB for 32 layers) and spread over the HBM channels instead of
+// concentrating every reader's polls on the one or two channels a contiguous vector would hit.
+enum XKind { X_QKV, X_ATTN, X_H1, X_ACT, X_X, NKIND };
 template <class G>
 struct WS {
-  static constexpr size_t PER_B = size_t(G::QKV) + 3 * G::H + G::I;  // qkv, attn, h1, act, x
-  static constexpr size_t LAYER = PER_B * MAX_B;
-  static constexpr size_t REC0 = HDR_WORDS + LAYER * G::L;
+  static constexpr int XSLOTS = G::L * NKIND;
+  static constexpr int XMAX = G::QKV > G::I ? (G::QKV > G::H ? G::QKV : G::H) : (G::I > G::H ? G::I : G::H);
+  static constexpr int XLINES = XMAX / 16;
+  static_assert(G::QKV % 16 == 0 && G::H % 16 == 0 && G::I % 16 == 0 && (G::H + G::KVH * 64) % 16 == 0,
+                "vector segments start on 64-byte lines");
+  static constexpr size_t X0 = HDR_WORDS;
+  static constexpr size_t XWORDS = size_t(MAX_B) * XLINES * XSLOTS * 16;
+  static constexpr size_t REC0 = X0 + XWORDS;
   static constexpr size_t REC_LAYER = size_t(NWG) * REC_WORDS * 2;
   static constexpr size_t STAT0 = REC0 + REC_LAYER * G::L;
   static constexpr size_t STAT_LAYER = size_t(NWG) * STAT_WORDS * 2;
   static constexpr size_t LM0 = STAT0 + STAT_LAYER * G::L;
   static constexpr size_t TOTAL = LM0 + size_t(MAX_B) * NWG * 2;
-  __device__ static size_t qkv(int l, int b) { return HDR_WORDS + l * LAYER + b * PER_B; }
-  __device__ static size_t attn(int l, int b) { return qkv(l, b) + G::QKV; }
-  __device__ static size_t h1(int l, int b) { return attn(l, b) + G::H; }
-  __device__ static size_t act(int l, int b) { return h1(l, b) + G::H; }
-  __device__ static size_t x(int l, int b) { return act(l, b) + G::I; }
+  // word offset of element i of vector (kind, layer l, sequence b)
+  __device__ static size_t xw(int kind, int l, int b, int i) {
+    return X0 + ((size_t(b) * XLINES + size_t(i >> 4)) * XSLOTS + size_t(l) * NKIND + kind) * 16 + size_t(i & 15);
+  }
   __device__ static size_t rec(int l, int item) { return REC0 + l * REC_LAYER + size_t(item) * REC_WORDS * 2; }
   __device__ static size_t stat(int l, size_t item) { return STAT0 + l * STAT_LAYER + item * STAT_WORDS * 2; }
   __device__ static size_t lm(int b, int wg) { return LM0 + (size_t(b) * NWG + wg) * 2; }
@@ -599,14 +608,15 @@ struct Consumer {
   // the values (fp32) to dst[] (and keep[] when given).  Every load of a thread is in flight at
   // once; only groups whose tags are stale are polled again.  Returns this wave's sum of squares.
   template <int MAXG>
-  __device__ __forceinline__ float poll_split(size_t off, int n, float* dst, float* keep) {
-    const __amdgpu_buffer_rsrc_t r = rsrc(p.ws + off);
+  __device__ __forceinline__ float poll_split(int kind, int l, int b, int n, float* dst, float* keep) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(p.ws);
+    auto at = [&](int i) { return uint32_t(WS<G>::xw(kind, l, b, i)) * 4u; };
     u32x4 v[MAXG];
     uint32_t pend = 0;
 #pragma unroll
     for (int g = 0; g < MAXG; ++g) {
       const int i = (ct + g * NCT) * 4;
-      if (i < n) { v[g] = ld_dev128(r, uint32_t(i) * 4u); pend |= 1u << g; }
+      if (i < n) { v[g] = ld_dev128(r, at(i)); pend |= 1u << g; }
     }
     float ss = 0.f;
     Spin spin(p.ws, 4);
@@ -628,20 +638,20 @@ struct Consumer {
       if (dead || !spin.again()) { dead = true; break; }
 #pragma unroll
       for (int g = 0; g < MAXG; ++g)
-        if ((pend >> g) & 1u) v[g] = ld_dev128(r, uint32_t((ct + g * NCT) * 4) * 4u);
+        if ((pend >> g) & 1u) v[g] = ld_dev128(r, at((ct + g * NCT) * 4));
     }
     return wave_sum(ss);
   }
 
-  // Poll three regions of tagged words (each a multiple of 4 words, total <= 512) with this wave
+  // Poll three element ranges [e0, e0+n0), [e1, e1+n1), [e2, e2+n2) of the qkv vector of layer l
+  // (each a multiple of 4 elements starting on a 4-element boundary, total <= 512) with this wave
   // alone (no barrier); values -> dst[0 .. n0 + n1 + n2).  Both loads of a lane are in flight at once.
-  __device__ __forceinline__ void poll_wave3(size_t off0, int n0, size_t off1, int n1, size_t off2, int n2,
+  __device__ __forceinline__ void poll_wave3(int l, int b, int e0, int n0, int e1, int n1, int e2, int n2,
                                              float* dst) {
-    const __amdgpu_buffer_rsrc_t r0 = rsrc(p.ws + off0), r1 = rsrc(p.ws + off1), r2 = rsrc(p.ws + off2);
+    const __amdgpu_buffer_rsrc_t r = rsrc(p.ws);
     auto load = [&](int i) -> u32x4 {
-      if (i < n0) return ld_dev128(r0, uint32_t(i) * 4u);
-      if (i < n0 + n1) return ld_dev128(r1, uint32_t(i - n0) * 4u);
-      return ld_dev128(r2, uint32_t(i - n0 - n1) * 4u);
+      const int e = i < n0 ? e0 + i : (i < n0 + n1 ? e1 + i - n0 : e2 + i - n0 - n1);
+      return ld_dev128(r, uint32_t(WS<G>::xw(X_QKV, l, b, e)) * 4u);
     };
     const int n = n0 + n1 + n2;
     const int i0 = lane * 4, i1 = (lane + 64) * 4;
@@ -812,13 +822,11 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   const bool has_new = P.leader && j1 == T && T > j0;
   if (P.q1 > P.q0) C.cbar();  // P1 of this workgroup read xs, which shares storage with sm.at
   float* in = sm.at.qkvw[w];
-  const size_t qkv = W::qkv(l, b);
 
   const int part = lane & 7, grp = lane >> 3;
   // queries of the 3 heads -> in[0, 192); the new key -> in[192, 256) and value -> in[256, 320).
   // The wave with the new token is the leader's last wave (edge(3) < T), which also appends K/V.
-  C.poll_wave3(qkv + size_t(g) * 192, 192, qkv + G::H + size_t(g) * 64, has_new ? 64 : 0,
-               qkv + G::H + G::KVH * 64 + size_t(g) * 64, has_new ? 64 : 0, in);
+  C.poll_wave3(l, b, g * 192, 192, G::H + g * 64, has_new ? 64 : 0, G::H + G::KVH * 64 + g * 64, has_new ? 64 : 0, in);
   C.wait_filled(C.pos);  // cos/sin row and KV chunk are in the ring
   // cos/sin of dims 8*part .. 8*part+7 (mod 32): contiguous in the table row of this position
   float cs8[8], sn8[8];
@@ -1110,7 +1118,7 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   }
   if (w == 0 && lane == 0) trace_at(p, l, 20, p.n_layers);
   O += o_own;
-  st_dev(p.ws + W::attn(l, b) + size_t(g * 3 + hh) * 64 + d, C.w16(O));
+  st_dev(p.ws + W::xw(X_ATTN, l, b, (g * 3 + hh) * 64 + d), C.w16(O));
   if (w == 0 && lane == 0) trace_at(p, l, 5, p.n_layers);
 }
 
@@ -1156,7 +1164,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
         }
         ss = wave_sum(s);
       } else {
-        ss = C.template poll_split<GH>(W::x(l - 1, b), G::H, sm.xs, sm.xkeep);
+        ss = C.template poll_split<GH>(X_X, l - 1, b, G::H, sm.xs, sm.xkeep);
       }
       const float rs = rms_scale(C.block_total(ss), G::H);
       tr(l, 1);
@@ -1168,7 +1176,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       C.release(C.pos);
       tr(l, 22);
       const int row = C.cw + NCW * C.lane;
-      if (C.lane < R::QKV && row < P.q1 - P.q0) st_dev(p.ws + W::qkv(l, b) + P.q0 + row, C.w16(pick(out, C.lane)));
+      if (C.lane < R::QKV && row < P.q1 - P.q0) st_dev(p.ws + W::xw(X_QKV, l, b, P.q0 + row), C.w16(pick(out, C.lane)));
       tr(l, 2);
     }
     // ---------------- P2: attention ----------------
@@ -1186,7 +1194,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       if (nrows > 0) {
         C.wait_filled(C.pos);
         tr(l, 6);
-        C.template poll_split<GH>(W::attn(l, b), G::H, sm.xs, nullptr);
+        C.template poll_split<GH>(X_ATTN, l, b, G::H, sm.xs, nullptr);
         C.cbar();
         tr(l, 7);
         uint4 x[Chunks<G::H>::CPL];
@@ -1198,7 +1206,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
         const int row = C.cw + NCW * C.lane;
         if (C.lane < R::O && row < nrows) {
           const int r = P.o0 + row;
-          st_dev(p.ws + W::h1(l, b) + r, C.w16(sm.xkeep[r] + rnd(pick(out, C.lane))));
+          st_dev(p.ws + W::xw(X_H1, l, b, r), C.w16(sm.xkeep[r] + rnd(pick(out, C.lane))));
         }
         tr(l, 8);
       } else {
@@ -1216,7 +1224,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       uint4 nw[Chunks<G::H>::CPL];
       load_normw<G, G::H>(C, nw, segn);
       tr(l, 9);
-      const float ss = C.template poll_split<GH>(W::h1(l, b), G::H, sm.xs, sm.h1keep);
+      const float ss = C.template poll_split<GH>(X_H1, l, b, G::H, sm.xs, sm.h1keep);
       const float rs = rms_scale(C.block_total(ss), G::H);
       tr(l, 10);
       uint4 x[Chunks<G::H>::CPL];
@@ -1229,7 +1237,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       if (C.lane < R::ACT && row < na) {
         const float gv = rnd(pick(og, C.lane)), uv = rnd(pick(ou, C.lane));
         const float silu = rnd(gv / (1.0f + expf(-gv)));
-        st_dev(p.ws + W::act(l, b) + P.a0 + row, C.w16(silu * uv));
+        st_dev(p.ws + W::xw(X_ACT, l, b, P.a0 + row), C.w16(silu * uv));
       }
       tr(l, 11);
     }
@@ -1240,7 +1248,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       const int nrows = P.d1 - P.d0;
       C.wait_filled(C.pos);
       tr(l, 12);
-      C.template poll_split<GI>(W::act(l, b), G::I, sm.xs, nullptr);
+      C.template poll_split<GI>(X_ACT, l, b, G::I, sm.xs, nullptr);
       C.cbar();
       tr(l, 13);
       uint4 x[Chunks<G::I>::CPL];
@@ -1253,7 +1261,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       if (C.lane < R::DOWN && row < nrows) {
         const int r = P.d0 + row;
         const float y = rnd(sm.h1keep[r] + rnd(pick(out, C.lane)));
-        st_dev(p.ws + W::x(l, b) + r, C.w16(y));
+        st_dev(p.ws + W::xw(X_X, l, b, r), C.w16(y));
         if (p.layer_outputs) p.layer_outputs[(size_t(l) * p.B + b) * G::H + r] = uint16_t(f2bf(y));
       }
       tr(l, 14);
@@ -1265,7 +1273,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
   uint4 nw[Chunks<G::H>::CPL];
   load_normw<G, G::H>(C, nw, segf);
   C.release(C.pos);
-  const float ss = C.template poll_split<GH>(W::x(p.n_layers - 1, b), G::H, sm.xs, nullptr);
+  const float ss = C.template poll_split<GH>(X_X, p.n_layers - 1, b, G::H, sm.xs, nullptr);
   const float rs = rms_scale(C.block_total(ss), G::H);
   uint4 x[Chunks<G::H>::CPL];
   load_x<G::H, true>(x, sm.xs, nw, rs, C.lane);
