@@ -74,6 +74,29 @@ int pk_decode(void* stream, int model, int B, int n_layers, const void* input_id
               int cs_fp32, void* out_hidden, void* layer_outputs, void* out_ids, void* out_logits,
               void* scratch, size_t scratch_bytes, int max_seq_len);
 
+/* pk_decode with MXFP8 projection weights (SmolLM2-360M only): `layers` is a device table
+ * [n_layers][10] of (norm1, qkv, qkv_scales, o, o_scales, norm2, gate_up, gate_up_scales, down,
+ * down_scales): e4m3 bytes [rows, cols] and e8m0 scale codes [rows, pk_mxfp8_scale_stride(cols)],
+ * one per 32 consecutive weights of a row, each row padded with zeros to a multiple of 16 bytes.
+ * Norms, embedding and the tied LM head stay bf16.  No reference counterpart: BASELINE config 5. */
+int pk_decode_mxfp8(void* stream, int model, int B, int n_layers, const void* input_ids, int ids_i64,
+                    const void* embed, const void* final_norm, const void* positions, const void* seq_lens,
+                    const void* block_table, int bt_stride, const void* slot_mapping, const void* layers,
+                    void* const* kv, long long k_off, long long v_off, long long block_stride,
+                    long long token_stride, long long head_stride, int block_size, const void* cos_sin,
+                    int cs_fp32, void* out_hidden, void* layer_outputs, void* out_ids, void* out_logits,
+                    void* scratch, size_t scratch_bytes, int max_seq_len);
+
+/* Bytes per row of the MXFP8 scale array for rows of `cols` weights (cols/32 rounded up to 16). */
+size_t pk_mxfp8_scale_stride(int cols);
+
+/* Quantise a bf16 matrix [rows, cols] (cols a multiple of 32) to MXFP8 on the device, asynchronously
+ * on `stream`: per 32 weights of a row, scale code s = e8m0(amax / 448) rounded toward +inf
+ * (saturating), weights e4m3(bf16(x * 2^(127-s))) rounded to nearest even, saturating at +-448 --
+ * the rule prime_kernels/rmsnorm/test.cu:126-144 applies.  q [rows, cols], scales
+ * [rows, pk_mxfp8_scale_stride(cols)]; all pointers 16-byte aligned. */
+int pk_quantize_mxfp8(void* stream, const void* src, void* q, void* scales, int rows, int cols);
+
 /* Device properties relevant to the launch (current device). Returns a status. */
 int pk_query(int* cu_count, int* coop, int* max_lds_per_block, int* is_gfx950, size_t* lds_bytes);
 

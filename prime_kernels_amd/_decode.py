@@ -33,6 +33,7 @@ class Model:
     head_dim: int = 64
     max_batch: int = 1
     max_seq: int = 12288
+    weight_format: str = "bf16"   # "bf16", or "mxfp8" (e4m3 projections + e8m0 scale per 32)
 
     @property
     def qkv_rows(self) -> int:
@@ -42,9 +43,30 @@ class Model:
         h, i = self.hidden, self.inter
         return ((h,), (self.qkv_rows, h), (h, h), (h,), (2 * i, h), (h, i))
 
+    def layer_spec(self):
+        """(name, dtype, shape) of each tensor of one layer tuple, in order."""
+        names = ("norm1", "qkv", "o", "norm2", "gate_up", "down")
+        if self.weight_format == "bf16":
+            return [(n, torch.bfloat16, sh) for n, sh in zip(names, self.shapes())]
+        spec = []
+        for n, sh in zip(names, self.shapes()):
+            if len(sh) == 1:
+                spec.append((n, torch.bfloat16, sh))
+            else:
+                spec.append((n, torch.uint8, sh))
+                spec.append((n + "_scales", torch.uint8, (sh[0], mxfp8_scale_stride(sh[1]))))
+        return spec
+
+
+def mxfp8_scale_stride(cols: int) -> int:
+    """Bytes per row of an MXFP8 scale array: one e8m0 code per 32 weights, padded to 16 bytes."""
+    return ((cols // 32 + 15) // 16) * 16
+
 
 SMOLLM2_360M = Model("decode_megakernel_360m", 360, hidden=960, inter=2560, heads=15, kv_heads=5, layers=32)
 SMOLLM2_135M = Model("decode_megakernel", 135, hidden=576, inter=1536, heads=9, kv_heads=3, layers=30)
+SMOLLM2_360M_MXFP8 = Model("decode_megakernel_360m_mxfp8", 360, hidden=960, inter=2560, heads=15, kv_heads=5,
+                           layers=32, weight_format="mxfp8")
 MODELS = {m.model_id: m for m in (SMOLLM2_360M, SMOLLM2_135M)}
 
 
@@ -95,7 +117,7 @@ _runtimes: dict = {}
 
 
 def runtime(model: Model, device: torch.device) -> _Runtime:
-    key = (model.model_id, device)
+    key = (model.name, device)
     if key not in _runtimes:
         _runtimes[key] = _Runtime(model, device)
     return _runtimes[key]
@@ -173,13 +195,16 @@ def decode_step(model: Model, *, input_ids, positions, seq_lens, block_table, sl
     _check_tensor(final_norm, "final_norm", dtype=torch.bfloat16, device=device, shape=(model.hidden,))
     if embed.ndim != 2 or embed.shape != (VOCAB, model.hidden) or not embed.is_contiguous():
         raise ValueError(f"embed must be contiguous BF16 [{VOCAB}, {model.hidden}]")
+    spec = model.layer_spec()
     for i, layer in enumerate(layers):
-        if len(layer) != 6:
-            raise ValueError(f"layer {i} must contain six weight tensors")
-        for name, tensor, shape in zip(("norm1", "qkv", "o", "norm2", "gate_up", "down"), layer, model.shapes()):
-            _check_tensor(tensor, f"layer {i} {name}", dtype=torch.bfloat16, device=device, shape=shape)
+        if len(layer) != len(spec):
+            raise ValueError(f"layer {i} must contain {'six' if len(spec) == 6 else len(spec)} weight tensors")
+        for (name, dtype, shape), tensor in zip(spec, layer):
+            _check_tensor(tensor, f"layer {i} {name}", dtype=dtype, device=device, shape=shape)
             if not tensor.is_contiguous():
                 raise ValueError(f"layer {i} {name} must be contiguous")
+            if tensor.data_ptr() % 16:
+                raise ValueError(f"layer {i} {name} must be 16-byte aligned")
     kv0 = kv_caches[0]
     _check_tensor(kv0, "kv_caches[0]", dtype=torch.bfloat16, device=device)
     if kv0.ndim != 4 or kv0.shape[1] != model.kv_heads or kv0.shape[3] != 2 * model.head_dim or kv0.stride(3) != 1:
@@ -209,7 +234,8 @@ def decode_step(model: Model, *, input_ids, positions, seq_lens, block_table, sl
     layers_t, kv_t = _tables(rt, layers, kv_caches)
     stream = torch.cuda.current_stream(device).cuda_stream
     want_ids = return_token_ids or logits_out is not None
-    rc = rt.lib.pk_decode(
+    launch = rt.lib.pk_decode_mxfp8 if model.weight_format == "mxfp8" else rt.lib.pk_decode
+    rc = launch(
         stream, model.model_id, batch, nl, input_ids.data_ptr(), int(input_ids.dtype == torch.int64),
         embed.data_ptr(), final_norm.data_ptr(), positions.data_ptr(), seq_lens.data_ptr(),
         block_table.data_ptr(), block_table.stride(0), slot_mapping.data_ptr(), layers_t.data_ptr(),
@@ -260,7 +286,8 @@ class StepLauncher:
     def launch(self, k: int, stream: int) -> None:
         m, rt = self.model, self.rt
         embed, layers, final_norm, kv_caches, block_table, cos_sin = self.keep
-        rc = self.lib.pk_decode(
+        launch = self.lib.pk_decode_mxfp8 if m.weight_format == "mxfp8" else self.lib.pk_decode
+        rc = launch(
             stream, m.model_id, 1, len(layers), self.ids.data_ptr() + 8 * k, 1, embed.data_ptr(),
             final_norm.data_ptr(), self.positions.data_ptr() + 8 * k, self.seq_lens.data_ptr() + 4 * k,
             block_table.data_ptr(), block_table.stride(0), self.slots.data_ptr() + 8 * k,

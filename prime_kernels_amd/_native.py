@@ -27,6 +27,10 @@ SIGNATURES = {
     "pk_workspace_read": (ci, [vp, sz, ctypes.POINTER(ctypes.c_uint), ci]),
     "pk_decode": (ci, [vp, ci, ci, ci, vp, ci, vp, vp, vp, vp, vp, ci, vp, vp, vp,
                        ll, ll, ll, ll, ll, ci, vp, ci, vp, vp, vp, vp, vp, sz, ci]),
+    "pk_decode_mxfp8": (ci, [vp, ci, ci, ci, vp, ci, vp, vp, vp, vp, vp, ci, vp, vp, vp,
+                             ll, ll, ll, ll, ll, ci, vp, ci, vp, vp, vp, vp, vp, sz, ci]),
+    "pk_mxfp8_scale_stride": (sz, [ci]),
+    "pk_quantize_mxfp8": (ci, [vp, vp, vp, vp, ci, ci]),
     "pk_query": (ci, [ctypes.POINTER(ci), ctypes.POINTER(ci), ctypes.POINTER(ci), ctypes.POINTER(ci),
                       ctypes.POINTER(sz)]),
     "prime_decode_status_string": (ctypes.c_char_p, [ci]),

@@ -48,10 +48,19 @@ struct Geom {
   static constexpr int H = H_, NH = NH_, KVH = KVH_, D = 64, I = I_, L = L_, V = 49152;
   static constexpr int QKV = (NH + 2 * KVH) * D;
   static constexpr int GQA = NH / KVH;
+  static constexpr int WF = 0;  // projection weights: 0 bf16, 1 MXFP8 (e4m3 + e8m0 scale per 32)
   static_assert(GQA == 3, "SmolLM2 uses 3 query heads per KV head");
 };
 using G360 = Geom<960, 15, 5, 2560, 32>;   // decode_megakernel_360m/__init__.py:27-35
 using G135 = Geom<576, 9, 3, 1536, 30>;    // decode_megakernel/__init__.py:37-43
+// SmolLM2-360M with MXFP8 projection weights (embedding / LM head and norms stay bf16).
+struct G360Q : G360 {
+  static constexpr int WF = 1;
+};
+
+// MXFP8 scales are stored one byte per 32 weights, each row padded to a multiple of 16 bytes so
+// that every row segment a workgroup streams starts and ends on a 16-byte boundary.
+__host__ __device__ constexpr int scale_stride(int K) { return ((K / 32 + 15) / 16) * 16; }
 
 constexpr int NWG = 256;                 // persistent workgroups (one per CU)
 #ifndef PK_PRODUCER_WAVES
@@ -86,16 +95,21 @@ constexpr int HDR_ABORT_WHERE = 2;
 constexpr size_t HDR_WORDS = 64;
 
 struct LayerW {
-  const uint16_t* norm1;    // [H]
-  const uint16_t* qkv;      // [(NH+2KVH)*D, H]: q rows, then k rows, then v rows
-  const uint16_t* o;        // [H, H]
-  const uint16_t* norm2;    // [H]
-  const uint16_t* gate_up;  // [2I, H]: gate rows, then up rows
-  const uint16_t* down;     // [H, I]
+  const void* norm1;        // [H] bf16
+  const void* qkv;          // [(NH+2KVH)*D, H]: q rows, then k rows, then v rows (bf16 or e4m3)
+  const void* o;            // [H, H]
+  const void* norm2;        // [H] bf16
+  const void* gate_up;      // [2I, H]: gate rows, then up rows
+  const void* down;         // [H, I]
+  const uint8_t* qkv_s;     // MXFP8 only: e8m0 scales [rows, scale_stride(K)] of the matrix above
+  const uint8_t* o_s;
+  const uint8_t* gate_up_s;
+  const uint8_t* down_s;
 };
 
 struct Params {
-  const LayerW* layers;
+  const void* const* layers;   // [L][6] bf16 (norm1, qkv, o, norm2, gate_up, down) or [L][10] MXFP8
+                               // (norm1, qkv, qkv_s, o, o_s, norm2, gate_up, gate_up_s, down, down_s)
   const uint16_t* embed;       // [V, H]
   const uint16_t* final_norm;  // [H]
   const void* input_ids;       // [B] int32 or int64 (ids_i64)
@@ -343,22 +357,31 @@ struct Rows {
 // rotary cos/sin row (attention workgroups), the KV chunk, O rows, norm2 weights, gate rows,
 // up rows, down rows; after the last layer: the final-norm weights and the LM-head segments.
 // Small vectors go through the ring too, so no consumer ever waits on a global load for them.
-enum SegKind { S_NORM1, S_QKV, S_CS, S_KV, S_O, S_NORM2, S_GATE, S_UP, S_DOWN, SEGS_PER_LAYER };
+enum SegKind {
+  S_NORM1, S_QKV, S_QKV_S, S_CS, S_KV, S_O, S_O_S, S_NORM2, S_GATE, S_GATE_S, S_UP, S_UP_S, S_DOWN, S_DOWN_S,
+  SEGS_PER_LAYER
+};
 constexpr int S_FNORM = 100, S_LM = 101;
 
 template <class G>
 __device__ __forceinline__ uint32_t seg_bytes(const Plan<G>& P, int kind, int lm_index, int cs_fp32) {
+  constexpr uint32_t WB = G::WF ? 1u : 2u;  // bytes per projection weight
   switch (kind) {
     case S_NORM1: return P.q1 > P.q0 ? G::H * 2 : 0u;
     case S_NORM2:
     case S_FNORM: return G::H * 2;
-    case S_QKV: return uint32_t(P.q1 - P.q0) * G::H * 2;
+    case S_QKV: return uint32_t(P.q1 - P.q0) * G::H * WB;
+    case S_QKV_S: return G::WF ? uint32_t(P.q1 - P.q0) * scale_stride(G::H) : 0u;
     case S_CS: return P.att ? (cs_fp32 ? 256u : 128u) : 0u;
     case S_KV: return P.att ? uint32_t(P.t1 - P.t0) * 256u : 0u;
-    case S_O: return uint32_t(P.o1 - P.o0) * G::H * 2;
+    case S_O: return uint32_t(P.o1 - P.o0) * G::H * WB;
+    case S_O_S: return G::WF ? uint32_t(P.o1 - P.o0) * scale_stride(G::H) : 0u;
     case S_GATE:
-    case S_UP: return uint32_t(P.a1 - P.a0) * G::H * 2;
-    case S_DOWN: return uint32_t(P.d1 - P.d0) * G::I * 2;
+    case S_UP: return uint32_t(P.a1 - P.a0) * G::H * WB;
+    case S_GATE_S:
+    case S_UP_S: return G::WF ? uint32_t(P.a1 - P.a0) * scale_stride(G::H) : 0u;
+    case S_DOWN: return uint32_t(P.d1 - P.d0) * G::I * WB;
+    case S_DOWN_S: return G::WF ? uint32_t(P.d1 - P.d0) * scale_stride(G::I) : 0u;
     default: {
       const int r0 = P.v0 + lm_index * LM_ROWS;
       const int r1 = min(r0 + LM_ROWS, P.v1);
@@ -484,14 +507,22 @@ __device__ __forceinline__ void producer(const Params& p, const Plan<G>& P, Smem
       base = reinterpret_cast<const uint8_t*>(p.cos_sin) + size_t(P.pos) * 64 * (p.cs_fp32 ? 4 : 2);
     } else {
       const LayerW& Lw = sm.lw[layer];
+      constexpr size_t WB = G::WF ? 1 : 2;
+      constexpr size_t SH = scale_stride(G::H), SI = scale_stride(G::I);
+      auto u8 = [](const void* q) { return reinterpret_cast<const uint8_t*>(q); };
       switch (kind) {
-        case S_NORM1: base = reinterpret_cast<const uint8_t*>(Lw.norm1); break;
-        case S_QKV: base = reinterpret_cast<const uint8_t*>(Lw.qkv) + size_t(P.q0) * G::H * 2; break;
-        case S_O: base = reinterpret_cast<const uint8_t*>(Lw.o) + size_t(P.o0) * G::H * 2; break;
-        case S_NORM2: base = reinterpret_cast<const uint8_t*>(Lw.norm2); break;
-        case S_GATE: base = reinterpret_cast<const uint8_t*>(Lw.gate_up) + size_t(P.a0) * G::H * 2; break;
-        case S_UP: base = reinterpret_cast<const uint8_t*>(Lw.gate_up) + size_t(G::I + P.a0) * G::H * 2; break;
-        default: base = reinterpret_cast<const uint8_t*>(Lw.down) + size_t(P.d0) * G::I * 2; break;
+        case S_NORM1: base = u8(Lw.norm1); break;
+        case S_QKV: base = u8(Lw.qkv) + size_t(P.q0) * G::H * WB; break;
+        case S_QKV_S: base = Lw.qkv_s + size_t(P.q0) * SH; break;
+        case S_O: base = u8(Lw.o) + size_t(P.o0) * G::H * WB; break;
+        case S_O_S: base = Lw.o_s + size_t(P.o0) * SH; break;
+        case S_NORM2: base = u8(Lw.norm2); break;
+        case S_GATE: base = u8(Lw.gate_up) + size_t(P.a0) * G::H * WB; break;
+        case S_GATE_S: base = Lw.gate_up_s + size_t(P.a0) * SH; break;
+        case S_UP: base = u8(Lw.gate_up) + size_t(G::I + P.a0) * G::H * WB; break;
+        case S_UP_S: base = Lw.gate_up_s + size_t(G::I + P.a0) * SH; break;
+        case S_DOWN: base = u8(Lw.down) + size_t(P.d0) * G::I * WB; break;
+        default: base = Lw.down_s + size_t(P.d0) * SI; break;
       }
     }
     for (uint32_t i = (uint32_t(pw) + NPW - n % NPW) % NPW; i < npk && !dead; i += NPW) {
@@ -687,50 +718,62 @@ struct Consumer {
   }
 };
 
-// A lane owns the 16-byte chunks j = lane + 64*c of every row (K bf16 per row).
-template <int K>
+// A lane owns the 16-byte weight chunks j = lane + 64*c of every row; a chunk holds EPC weights
+// (8 bf16, or 16 e4m3 values), i.e. EPC/8 blocks of 8 activations.
+template <int K, int EPC = 8>
 struct Chunks {
-  static constexpr int CH = K / 8;
+  static constexpr int CH = K / EPC;
   static constexpr int CPL = (CH + 63) / 64;
+  static constexpr int SUB = EPC / 8;
 };
+// A lane's activation (or norm-weight) operand for K-long rows of chunk size EPC: 8 values per uint4.
+template <int K, int EPC = 8>
+using XChunks = uint4[Chunks<K, EPC>::CPL][EPC / 8];
 
-// Norm-weight chunks of a lane, from the ring segment that carries them.
-template <class G, int K>
-__device__ __forceinline__ void load_normw(const Consumer<G>& C, uint4 (&nw)[Chunks<K>::CPL], uint32_t seg) {
+// Norm weights of a lane's chunks (8-element blocks), from the ring segment that carries them.
+template <class G, int K, int EPC>
+__device__ __forceinline__ void load_normw(const Consumer<G>& C, XChunks<K, EPC>& nw,
+                                           uint32_t seg) {
 #pragma unroll
-  for (int c = 0; c < Chunks<K>::CPL; ++c) {
+  for (int c = 0; c < Chunks<K, EPC>::CPL; ++c) {
     const int ch = C.lane + 64 * c;
-    nw[c] = ch < Chunks<K>::CH ? C.ring16(seg + uint32_t(ch) * 16u) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < EPC / 8; ++i)
+      nw[c][i] = ch < Chunks<K, EPC>::CH ? C.ring16(seg + uint32_t(ch * EPC + 8 * i) * 2u) : make_uint4(0, 0, 0, 0);
   }
 }
 
-// x chunks of a lane from LDS as packed bf16 pairs: plain (the values are bf16 already), or
-// RMS-normalised with LlamaRMSNorm rounding y = bf16(w * bf16(x * rs)) (modeling_llama.py:62-67).
-template <int K, bool NORM>
-__device__ __forceinline__ void load_x(uint4 (&x)[Chunks<K>::CPL], const float* xs,
-                                       const uint4 (&nw)[Chunks<K>::CPL], float rs, int lane) {
+// Activation chunks of a lane from LDS as packed bf16 pairs: plain (the values are bf16 already),
+// or RMS-normalised with LlamaRMSNorm rounding y = bf16(w * bf16(x * rs)) (modeling_llama.py:62-67).
+template <int K, int EPC, bool NORM>
+__device__ __forceinline__ void load_x(XChunks<K, EPC>& x, const float* xs,
+                                       const XChunks<K, EPC>& nw, float rs, int lane) {
 #pragma unroll
-  for (int c = 0; c < Chunks<K>::CPL; ++c) {
+  for (int c = 0; c < Chunks<K, EPC>::CPL; ++c) {
     const int ch = lane + 64 * c;
-    if (ch < Chunks<K>::CH) {
-      const float4 a = *reinterpret_cast<const float4*>(xs + ch * 8);
-      const float4 b = *reinterpret_cast<const float4*>(xs + ch * 8 + 4);
-      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-      uint32_t o[4];
-      if (NORM) {
-        const uint32_t u[4] = {nw[c].x, nw[c].y, nw[c].z, nw[c].w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t t = pack2(v[2 * e] * rs, v[2 * e + 1] * rs);
-          o[e] = pack2(bf_lo(u[e]) * bf_lo(t), bf_hi(u[e]) * bf_hi(t));
+    for (int i = 0; i < EPC / 8; ++i) {
+      if (ch < Chunks<K, EPC>::CH) {
+        const float* src = xs + ch * EPC + 8 * i;
+        const float4 a = *reinterpret_cast<const float4*>(src);
+        const float4 b = *reinterpret_cast<const float4*>(src + 4);
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        uint32_t o[4];
+        if (NORM) {
+          const uint32_t u[4] = {nw[c][i].x, nw[c][i].y, nw[c][i].z, nw[c][i].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t t = pack2(v[2 * e] * rs, v[2 * e + 1] * rs);
+            o[e] = pack2(bf_lo(u[e]) * bf_lo(t), bf_hi(u[e]) * bf_hi(t));
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = pack2(v[2 * e], v[2 * e + 1]);
         }
+        x[c][i] = make_uint4(o[0], o[1], o[2], o[3]);
       } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = pack2(v[2 * e], v[2 * e + 1]);
+        x[c][i] = make_uint4(0, 0, 0, 0);
       }
-      x[c] = make_uint4(o[0], o[1], o[2], o[3]);
-    } else {
-      x[c] = make_uint4(0, 0, 0, 0);
     }
   }
 }
@@ -741,7 +784,7 @@ __device__ __forceinline__ void load_x(uint4 (&x)[Chunks<K>::CPL], const float* 
 // chunks past the row end (K/8 not a multiple of 64) are zeroed, since their lanes join the sum.
 template <class G, int K, int MAXR>
 __device__ __forceinline__ void dots_ring(const Consumer<G>& C, uint32_t seg, int nrows,
-                                          const uint4 (&x)[Chunks<K>::CPL], float (&out)[MAXR]) {
+                                          const XChunks<K, 8>& x, float (&out)[MAXR]) {
   (void)nrows;
   constexpr int CPL = Chunks<K>::CPL, CH = Chunks<K>::CH;
   uint4 w[MAXR][CPL];
@@ -763,15 +806,80 @@ __device__ __forceinline__ void dots_ring(const Consumer<G>& C, uint32_t seg, in
     float acc = 0.f;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-      acc = dot2(w[r][c].x, x[c].x, acc);
-      acc = dot2(w[r][c].y, x[c].y, acc);
-      acc = dot2(w[r][c].z, x[c].z, acc);
-      acc = dot2(w[r][c].w, x[c].w, acc);
+      acc = dot2(w[r][c].x, x[c][0].x, acc);
+      acc = dot2(w[r][c].y, x[c][0].y, acc);
+      acc = dot2(w[r][c].z, x[c][0].z, acc);
+      acc = dot2(w[r][c].w, x[c][0].w, acc);
     }
     out[r] = acc;
   }
 #pragma unroll
   for (int r = 0; r < MAXR; ++r) out[r] = wave_sum(out[r]);
+}
+
+// E8M0 scale code -> fp32 2^(s-127) (code 0 is the fp32 denormal 2^-127; 255 is NaN).
+__device__ __forceinline__ float e8m0_f32(uint32_t s) {
+  return __uint_as_float(s == 0 ? 0x00400000u : s == 255 ? 0x7fc00000u : s << 23);
+}
+
+// MXFP8 rows: out[r] = row (cw + NCW*r) . x with the row's e4m3 weights (K bytes in segment
+// `segq`) scaled by its e8m0 codes (scale_stride(K) bytes per row in segment `segs`).  Each 16-byte
+// chunk (16 weights, one scale block of 32 covers two chunks) becomes 8 bf16 pairs with
+// v_cvt_scalef32_pk_bf16_fp8 -- exactly bf16(e4m3 * 2^(s-127)), the dequantised weight -- and
+// meets the activations in v_dot2_f32_bf16, so the sums equal the bf16 path's on the
+// dequantised matrix.  Rows past `nrows` read stale ring bytes and are never stored.
+template <class G, int K, int MAXR>
+__device__ __forceinline__ void dots_ring_q(const Consumer<G>& C, uint32_t segq, uint32_t segs,
+                                            const XChunks<K, 16>& x, float (&out)[MAXR]) {
+  constexpr int CPL = Chunks<K, 16>::CPL, CH = Chunks<K, 16>::CH;
+  constexpr uint32_t SK = scale_stride(K);
+  uint4 w[MAXR][CPL];
+  uint32_t sc[MAXR][CPL];
+#pragma unroll
+  for (int r = 0; r < MAXR; ++r) {
+    const uint32_t row = uint32_t(C.cw + NCW * r);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const uint32_t ch = uint32_t(C.lane + 64 * c);
+      w[r][c] = C.ring16(segq + row * uint32_t(K) + ch * 16u);
+      sc[r][c] = C.sm.ring[(segs + row * SK + (ch >> 1)) & (RING - 1)];
+    }
+  }
+  if (CH % 64 != 0) {
+    const bool tail_ok = C.lane + 64 * (CPL - 1) < CH;
+#pragma unroll
+    for (int r = 0; r < MAXR; ++r)
+      if (!tail_ok) { w[r][CPL - 1] = make_uint4(0, 0, 0, 0); sc[r][CPL - 1] = 127u; }
+  }
+#pragma unroll
+  for (int r = 0; r < MAXR; ++r) {
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const float f = e8m0_f32(sc[r][c]);
+      const uint32_t q[4] = {w[r][c].x, w[r][c].y, w[r][c].z, w[r][c].w};
+      const uint32_t a[8] = {x[c][0].x, x[c][0].y, x[c][0].z, x[c][0].w, x[c][1].x, x[c][1].y, x[c][1].z, x[c][1].w};
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const bf16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(int(q[d]), f, false);
+        const bf16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(int(q[d]), f, true);
+        acc = dot2(__builtin_bit_cast(uint32_t, lo), a[2 * d], acc);
+        acc = dot2(__builtin_bit_cast(uint32_t, hi), a[2 * d + 1], acc);
+      }
+    }
+    out[r] = acc;
+  }
+#pragma unroll
+  for (int r = 0; r < MAXR; ++r) out[r] = wave_sum(out[r]);
+}
+
+// Projection rows of a phase in the workgroup's weight format.
+template <class G, int K, int MAXR>
+__device__ __forceinline__ void gemv(const Consumer<G>& C, uint32_t segw, uint32_t segs, int nrows,
+                                     const XChunks<K, G::WF ? 16 : 8>& x,
+                                     float (&out)[MAXR]) {
+  if constexpr (G::WF) dots_ring_q<G, K, MAXR>(C, segw, segs, x, out);
+  else dots_ring<G, K, MAXR>(C, segw, nrows, x, out);
 }
 
 // Lane r (r < MAXR) gets out[r] (wave-uniform values), for one store instruction per wave.  The
@@ -1134,6 +1242,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
   using R = Rows<G>;
   constexpr int GH = (G::H + NCT * 4 - 1) / (NCT * 4);   // poll groups per thread, H words
   constexpr int GI = (G::I + NCT * 4 - 1) / (NCT * 4);   // ... I words
+  constexpr int EW = G::WF ? 16 : 8;                      // activations per 16-byte weight chunk
   const int b = 0;
   auto tr = [&](int l, int ev) { if (C.ct == 0) trace_at(p, l, ev, p.n_layers); };
   if (C.ct == 0 && p.trace)
@@ -1146,10 +1255,11 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
     if (P.q1 > P.q0) {
       const uint32_t segn = C.next_seg(seg_bytes(P, S_NORM1, 0, p.cs_fp32));
       const uint32_t seg = C.next_seg(seg_bytes(P, S_QKV, 0, p.cs_fp32));
+      const uint32_t segs = C.next_seg(seg_bytes(P, S_QKV_S, 0, p.cs_fp32));
       C.wait_filled(C.pos);
       tr(l, 0);
-      uint4 nw[Chunks<G::H>::CPL];
-      load_normw<G, G::H>(C, nw, segn);
+      XChunks<G::H, EW> nw;
+      load_normw<G, G::H, EW>(C, nw, segn);
       float ss;
       if (l == 0) {
         const long long id = p.ids_i64 ? reinterpret_cast<const int64_t*>(p.input_ids)[b]
@@ -1168,11 +1278,11 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       }
       const float rs = rms_scale(C.block_total(ss), G::H);
       tr(l, 1);
-      uint4 x[Chunks<G::H>::CPL];
-      load_x<G::H, true>(x, sm.xs, nw, rs, C.lane);
+      XChunks<G::H, EW> x;
+      load_x<G::H, EW, true>(x, sm.xs, nw, rs, C.lane);
       tr(l, 21);
       float out[R::QKV];
-      dots_ring<G, G::H, R::QKV>(C, seg, P.q1 - P.q0, x, out);
+      gemv<G, G::H, R::QKV>(C, seg, segs, P.q1 - P.q0, x, out);
       C.release(C.pos);
       tr(l, 22);
       const int row = C.cw + NCW * C.lane;
@@ -1190,6 +1300,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
     C.refresh();
     {
       const uint32_t seg = C.next_seg(seg_bytes(P, S_O, 0, p.cs_fp32));
+      const uint32_t segs = C.next_seg(seg_bytes(P, S_O_S, 0, p.cs_fp32));
       const int nrows = P.o1 - P.o0;
       if (nrows > 0) {
         C.wait_filled(C.pos);
@@ -1197,11 +1308,11 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
         C.template poll_split<GH>(X_ATTN, l, b, G::H, sm.xs, nullptr);
         C.cbar();
         tr(l, 7);
-        uint4 x[Chunks<G::H>::CPL];
-        const uint4 none[Chunks<G::H>::CPL] = {};
-        load_x<G::H, false>(x, sm.xs, none, 1.f, C.lane);
+        XChunks<G::H, EW> x;
+        const XChunks<G::H, EW> none = {};
+        load_x<G::H, EW, false>(x, sm.xs, none, 1.f, C.lane);
         float out[R::O];
-        dots_ring<G, G::H, R::O>(C, seg, nrows, x, out);
+        gemv<G, G::H, R::O>(C, seg, segs, nrows, x, out);
         C.release(C.pos);
         const int row = C.cw + NCW * C.lane;
         if (C.lane < R::O && row < nrows) {
@@ -1218,20 +1329,22 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
     {
       const uint32_t segn = C.next_seg(seg_bytes(P, S_NORM2, 0, p.cs_fp32));
       const uint32_t segg = C.next_seg(seg_bytes(P, S_GATE, 0, p.cs_fp32));
+      const uint32_t segg_s = C.next_seg(seg_bytes(P, S_GATE_S, 0, p.cs_fp32));
       const uint32_t segu = C.next_seg(seg_bytes(P, S_UP, 0, p.cs_fp32));
+      const uint32_t segu_s = C.next_seg(seg_bytes(P, S_UP_S, 0, p.cs_fp32));
       const int na = P.a1 - P.a0;
       C.wait_filled(C.pos);
-      uint4 nw[Chunks<G::H>::CPL];
-      load_normw<G, G::H>(C, nw, segn);
+      XChunks<G::H, EW> nw;
+      load_normw<G, G::H, EW>(C, nw, segn);
       tr(l, 9);
       const float ss = C.template poll_split<GH>(X_H1, l, b, G::H, sm.xs, sm.h1keep);
       const float rs = rms_scale(C.block_total(ss), G::H);
       tr(l, 10);
-      uint4 x[Chunks<G::H>::CPL];
-      load_x<G::H, true>(x, sm.xs, nw, rs, C.lane);
+      XChunks<G::H, EW> x;
+      load_x<G::H, EW, true>(x, sm.xs, nw, rs, C.lane);
       float og[R::ACT], ou[R::ACT];
-      dots_ring<G, G::H, R::ACT>(C, segg, na, x, og);
-      dots_ring<G, G::H, R::ACT>(C, segu, na, x, ou);
+      gemv<G, G::H, R::ACT>(C, segg, segg_s, na, x, og);
+      gemv<G, G::H, R::ACT>(C, segu, segu_s, na, x, ou);
       C.release(C.pos);
       const int row = C.cw + NCW * C.lane;
       if (C.lane < R::ACT && row < na) {
@@ -1245,17 +1358,18 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
     C.refresh();
     {
       const uint32_t seg = C.next_seg(seg_bytes(P, S_DOWN, 0, p.cs_fp32));
+      const uint32_t segs = C.next_seg(seg_bytes(P, S_DOWN_S, 0, p.cs_fp32));
       const int nrows = P.d1 - P.d0;
       C.wait_filled(C.pos);
       tr(l, 12);
       C.template poll_split<GI>(X_ACT, l, b, G::I, sm.xs, nullptr);
       C.cbar();
       tr(l, 13);
-      uint4 x[Chunks<G::I>::CPL];
-      const uint4 none[Chunks<G::I>::CPL] = {};
-      load_x<G::I, false>(x, sm.xs, none, 1.f, C.lane);
+      XChunks<G::I, EW> x;
+      const XChunks<G::I, EW> none = {};
+      load_x<G::I, EW, false>(x, sm.xs, none, 1.f, C.lane);
       float out[R::DOWN];
-      dots_ring<G, G::I, R::DOWN>(C, seg, nrows, x, out);
+      gemv<G, G::I, R::DOWN>(C, seg, segs, nrows, x, out);
       C.release(C.pos);
       const int row = C.cw + NCW * C.lane;
       if (C.lane < R::DOWN && row < nrows) {
@@ -1270,20 +1384,20 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
   // ---------------- final RMSNorm + LM head + argmax ----------------
   const uint32_t segf = C.next_seg(seg_bytes(P, S_FNORM, 0, p.cs_fp32));
   C.wait_filled(C.pos);
-  uint4 nw[Chunks<G::H>::CPL];
-  load_normw<G, G::H>(C, nw, segf);
+  XChunks<G::H> nw;  // the final norm and the tied LM head stay bf16
+  load_normw<G, G::H, 8>(C, nw, segf);
   C.release(C.pos);
   const float ss = C.template poll_split<GH>(X_X, p.n_layers - 1, b, G::H, sm.xs, nullptr);
   const float rs = rms_scale(C.block_total(ss), G::H);
-  uint4 x[Chunks<G::H>::CPL];
-  load_x<G::H, true>(x, sm.xs, nw, rs, C.lane);
+  XChunks<G::H> x;
+  load_x<G::H, 8, true>(x, sm.xs, nw, rs, C.lane);
   if (P.wg == 0) {
     // final-normed hidden state (the reference's out_hidden, block360_kernel.inc:810-815)
 #pragma unroll
     for (int c = 0; c < Chunks<G::H>::CPL; ++c) {
       const int ch = C.lane + 64 * c;
       if (C.cw == 0 && ch < Chunks<G::H>::CH)
-        *reinterpret_cast<uint4*>(p.out_hidden + size_t(b) * G::H + ch * 8) = x[c];
+        *reinterpret_cast<uint4*>(p.out_hidden + size_t(b) * G::H + ch * 8) = x[c][0];
     }
   }
   if (!p.lm_head) return;
@@ -1373,7 +1487,18 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel(Params p) {
   }
   // pointer tables into LDS, so the producers never wait on a vector-memory load of their own
   for (int i = threadIdx.x; i < p.n_layers; i += WG_THREADS) {
-    sm.lw[i] = p.layers[i];
+    LayerW w{};
+    if (G::WF) {
+      const void* const* t = p.layers + size_t(i) * 10;
+      w.norm1 = t[0]; w.qkv = t[1]; w.qkv_s = static_cast<const uint8_t*>(t[2]);
+      w.o = t[3]; w.o_s = static_cast<const uint8_t*>(t[4]); w.norm2 = t[5];
+      w.gate_up = t[6]; w.gate_up_s = static_cast<const uint8_t*>(t[7]);
+      w.down = t[8]; w.down_s = static_cast<const uint8_t*>(t[9]);
+    } else {
+      const void* const* t = p.layers + size_t(i) * 6;
+      w.norm1 = t[0]; w.qkv = t[1]; w.o = t[2]; w.norm2 = t[3]; w.gate_up = t[4]; w.down = t[5];
+    }
+    sm.lw[i] = w;
     sm.kvp[i] = p.kv[i];
   }
   __syncthreads();
@@ -1391,6 +1516,63 @@ template <class G>
 constexpr size_t lds_bytes() { return sizeof(Smem<G>); }
 static_assert(sizeof(Smem<G360>) <= 160 * 1024, "LDS budget of one gfx950 workgroup");
 static_assert(sizeof(Smem<G135>) <= 160 * 1024, "LDS budget of one gfx950 workgroup");
+static_assert(sizeof(Smem<G360Q>) <= 160 * 1024, "LDS budget of one gfx950 workgroup");
+
+// ------------------------------------------------------------------------------------------------
+// MXFP8 quantisation of bf16 weights: per 32 consecutive elements of a row, scale code
+// s = e8m0(amax / 448) rounded toward +inf (saturating at 254), then each element becomes
+// e4m3(bf16(x * 2^(127-s))) with round-to-nearest-even and saturation to +-448
+// (the OCP MX rule as prime_kernels/rmsnorm/test.cu:126-144 applies it).  One thread per block.
+// ------------------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t e8m0_ceil(float f) {
+  if (f != f) return 255u;
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t e = (u >> 23) & 255u, m = u & 0x7fffffu;
+  if (e == 255u) return 254u;
+  if (e == 0u) return m > 0x400000u ? 1u : 0u;  // zero and values up to 2^-127 -> 2^-127
+  const uint32_t c = e + (m ? 1u : 0u);
+  return c > 254u ? 254u : c;
+}
+
+__device__ __forceinline__ uint32_t e4m3_sat(float v) {  // v holds a bf16 value
+  const uint32_t sgn = (__float_as_uint(v) >> 31) << 7;
+  if (v != v) return sgn | 0x7fu;
+  const float a = fabsf(v);
+  if (a >= 448.f) return sgn | 0x7eu;
+  if (a < 0.015625f) return sgn | uint32_t(__builtin_rintf(a * 512.f));  // subnormal steps of 2^-9
+  int e = int((__float_as_uint(a) >> 23) & 255u) - 127;
+  const float mant = a * __uint_as_float(uint32_t(127 - e) << 23);  // in [1, 2), exact
+  uint32_t m = uint32_t(__builtin_rintf((mant - 1.f) * 8.f));
+  if (m == 8u) { m = 0u; ++e; }
+  return sgn | (uint32_t(e + 7) << 3) | m;
+}
+
+__global__ void __launch_bounds__(256) quantize_mxfp8(const uint16_t* src, uint8_t* q, uint8_t* sc, int rows,
+                                                      int cols, int sk) {
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (long long)rows * sk) return;
+  const int row = int(t / sk), blk = int(t % sk);
+  uint8_t* srow = sc + size_t(row) * sk;
+  if (blk >= cols / 32) {  // row padding of the scale array
+    srow[blk] = 0;
+    return;
+  }
+  const uint16_t* x = src + size_t(row) * cols + size_t(blk) * 32;
+  float amax = 0.f;
+  for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(bf2f(x[k])));
+  const uint32_t code = e8m0_ceil(amax * (1.f / 448.f));
+  const float inv = __uint_as_float(code >= 254u ? 0x00400000u : (254u - code) << 23);  // 2^(127-s)
+  uint32_t packed[8];
+  for (int k = 0; k < 32; k += 4) {
+    uint32_t w = 0;
+    for (int i = 0; i < 4; ++i) w |= e4m3_sat(rnd(bf2f(x[k + i]) * inv)) << (8 * i);
+    packed[k / 4] = w;
+  }
+  uint4* qo = reinterpret_cast<uint4*>(q + size_t(row) * cols + size_t(blk) * 32);
+  qo[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  qo[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+  srow[blk] = uint8_t(code);
+}
 
 struct DeviceInfo {
   int ok = 0, status = 0, cus = 0, coop = 0, max_lds = 0, gfx950 = 0;
@@ -1539,7 +1721,7 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
       (layer_outputs && mis(layer_outputs)) || (out_logits && mis(out_logits)))
     return PK_ERR_ALIGN;
   Params p{};
-  p.layers = reinterpret_cast<const LayerW*>(layers);
+  p.layers = reinterpret_cast<const void* const*>(layers);
   p.embed = reinterpret_cast<const uint16_t*>(embed);
   p.final_norm = reinterpret_cast<const uint16_t*>(final_norm);
   p.input_ids = input_ids;
@@ -1655,6 +1837,37 @@ extern "C" int pk_decode(void* stream, int model, int B, int n_layers, const voi
                                      out_hidden, layer_outputs, out_ids, out_logits, scratch, scratch_bytes,
                                      max_seq_len);
   return PK_ERR_MODEL;
+}
+
+extern "C" int pk_decode_mxfp8(void* stream, int model, int B, int n_layers, const void* input_ids, int ids_i64,
+                               const void* embed, const void* final_norm, const void* positions,
+                               const void* seq_lens, const void* block_table, int bt_stride,
+                               const void* slot_mapping, const void* layers, void* const* kv, long long k_off,
+                               long long v_off, long long block_stride, long long token_stride,
+                               long long head_stride, int block_size, const void* cos_sin, int cs_fp32,
+                               void* out_hidden, void* layer_outputs, void* out_ids, void* out_logits,
+                               void* scratch, size_t scratch_bytes, int max_seq_len) {
+  if (model != PK_MODEL_SMOLLM2_360M) return PK_ERR_MODEL;
+  return pk::decode_impl<pk::G360Q>(stream, B, n_layers, input_ids, ids_i64, embed, final_norm, positions,
+                                    seq_lens, block_table, bt_stride, slot_mapping, layers, kv, k_off, v_off,
+                                    block_stride, token_stride, head_stride, block_size, cos_sin, cs_fp32,
+                                    out_hidden, layer_outputs, out_ids, out_logits, scratch, scratch_bytes,
+                                    max_seq_len);
+}
+
+extern "C" size_t pk_mxfp8_scale_stride(int cols) { return cols > 0 ? size_t(pk::scale_stride(cols)) : 0; }
+
+extern "C" int pk_quantize_mxfp8(void* stream, const void* src, void* q, void* scales, int rows, int cols) {
+  if (!src || !q || !scales) return PK_ERR_NULL;
+  if (rows < 1 || cols < 32 || cols % 32) return PK_ERR_BLOCK;
+  if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(scales)) & 15u)
+    return PK_ERR_ALIGN;
+  const int sk = pk::scale_stride(cols);
+  const long long n = (long long)rows * sk;
+  hipLaunchKernelGGL(pk::quantize_mxfp8, dim3(unsigned((n + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const uint16_t*>(src),
+                     reinterpret_cast<uint8_t*>(q), reinterpret_cast<uint8_t*>(scales), rows, cols, sk);
+  return hipGetLastError();
 }
 
 extern "C" int pk_query(int* cu_count, int* coop, int* max_lds_per_block, int* is_gfx950, size_t* lds_bytes) {

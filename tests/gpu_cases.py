@@ -35,6 +35,7 @@ class Case:
         self.btd = kv.block_table.to(self.dev)
         self.csd = self.cos_sin.to(self.dev)
         self.mod = module_for(geom)
+        self.kernel_layers = self.wd.layers  # what the kernel is given (bf16, or MXFP8 10-tuples)
 
     def sync_kv_from_oracle(self) -> None:
         for g, c in zip(self.kvd, self.kv.caches):
@@ -54,7 +55,7 @@ class Case:
         cs = self.csd.float().contiguous() if cs_fp32 else self.csd
         hid, out_ids = self.mod.decode_step(
             input_ids=torch.tensor(ids, dtype=ids_dtype, device=dev), positions=pos, seq_lens=sl,
-            block_table=self.btd, slot_mapping=slots, embed=self.wd.embed, layers=self.wd.layers,
+            block_table=self.btd, slot_mapping=slots, embed=self.wd.embed, layers=self.kernel_layers,
             final_norm=self.wd.final_norm, kv_caches=self.kvd, cos_sin_cache=cs, eps=1e-5,
             num_layers=self.geom.layers, return_token_ids=True, logits_out=lg, layer_outputs=lo)
         torch.cuda.synchronize()
@@ -99,7 +100,7 @@ class Case:
             input_ids=torch.tensor([self.TF_ROW], device=dev), positions=torch.tensor([position], device=dev),
             seq_lens=torch.tensor([position + 1], dtype=torch.int32, device=dev), block_table=self.btd,
             slot_mapping=torch.tensor([self.kv.slot(0, position)], device=dev), embed=self._embed_tf,
-            layers=[self.wd.layers[li]], final_norm=self.wd.final_norm, kv_caches=[self.kvd[li]],
+            layers=[self.kernel_layers[li]], final_norm=self.wd.final_norm, kv_caches=[self.kvd[li]],
             cos_sin_cache=self.csd, eps=1e-5, num_layers=1, return_token_ids=True, logits_out=lg,
             layer_outputs=lo)
         torch.cuda.synchronize()
@@ -107,6 +108,28 @@ class Case:
         if logits:
             res["logits"] = lg[0].cpu()
         return res
+
+
+def mxfp8_case(geom: O.Geometry, seed: int, contexts, *, norm_jitter=0.05, fill_seed: int | None = None) -> Case:
+    """A case whose kernel runs MXFP8 weights quantised on the GPU by the library, while the
+    oracle (and the eager-GPU floor) run the exact bf16 dequantisation of those same codes."""
+    from oracle import mxfp8 as MX
+    import prime_kernels_amd as pk
+
+    w = O.make_weights(geom, seed, norm_jitter=norm_jitter)
+    mod = pk.load("decode_megakernel_360m_mxfp8")
+    dev = torch.device("cuda:0")
+    qlayers = mod.quantize_layers([tuple(t.to(dev) for t in layer) for layer in w.layers])
+    torch.cuda.synchronize()
+    deq = [MX.dequantize_layer(tuple(t.cpu().numpy() if t.dtype == torch.uint8 else t.cpu() for t in ql))
+           for ql in qlayers]
+    wq = O.Weights(geom, w.embed, w.final_norm, deq)
+    cap = max(contexts) + 16
+    kv = O.make_paged_kv(geom, len(contexts), cap, seed=fill_seed if fill_seed is not None else seed + 3)
+    case = Case(geom, wq, kv, cap + 16)
+    case.mod = mod
+    case.kernel_layers = qlayers
+    return case
 
 
 def compare_logits(k: torch.Tensor, r: torch.Tensor) -> dict:

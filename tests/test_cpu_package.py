@@ -16,7 +16,7 @@ HEADER = ROOT / "include" / "prime_decode.h"
 
 
 def test_registry_surface():
-    assert pk.KERNELS == ("decode_megakernel_360m", "decode_megakernel")
+    assert pk.KERNELS == ("decode_megakernel_360m", "decode_megakernel", "decode_megakernel_360m_mxfp8")
     s = pk.spec("decode_megakernel_360m")
     assert s.module == "prime_kernels_amd.decode_megakernel_360m"
     assert [str(a) for a in s.archs] == ["gfx950"] and s.ops == "prime_decode"
