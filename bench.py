@@ -24,15 +24,17 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 CONTEXT = 1024
-W_LAYER_360M = 19_664_640
+W_LAYER_360M = 19_664_640        # bf16 projections + norms of one layer
+W_LAYER_360M_MXFP8 = 10_141_440  # e4m3 projections + one e8m0 byte per 32 weights + bf16 norms
 E_LMHEAD_360M = 94_371_840
 KV_TOKEN_360M = 40_960
 HIDDEN_BYTES = 1_920
 
 
-def step_bytes(S: int, layers: int = 32) -> int:
+def step_bytes(S: int, layers: int = 32, weights: str = "bf16") -> int:
     """Algorithmic bytes of one step attending S tokens (S counts the new one)."""
-    return layers * W_LAYER_360M + E_LMHEAD_360M + HIDDEN_BYTES + KV_TOKEN_360M * S + KV_TOKEN_360M + HIDDEN_BYTES
+    w = W_LAYER_360M if weights == "bf16" else W_LAYER_360M_MXFP8
+    return layers * w + E_LMHEAD_360M + HIDDEN_BYTES + KV_TOKEN_360M * S + KV_TOKEN_360M + HIDDEN_BYTES
 
 
 def cpu_baseline(seconds: float = 15.0) -> dict:
@@ -71,7 +73,12 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--weights", choices=("bf16", "mxfp8"), default="bf16",
+                    help="projection weights: bf16 (BASELINE config 3, the default) or MXFP8 (config 5)")
+    ap.add_argument("--context", type=int, default=None,
+                    help="cached tokens before the first timed step (default 1024; 8192 with --weights mxfp8)")
     args = ap.parse_args()
+    context = args.context if args.context is not None else (CONTEXT if args.weights == "bf16" else 8192)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: every box in this setup has one MI355X and the decode "
               f"path shards by data parallelism with no exchange (see DESIGN.md); --gpus {args.gpus} is not run.",
@@ -83,22 +90,24 @@ def main() -> None:
     from prime_kernels_amd import workload as WL
     from prime_kernels_amd._decode import StepLauncher
 
-    mod = pk.load("decode_megakernel_360m")
+    mod = pk.load("decode_megakernel_360m" if args.weights == "bf16" else "decode_megakernel_360m_mxfp8")
     model = mod.MODEL
     dev = torch.device("cuda:0")
     K, W = args.steps, args.warmup
-    embed, final_norm, layers = WL.random_weights(model, 1234, dev)
-    kv = WL.PagedKV(model, 1, CONTEXT + max(K, W) + 16, device=dev, seed=5, fill="randn")
-    cos_sin = WL.rope_table(CONTEXT + max(K, W) + 16, device=dev)
+    embed, final_norm, layers = WL.random_weights(pk.load("decode_megakernel_360m").MODEL, 1234, dev)
+    if args.weights == "mxfp8":
+        layers = mod.quantize_layers(layers)
+    kv = WL.PagedKV(model, 1, context + max(K, W) + 16, device=dev, seed=5, fill="randn")
+    cos_sin = WL.rope_table(context + max(K, W) + 16, device=dev)
     torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream(dev)
     warm = StepLauncher(model, embed=embed, layers=layers, final_norm=final_norm, kv_caches=kv.caches,
-                        block_table=kv.block_table, cos_sin_cache=cos_sin, first_id=17, start_pos=CONTEXT, steps=max(W, 1))
+                        block_table=kv.block_table, cos_sin_cache=cos_sin, first_id=17, start_pos=context, steps=max(W, 1))
     for k in range(W):
         warm.launch(k, stream.cuda_stream)
     timed = StepLauncher(model, embed=embed, layers=layers, final_norm=final_norm, kv_caches=kv.caches,
-                         block_table=kv.block_table, cos_sin_cache=cos_sin, first_id=17, start_pos=CONTEXT, steps=K)
+                         block_table=kv.block_table, cos_sin_cache=cos_sin, first_id=17, start_pos=context, steps=K)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
@@ -116,15 +125,16 @@ def main() -> None:
     if not bool(((ids >= 0) & (ids < 49152)).all()):
         raise RuntimeError("greedy ids out of range")
 
-    total_bytes = sum(step_bytes(CONTEXT + 1 + k) for k in range(K))
+    total_bytes = sum(step_bytes(context + 1 + k, weights=args.weights) for k in range(K))
     ms_per_step = ms / K
     achieved = total_bytes / (ms * 1e-3) / 1e9
     traffic = None
-    tfile = ROOT / "profiles" / "decode360_ctx1024_traffic.json"
+    tfile = ROOT / "profiles" / f"decode360_{'' if args.weights == 'bf16' else 'mxfp8_'}ctx{context}_traffic.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+    wname = "bf16" if args.weights == "bf16" else "MXFP8-weight"
     line = {
-        "metric": "decode tok/s, SmolLM2-360M bf16 bs=1 ctx=1024; % of HBM roofline",
+        "metric": f"decode tok/s, SmolLM2-360M {wname} bs=1 ctx={context}; % of HBM roofline",
         "value": round(K / (ms * 1e-3), 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -134,17 +144,20 @@ def main() -> None:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded random-init weights N(0,0.02) bf16, KV context N(0,1) bf16, greedy ids fed back on device)",
-        "config": {"workload": "smollm2-360m greedy decode, batch 1, 1024-token context, K steps at context 1025..1024+K",
-                   "batch": 1, "context": CONTEXT, "layers": 32, "lm_head": "tied, fused argmax",
-                   "launch": "one cooperative kernel per step, 256 workgroups"},
+        "dtype": "bf16" if args.weights == "bf16" else "e4m3 weights, bf16 activations",
+        "data": "synthetic (seeded random-init weights N(0,0.02) bf16" +
+                (", projections quantised to MXFP8 on the GPU" if args.weights == "mxfp8" else "") +
+                ", KV context N(0,1) bf16, greedy ids fed back on device)",
+        "config": {"workload": f"smollm2-360m greedy decode, batch 1, {context}-token context, K steps at context "
+                               f"{context + 1}..{context}+K" + (", MXFP8 projection weights" if args.weights == "mxfp8" else ""),
+                   "batch": 1, "context": context, "layers": 32, "weights": args.weights,
+                   "lm_head": "tied, fused argmax", "launch": "one cooperative kernel per step, 256 workgroups"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "bytes_per_step": round(total_bytes / K)},
         "host_wall_ms_per_step": round(wall * 1e3 / K, 5),
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.weights == "bf16":
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)
 
