@@ -31,7 +31,7 @@ class Model:
     kv_heads: int
     layers: int
     head_dim: int = 64
-    max_batch: int = 1
+    max_batch: int = 16
     max_seq: int = 12288
     weight_format: str = "bf16"   # "bf16", or "mxfp8" (e4m3 projections + e8m0 scale per 32)
 
@@ -66,7 +66,7 @@ def mxfp8_scale_stride(cols: int) -> int:
 SMOLLM2_360M = Model("decode_megakernel_360m", 360, hidden=960, inter=2560, heads=15, kv_heads=5, layers=32)
 SMOLLM2_135M = Model("decode_megakernel", 135, hidden=576, inter=1536, heads=9, kv_heads=3, layers=30)
 SMOLLM2_360M_MXFP8 = Model("decode_megakernel_360m_mxfp8", 360, hidden=960, inter=2560, heads=15, kv_heads=5,
-                           layers=32, weight_format="mxfp8")
+                           layers=32, max_batch=1, weight_format="mxfp8")
 MODELS = {m.model_id: m for m in (SMOLLM2_360M, SMOLLM2_135M)}
 
 

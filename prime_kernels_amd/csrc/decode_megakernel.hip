@@ -130,6 +130,7 @@ struct Params {
   int B;
   int n_layers;
   int lm_head;                 // 1: run the LM head + argmax
+  int max_seq;                 // block_table capacity in tokens (seq_lens are clamped to it)
   int ids_i64;
   unsigned long long* trace;   // optional per-phase timestamps (diagnostics)
 };
@@ -301,7 +302,7 @@ struct Plan {
 
   __device__ __forceinline__ void init(const Params& p, int wg_) {
     wg = wg_;
-    S = max(p.seq_lens[0], 1);
+    S = min(max(p.seq_lens[0], 1), p.max_seq);
     pos = int(max(p.positions[0], (int64_t)0));
     slot = p.slot_mapping[0];
     const int old = S - 1;
@@ -570,18 +571,19 @@ __device__ __forceinline__ void producer(const Params& p, const Plan<G>& P, Smem
 // Consumer waves
 // ------------------------------------------------------------------------------------------------
 
-template <class G>
+template <class G, class SM = Smem<G>, class PL = Plan<G>>
 struct Consumer {
+  static constexpr uint32_t RB = sizeof(SM::ring);  // ring bytes (a power of two)
   const Params& p;
-  const Plan<G>& P;
-  Smem<G>& sm;
+  const PL& P;
+  SM& sm;
   int cw, lane, ct;          // consumer wave, lane, consumer thread id
   uint32_t pos = 0;          // stream cursor (mirrors the producer)
   uint32_t bar_gen = 0;
   uint32_t tag16, tag32;
   bool dead = false;
 
-  __device__ __forceinline__ Consumer(const Params& p_, const Plan<G>& P_, Smem<G>& sm_, uint32_t ep)
+  __device__ __forceinline__ Consumer(const Params& p_, const PL& P_, SM& sm_, uint32_t ep)
       : p(p_), P(P_), sm(sm_) {
     cw = (threadIdx.x >> 6) - NPW;
     lane = threadIdx.x & 63;
@@ -625,10 +627,10 @@ struct Consumer {
       if (!spin.again()) { dead = true; break; }
   }
   __device__ __forceinline__ uint4 ring16(uint32_t at) const {
-    return *reinterpret_cast<const uint4*>(sm.ring + (at & (RING - 1)));
+    return *reinterpret_cast<const uint4*>(sm.ring + (at & (RB - 1)));
   }
   __device__ __forceinline__ uint32_t ring4(uint32_t at) const {
-    return *reinterpret_cast<const uint32_t*>(sm.ring + (at & (RING - 1)));
+    return *reinterpret_cast<const uint32_t*>(sm.ring + (at & (RB - 1)));
   }
   __device__ __forceinline__ uint32_t w16(float v) const { return (tag16 << 16) | f2bf(v); }
   __device__ __forceinline__ bool ok4(u32x4 v) const {
@@ -842,7 +844,7 @@ __device__ __forceinline__ void dots_ring_q(const Consumer<G>& C, uint32_t segq,
     for (int c = 0; c < CPL; ++c) {
       const uint32_t ch = uint32_t(C.lane + 64 * c);
       w[r][c] = C.ring16(segq + row * uint32_t(K) + ch * 16u);
-      sc[r][c] = C.sm.ring[(segs + row * SK + (ch >> 1)) & (RING - 1)];
+      sc[r][c] = C.sm.ring[(segs + row * SK + (ch >> 1)) & (C.RB - 1)];
     }
   }
   if (CH % 64 != 0) {
@@ -1262,8 +1264,9 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       load_normw<G, G::H, EW>(C, nw, segn);
       float ss;
       if (l == 0) {
-        const long long id = p.ids_i64 ? reinterpret_cast<const int64_t*>(p.input_ids)[b]
-                                       : reinterpret_cast<const int32_t*>(p.input_ids)[b];
+        long long id = p.ids_i64 ? reinterpret_cast<const int64_t*>(p.input_ids)[b]
+                                 : reinterpret_cast<const int32_t*>(p.input_ids)[b];
+        id = min(max(id, 0LL), (long long)G::V - 1);  // an out-of-range id must not read past the table
         const uint16_t* e = p.embed + size_t(id) * G::H;
         float s = 0.f;
         for (int i = C.ct; i < G::H; i += NCT) {
@@ -1512,8 +1515,927 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel(Params p) {
   if (blockIdx.x == 0 && threadIdx.x == 0) st_dev(p.ws + HDR_EPOCH, epoch);
 }
 
+// ================================================================================================
+// Batched decode: 2..16 sequences per launch, ragged contexts.  The same persistent
+// producer/consumer structure as the batch-1 kernel, with three differences:
+//  * projections are [rows x 16 tokens] products on the matrix cores (v_mfma_f32_16x16x32_bf16:
+//    weight rows from the LDS ring as A, the staged bf16 activations [token][k] as B), the K range
+//    split over the four consumer waves and the partial tiles summed in LDS in a fixed order;
+//  * the large activation exchanges (x, attn, h1, act: B x K values) are plain bf16 arrays: each
+//    workgroup stores its rows, waits for the stores to complete and then sets its flag; readers
+//    poll the 256 flags and pull the [B][K] block into LDS with LDS-DMA (half the bytes of tagged
+//    words, and no per-word polling); q/k/v stay tagged words as in the batch-1 kernel;
+//  * attention is split into (sequence, KV head, chunk) items, several per workgroup, processed
+//    in three passes so that no workgroup waits on another while holding work others need:
+//    A) scores of every item (K streamed through the ring) and the chunk softmax statistics;
+//    B) the global statistics of each (sequence, KV head), probabilities rounded as HF does,
+//       P.V (V streamed), partial sums published; C) leaders add their chunks' partials.
+// ================================================================================================
+constexpr int BMAX = 16;                  // sequences per launch (the MFMA N dimension)
+constexpr uint32_t RING_B = 64u * 1024u;  // ring bytes (the staged activations take the rest of LDS)
+constexpr int TCB = 256;                  // max cached tokens per attention item
+constexpr int IPW = 16;                   // max attention items per workgroup
+constexpr int MAX_ITEMS = NWG * IPW;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// Batched workspace regions, after the batch-1 layout (so one workspace serves both kernels).
+template <class G>
+struct WSB {
+  static constexpr int XMAX = WS<G>::XMAX;
+  static constexpr size_t REC0 = WS<G>::TOTAL;                       // P.V partials, 3 x 64 tagged fp32
+  static constexpr size_t STAT0 = REC0 + size_t(MAX_ITEMS) * REC_WORDS * 2;
+  static constexpr size_t FLAG0 = STAT0 + size_t(MAX_ITEMS) * STAT_WORDS * 2;
+  static constexpr size_t DATA0 = FLAG0 + size_t(NKIND) * G::L * NWG;  // 64-byte aligned below
+  static constexpr size_t DATA_WORDS = size_t(BMAX) * XMAX / 2;        // one [B][K] bf16 array
+  static constexpr size_t TOTAL = DATA0 + size_t(NKIND) * G::L * DATA_WORDS;
+  static_assert(DATA0 % 16 == 0 && DATA_WORDS % 256 == 0, "bf16 arrays start on 64-byte lines");
+  __device__ static size_t rec(int item) { return REC0 + size_t(item) * REC_WORDS * 2; }
+  __device__ static size_t stat(int item) { return STAT0 + size_t(item) * STAT_WORDS * 2; }
+  __device__ static size_t flag(int kind, int l, int wg) { return FLAG0 + (size_t(kind) * G::L + l) * NWG + wg; }
+  __device__ static size_t data(int kind, int l) { return DATA0 + (size_t(kind) * G::L + l) * DATA_WORDS; }
+};
+
+template <class G>
+struct SmemB {
+  static constexpr int XS = G::I > G::H ? G::I : G::H;
+  struct Attn {
+    float qkvw[NCW][5 * 64];          // per-wave attention inputs of the current item
+    uint16_t sc[IPW][3][TCB + 2];     // bf16 scores of every item of this workgroup
+    uint16_t pb[3][TCB + 4];          // bf16 probabilities of the current item
+    float own[IPW][3 * 64];           // leader items: this chunk's partial sums of p.v
+    float cst[IPW][2][3];             // chunk softmax max / sum per item and head
+    float csr[BMAX][64];              // rotary cos | sin of each sequence's position
+  };
+  uint8_t ring[RING_B];
+  union {
+    uint16_t xs[BMAX * XS];           // staged activations, [token][K] bf16
+    Attn at;
+  };
+  float tile[NCW][256];               // per-wave MFMA partial tiles
+  float xk[BMAX][8];                  // residual x of this workgroup's O rows
+  float hk[BMAX][8];                  // residual h1 of this workgroup's down rows
+  float rsb[BMAX];                    // per-sequence RMS scale
+  float red[NCW];
+  float wml[NCW][2][3];
+  float wo[NCW][3][64];
+  LayerW lw[G::L];
+  const void* kvp[G::L];
+  int32_t blk[IPW][TCB / 16 + 2];     // block ids of each item's chunk
+  int32_t sS[BMAX], sPos[BMAX], sId[BMAX];
+  long long sSlot[BMAX];
+  float lm_val[NCW][BMAX];
+  int32_t lm_idx[NCW][BMAX];
+  uint32_t front[NPW];
+  uint32_t consumed[NCW];
+  uint32_t cbar;
+};
+static_assert(sizeof(typename SmemB<G135>::Attn) <= sizeof(uint16_t) * BMAX * SmemB<G135>::XS, "union sizing");
+
+template <class G>
+struct PlanB {
+  int wg, B;
+  int q0, q1, o0, o1, a0, a1, d0, d1, v0, v1, n_lm;
+  int tc;      // cached tokens per attention chunk
+  int nitems;  // attention items over all workgroups
+  int ni;      // items of this workgroup: wg, wg + NWG, ...
+
+  __device__ __forceinline__ int chunks(int S) const {
+    const int old = max(S, 1) - 1;
+    return old == 0 ? 1 : (old + tc - 1) / tc;
+  }
+  __device__ __forceinline__ void init(const Params& p, const int32_t* sS, int wg_) {
+    wg = wg_;
+    B = p.B;
+    q0 = split_lo(G::QKV, NWG, wg); q1 = split_lo(G::QKV, NWG, wg + 1);
+    o0 = split_lo(G::H, NWG, wg);   o1 = split_lo(G::H, NWG, wg + 1);
+    a0 = split_lo(G::I, NWG, wg);   a1 = split_lo(G::I, NWG, wg + 1);
+    d0 = split_lo(G::H, NWG, wg);   d1 = split_lo(G::H, NWG, wg + 1);
+    if (p.lm_head) { v0 = split_lo(G::V, NWG, wg); v1 = split_lo(G::V, NWG, wg + 1); }
+    else { v0 = v1 = 0; }
+    n_lm = (v1 - v0 + LM_ROWS - 1) / LM_ROWS;
+    // chunks of about two items per workgroup, 64..TCB tokens, a multiple of 16
+    long long tot = 0;
+    for (int b = 0; b < B; ++b) tot += max(sS[b], 1) - 1;
+    int t = int((tot * G::KVH + 2LL * NWG - 1) / (2LL * NWG));
+    t = (t + 15) / 16 * 16;
+    tc = min(max(t, 64), TCB);
+    nitems = 0;
+    for (int b = 0; b < B; ++b) nitems += G::KVH * chunks(sS[b]);
+    ni = nitems > wg ? (nitems - wg + NWG - 1) / NWG : 0;
+  }
+  // item index -> sequence b, KV head g, chunk c of C, index of chunk 0 of (b, g), cached tokens [t0, t1)
+  __device__ __forceinline__ void item(const int32_t* sS, int it, int& b, int& g, int& c, int& C, int& base,
+                                       int& t0, int& t1) const {
+    int acc = 0;
+    b = 0;
+    C = chunks(sS[0]);
+    for (; b < B; ++b) {
+      C = chunks(sS[b]);
+      if (it < acc + G::KVH * C) break;
+      acc += G::KVH * C;
+    }
+    const int r = it - acc;
+    g = r / C;
+    c = r % C;
+    base = acc + g * C;
+    const int old = max(sS[b], 1) - 1;
+    t0 = min(c * tc, old);
+    t1 = min((c + 1) * tc, old);
+  }
+};
+
+// K (v = 0) or V (v = 1) slot of 16-byte piece `part` of chunk token j in an item's segment
+// (128 bytes per token; piece (s - j) mod 8 in slot s, so 8 consecutive tokens hit 8 banks).
+__device__ __forceinline__ uint32_t kvb_slot(int j, int part) {
+  return uint32_t(j) * 128u + uint32_t((part + j) & 7) * 16u;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Batched producer: per layer norm1, QKV rows, the B rotary rows, the K of every item, the V of
+// every item, O rows, norm2, gate rows, up rows, down rows; then the final norm and LM-head rows.
+// ------------------------------------------------------------------------------------------------
+enum SegB { B_NORM1, B_QKV, B_CS, B_K, B_V, B_O, B_NORM2, B_GATE, B_UP, B_DOWN, B_FNORM, B_LM };
+
+template <class G>
+__device__ __forceinline__ uint32_t segb_bytes(const PlanB<G>& P, const int32_t* sS, int kind, int idx, int cs_fp32) {
+  switch (kind) {
+    case B_NORM1: case B_NORM2: case B_FNORM: return G::H * 2;
+    case B_QKV: return uint32_t(P.q1 - P.q0) * G::H * 2;
+    case B_CS: return P.ni ? uint32_t(P.B) * (cs_fp32 ? 256u : 128u) : 0u;
+    case B_K: case B_V: {
+      int b, g, c, C, base, t0, t1;
+      P.item(sS, P.wg + idx * NWG, b, g, c, C, base, t0, t1);
+      return uint32_t(t1 - t0) * 128u;
+    }
+    case B_O: return uint32_t(P.o1 - P.o0) * G::H * 2;
+    case B_GATE: case B_UP: return uint32_t(P.a1 - P.a0) * G::H * 2;
+    case B_DOWN: return uint32_t(P.d1 - P.d0) * G::I * 2;
+    default: {
+      const int r0 = P.v0 + idx * LM_ROWS;
+      return uint32_t(min(r0 + LM_ROWS, P.v1) - r0) * G::H * 2;
+    }
+  }
+}
+
+template <class G>
+__device__ __forceinline__ void producer_b(const Params& p, const PlanB<G>& P, SmemB<G>& sm) {
+  const int pw = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const uint32_t ring_base = uint32_t(reinterpret_cast<uintptr_t>(sm.ring));
+  if (pw == 0) {  // block ids of every item's chunk (the same for every layer)
+    for (int k = 0; k < P.ni; ++k) {
+      int b, g, c, C, base, t0, t1;
+      P.item(sm.sS, P.wg + k * NWG, b, g, c, C, base, t0, t1);
+      const int nb = t1 > t0 ? (t1 - 1) / 16 - t0 / 16 + 1 : 0;
+      for (int i = lane; i < nb; i += 64) sm.blk[k][i] = p.block_table[size_t(b) * p.bt_stride + t0 / 16 + i];
+    }
+  }
+  wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+  uint32_t n = 0;
+  Spin spin(p.ws, 1);
+  bool dead = false;
+  auto cmin = [&]() -> uint32_t {
+    uint32_t c = ld_lds(&sm.consumed[0]);
+#pragma unroll
+    for (int w = 1; w < NCW; ++w) c = min(c, ld_lds(&sm.consumed[w]));
+    return c;
+  };
+  auto publish = [&](uint32_t first_pending_packet) {
+    if (lane == 0) st_lds(&sm.front[pw], first_pending_packet * PKT);
+  };
+  auto issue_segment = [&](int kind, int layer, int idx) {
+    const uint32_t bytes = segb_bytes(P, sm.sS, kind, idx, p.cs_fp32);
+    const uint32_t npk = pad_pkt(bytes) / PKT;
+    if (npk == 0) return;
+    const uint8_t* base = nullptr;
+    int ib = 0, ig = 0, it0 = 0;
+    const uint8_t* cache = nullptr;
+    const LayerW& Lw = sm.lw[layer];
+    auto u8 = [](const void* q) { return reinterpret_cast<const uint8_t*>(q); };
+    switch (kind) {
+      case B_NORM1: base = u8(Lw.norm1); break;
+      case B_QKV: base = u8(Lw.qkv) + size_t(P.q0) * G::H * 2; break;
+      case B_K: case B_V: {
+        int c, C, bs, t1;
+        P.item(sm.sS, P.wg + idx * NWG, ib, ig, c, C, bs, it0, t1);
+        cache = u8(sm.kvp[layer]);
+        break;
+      }
+      case B_O: base = u8(Lw.o) + size_t(P.o0) * G::H * 2; break;
+      case B_NORM2: base = u8(Lw.norm2); break;
+      case B_GATE: base = u8(Lw.gate_up) + size_t(P.a0) * G::H * 2; break;
+      case B_UP: base = u8(Lw.gate_up) + size_t(G::I + P.a0) * G::H * 2; break;
+      case B_DOWN: base = u8(Lw.down) + size_t(P.d0) * G::I * 2; break;
+      case B_FNORM: base = u8(p.final_norm); break;
+      case B_LM: base = u8(p.embed) + size_t(P.v0 + idx * LM_ROWS) * G::H * 2; break;
+      default: break;
+    }
+    const uint32_t cs_row = p.cs_fp32 ? 256u : 128u;
+    for (uint32_t i = (uint32_t(pw) + NPW - n % NPW) % NPW; i < npk && !dead; i += NPW) {
+      const uint32_t gn = n + i;
+      if ((gn + 1) * PKT > cmin() + RING_B) {
+        wait_vmcnt<0>();
+        publish(gn);
+        while ((gn + 1) * PKT > cmin() + RING_B)
+          if (!spin.again()) { dead = true; break; }
+        if (dead) break;
+      }
+      const uint32_t off = i * PKT + uint32_t(lane) * 16u;
+      const uint8_t* src = nullptr;
+      if (off < bytes) {
+        if (kind == B_K || kind == B_V) {
+          const int jt = int(off >> 7);
+          const int part = int(((off >> 4) - uint32_t(jt)) & 7u);
+          const int t = it0 + jt;
+          const int blk = sm.blk[idx][t / 16 - it0 / 16];
+          const long long e = (long long)blk * p.block_stride + (long long)(t & 15) * p.token_stride +
+                              (long long)ig * p.head_stride + (kind == B_V ? p.v_off : p.k_off) + part * 8;
+          src = cache + e * 2;
+        } else if (kind == B_CS) {
+          const int b = int(off / cs_row);
+          src = reinterpret_cast<const uint8_t*>(p.cos_sin) + size_t(sm.sPos[b]) * cs_row + (off % cs_row);
+        } else {
+          src = base + off;
+        }
+        dma16(src, __builtin_amdgcn_readfirstlane(ring_base + ((gn * PKT) & (RING_B - 1))));
+      }
+      wait_vmcnt<DEPTH>();
+      if (gn >= uint32_t(DEPTH - 1) * NPW) publish(gn - uint32_t(DEPTH - 1) * NPW);
+    }
+    n += npk;
+  };
+  for (int l = 0; l < p.n_layers && !dead; ++l) {
+    issue_segment(B_NORM1, l, 0);
+    issue_segment(B_QKV, l, 0);
+    issue_segment(B_CS, l, 0);
+    for (int k = 0; k < P.ni && !dead; ++k) issue_segment(B_K, l, k);
+    for (int k = 0; k < P.ni && !dead; ++k) issue_segment(B_V, l, k);
+    issue_segment(B_O, l, 0);
+    issue_segment(B_NORM2, l, 0);
+    issue_segment(B_GATE, l, 0);
+    issue_segment(B_UP, l, 0);
+    issue_segment(B_DOWN, l, 0);
+  }
+  if (!dead) issue_segment(B_FNORM, 0, 0);
+  for (int j = 0; j < P.n_lm && !dead; ++j) issue_segment(B_LM, 0, j);
+  wait_vmcnt<0>();
+  publish(dead ? 0x3fffffu : n);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Batched consumer helpers
+// ------------------------------------------------------------------------------------------------
+template <class G>
+using ConsumerB = Consumer<G, SmemB<G>, PlanB<G>>;
+
+// One 16-byte LDS-DMA piece per lane of a coherent (sc1) global read: lane i copies g to m0 + 16 i.
+__device__ __forceinline__ void dma16_sc1(const void* g, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off sc1" ::"s"(lds_addr), "v"(g) : "memory", "m0");
+}
+
+// Publish this workgroup's part of exchange (kind, l): every wave's stores have completed, then
+// one flag word carries the step's tag.
+template <class G>
+__device__ __forceinline__ void publish_flag(ConsumerB<G>& C, int kind, int l) {
+  wait_vmcnt<0>();
+  C.cbar();
+  if (C.ct == 0) st_dev(C.p.ws + WSB<G>::flag(kind, l, C.P.wg), C.tag32);
+}
+
+// Wait until all workgroups have published (kind, l), then copy the [B][K] bf16 array into xs.
+template <class G>
+__device__ __forceinline__ void stage_flagged(ConsumerB<G>& C, int kind, int l, int K) {
+  const uint32_t* flags = C.p.ws + WSB<G>::flag(kind, l, 0);
+  {
+    Spin spin(C.p.ws, 8);
+    for (int w = C.ct; w < NWG; w += NCT)
+      while (ld_dev(flags + w) != C.tag32)
+        if (C.dead || !spin.again()) { C.dead = true; break; }
+  }
+  C.cbar();
+  const uint8_t* src = reinterpret_cast<const uint8_t*>(C.p.ws + WSB<G>::data(kind, l));
+  const uint32_t bytes = uint32_t(C.P.B) * uint32_t(K) * 2u;
+  const uint32_t lds = uint32_t(reinterpret_cast<uintptr_t>(C.sm.xs));
+  for (uint32_t pk = uint32_t(C.cw); pk * PKT < bytes; pk += NCW) {
+    const uint32_t off = pk * PKT + uint32_t(C.lane) * 16u;
+    if (off < bytes) dma16_sc1(src + off, __builtin_amdgcn_readfirstlane(lds + pk * PKT));
+  }
+  wait_vmcnt<0>();
+  C.cbar();
+}
+
+// Store one bf16 of exchange array (kind, l) at [b][i] (coherent store; completes before the flag).
+template <class G>
+__device__ __forceinline__ void put_bf16(const ConsumerB<G>& C, int kind, int l, int K, int b, int i, float v) {
+  const __amdgpu_buffer_rsrc_t r = rsrc(C.p.ws + WSB<G>::data(kind, l));
+  __builtin_amdgcn_raw_buffer_store_b16(uint16_t(f2bf(v)), r, (b * K + i) * 2, 0, 16);
+}
+
+// Per-sequence RMS scale of the staged rows, then the rows normalised in place with
+// LlamaRMSNorm rounding y = bf16(w * bf16(x * rs)) (modeling_llama.py:62-67); w from a ring segment.
+template <class G>
+__device__ __forceinline__ void norm_staged(ConsumerB<G>& C, uint32_t segw) {
+  SmemB<G>& sm = C.sm;
+  for (int b = C.cw; b < C.P.B; b += NCW) {
+    float s = 0.f;
+    for (int k = C.lane; k < G::H; k += 64) {
+      const float v = bf2f(sm.xs[b * G::H + k]);
+      s += v * v;
+    }
+    s = wave_sum(s);
+    if (C.lane == 0) sm.rsb[b] = rms_scale(s, G::H);
+  }
+  C.cbar();
+  const int n = C.P.B * G::H;
+  for (int i = C.ct; i < n; i += NCT) {
+    const int b = i / G::H, k = i - b * G::H;
+    const float w = bf2f(*reinterpret_cast<const uint16_t*>(sm.ring + ((segw + uint32_t(k) * 2u) & (RING_B - 1))));
+    sm.xs[i] = uint16_t(f2bf(w * rnd(bf2f(sm.xs[i]) * sm.rsb[b])));
+  }
+  C.cbar();
+}
+
+// This wave's share of D[row][token] = sum_k W[row][k] * X[token][k] for rows 0..15 of ring segment
+// `seg` (K bf16 per row; rows past the segment read stale ring bytes and are discarded) and the
+// 16 staged token rows.  Lane l holds D[4*(l/16) + j][l % 16] (v_mfma_f32_16x16x32_bf16 layout).
+template <class G, int K>
+__device__ __forceinline__ floatx4 mfma_part(const ConsumerB<G>& C, uint32_t seg, int w, int nw) {
+  constexpr int KS = K / 32;
+  const int s0 = KS * w / nw, s1 = KS * (w + 1) / nw;
+  const int row = C.lane & 15, kq = (C.lane >> 4) * 8;
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s = s0; s < s1; ++s) {
+    const int k = s * 32 + kq;
+    const uint4 a = C.ring16(seg + uint32_t(row * K + k) * 2u);
+    const uint4 x = *reinterpret_cast<const uint4*>(C.sm.xs + row * K + k);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, x), acc,
+                                                 0, 0, 0);
+  }
+  return acc;
+}
+
+// Two tiles (gate and up rows of P4), each over the full K by two waves: waves 0-1 the first,
+// waves 2-3 the second; the pair sums are valid in wave 0.
+template <class G, int K>
+__device__ __forceinline__ void mfma_tile_pair(ConsumerB<G>& C, uint32_t seg0, uint32_t seg1, float (*tile)[256],
+                                               floatx4& t0, floatx4& t1) {
+  const floatx4 part = mfma_part<G, K>(C, C.cw < 2 ? seg0 : seg1, C.cw & 1, 2);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) tile[C.cw][C.lane * 4 + j] = part[j];
+  C.cbar();
+  if (C.cw == 0)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      t0[j] = tile[0][C.lane * 4 + j] + tile[1][C.lane * 4 + j];
+      t1[j] = tile[2][C.lane * 4 + j] + tile[3][C.lane * 4 + j];
+    }
+}
+
+// Full tile, K split over the four waves; the partials are summed in wave order (deterministic)
+// and the result is valid in wave 0.
+template <class G, int K>
+__device__ __forceinline__ floatx4 mfma_tile(ConsumerB<G>& C, uint32_t seg, float (*tile)[256]) {
+  const floatx4 part = mfma_part<G, K>(C, seg, C.cw, NCW);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) tile[C.cw][C.lane * 4 + j] = part[j];
+  C.cbar();
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (C.cw == 0)
+#pragma unroll
+    for (int v = 0; v < NCW; ++v)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] += tile[v][C.lane * 4 + j];
+  return acc;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Batched attention: passes A / B / C over this workgroup's items (see the section comment).
+// Records and statistics are reused by every layer, so their tags carry the layer as well.
+// ------------------------------------------------------------------------------------------------
+template <class G>
+__device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t segcs) {
+  const Params& p = C.p;
+  const PlanB<G>& P = C.P;
+  SmemB<G>& sm = C.sm;
+  const int lane = C.lane, w = C.cw;
+  const int part = lane & 7, grp = lane >> 3;
+  const uint32_t tagb = (C.tag32 << 5) | uint32_t(l);
+  const uint64_t tg = uint64_t(tagb) << 32;
+  float* in = sm.at.qkvw[w];
+  C.cbar();  // P1's reads of xs (which shares storage with sm.at) are done
+  if (P.ni) {  // every sequence's rotary row, out of the ring (its segment is released with item 0's K)
+    C.wait_filled(C.pos);
+    for (int i = C.ct; i < P.B * 64; i += NCT) {
+      const int b = i >> 6, f = i & 63;
+      sm.at.csr[b][f] = p.cs_fp32 ? __uint_as_float(C.ring4(segcs + uint32_t(b) * 256u + uint32_t(f) * 4u))
+                                  : bf2f(*reinterpret_cast<const uint16_t*>(
+                                        sm.ring + ((segcs + uint32_t(b) * 128u + uint32_t(f) * 2u) & (RING_B - 1))));
+    }
+    C.cbar();
+  }
+  const float sgn = part < 4 ? -1.f : 1.f;
+  // ---- pass A: scores and chunk statistics of every item ----
+  for (int k = 0; k < P.ni; ++k) {
+    int b, g, c, Cc, base, t0, t1;
+    P.item(sm.sS, P.wg + k * NWG, b, g, c, Cc, base, t0, t1);
+    const bool leader = c == Cc - 1;
+    const int T_old = t1 - t0, T = T_old + (leader ? 1 : 0);
+    auto edge = [&](int q) { return q >= NCW ? T : ((T * q) / NCW) & ~1; };
+    const int j0 = edge(w), j1 = edge(w + 1);
+    const bool has_new = leader && j1 == T && T > j0;
+    const uint32_t segk = C.next_seg(uint32_t(T_old) * 128u);
+    C.poll_wave3(l, b, g * 192, 192, G::H + g * 64, has_new ? 64 : 0, G::H + G::KVH * 64 + g * 64,
+                 has_new ? 64 : 0, in);
+    C.wait_filled(C.pos);
+    // cos/sin of this sequence's position, dims 8*part .. 8*part+7 (mod 32)
+    float cs8[8], sn8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      cs8[e] = sm.at.csr[b][(part & 3) * 8 + e];
+      sn8[e] = sm.at.csr[b][32 + (part & 3) * 8 + e];
+    }
+    auto rope8 = [&](const float* head, uint32_t (&out)[4]) {
+      const float4 a0 = *reinterpret_cast<const float4*>(head + part * 8);
+      const float4 a1 = *reinterpret_cast<const float4*>(head + part * 8 + 4);
+      const float4 b0 = *reinterpret_cast<const float4*>(head + (part ^ 4) * 8);
+      const float4 b1 = *reinterpret_cast<const float4*>(head + (part ^ 4) * 8 + 4);
+      const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      const float y[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+      float r[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = rnd(rnd(x[e] * cs8[e]) + rnd((sgn * y[e]) * sn8[e]));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[e] = pack2(r[2 * e], r[2 * e + 1]);
+    };
+    wait_lgkm0();
+    uint32_t q[3][4], kn[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int h = 0; h < 3; ++h) rope8(in + h * 64, q[h]);
+    if (has_new) rope8(in + 192, kn);
+    if (has_new && sm.sSlot[b] >= 0 && grp < 2) {  // KV append (block360_kernel.inc:124-135)
+      const long long slot = sm.sSlot[b];
+      uint16_t* cache = reinterpret_cast<uint16_t*>(const_cast<void*>(sm.kvp[l]));
+      const long long e = (slot / 16) * p.block_stride + (slot % 16) * p.token_stride +
+                          (long long)g * p.head_stride + (grp ? p.v_off : p.k_off) + part * 8;
+      uint32_t val[4];
+      if (grp == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) val[i] = kn[i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) val[i] = pack2(in[256 + part * 8 + 2 * i], in[256 + part * 8 + 2 * i + 1]);
+      }
+      uint16_t* dst = cache + e;
+      if ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+        *reinterpret_cast<uint4*>(dst) = make_uint4(val[0], val[1], val[2], val[3]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { dst[2 * i] = uint16_t(val[i] & 0xffffu); dst[2 * i + 1] = uint16_t(val[i] >> 16); }
+      }
+    }
+    for (int jb = j0; jb < j1; jb += 8) {
+      const int j = jb + grp;
+      const uint4 kk = j < T_old ? C.ring16(segk + kvb_slot(j, part)) : make_uint4(kn[0], kn[1], kn[2], kn[3]);
+      float s3[3];
+#pragma unroll
+      for (int h = 0; h < 3; ++h) {
+        float a = dot2(q[h][0], kk.x, 0.f);
+        a = dot2(q[h][1], kk.y, a);
+        a = dot2(q[h][2], kk.z, a);
+        a = dot2(q[h][3], kk.w, a);
+        s3[h] = group8_sum(a);
+      }
+      if (part == 0 && j < j1)
+#pragma unroll
+        for (int h = 0; h < 3; ++h) sm.at.sc[k][h][j] = uint16_t(f2bf(rnd(s3[h]) * 0.125f));
+    }
+    wait_lgkm0();
+    C.release(C.pos);  // this item's K is no longer read
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      float sv[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int j = j0 + lane + 64 * i;
+        sv[i] = j < j1 ? bf2f(sm.at.sc[k][h][j]) : -INFINITY;
+      }
+      const float m = wave_max(fmaxf(sv[0], sv[1]));
+      float ls = 0.f;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) ls += sv[i] == -INFINITY ? 0.f : expf(sv[i] - m);
+      ls = wave_sum(ls);
+      if (lane == 0) { sm.wml[w][0][h] = m; sm.wml[w][1][h] = ls; }
+    }
+    C.cbar();
+    if (w == 0) {
+      float mq = -INFINITY, lq = 0.f;
+      if (lane < 12) { mq = sm.wml[lane & 3][0][lane >> 2]; lq = sm.wml[lane & 3][1][lane >> 2]; }
+      float mx = fmaxf(mq, dpp<0xb1>(mq, mq));
+      mx = fmaxf(mx, dpp<0x4e>(mx, mx));
+      float ex = mq == -INFINITY ? 0.f : lq * expf(mq - mx);
+      ex += dpp<0xb1>(0.f, ex);
+      ex += dpp<0x4e>(0.f, ex);
+      if (lane < 12 && (lane & 3) == 0) { sm.at.cst[k][0][lane >> 2] = mx; sm.at.cst[k][1][lane >> 2] = ex; }
+      if (Cc > 1 && lane < 12 && (lane & 3) == 0) {
+        uint64_t* st = reinterpret_cast<uint64_t*>(p.ws + WSB<G>::stat(P.wg + k * NWG));
+        st_dev64(st + 2 * (lane >> 2), tg | __float_as_uint(mx));
+        st_dev64(st + 2 * (lane >> 2) + 1, tg | __float_as_uint(ex));
+      }
+    }
+    C.cbar();  // wml is reused by the next item
+  }
+  // ---- pass B: global statistics, probabilities, P.V of every item ----
+  for (int k = 0; k < P.ni; ++k) {
+    int b, g, c, Cc, base, t0, t1;
+    P.item(sm.sS, P.wg + k * NWG, b, g, c, Cc, base, t0, t1);
+    const bool leader = c == Cc - 1;
+    const int T_old = t1 - t0, T = T_old + (leader ? 1 : 0);
+    auto edge = [&](int q) { return q >= NCW ? T : ((T * q) / NCW) & ~1; };
+    const int j0 = edge(w), j1 = edge(w + 1);
+    const bool has_new = leader && j1 == T && T > j0;
+    const uint32_t segv = C.next_seg(uint32_t(T_old) * 128u);
+    float Mh[3], Lh[3];
+    if (Cc > 1) {
+      // lane k2 (and k2 + 64, ...) reads chunk k2's (max, sum) of the three heads
+      const __amdgpu_buffer_rsrc_t r = rsrc(p.ws + WSB<G>::stat(base));
+      float mk[4][3], lk[4][3];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int h = 0; h < 3; ++h) { mk[i][h] = -INFINITY; lk[i][h] = 0.f; }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kc = lane + 64 * i;
+        if (kc < Cc) {
+          Spin spin(p.ws, 9);
+          u32x4 v[3];
+          while (true) {
+#pragma unroll
+            for (int h = 0; h < 3; ++h) v[h] = ld_dev128(r, uint32_t(kc * STAT_WORDS + 2 * h) * 8u);
+            bool ok = true;
+#pragma unroll
+            for (int h = 0; h < 3; ++h) ok = ok && v[h].y == tagb && v[h].w == tagb;
+            if (ok) break;
+            if (C.dead || !spin.again()) { C.dead = true; break; }
+          }
+#pragma unroll
+          for (int h = 0; h < 3; ++h) { mk[i][h] = __uint_as_float(v[h].x); lk[i][h] = __uint_as_float(v[h].z); }
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < 3; ++h) {
+        float m = fmaxf(fmaxf(mk[0][h], mk[1][h]), fmaxf(mk[2][h], mk[3][h]));
+        m = wave_max(m);
+        float ls = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ls += mk[i][h] == -INFINITY ? 0.f : lk[i][h] * expf(mk[i][h] - m);
+        Mh[h] = m;
+        Lh[h] = wave_sum(ls);
+      }
+    } else {
+#pragma unroll
+      for (int h = 0; h < 3; ++h) { Mh[h] = sm.at.cst[k][0][h]; Lh[h] = sm.at.cst[k][1][h]; }
+    }
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      const float inv = 1.0f / Lh[h];
+      for (int j = j0 + lane; j < j1; j += 64)
+        sm.at.pb[h][j] = uint16_t(f2bf(expf(bf2f(sm.at.sc[k][h][j]) - Mh[h]) * inv));
+    }
+    if (has_new)  // the new token's v (this wave's input buffer has since held other items)
+      C.poll_wave3(l, b, 0, 0, 0, 0, G::H + G::KVH * 64 + g * 64, 64, in + 256);
+    wait_lgkm0();
+    C.wait_filled(C.pos);  // this item's V
+    const int half = lane >> 5, d2 = lane & 31;
+    const int jo1 = min(j1, T_old);
+    const int npairs = jo1 > j0 ? (jo1 - j0) / 2 : 0;
+    const uint32_t voff = uint32_t(d2 & 3) * 4u;
+    float acc[3][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
+    for (int kp = half; kp < npairs; kp += 2) {
+      const int j = j0 + 2 * kp;
+      const uint32_t va = C.ring4(segv + kvb_slot(j, d2 >> 2) + voff);
+      const uint32_t vb = C.ring4(segv + kvb_slot(j + 1, d2 >> 2) + voff);
+      const uint32_t lo = __builtin_amdgcn_perm(vb, va, 0x05040100u);
+      const uint32_t hi = __builtin_amdgcn_perm(vb, va, 0x07060302u);
+#pragma unroll
+      for (int h = 0; h < 3; ++h) {
+        const uint32_t pp = *reinterpret_cast<const uint32_t*>(&sm.at.pb[h][j]);
+        acc[h][0] = dot2(pp, lo, acc[h][0]);
+        acc[h][1] = dot2(pp, hi, acc[h][1]);
+      }
+    }
+    if (half == 0) {
+      if (jo1 > j0 && ((jo1 - j0) & 1)) {
+        const int j = jo1 - 1;
+        const uint32_t v = C.ring4(segv + kvb_slot(j, d2 >> 2) + voff);
+#pragma unroll
+        for (int h = 0; h < 3; ++h) {
+          const float pj = bf2f(sm.at.pb[h][j]);
+          acc[h][0] = fmaf(pj, bf_lo(v), acc[h][0]);
+          acc[h][1] = fmaf(pj, bf_hi(v), acc[h][1]);
+        }
+      }
+      if (has_new) {
+#pragma unroll
+        for (int h = 0; h < 3; ++h) {
+          const float pj = bf2f(sm.at.pb[h][T_old]);
+          acc[h][0] = fmaf(pj, in[256 + 2 * d2], acc[h][0]);
+          acc[h][1] = fmaf(pj, in[256 + 2 * d2 + 1], acc[h][1]);
+        }
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      acc[h][0] += __shfl_xor(acc[h][0], 32);
+      acc[h][1] += __shfl_xor(acc[h][1], 32);
+    }
+    C.release(C.pos);  // this item's V is no longer read
+    if (lane < 32)
+#pragma unroll
+      for (int h = 0; h < 3; ++h) { sm.wo[w][h][2 * d2] = acc[h][0]; sm.wo[w][h][2 * d2 + 1] = acc[h][1]; }
+    C.cbar();
+    if (w < 3) {
+      float O = 0.f;
+#pragma unroll
+      for (int v = 0; v < NCW; ++v) O += sm.wo[v][w][lane];
+      if (leader) sm.at.own[k][w * 64 + lane] = O;
+      else st_dev64(reinterpret_cast<uint64_t*>(p.ws + WSB<G>::rec(P.wg + k * NWG)) + w * 64 + lane, tg | __float_as_uint(O));
+    }
+    C.cbar();  // wo and pb are reused by the next item
+  }
+  // ---- pass C: leaders add their chunks' partials (chunk order) and publish attn ----
+  for (int k = 0; k < P.ni; ++k) {
+    int b, g, c, Cc, base, t0, t1;
+    P.item(sm.sS, P.wg + k * NWG, b, g, c, Cc, base, t0, t1);
+    if (c != Cc - 1 || w >= 3) continue;
+    float O = 0.f;
+    constexpr int MB = 8;
+    for (int c0 = 0; c0 < Cc - 1; c0 += MB) {
+      const int nc = min(MB, Cc - 1 - c0);
+      uint64_t ro[MB];
+      uint32_t pend = 0;
+#pragma unroll
+      for (int kk = 0; kk < MB; ++kk)
+        if (kk < nc) {
+          ro[kk] = ld_dev64(reinterpret_cast<const uint64_t*>(p.ws + WSB<G>::rec(base + c0 + kk)) + w * 64 + lane);
+          pend |= 1u << kk;
+        }
+      Spin spin(p.ws, 10);
+      while (true) {
+#pragma unroll
+        for (int kk = 0; kk < MB; ++kk)
+          if (((pend >> kk) & 1u) && uint32_t(ro[kk] >> 32) == tagb) pend &= ~(1u << kk);
+        if (!pend) break;
+        if (C.dead || !spin.again()) { C.dead = true; break; }
+#pragma unroll
+        for (int kk = 0; kk < MB; ++kk)
+          if ((pend >> kk) & 1u)
+            ro[kk] = ld_dev64(reinterpret_cast<const uint64_t*>(p.ws + WSB<G>::rec(base + c0 + kk)) + w * 64 + lane);
+      }
+#pragma unroll
+      for (int kk = 0; kk < MB; ++kk)
+        if (kk < nc) O += __uint_as_float(uint32_t(ro[kk]));
+    }
+    O += sm.at.own[k][w * 64 + lane];
+    put_bf16<G>(C, X_ATTN, l, G::H, b, (g * 3 + w) * 64 + lane, O);
+  }
+  publish_flag<G>(C, X_ATTN, l);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Batched consumer
+// ------------------------------------------------------------------------------------------------
+template <class G>
+__device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, SmemB<G>& sm, uint32_t epoch) {
+  ConsumerB<G> C(p, P, sm, epoch);
+  __builtin_amdgcn_s_barrier();  // pairs with the producer's barrier (blk[] ready)
+  using W = WS<G>;
+  const int B = P.B;
+  const int nq = P.q1 - P.q0, no = P.o1 - P.o0, na = P.a1 - P.a0, nd = P.d1 - P.d0;
+  const int orow = 4 * (C.lane >> 4), tok = C.lane & 15;  // this lane's MFMA output rows / token
+  for (int l = 0; l < p.n_layers; ++l) {
+    // ---------------- P1: RMSNorm(x) + QKV ----------------
+    C.refresh();
+    {
+      const uint32_t segn = C.next_seg(G::H * 2);
+      const uint32_t segq = C.next_seg(uint32_t(nq) * G::H * 2);
+      if (l == 0) {
+        for (int i = C.ct; i < B * (G::H / 8); i += NCT) {
+          const int b = i / (G::H / 8), c8 = i - b * (G::H / 8);
+          *reinterpret_cast<uint4*>(sm.xs + b * G::H + c8 * 8) =
+              *reinterpret_cast<const uint4*>(p.embed + size_t(sm.sId[b]) * G::H + c8 * 8);
+        }
+        C.cbar();
+      } else {
+        stage_flagged<G>(C, X_X, l - 1, G::H);
+      }
+      for (int i = C.ct; i < B * no; i += NCT) {
+        const int b = i / no, r = i - b * no;
+        sm.xk[b][r] = bf2f(sm.xs[b * G::H + P.o0 + r]);
+      }
+      C.wait_filled(C.pos);
+      norm_staged<G>(C, segn);
+      const floatx4 acc = mfma_tile<G, G::H>(C, segq, sm.tile);
+      C.release(C.pos);
+      if (C.cw == 0 && tok < B)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (orow + j < nq) st_dev(p.ws + W::xw(X_QKV, l, tok, P.q0 + orow + j), C.w16(acc[j]));
+    }
+    // ---------------- P2: attention ----------------
+    C.refresh();
+    {
+      const uint32_t segcs = C.next_seg(P.ni ? uint32_t(B) * (p.cs_fp32 ? 256u : 128u) : 0u);
+      attention_b<G>(C, l, segcs);
+    }
+    // ---------------- P3: O + residual ----------------
+    C.refresh();
+    {
+      const uint32_t sego = C.next_seg(uint32_t(no) * G::H * 2);
+      stage_flagged<G>(C, X_ATTN, l, G::H);
+      C.wait_filled(C.pos);
+      const floatx4 acc = mfma_tile<G, G::H>(C, sego, sm.tile);
+      C.release(C.pos);
+      if (C.cw == 0 && tok < B)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (orow + j < no) put_bf16<G>(C, X_H1, l, G::H, tok, P.o0 + orow + j, sm.xk[tok][orow + j] + rnd(acc[j]));
+      publish_flag<G>(C, X_H1, l);
+    }
+    // ---------------- P4: RMSNorm(h1) + gate/up + SwiGLU ----------------
+    C.refresh();
+    {
+      const uint32_t segn = C.next_seg(G::H * 2);
+      const uint32_t segg = C.next_seg(uint32_t(na) * G::H * 2);
+      const uint32_t segu = C.next_seg(uint32_t(na) * G::H * 2);
+      stage_flagged<G>(C, X_H1, l, G::H);
+      for (int i = C.ct; i < B * nd; i += NCT) {
+        const int b = i / nd, r = i - b * nd;
+        sm.hk[b][r] = bf2f(sm.xs[b * G::H + P.d0 + r]);
+      }
+      C.wait_filled(C.pos);
+      norm_staged<G>(C, segn);
+      floatx4 gt = {0.f, 0.f, 0.f, 0.f}, up = {0.f, 0.f, 0.f, 0.f};
+      mfma_tile_pair<G, G::H>(C, segg, segu, sm.tile, gt, up);
+      C.release(C.pos);
+      if (C.cw == 0 && tok < B)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (orow + j < na) {
+            const float gv = rnd(gt[j]), uv = rnd(up[j]);
+            const float silu = rnd(gv / (1.0f + expf(-gv)));
+            put_bf16<G>(C, X_ACT, l, G::I, tok, P.a0 + orow + j, silu * uv);
+          }
+      publish_flag<G>(C, X_ACT, l);
+    }
+    // ---------------- P5: down + residual ----------------
+    C.refresh();
+    {
+      const uint32_t segd = C.next_seg(uint32_t(nd) * G::I * 2);
+      stage_flagged<G>(C, X_ACT, l, G::I);
+      C.wait_filled(C.pos);
+      const floatx4 acc = mfma_tile<G, G::I>(C, segd, sm.tile);
+      C.release(C.pos);
+      if (C.cw == 0 && tok < B)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (orow + j < nd) {
+            const float y = rnd(sm.hk[tok][orow + j] + rnd(acc[j]));
+            put_bf16<G>(C, X_X, l, G::H, tok, P.d0 + orow + j, y);
+            if (p.layer_outputs) p.layer_outputs[(size_t(l) * B + tok) * G::H + P.d0 + orow + j] = uint16_t(f2bf(y));
+          }
+      publish_flag<G>(C, X_X, l);
+    }
+  }
+  // ---------------- final RMSNorm + LM head + argmax ----------------
+  const uint32_t segf = C.next_seg(G::H * 2);
+  stage_flagged<G>(C, X_X, p.n_layers - 1, G::H);
+  C.wait_filled(C.pos);
+  norm_staged<G>(C, segf);
+  C.release(C.pos);
+  if (P.wg == 0)
+    for (int i = C.ct; i < B * G::H; i += NCT) p.out_hidden[i] = sm.xs[i];
+  if (!p.lm_head) return;
+  // LM segment j (16 rows, one MFMA tile over the full K) is computed by wave j % NCW
+  float best = -INFINITY;
+  int bidx = 0x7fffffff;
+  for (int j = 0; j < P.n_lm; ++j) {
+    const int r0 = P.v0 + j * LM_ROWS;
+    const int nrows = min(LM_ROWS, P.v1 - r0);
+    const uint32_t seg = C.next_seg(uint32_t(nrows) * G::H * 2);
+    if (j % NCW != C.cw) continue;
+    C.wait_filled(C.pos);
+    const floatx4 acc = mfma_part<G, G::H>(C, seg, 0, 1);
+    C.release(C.pos);
+    if (tok < B)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+        if (orow + jj < nrows) {
+          const float v = rnd(acc[jj]);
+          const int idx = r0 + orow + jj;
+          if (v > best || (v == best && idx < bidx)) { best = v; bidx = idx; }
+          if (p.out_logits) p.out_logits[size_t(tok) * G::V + idx] = uint16_t(f2bf(acc[jj]));
+        }
+  }
+  C.release(C.pos);
+#pragma unroll
+  for (int o = 16; o <= 32; o <<= 1) {  // lanes l, l+16, l+32, l+48 hold the same token
+    const float ov = __shfl_xor(best, o);
+    const int oi = __shfl_xor(bidx, o);
+    if (ov > best || (ov == best && oi < bidx)) { best = ov; bidx = oi; }
+  }
+  if (C.lane < BMAX) { sm.lm_val[C.cw][C.lane] = best; sm.lm_idx[C.cw][C.lane] = bidx; }
+  C.cbar();
+  if (C.ct < B) {
+    float bv = sm.lm_val[0][C.ct];
+    int bi = sm.lm_idx[0][C.ct];
+    for (int v = 1; v < NCW; ++v)
+      if (sm.lm_val[v][C.ct] > bv || (sm.lm_val[v][C.ct] == bv && sm.lm_idx[v][C.ct] < bi)) {
+        bv = sm.lm_val[v][C.ct];
+        bi = sm.lm_idx[v][C.ct];
+      }
+    const uint64_t rec = (uint64_t(C.tag32) << 32) | (uint64_t(uint32_t(bi) & 0xffffu) << 16) | f2bf(bv);
+    st_dev64(reinterpret_cast<uint64_t*>(p.ws + W::lm(C.ct, P.wg)), rec);
+  }
+  if (P.wg != 0) return;
+  C.cbar();  // lm_val is reused below
+  // workgroup 0: per sequence, argmax over the NWG candidates (first index on ties, as torch.argmax)
+  for (int b = 0; b < B; ++b) {
+    const uint64_t* src = reinterpret_cast<const uint64_t*>(p.ws + W::lm(b, C.ct));
+    Spin spin(p.ws, 11);
+    uint64_t r = ld_dev64(src);
+    while (uint32_t(r >> 32) != C.tag32) {
+      if (C.dead || !spin.again()) { C.dead = true; break; }
+      r = ld_dev64(src);
+    }
+    float bv = bf2f(uint32_t(r) & 0xffffu);
+    int bi = int((uint32_t(r) >> 16) & 0xffffu);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oi = __shfl_xor(bi, o);
+      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if (C.lane == 0) { sm.lm_val[C.cw][b] = bv; sm.lm_idx[C.cw][b] = bi; }
+  }
+  C.cbar();
+  if (C.ct < B) {
+    float bv = sm.lm_val[0][C.ct];
+    int bi = sm.lm_idx[0][C.ct];
+    for (int v = 1; v < NCW; ++v)
+      if (sm.lm_val[v][C.ct] > bv || (sm.lm_val[v][C.ct] == bv && sm.lm_idx[v][C.ct] < bi)) {
+        bv = sm.lm_val[v][C.ct];
+        bi = sm.lm_idx[v][C.ct];
+      }
+    if (p.out_ids) p.out_ids[C.ct] = bi;
+  }
+}
+
+template <class G>
+__global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel_b(Params p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
+  SmemB<G>& sm = *reinterpret_cast<SmemB<G>*>(smem_raw);
+  if (threadIdx.x == 0) {
+    for (int w = 0; w < NPW; ++w) sm.front[w] = 0;
+    for (int w = 0; w < NCW; ++w) sm.consumed[w] = 0;
+    sm.cbar = 0;
+  }
+  for (int i = threadIdx.x; i < p.n_layers; i += WG_THREADS) {
+    const void* const* t = p.layers + size_t(i) * 6;
+    LayerW w{};
+    w.norm1 = t[0]; w.qkv = t[1]; w.o = t[2]; w.norm2 = t[3]; w.gate_up = t[4]; w.down = t[5];
+    sm.lw[i] = w;
+    sm.kvp[i] = p.kv[i];
+  }
+  if (threadIdx.x < p.B) {
+    const int t = threadIdx.x;
+    sm.sS[t] = min(max(p.seq_lens[t], 1), p.max_seq);
+    sm.sPos[t] = int(max(p.positions[t], (int64_t)0));
+    sm.sSlot[t] = p.slot_mapping[t];
+    const long long id = p.ids_i64 ? reinterpret_cast<const int64_t*>(p.input_ids)[t]
+                                   : reinterpret_cast<const int32_t*>(p.input_ids)[t];
+    sm.sId[t] = int(min(max(id, 0LL), (long long)G::V - 1));
+  }
+  __syncthreads();
+  PlanB<G> P;
+  P.init(p, sm.sS, blockIdx.x);
+  uint32_t epoch = ld_dev(p.ws + HDR_EPOCH) + 1u;
+  if (epoch == 0) epoch = 1;
+  if (threadIdx.x < 64 * NPW) producer_b<G>(p, P, sm);
+  else consumer_b<G>(p, P, sm, epoch);
+  __syncthreads();
+  if (blockIdx.x == 0 && threadIdx.x == 0) st_dev(p.ws + HDR_EPOCH, epoch);
+}
+
 template <class G>
 constexpr size_t lds_bytes() { return sizeof(Smem<G>); }
+template <class G>
+constexpr size_t lds_bytes_b() { return sizeof(SmemB<G>); }
+static_assert(sizeof(SmemB<G360>) <= 160 * 1024, "LDS budget of one gfx950 workgroup");
+static_assert(sizeof(SmemB<G135>) <= 160 * 1024, "LDS budget of one gfx950 workgroup");
 static_assert(sizeof(Smem<G360>) <= 160 * 1024, "LDS budget of one gfx950 workgroup");
 static_assert(sizeof(Smem<G135>) <= 160 * 1024, "LDS budget of one gfx950 workgroup");
 static_assert(sizeof(Smem<G360Q>) <= 160 * 1024, "LDS budget of one gfx950 workgroup");
@@ -1665,9 +2587,18 @@ static int ensure_workspace(void* ws, size_t bytes, hipStream_t stream) {
   return PK_OK;
 }
 
-template <class G>
+template <class G, bool BATCHED>
 static int launch(const Params& p, hipStream_t stream) {
   static LaunchCache<G> cache;
+  const void* fn;
+  size_t lds;
+  if constexpr (BATCHED) {
+    fn = reinterpret_cast<const void*>(decode_kernel_b<G>);
+    lds = lds_bytes_b<G>();
+  } else {
+    fn = reinterpret_cast<const void*>(decode_kernel<G>);
+    lds = lds_bytes<G>();
+  }
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
@@ -1678,10 +2609,9 @@ static int launch(const Params& p, hipStream_t stream) {
     if (!d.ok) st = d.status;
     else if (!d.gfx950) st = PK_ERR_ARCH;
     else if (!d.coop) st = PK_ERR_COOP;
-    else if (d.cus < NWG || size_t(d.max_lds) < lds_bytes<G>()) st = PK_ERR_RESIDENCY;
+    else if (d.cus < NWG || size_t(d.max_lds) < lds) st = PK_ERR_RESIDENCY;
     else {
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<G>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes<G>()));
+      e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
       if (e != hipSuccess) st = e;
     }
     cache.status[dev] = st;
@@ -1690,8 +2620,7 @@ static int launch(const Params& p, hipStream_t stream) {
   if (cache.status[dev]) return cache.status[dev];
   Params q = p;
   void* args[] = {&q};
-  e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(decode_kernel<G>), dim3(NWG),
-                                 dim3(WG_THREADS), args, lds_bytes<G>(), stream);
+  e = hipLaunchCooperativeKernel(fn, dim3(NWG), dim3(WG_THREADS), args, lds, stream);
   if (e != hipSuccess) return e;
   return hipGetLastError();
 }
@@ -1705,13 +2634,13 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
                        long long head_stride, int block_size, const void* cos_sin, int cs_fp32,
                        void* out_hidden, void* layer_outputs, void* out_ids, void* out_logits,
                        void* scratch, size_t scratch_bytes, int max_seq_len) {
-  if (B != 1) return PK_ERR_BATCH;
+  if (B < 1 || B > (G::WF ? 1 : BMAX)) return PK_ERR_BATCH;  // MXFP8 weights: batch 1 only
   if (n_layers < 1 || n_layers > G::L) return PK_ERR_MODEL;
   if (max_seq_len < 1 || max_seq_len > kMaxSeq) return PK_ERR_MAX_SEQ;
   if (!input_ids || !embed || !final_norm || !positions || !seq_lens || !block_table ||
       !slot_mapping || !layers || !kv || !cos_sin || !out_hidden || !scratch)
     return PK_ERR_NULL;
-  if (scratch_bytes < WS<G>::TOTAL * 4) return PK_ERR_SCRATCH;
+  if (scratch_bytes < WSB<G>::TOTAL * 4) return PK_ERR_SCRATCH;
   if (block_size != 16 || bt_stride < 1 || (long long)bt_stride * block_size < max_seq_len) return PK_ERR_BLOCK;
   if (k_off % 8 || v_off % 8 || block_stride % 8 || token_stride % 8 || head_stride % 8 || k_off < 0 ||
       v_off < 0 || block_stride < 0 || token_stride < 0 || head_stride < 0)
@@ -1747,11 +2676,14 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
   p.B = B;
   p.n_layers = n_layers;
   p.lm_head = (out_ids || out_logits) ? 1 : 0;
+  p.max_seq = max_seq_len;
   p.trace = g_trace;
-  static_assert((WS<G>::TOTAL * 4) % 16 == 0, "workspace is zero-filled in 16-byte units");
-  const int st = ensure_workspace(scratch, WS<G>::TOTAL * 4, reinterpret_cast<hipStream_t>(stream));
+  static_assert((WSB<G>::TOTAL * 4) % 16 == 0, "workspace is zero-filled in 16-byte units");
+  const int st = ensure_workspace(scratch, WSB<G>::TOTAL * 4, reinterpret_cast<hipStream_t>(stream));
   if (st != PK_OK) return st;
-  return launch<G>(p, reinterpret_cast<hipStream_t>(stream));
+  if constexpr (G::WF == 0)
+    if (B > 1) return launch<G, true>(p, reinterpret_cast<hipStream_t>(stream));
+  return launch<G, false>(p, reinterpret_cast<hipStream_t>(stream));
 }
 
 }  // namespace pk
@@ -1811,8 +2743,8 @@ extern "C" int pk_workspace_read(const void* ws, size_t word, unsigned* out, int
 }
 
 extern "C" size_t pk_workspace_bytes(int model) {
-  if (model == PK_MODEL_SMOLLM2_360M) return pk::WS<pk::G360>::TOTAL * 4;
-  if (model == PK_MODEL_SMOLLM2_135M) return pk::WS<pk::G135>::TOTAL * 4;
+  if (model == PK_MODEL_SMOLLM2_360M) return pk::WSB<pk::G360>::TOTAL * 4;
+  if (model == PK_MODEL_SMOLLM2_135M) return pk::WSB<pk::G135>::TOTAL * 4;
   return 0;
 }
 

@@ -79,7 +79,7 @@ def _args(**over):
 
 
 @pytest.mark.parametrize("over,code", [
-    (dict(B=0), 9101), (dict(B=2), 9101), (dict(n_layers=0), 9110), (dict(n_layers=33), 9110),
+    (dict(B=0), 9101), (dict(B=17), 9101), (dict(n_layers=0), 9110), (dict(n_layers=33), 9110),
     (dict(model=7), 9110), (dict(max_seq_len=0), 9102), (dict(max_seq_len=1 << 20), 9102),
     (dict(embed=None), 9103), (dict(scratch=None), 9103), (dict(scratch_bytes=1024), 9108),
     (dict(block_size=32), 9109), (dict(bt_stride=1), 9109), (dict(k_off=4), 9107),
@@ -90,18 +90,24 @@ def test_pk_decode_rejects_bad_arguments_without_gpu(over, code):
     assert lib.pk_decode(*_args(**over)) == code
 
 
+def test_mxfp8_decode_is_batch_one():
+    lib = _native.library()
+    assert lib.pk_decode_mxfp8(*_args(B=2)) == 9101
+    assert lib.pk_decode_mxfp8(*_args(model=135)) == 9110
+
+
 def test_reference_abi_validation():
     lib = _native.library()
     vp = 16
     base = [None, 1, vp, vp, vp, vp, vp, vp, 64, vp, vp, vp, 0, 64, 10240, 128, 2048, 16, vp, 0, vp, None, vp,
             1 << 40, None, 0, 1024, -1]
-    bad = list(base); bad[1] = 3
+    bad = list(base); bad[1] = 17  # batch 1..16
     assert lib.decode360(*bad) == 9101
     bad = list(base); bad[-1] = 40
     assert lib.decode360(*bad) == 9109
     bad = list(base); bad[24] = vp
     assert lib.decode360(*bad) == 9111
-    mk = [None, 5, vp, 1, vp, vp, vp, 64, vp, vp, vp, vp, vp, 0, 64, 10240, 128, 2048, 16, vp, 0, vp, vp, 1 << 40, 1024]
+    mk = [None, 17, vp, 1, vp, vp, vp, 64, vp, vp, vp, vp, vp, 0, 64, 10240, 128, 2048, 16, vp, 0, vp, vp, 1 << 40, 1024]
     assert lib.mk_decode(*mk) == 9101
 
 
@@ -116,7 +122,10 @@ def test_wrapper_contract_errors_on_cpu_tensors():
     with pytest.raises(ValueError, match="rms eps"):
         m.decode_step(**dict(kw, eps=1e-6))
     with pytest.raises(ValueError, match="batch"):
-        m.decode_step(**dict(kw, input_ids=torch.zeros(2, dtype=torch.int64)))
+        m.decode_step(**dict(kw, input_ids=torch.zeros(17, dtype=torch.int64)))
+    from prime_kernels_amd import decode_megakernel_360m_mxfp8 as mq
+    with pytest.raises(ValueError, match="batch"):
+        mq.decode_step(**dict(kw, input_ids=torch.zeros(2, dtype=torch.int64)))
     with pytest.raises(ValueError, match="layers"):
         m.decode_step(**dict(kw, layers=[()] * 3))
 

@@ -1,0 +1,113 @@
+"""GPU parity of the batched decode kernel (2..16 sequences per launch, ragged contexts, MFMA
+projections): every sequence against the oracle (which runs each sequence on its own), KV appends,
+agreement with the batch-1 kernel, and the BASELINE config-4 shape (full 360M, 16 sequences,
+contexts 128..4096).  Bars as in test_gpu_decode.py."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import smollm2 as O
+from tests import gpu_cases as GC
+
+pytestmark = pytest.mark.gpu
+
+
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+def _kv_appends_match(case, contexts, label):
+    for li in range(case.geom.layers):
+        for b, S in enumerate(contexts):
+            slot = case.kv.slot(b, S - 1)
+            got = case.kvd[li][slot // 16, :, slot % 16].cpu().float()
+            want = case.kv.caches[li][slot // 16, :, slot % 16].float()
+            assert torch.allclose(got, want, rtol=2 ** -6, atol=2e-2), (label, li, b)
+
+
+@pytest.mark.parametrize("contexts", [[37, 300], [1, 2, 65, 129, 1000, 17], [5] * 16],
+                         ids=["b2", "b6_edges", "b16_short"])
+def test_batched_two_layers(contexts):
+    _need_gpu()
+    geom = O.with_layers(O.SMOLLM2_360M, 2)
+    case = GC.random_kv_case(geom, 60 + len(contexts), contexts)
+    ids = [100 + 7 * b for b in range(len(contexts))]
+    pos = [S - 1 for S in contexts]
+    k = case.kernel_step(ids, pos, layer_outputs=True)
+    r = case.oracle_step(ids, pos, layer_outputs=True)
+    GC.assert_step_parity(k, r, f"batched {contexts}")
+    _kv_appends_match(case, contexts, "two layers")
+
+
+def test_batched_ragged_16_two_layers():
+    _need_gpu()
+    rng = np.random.default_rng(8)
+    contexts = [int(x) for x in rng.integers(1, 2500, 16)]
+    geom = O.with_layers(O.SMOLLM2_360M, 2)
+    case = GC.random_kv_case(geom, 71, contexts)
+    ids = [int(x) for x in rng.integers(0, 49152, 16)]
+    k = case.kernel_step(ids, [S - 1 for S in contexts])
+    r = case.oracle_step(ids, [S - 1 for S in contexts])
+    GC.assert_step_parity(k, r, "ragged16")
+    _kv_appends_match(case, contexts, "ragged16")
+
+
+def test_batched_135m_four_sequences():
+    _need_gpu()
+    geom = O.with_layers(O.SMOLLM2_135M, 3)
+    contexts = [513, 64, 2048, 200]
+    case = GC.random_kv_case(geom, 81, contexts)
+    ids = [5, 6, 7, 8]
+    k = case.kernel_step(ids, [S - 1 for S in contexts])
+    f = case.eager_gpu_step(ids, [S - 1 for S in contexts])
+    r = case.oracle_step(ids, [S - 1 for S in contexts])
+    GC.assert_within_floor(k, r, f, "135m b4")
+
+
+def test_batched_agrees_with_batch_one_kernel():
+    """A sequence decoded inside a batch of 8 gives what the batch-1 kernel gives for it alone,
+    within the bf16 bar (the two kernels sum in different orders)."""
+    _need_gpu()
+    geom = O.with_layers(O.SMOLLM2_360M, 2)
+    contexts = [700, 33, 1500, 90, 4, 260, 1024, 2]
+    case = GC.random_kv_case(geom, 91, contexts)
+    ids = [int(40 + 3 * b) for b in range(8)]
+    kb = case.kernel_step(ids, [S - 1 for S in contexts])
+    for b in range(8):
+        case.sync_kv_from_oracle()
+        ks = case.kernel_step([ids[b]], [contexts[b] - 1], seq_lens=[contexts[b]],
+                              slot_mapping=[case.kv.slot(b, contexts[b] - 1)], block_rows=[b])
+        c = GC.compare_logits(kb["logits"][b], ks["logits"][0])
+        assert c["max_abs"] <= GC.LOGIT_ATOL and c["cos"] >= GC.COS_MIN, (b, c)
+
+
+def test_batched_deterministic():
+    _need_gpu()
+    geom = O.with_layers(O.SMOLLM2_360M, 2)
+    contexts = [300, 1200, 45]
+    case = GC.random_kv_case(geom, 95, contexts)
+    outs = []
+    for _ in range(3):
+        case.sync_kv_from_oracle()
+        outs.append(case.kernel_step([1, 2, 3], [S - 1 for S in contexts]))
+    for o in outs[1:]:
+        assert torch.equal(o["logits"], outs[0]["logits"]) and torch.equal(o["ids"], outs[0]["ids"])
+
+
+def test_batched_full_360m_config4_shape():
+    """BASELINE config 4 shape: the full 32-layer 360M, 16 sequences with contexts drawn from
+    128..4096; each sequence within the eager floor of the oracle."""
+    _need_gpu()
+    rng = np.random.default_rng(4)
+    contexts = [int(x) for x in rng.integers(128, 4097, 16)]
+    case = GC.random_kv_case(O.SMOLLM2_360M, 99, contexts, norm_jitter=0.0)
+    ids = [int(x) for x in rng.integers(0, 49152, 16)]
+    pos = [S - 1 for S in contexts]
+    k = case.kernel_step(ids, pos)
+    f = case.eager_gpu_step(ids, pos)
+    r = case.oracle_step(ids, pos)
+    out = GC.assert_within_floor(k, r, f, "config4")
+    print("config4 worst", max(v["kernel"]["max_abs"] for v in out.values()),
+          "floor worst", max(v["eager_gpu_floor"]["max_abs"] for v in out.values()))
