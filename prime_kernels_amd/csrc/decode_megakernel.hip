@@ -1592,6 +1592,10 @@ struct SmemB {
   uint32_t cbar;
 };
 static_assert(sizeof(typename SmemB<G135>::Attn) <= sizeof(uint16_t) * BMAX * SmemB<G135>::XS, "union sizing");
+// Attention items at the largest batch and context: each (sequence, KV head) has at most
+// ceil((kMaxSeq - 1) / TCB) chunks, and every workgroup holds at most IPW items.
+static_assert((G360::KVH > G135::KVH ? G360::KVH : G135::KVH) * BMAX * ((kMaxSeq - 1 + TCB - 1) / TCB) <= MAX_ITEMS,
+              "item arrays hold every chunk");
 
 template <class G>
 struct PlanB {
@@ -2326,7 +2330,10 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
     const int r0 = P.v0 + j * LM_ROWS;
     const int nrows = min(LM_ROWS, P.v1 - r0);
     const uint32_t seg = C.next_seg(uint32_t(nrows) * G::H * 2);
-    if (j % NCW != C.cw) continue;
+    if (j % NCW != C.cw) {  // another wave's segment: this wave will not read it
+      C.release(C.pos);
+      continue;
+    }
     C.wait_filled(C.pos);
     const floatx4 acc = mfma_part<G, G::H>(C, seg, 0, 1);
     C.release(C.pos);

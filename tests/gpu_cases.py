@@ -62,7 +62,8 @@ class Case:
             num_layers=self.geom.layers, return_token_ids=True, logits_out=lg, layer_outputs=lo)
         torch.cuda.synchronize()
         rt = self.mod.workspace(dev)
-        assert rt.abort_word() == 0, "kernel abandoned a bounded wait"
+        hdr = rt.header(3)
+        assert hdr[1] == 0, f"kernel abandoned a bounded wait (wait site {hdr[2]}, epoch {hdr[0]})"
         res = {"hidden": hid.clone().cpu(), "ids": out_ids.clone().cpu()}
         if logits:
             res["logits"] = lg.cpu()
@@ -110,6 +111,31 @@ class Case:
         if logits:
             res["logits"] = lg[0].cpu()
         return res
+
+
+def teacher_forced_layer_batch(case: "Case", li: int, x_in: torch.Tensor, positions, *, logits=False):
+    """Layer `li` alone through the kernel for B sequences at once: x_in [B, H] is placed in
+    embedding rows 0..B-1 of a copy of the embedding and token b is row b.  Returns the layer
+    outputs [B, H] (and the logits [B, V] if asked; logits 0..B-1 are the inputs' own rows)."""
+    B = x_in.shape[0]
+    dev = case.dev
+    if not hasattr(case, "_embed_tfb"):
+        case._embed_tfb = case.wd.embed.clone()
+    case._embed_tfb[:B] = x_in.to(dev, BF16)
+    lo = torch.empty((1, B, case.geom.hidden), dtype=BF16, device=dev)
+    lg = torch.empty((B, case.geom.vocab), dtype=BF16, device=dev) if logits else None
+    slots = [case.kv.slot(b, positions[b]) for b in range(B)]
+    case.mod.decode_step(
+        input_ids=torch.arange(B, device=dev), positions=torch.tensor(positions, device=dev),
+        seq_lens=torch.tensor([p + 1 for p in positions], dtype=torch.int32, device=dev), block_table=case.btd,
+        slot_mapping=torch.tensor(slots, device=dev), embed=case._embed_tfb, layers=[case.kernel_layers[li]],
+        final_norm=case.wd.final_norm, kv_caches=[case.kvd[li]], cos_sin_cache=case.csd, eps=1e-5, num_layers=1,
+        return_token_ids=True, logits_out=lg, layer_outputs=lo)
+    torch.cuda.synchronize()
+    res = {"out": lo[0].cpu()}
+    if logits:
+        res["logits"] = lg.cpu()
+    return res
 
 
 def mxfp8_case(geom: O.Geometry, seed: int, contexts, *, norm_jitter=0.05, fill_seed: int | None = None) -> Case:

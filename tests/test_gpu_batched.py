@@ -1,7 +1,14 @@
 """GPU parity of the batched decode kernel (2..16 sequences per launch, ragged contexts, MFMA
 projections): every sequence against the oracle (which runs each sequence on its own), KV appends,
 agreement with the batch-1 kernel, and the BASELINE config-4 shape (full 360M, 16 sequences,
-contexts 128..4096).  Bars as in test_gpu_decode.py."""
+contexts 128..4096).
+
+Bars as in test_gpu_decode.py.  A free-running step is held to the north-star bound or to twice
+the eager-GPU floor of the same sequence, whichever is larger: a single bf16 rounding flip (a
+different fp32 summation order in attention or a projection) changes the next RMSNorm scale and so
+hundreds of normed values, and random-init layers carry that on.  The eager GPU path shows the same
+on other sequences of the same batch.  Layers fed the oracle's own inputs (teacher forced) are held
+to the north-star bound itself."""
 
 import numpy as np
 import pytest
@@ -36,8 +43,9 @@ def test_batched_two_layers(contexts):
     ids = [100 + 7 * b for b in range(len(contexts))]
     pos = [S - 1 for S in contexts]
     k = case.kernel_step(ids, pos, layer_outputs=True)
+    f = case.eager_gpu_step(ids, pos)
     r = case.oracle_step(ids, pos, layer_outputs=True)
-    GC.assert_step_parity(k, r, f"batched {contexts}")
+    GC.assert_within_floor(k, r, f, f"batched {contexts}")
     _kv_appends_match(case, contexts, "two layers")
 
 
@@ -48,9 +56,11 @@ def test_batched_ragged_16_two_layers():
     geom = O.with_layers(O.SMOLLM2_360M, 2)
     case = GC.random_kv_case(geom, 71, contexts)
     ids = [int(x) for x in rng.integers(0, 49152, 16)]
-    k = case.kernel_step(ids, [S - 1 for S in contexts])
-    r = case.oracle_step(ids, [S - 1 for S in contexts])
-    GC.assert_step_parity(k, r, "ragged16")
+    pos = [S - 1 for S in contexts]
+    k = case.kernel_step(ids, pos)
+    f = case.eager_gpu_step(ids, pos)
+    r = case.oracle_step(ids, pos)
+    GC.assert_within_floor(k, r, f, "ragged16")
     _kv_appends_match(case, contexts, "ragged16")
 
 
@@ -111,3 +121,33 @@ def test_batched_full_360m_config4_shape():
     out = GC.assert_within_floor(k, r, f, "config4")
     print("config4 worst", max(v["kernel"]["max_abs"] for v in out.values()),
           "floor worst", max(v["eager_gpu_floor"]["max_abs"] for v in out.values()))
+
+
+def test_batched_full_360m_config4_teacher_forced_layers():
+    """Config 4 shape, every layer of the full 360M fed the oracle's inputs for all 16 sequences at
+    once: each layer output within the north-star bound of the oracle's, mostly bit-identical."""
+    _need_gpu()
+    rng = np.random.default_rng(44)
+    contexts = [int(x) for x in rng.integers(128, 4097, 16)]
+    geom = O.SMOLLM2_360M
+    case = GC.random_kv_case(geom, 98, contexts, norm_jitter=0.0)
+    ids = [int(x) for x in rng.integers(16, 49152, 16)]
+    pos = [S - 1 for S in contexts]
+    r = case.oracle_step(ids, pos, layer_outputs=True)
+    lo = r["layer_outputs"]                                  # [L, B, H]
+    case.sync_kv_from_oracle()                               # caches the oracle saw, new tokens included
+    fracs = []
+    for li in range(geom.layers):
+        x_in = case.w.embed[ids] if li == 0 else lo[li - 1]
+        k = GC.teacher_forced_layer_batch(case, li, x_in, pos, logits=li == geom.layers - 1)
+        for b in range(16):
+            c = GC.compare_logits(k["out"][b], lo[li, b])
+            assert c["max_abs"] <= GC.LOGIT_ATOL and c["cos"] >= GC.COS_MIN, (li, b, c)
+            fracs.append(GC.identical_fraction(k["out"][b], lo[li, b]))
+    assert sum(fracs) / len(fracs) >= 0.9, sum(fracs) / len(fracs)
+    keep = torch.ones(geom.vocab, dtype=torch.bool)
+    keep[:16] = False
+    for b in range(16):
+        c = GC.compare_logits(k["logits"][b][keep], r["logits"][b][keep])
+        assert c["max_abs"] <= GC.LOGIT_ATOL and c["cos"] >= GC.COS_MIN, (b, c)
+    print("config4 teacher-forced mean bit-identical fraction", round(sum(fracs) / len(fracs), 4))
