@@ -1,4 +1,5 @@
 """Decode throughput of SmolLM2-360M (bf16, batch 1, 1024-token context) on one MI355X.
+(--batch 16: BASELINE config 4, 16 sequences with ragged contexts; --weights mxfp8: config 5.)
 
 One step = one greedy decode step of the full model (32 layers + tied LM head + argmax), i.e. one
 launch of the persistent megakernel.  The KV cache holds a synthetic 1024-token context
@@ -31,10 +32,13 @@ KV_TOKEN_360M = 40_960
 HIDDEN_BYTES = 1_920
 
 
-def step_bytes(S: int, layers: int = 32, weights: str = "bf16") -> int:
-    """Algorithmic bytes of one step attending S tokens (S counts the new one)."""
+def step_bytes(S, layers: int = 32, weights: str = "bf16") -> int:
+    """Algorithmic bytes of one step whose sequences attend S tokens each (S counts the new one;
+    an int for one sequence or a list for a batch): the weights and the LM head once per step,
+    per sequence its cached K/V, the appended K/V and the hidden state in and out."""
     w = W_LAYER_360M if weights == "bf16" else W_LAYER_360M_MXFP8
-    return layers * w + E_LMHEAD_360M + HIDDEN_BYTES + KV_TOKEN_360M * S + KV_TOKEN_360M + HIDDEN_BYTES
+    seqs = [S] if isinstance(S, int) else list(S)
+    return layers * w + E_LMHEAD_360M + sum(KV_TOKEN_360M * s + KV_TOKEN_360M + 2 * HIDDEN_BYTES for s in seqs)
 
 
 def cpu_baseline(seconds: float = 15.0) -> dict:
@@ -77,11 +81,19 @@ def main() -> None:
                     help="projection weights: bf16 (BASELINE config 3, the default) or MXFP8 (config 5)")
     ap.add_argument("--context", type=int, default=None,
                     help="cached tokens before the first timed step (default 1024; 8192 with --weights mxfp8)")
+    ap.add_argument("--batch", type=int, default=1,
+                    help="sequences per step; above 1 each sequence's context is drawn uniformly from "
+                         "128..4096 (BASELINE config 4 at 16; bf16 weights only)")
+    ap.add_argument("--seed", type=int, default=4, help="seed of the ragged contexts and token ids")
     args = ap.parse_args()
     context = args.context if args.context is not None else (CONTEXT if args.weights == "bf16" else 8192)
+    B = args.batch
+    if not 1 <= B <= 16 or (B > 1 and args.weights != "bf16"):
+        print("--batch takes 1..16 sequences, with bf16 weights above 1", file=sys.stderr)
+        sys.exit(2)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: every box in this setup has one MI355X and the decode "
-              f"path shards by data parallelism with no exchange (see DESIGN.md); --gpus {args.gpus} is not run.",
+              f"path shards by data parallelism with no exchange between GPUs; --gpus {args.gpus} is not run.",
               file=sys.stderr)
         sys.exit(2)
 
@@ -94,20 +106,28 @@ def main() -> None:
     model = mod.MODEL
     dev = torch.device("cuda:0")
     K, W = args.steps, args.warmup
+    if B == 1:
+        contexts, first_ids = [context], [17]
+    else:
+        import numpy as np
+        rng = np.random.default_rng(args.seed)
+        contexts = [int(x) for x in rng.integers(128, 4097, B)]
+        first_ids = [int(x) for x in rng.integers(0, 49152, B)]
     embed, final_norm, layers = WL.random_weights(pk.load("decode_megakernel_360m").MODEL, 1234, dev)
     if args.weights == "mxfp8":
         layers = mod.quantize_layers(layers)
-    kv = WL.PagedKV(model, 1, context + max(K, W) + 16, device=dev, seed=5, fill="randn")
-    cos_sin = WL.rope_table(context + max(K, W) + 16, device=dev)
+    cap = max(contexts) + max(K, W) + 16
+    kv = WL.PagedKV(model, B, cap, device=dev, seed=5, fill="randn")
+    cos_sin = WL.rope_table(cap, device=dev)
     torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream(dev)
-    warm = StepLauncher(model, embed=embed, layers=layers, final_norm=final_norm, kv_caches=kv.caches,
-                        block_table=kv.block_table, cos_sin_cache=cos_sin, first_id=17, start_pos=context, steps=max(W, 1))
+    common = dict(embed=embed, layers=layers, final_norm=final_norm, kv_caches=kv.caches, block_table=kv.block_table,
+                  cos_sin_cache=cos_sin, first_id=first_ids, start_pos=contexts, batch=B)
+    warm = StepLauncher(model, steps=max(W, 1), **common)
     for k in range(W):
         warm.launch(k, stream.cuda_stream)
-    timed = StepLauncher(model, embed=embed, layers=layers, final_norm=final_norm, kv_caches=kv.caches,
-                         block_table=kv.block_table, cos_sin_cache=cos_sin, first_id=17, start_pos=context, steps=K)
+    timed = StepLauncher(model, steps=K, **common)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
@@ -125,17 +145,25 @@ def main() -> None:
     if not bool(((ids >= 0) & (ids < 49152)).all()):
         raise RuntimeError("greedy ids out of range")
 
-    total_bytes = sum(step_bytes(context + 1 + k, weights=args.weights) for k in range(K))
+    total_bytes = sum(step_bytes([c + 1 + k for c in contexts], weights=args.weights) for k in range(K))
     ms_per_step = ms / K
     achieved = total_bytes / (ms * 1e-3) / 1e9
     traffic = None
-    tfile = ROOT / "profiles" / f"decode360_{'' if args.weights == 'bf16' else 'mxfp8_'}ctx{context}_traffic.json"
+    tname = (f"decode360_b{B}_ragged" if B > 1 else
+             f"decode360_{'' if args.weights == 'bf16' else 'mxfp8_'}ctx{context}")
+    tfile = ROOT / "profiles" / f"{tname}_traffic.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
     wname = "bf16" if args.weights == "bf16" else "MXFP8-weight"
+    ctx_name = f"ctx={context}" if B == 1 else "ragged ctx 128..4096"
+    workload = (f"smollm2-360m greedy decode, batch 1, {context}-token context, K steps at context "
+                f"{context + 1}..{context}+K" + (", MXFP8 projection weights" if args.weights == "mxfp8" else "")
+                if B == 1 else
+                f"smollm2-360m greedy decode, batch {B}, contexts drawn uniformly from 128..4096 "
+                f"(seed {args.seed}, mean {sum(contexts) / B:.0f}), K steps per sequence")
     line = {
-        "metric": f"decode tok/s, SmolLM2-360M {wname} bs=1 ctx={context}; % of HBM roofline",
-        "value": round(K / (ms * 1e-3), 2),
+        "metric": f"decode tok/s, SmolLM2-360M {wname} bs={B} {ctx_name}; % of HBM roofline",
+        "value": round(B * K / (ms * 1e-3), 2),
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": K,
@@ -148,16 +176,15 @@ def main() -> None:
         "data": "synthetic (seeded random-init weights N(0,0.02) bf16" +
                 (", projections quantised to MXFP8 on the GPU" if args.weights == "mxfp8" else "") +
                 ", KV context N(0,1) bf16, greedy ids fed back on device)",
-        "config": {"workload": f"smollm2-360m greedy decode, batch 1, {context}-token context, K steps at context "
-                               f"{context + 1}..{context}+K" + (", MXFP8 projection weights" if args.weights == "mxfp8" else ""),
-                   "batch": 1, "context": context, "layers": 32, "weights": args.weights,
+        "config": {"workload": workload,
+                   "batch": B, "context": context if B == 1 else contexts, "layers": 32, "weights": args.weights,
                    "lm_head": "tied, fused argmax", "launch": "one cooperative kernel per step, 256 workgroups"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "bytes_per_step": round(total_bytes / K)},
         "host_wall_ms_per_step": round(wall * 1e3 / K, 5),
     }
-    if not args.no_cpu_baseline and args.weights == "bf16":
+    if not args.no_cpu_baseline and args.weights == "bf16" and B == 1:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)
 

@@ -60,7 +60,11 @@ int pk_workspace_forget(const void* ptr);
 /* Synchronous copy of n header words of a workspace to the host (0 epoch, 1 abort, 2 abort site). */
 int pk_workspace_read(const void* ws, size_t word, unsigned* out, int n);
 
-/* One greedy decode step for B sequences (vLLM FLASH_ATTN metadata, paged KV [blocks, KVH, 16, 128]).
+/* One greedy decode step for B = 1..16 sequences (vLLM FLASH_ATTN metadata, paged KV
+ * [blocks, KVH, 16, 128]; contexts may differ per sequence).  B = 1 runs the GEMV kernel; B >= 2
+ * runs the batched kernel, whose projections and LM head are MFMA tiles over all B tokens, so the
+ * weights are read once per step for the whole batch.  The reference caps SmolLM2-360M at B <= 2
+ * (decode_megakernel_360m/__init__.py:46).
  *   layers: device table [n_layers][6] of pointers (norm1, qkv, o, norm2, gate_up, down), bf16.
  *   kv: device table [n_layers] of cache base pointers; K at k_off, V at v_off (elements).
  *   out_hidden [B, H] bf16 receives the final-normed hidden state.
@@ -78,7 +82,8 @@ int pk_decode(void* stream, int model, int B, int n_layers, const void* input_id
  * [n_layers][10] of (norm1, qkv, qkv_scales, o, o_scales, norm2, gate_up, gate_up_scales, down,
  * down_scales): e4m3 bytes [rows, cols] and e8m0 scale codes [rows, pk_mxfp8_scale_stride(cols)],
  * one per 32 consecutive weights of a row, each row padded with zeros to a multiple of 16 bytes.
- * Norms, embedding and the tied LM head stay bf16.  No reference counterpart: BASELINE config 5. */
+ * Norms, embedding and the tied LM head stay bf16.  B must be 1 (PK_ERR_BATCH otherwise).
+ * No reference counterpart: BASELINE config 5. */
 int pk_decode_mxfp8(void* stream, int model, int B, int n_layers, const void* input_ids, int ids_i64,
                     const void* embed, const void* final_norm, const void* positions, const void* seq_lens,
                     const void* block_table, int bt_stride, const void* slot_mapping, const void* layers,

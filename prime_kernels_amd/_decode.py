@@ -253,47 +253,59 @@ def decode_step(model: Model, *, input_ids, positions, seq_lens, block_table, sl
 
 
 class StepLauncher:
-    """Pre-validated, allocation-free launcher for a run of greedy decode steps (batch 1).
+    """Pre-validated, allocation-free launcher for a run of greedy decode steps of B sequences.
 
-    All per-step metadata lives in device arrays prepared once: step k reads its input id from
-    ids[k] and writes the greedy id to ids[k+1], so consecutive steps chain on the device with no
+    All per-step metadata lives in device arrays prepared once: step k reads its input ids from
+    ids[k] and writes the greedy ids to ids[k+1], so consecutive steps chain on the device with no
     host synchronisation (the way graph-replayed serving steps run, decode_backend.after.py:276-277).
+    `first_id` and `start_pos` are one value for every sequence or one per sequence (ragged
+    contexts: sequence b decodes positions start_pos[b] .. start_pos[b] + steps - 1).
     """
 
     def __init__(self, model: Model, *, embed, layers, final_norm, kv_caches, block_table, cos_sin_cache,
-                 first_id: int, start_pos: int, steps: int, logits: bool = False):
+                 first_id, start_pos, steps: int, logits: bool = False, batch: int = 1):
         dev = embed.device
+        B = batch
+        if not 1 <= B <= model.max_batch:
+            raise ValueError(f"{model.name}: batch must be 1..{model.max_batch}, got {B}")
+        if block_table.shape[0] < B:
+            raise ValueError("block table has fewer rows than the batch")
         self.model = model
+        self.batch = B
         self.rt = runtime(model, dev)
         self.lib = self.rt.lib
         self.layers_t, self.kv_t = _tables(self.rt, layers, kv_caches)
         self.keep = (embed, layers, final_norm, kv_caches, block_table, cos_sin_cache)
         kv0 = kv_caches[0]
         self.kv_strides = (0, model.head_dim, kv0.stride(0), kv0.stride(2), kv0.stride(1))
-        pos = torch.arange(start_pos, start_pos + steps, dtype=torch.int64)
-        bt = block_table[0].cpu().to(torch.int64)
-        self.positions = pos.to(dev)
-        self.seq_lens = (pos + 1).to(torch.int32).to(dev)
-        self.slots = (bt[pos // 16] * 16 + pos % 16).to(dev)
-        self.ids = torch.zeros(steps + 1, dtype=torch.int64, device=dev)
-        self.ids[0] = first_id
-        self.logits = torch.empty((1, VOCAB), dtype=torch.bfloat16, device=dev) if logits else None
-        self.steps = steps
+        starts = torch.tensor([start_pos] * B if isinstance(start_pos, int) else list(start_pos), dtype=torch.int64)
+        firsts = torch.tensor([first_id] * B if isinstance(first_id, int) else list(first_id), dtype=torch.int64)
+        if starts.numel() != B or firsts.numel() != B:
+            raise ValueError("start_pos / first_id must give one value per sequence")
+        pos = starts[None, :] + torch.arange(steps, dtype=torch.int64)[:, None]          # [steps, B]
+        bt = block_table[:B].cpu().to(torch.int64)
         self.max_seq = block_table.shape[1] * BLOCK_SIZE
-        if start_pos + steps > self.max_seq:
+        if int(pos.max()) + 1 > self.max_seq or int(starts.min()) < 0:
             raise ValueError("block table too small for the requested steps")
+        self.positions = pos.contiguous().to(dev)
+        self.seq_lens = (pos + 1).to(torch.int32).contiguous().to(dev)
+        self.slots = (torch.gather(bt, 1, (pos // 16).t()).t() * 16 + pos % 16).contiguous().to(dev)
+        self.ids = torch.zeros((steps + 1, B), dtype=torch.int64, device=dev)
+        self.ids[0] = firsts.to(dev)
+        self.logits = torch.empty((B, VOCAB), dtype=torch.bfloat16, device=dev) if logits else None
+        self.steps = steps
 
     def launch(self, k: int, stream: int) -> None:
-        m, rt = self.model, self.rt
+        m, rt, B = self.model, self.rt, self.batch
         embed, layers, final_norm, kv_caches, block_table, cos_sin = self.keep
         launch = self.lib.pk_decode_mxfp8 if m.weight_format == "mxfp8" else self.lib.pk_decode
         rc = launch(
-            stream, m.model_id, 1, len(layers), self.ids.data_ptr() + 8 * k, 1, embed.data_ptr(),
-            final_norm.data_ptr(), self.positions.data_ptr() + 8 * k, self.seq_lens.data_ptr() + 4 * k,
-            block_table.data_ptr(), block_table.stride(0), self.slots.data_ptr() + 8 * k,
+            stream, m.model_id, B, len(layers), self.ids.data_ptr() + 8 * B * k, 1, embed.data_ptr(),
+            final_norm.data_ptr(), self.positions.data_ptr() + 8 * B * k, self.seq_lens.data_ptr() + 4 * B * k,
+            block_table.data_ptr(), block_table.stride(0), self.slots.data_ptr() + 8 * B * k,
             self.layers_t.data_ptr(), self.kv_t.data_ptr(), *self.kv_strides, BLOCK_SIZE,
             cos_sin.data_ptr(), int(cos_sin.dtype == torch.float32), rt.out.data_ptr(), None,
-            self.ids.data_ptr() + 8 * (k + 1), self.logits.data_ptr() if self.logits is not None else None,
+            self.ids.data_ptr() + 8 * B * (k + 1), self.logits.data_ptr() if self.logits is not None else None,
             rt.scratch_ptr, rt.scratch_bytes, self.max_seq)
         if rc != 0:
             raise RuntimeError(f"{m.name} failed: {_native.status_string(rc)}")

@@ -1940,6 +1940,7 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
     }
     C.cbar();
   }
+  if (C.ct == 0) trace_at(p, l, 4, p.n_layers);
   const float sgn = part < 4 ? -1.f : 1.f;
   // ---- pass A: scores and chunk statistics of every item ----
   for (int k = 0; k < P.ni; ++k) {
@@ -2051,6 +2052,7 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
     }
     C.cbar();  // wml is reused by the next item
   }
+  if (C.ct == 0) trace_at(p, l, 5, p.n_layers);
   // ---- pass B: global statistics, probabilities, P.V of every item ----
   for (int k = 0; k < P.ni; ++k) {
     int b, g, c, Cc, base, t0, t1;
@@ -2170,6 +2172,7 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
     }
     C.cbar();  // wo and pb are reused by the next item
   }
+  if (C.ct == 0) trace_at(p, l, 6, p.n_layers);
   // ---- pass C: leaders add their chunks' partials (chunk order) and publish attn ----
   for (int k = 0; k < P.ni; ++k) {
     int b, g, c, Cc, base, t0, t1;
@@ -2206,6 +2209,7 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
     O += sm.at.own[k][w * 64 + lane];
     put_bf16<G>(C, X_ATTN, l, G::H, b, (g * 3 + w) * 64 + lane, O);
   }
+  if (C.ct == 0) trace_at(p, l, 7, p.n_layers);
   publish_flag<G>(C, X_ATTN, l);
 }
 
@@ -2220,9 +2224,16 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
   const int B = P.B;
   const int nq = P.q1 - P.q0, no = P.o1 - P.o0, na = P.a1 - P.a0, nd = P.d1 - P.d0;
   const int orow = 4 * (C.lane >> 4), tok = C.lane & 15;  // this lane's MFMA output rows / token
+  // Diagnostic timestamps (events per layer: 0 P1 start, 1 staged, 2 weights in, 3 QKV stored,
+  // 4 attention start, 5-7 passes A-C done, 8 attn published, 9-11 P3, 12-14 P4, 15-17 P5).
+  auto tr = [&](int l, int ev) { if (C.ct == 0) trace_at(p, l, ev, p.n_layers); };
+  if (C.ct == 0 && p.trace)
+    p.trace[size_t(blockIdx.x) * (size_t(p.n_layers) * TR_EVENTS + TR_TAIL) + size_t(p.n_layers) * TR_EVENTS] =
+        wall_clock64();
   for (int l = 0; l < p.n_layers; ++l) {
     // ---------------- P1: RMSNorm(x) + QKV ----------------
     C.refresh();
+    tr(l, 0);
     {
       const uint32_t segn = C.next_seg(G::H * 2);
       const uint32_t segq = C.next_seg(uint32_t(nq) * G::H * 2);
@@ -2236,11 +2247,13 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
       } else {
         stage_flagged<G>(C, X_X, l - 1, G::H);
       }
+      tr(l, 1);
       for (int i = C.ct; i < B * no; i += NCT) {
         const int b = i / no, r = i - b * no;
         sm.xk[b][r] = bf2f(sm.xs[b * G::H + P.o0 + r]);
       }
       C.wait_filled(C.pos);
+      tr(l, 2);
       norm_staged<G>(C, segn);
       const floatx4 acc = mfma_tile<G, G::H>(C, segq, sm.tile);
       C.release(C.pos);
@@ -2248,19 +2261,23 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           if (orow + j < nq) st_dev(p.ws + W::xw(X_QKV, l, tok, P.q0 + orow + j), C.w16(acc[j]));
+      tr(l, 3);
     }
     // ---------------- P2: attention ----------------
     C.refresh();
     {
       const uint32_t segcs = C.next_seg(P.ni ? uint32_t(B) * (p.cs_fp32 ? 256u : 128u) : 0u);
       attention_b<G>(C, l, segcs);
+      tr(l, 8);
     }
     // ---------------- P3: O + residual ----------------
     C.refresh();
     {
       const uint32_t sego = C.next_seg(uint32_t(no) * G::H * 2);
       stage_flagged<G>(C, X_ATTN, l, G::H);
+      tr(l, 9);
       C.wait_filled(C.pos);
+      tr(l, 10);
       const floatx4 acc = mfma_tile<G, G::H>(C, sego, sm.tile);
       C.release(C.pos);
       if (C.cw == 0 && tok < B)
@@ -2268,6 +2285,7 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
         for (int j = 0; j < 4; ++j)
           if (orow + j < no) put_bf16<G>(C, X_H1, l, G::H, tok, P.o0 + orow + j, sm.xk[tok][orow + j] + rnd(acc[j]));
       publish_flag<G>(C, X_H1, l);
+      tr(l, 11);
     }
     // ---------------- P4: RMSNorm(h1) + gate/up + SwiGLU ----------------
     C.refresh();
@@ -2276,11 +2294,13 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
       const uint32_t segg = C.next_seg(uint32_t(na) * G::H * 2);
       const uint32_t segu = C.next_seg(uint32_t(na) * G::H * 2);
       stage_flagged<G>(C, X_H1, l, G::H);
+      tr(l, 12);
       for (int i = C.ct; i < B * nd; i += NCT) {
         const int b = i / nd, r = i - b * nd;
         sm.hk[b][r] = bf2f(sm.xs[b * G::H + P.d0 + r]);
       }
       C.wait_filled(C.pos);
+      tr(l, 13);
       norm_staged<G>(C, segn);
       floatx4 gt = {0.f, 0.f, 0.f, 0.f}, up = {0.f, 0.f, 0.f, 0.f};
       mfma_tile_pair<G, G::H>(C, segg, segu, sm.tile, gt, up);
@@ -2294,13 +2314,16 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
             put_bf16<G>(C, X_ACT, l, G::I, tok, P.a0 + orow + j, silu * uv);
           }
       publish_flag<G>(C, X_ACT, l);
+      tr(l, 14);
     }
     // ---------------- P5: down + residual ----------------
     C.refresh();
     {
       const uint32_t segd = C.next_seg(uint32_t(nd) * G::I * 2);
       stage_flagged<G>(C, X_ACT, l, G::I);
+      tr(l, 15);
       C.wait_filled(C.pos);
+      tr(l, 16);
       const floatx4 acc = mfma_tile<G, G::I>(C, segd, sm.tile);
       C.release(C.pos);
       if (C.cw == 0 && tok < B)
@@ -2312,6 +2335,7 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
             if (p.layer_outputs) p.layer_outputs[(size_t(l) * B + tok) * G::H + P.d0 + orow + j] = uint16_t(f2bf(y));
           }
       publish_flag<G>(C, X_X, l);
+      tr(l, 17);
     }
   }
   // ---------------- final RMSNorm + LM head + argmax ----------------
@@ -2356,6 +2380,9 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
   }
   if (C.lane < BMAX) { sm.lm_val[C.cw][C.lane] = best; sm.lm_idx[C.cw][C.lane] = bidx; }
   C.cbar();
+  if (C.ct == 0 && p.trace)
+    p.trace[size_t(blockIdx.x) * (size_t(p.n_layers) * TR_EVENTS + TR_TAIL) + size_t(p.n_layers) * TR_EVENTS + 1] =
+        wall_clock64();
   if (C.ct < B) {
     float bv = sm.lm_val[0][C.ct];
     int bi = sm.lm_idx[0][C.ct];
