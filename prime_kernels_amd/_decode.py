@@ -153,7 +153,7 @@ def _tables(rt: _Runtime, layers, kv_caches):
 
 def decode_step(model: Model, *, input_ids, positions, seq_lens, block_table, slot_mapping, embed, layers,
                 final_norm, kv_caches, cos_sin_cache, eps, layer_outputs=None, debug=None,
-                debug_layer_index=-1, return_token_ids=False, logits_out=None, num_layers=None):
+                debug_layer_index=-1, return_token_ids=False, logits_out=None, num_layers=None, encoded_gu=None):
     """One decode step; inputs follow vLLM FLASH_ATTN metadata (reference signature
     decode_megakernel_360m/__init__.py:142-144).
 
@@ -161,7 +161,9 @@ def decode_step(model: Model, *, input_ids, positions, seq_lens, block_table, sl
     next call overwrites.  With `return_token_ids=True` returns (hidden, ids[B] int64) where ids
     are the greedy tokens of the tied LM head (also a reused buffer).  `logits_out` ([B, 49152]
     bf16, caller-owned) receives the LM-head logits.  `num_layers` runs only the first N layers
-    (default: all), for tests on truncated models."""
+    (default: all), for tests on truncated models.  `encoded_gu` (a lossless_bf16.EncodedGUCache of
+    the same gate_up matrices, SmolLM2-360M only) makes the batch-1 step stream the encoded gate/up
+    weights of every enabled layer."""
     nl = model.layers if num_layers is None else int(num_layers)
     batch = input_ids.shape[0]
     if not 1 <= batch <= model.max_batch:
@@ -230,11 +232,24 @@ def decode_step(model: Model, *, input_ids, positions, seq_lens, block_table, sl
         if not logits_out.is_contiguous():
             raise ValueError("logits_out must be contiguous")
 
+    extra = ()
+    if encoded_gu is not None:
+        if model.model_id != 360 or model.weight_format != "bf16":
+            raise ValueError("the lossless gate/up cache is for SmolLM2-360M bf16 weights")
+        if encoded_gu.device != device:
+            raise ValueError(f"encoded_gu must be on {device}")
+        if tuple(t.data_ptr() for t in encoded_gu._weights[:nl]) != tuple(layer[4].data_ptr() for layer in layers):
+            raise ValueError("encoded_gu was prepared for other gate_up tensors")
+
     rt = runtime(model, device)
     layers_t, kv_t = _tables(rt, layers, kv_caches)
     stream = torch.cuda.current_stream(device).cuda_stream
     want_ids = return_token_ids or logits_out is not None
-    launch = rt.lib.pk_decode_mxfp8 if model.weight_format == "mxfp8" else rt.lib.pk_decode
+    if encoded_gu is not None:
+        launch = rt.lib.pk_decode_lossless
+        extra = (encoded_gu.table.data_ptr(),)
+    else:
+        launch = rt.lib.pk_decode_mxfp8 if model.weight_format == "mxfp8" else rt.lib.pk_decode
     rc = launch(
         stream, model.model_id, batch, nl, input_ids.data_ptr(), int(input_ids.dtype == torch.int64),
         embed.data_ptr(), final_norm.data_ptr(), positions.data_ptr(), seq_lens.data_ptr(),
@@ -244,7 +259,7 @@ def decode_step(model: Model, *, input_ids, positions, seq_lens, block_table, sl
         layer_outputs.data_ptr() if layer_outputs is not None else None,
         rt.ids.data_ptr() if want_ids else None,
         logits_out.data_ptr() if logits_out is not None else None,
-        rt.scratch_ptr, rt.scratch_bytes, block_table.shape[1] * BLOCK_SIZE)
+        rt.scratch_ptr, rt.scratch_bytes, block_table.shape[1] * BLOCK_SIZE, *extra)
     if rc != 0:
         raise RuntimeError(f"{model.name} failed: {_native.status_string(rc)}")
     if return_token_ids:

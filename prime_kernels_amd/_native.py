@@ -44,6 +44,15 @@ SIGNATURES = {
                        ci, vp, vp, sz, ci]),
     "mk_workspace_bytes": (sz, [ci, ci]),
     "mk_status_string": (ctypes.c_char_p, [ci]),
+    # include/prime_lossless.h
+    "lossless_scan_workspace_bytes": (sz, []),
+    "lossless_encode_layer": (ci, [vp, vp, vp, vp, vp, vp, vp, vp, sz, vp, ctypes.c_uint, vp]),
+    "lossless_decode_layer": (ci, [vp, vp, vp, vp, vp]),
+    "lossless_write_descriptor": (ci, [vp, ci, vp, vp, vp, vp, vp, vp]),
+    "decode360_lossless": (ci, [vp, ci, vp, vp, vp, vp, vp, vp, ci, vp, vp, vp, ll, ll, ll, ll, ll, ci, vp, ci,
+                                vp, vp, vp, sz, vp, sz, ci, ci, vp]),
+    "pk_decode_lossless": (ci, [vp, ci, ci, ci, vp, ci, vp, vp, vp, vp, vp, ci, vp, vp, vp,
+                                ll, ll, ll, ll, ll, ci, vp, ci, vp, vp, vp, vp, vp, sz, ci, vp]),
 }
 
 

@@ -17,7 +17,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 LIB_DIR = PKG / "_lib"
 LIB = LIB_DIR / "libprime_decode.so"
-SOURCES = [PKG / "csrc" / "decode_megakernel.hip"]
+SOURCES = [PKG / "csrc" / "decode_megakernel.hip", PKG / "csrc" / "lossless_bf16.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

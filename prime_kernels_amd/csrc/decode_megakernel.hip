@@ -34,6 +34,7 @@
 #include <cstdint>
 
 #include "../../include/prime_decode.h"
+#include "../../include/prime_lossless.h"
 
 namespace pk {
 
@@ -133,6 +134,19 @@ struct Params {
   int max_seq;                 // block_table capacity in tokens (seq_lens are clamped to it)
   int ids_i64;
   unsigned long long* trace;   // optional per-phase timestamps (diagnostics)
+  const EncodedGULayer* encoded_gu;  // optional [L] lossless gate/up encodings (batch-1 bf16 kernel)
+};
+
+// A layer's lossless gate/up encoding as this workgroup streams it (on = 0: dense gate/up): the
+// plane / header / escape arrays, and for gate (0) and up (1) the first escape ordinal of the
+// workgroup's rows and their number of escapes.
+struct GUE {
+  const uint8_t* plane;
+  const uint32_t* hdr;
+  const uint16_t* raw;
+  uint32_t on;
+  uint32_t first[2];
+  uint32_t cnt[2];
 };
 
 // Exchange-buffer layout (32-bit words).  The per-layer vectors (qkv, attn, h1, act, x) of tagged
@@ -359,14 +373,19 @@ struct Rows {
 // up rows, down rows; after the last layer: the final-norm weights and the LM-head segments.
 // Small vectors go through the ring too, so no consumer ever waits on a global load for them.
 enum SegKind {
-  S_NORM1, S_QKV, S_QKV_S, S_CS, S_KV, S_O, S_O_S, S_NORM2, S_GATE, S_GATE_S, S_UP, S_UP_S, S_DOWN, S_DOWN_S,
-  SEGS_PER_LAYER
+  S_NORM1, S_QKV, S_QKV_S, S_CS, S_KV, S_O, S_O_S, S_NORM2, S_GATE, S_GATE_S, S_GATE_H, S_GATE_R, S_UP, S_UP_S,
+  S_UP_H, S_UP_R, S_DOWN, S_DOWN_S, SEGS_PER_LAYER
 };
 constexpr int S_FNORM = 100, S_LM = 101;
 
+// Lossless gate/up (e != nullptr with e->on, bf16 weights only): S_GATE / S_UP carry the plane rows
+// (1 byte per weight), S_*_H the header rows (4 bytes per 8 weights), S_*_R the escaped chunks of the
+// workgroup's rows (16 bytes each); dense layers have empty S_*_H / S_*_R segments.
 template <class G>
-__device__ __forceinline__ uint32_t seg_bytes(const Plan<G>& P, int kind, int lm_index, int cs_fp32) {
+__device__ __forceinline__ uint32_t seg_bytes(const Plan<G>& P, int kind, int lm_index, int cs_fp32,
+                                              const GUE* e = nullptr) {
   constexpr uint32_t WB = G::WF ? 1u : 2u;  // bytes per projection weight
+  const bool enc = G::WF == 0 && e != nullptr && e->on != 0u;
   switch (kind) {
     case S_NORM1: return P.q1 > P.q0 ? G::H * 2 : 0u;
     case S_NORM2:
@@ -378,9 +397,13 @@ __device__ __forceinline__ uint32_t seg_bytes(const Plan<G>& P, int kind, int lm
     case S_O: return uint32_t(P.o1 - P.o0) * G::H * WB;
     case S_O_S: return G::WF ? uint32_t(P.o1 - P.o0) * scale_stride(G::H) : 0u;
     case S_GATE:
-    case S_UP: return uint32_t(P.a1 - P.a0) * G::H * WB;
+    case S_UP: return uint32_t(P.a1 - P.a0) * G::H * (enc ? 1u : WB);
     case S_GATE_S:
     case S_UP_S: return G::WF ? uint32_t(P.a1 - P.a0) * scale_stride(G::H) : 0u;
+    case S_GATE_H:
+    case S_UP_H: return enc ? uint32_t(P.a1 - P.a0) * (G::H / 8) * 4u : 0u;
+    case S_GATE_R: return enc ? e->cnt[0] * 16u : 0u;
+    case S_UP_R: return enc ? e->cnt[1] * 16u : 0u;
     case S_DOWN: return uint32_t(P.d1 - P.d0) * G::I * WB;
     case S_DOWN_S: return G::WF ? uint32_t(P.d1 - P.d0) * scale_stride(G::I) : 0u;
     default: {
@@ -425,6 +448,7 @@ struct Smem {
   float wo[NCW][3][64];          // per-wave P.V partial per head
   LayerW lw[G::L];               // layer pointer table (read by the producers from LDS)
   const void* kvp[G::L];         // per-layer KV cache base
+  GUE gue[G::L];                 // per-layer lossless gate/up streams of this workgroup
   int32_t blk[TC_MAX / 16 + 2];
   float lm_val[NCW];
   int32_t lm_idx[NCW];
@@ -493,7 +517,8 @@ __device__ __forceinline__ void producer(const Params& p, const Plan<G>& P, Smem
     if (lane == 0) st_lds(&sm.front[pw], first_pending_packet * PKT);
   };
   auto issue_segment = [&](int kind, int layer, int lm_index) {
-    const uint32_t bytes = seg_bytes(P, kind, lm_index, p.cs_fp32);
+    const GUE* ge = kind >= S_GATE && kind <= S_UP_R ? &sm.gue[layer] : nullptr;
+    const uint32_t bytes = seg_bytes(P, kind, lm_index, p.cs_fp32, ge);
     const uint32_t npk = pad_pkt(bytes) / PKT;
     if (npk == 0) return;
     const uint8_t* base = nullptr;
@@ -518,10 +543,19 @@ __device__ __forceinline__ void producer(const Params& p, const Plan<G>& P, Smem
         case S_O: base = u8(Lw.o) + size_t(P.o0) * G::H * WB; break;
         case S_O_S: base = Lw.o_s + size_t(P.o0) * SH; break;
         case S_NORM2: base = u8(Lw.norm2); break;
-        case S_GATE: base = u8(Lw.gate_up) + size_t(P.a0) * G::H * WB; break;
+        case S_GATE:
+          base = ge->on ? ge->plane + size_t(P.a0) * G::H : u8(Lw.gate_up) + size_t(P.a0) * G::H * WB;
+          break;
         case S_GATE_S: base = Lw.gate_up_s + size_t(P.a0) * SH; break;
-        case S_UP: base = u8(Lw.gate_up) + size_t(G::I + P.a0) * G::H * WB; break;
+        case S_GATE_H: base = u8(ge->hdr + size_t(P.a0) * (G::H / 8)); break;
+        case S_GATE_R: base = u8(ge->raw + size_t(ge->first[0]) * 8); break;
+        case S_UP:
+          base = ge->on ? ge->plane + size_t(G::I + P.a0) * G::H
+                        : u8(Lw.gate_up) + size_t(G::I + P.a0) * G::H * WB;
+          break;
         case S_UP_S: base = Lw.gate_up_s + size_t(G::I + P.a0) * SH; break;
+        case S_UP_H: base = u8(ge->hdr + size_t(G::I + P.a0) * (G::H / 8)); break;
+        case S_UP_R: base = u8(ge->raw + size_t(ge->first[1]) * 8); break;
         case S_DOWN: base = u8(Lw.down) + size_t(P.d0) * G::I * WB; break;
         default: base = Lw.down_s + size_t(P.d0) * SI; break;
       }
@@ -631,6 +665,9 @@ struct Consumer {
   }
   __device__ __forceinline__ uint32_t ring4(uint32_t at) const {
     return *reinterpret_cast<const uint32_t*>(sm.ring + (at & (RB - 1)));
+  }
+  __device__ __forceinline__ uint2 ring8(uint32_t at) const {
+    return *reinterpret_cast<const uint2*>(sm.ring + (at & (RB - 1)));
   }
   __device__ __forceinline__ uint32_t w16(float v) const { return (tag16 << 16) | f2bf(v); }
   __device__ __forceinline__ bool ok4(u32x4 v) const {
@@ -868,6 +905,66 @@ __device__ __forceinline__ void dots_ring_q(const Consumer<G>& C, uint32_t segq,
         acc = dot2(__builtin_bit_cast(uint32_t, lo), a[2 * d], acc);
         acc = dot2(__builtin_bit_cast(uint32_t, hi), a[2 * d + 1], acc);
       }
+    }
+    out[r] = acc;
+  }
+#pragma unroll
+  for (int r = 0; r < MAXR; ++r) out[r] = wave_sum(out[r]);
+}
+
+// The 8 bf16 words (4 packed pairs) of a lossless chunk: plane bytes p (sign | mantissa) and the
+// header's base exponent and 3-bit deltas give word_i = (p_i & 0x80) << 8 | (base + d_i) << 7 |
+// (p_i & 0x7f) (prime_kernels/lossless_bf16/csrc/lossless_bf16.cu:94-101).  A pair is built in one
+// register: v_perm places bytes 2j, 2j+1 in bits 0-7 / 16-23, both exponents are added at once.
+__device__ __forceinline__ uint4 lossless_chunk(uint2 p, uint32_t h) {
+  const uint32_t base2 = (h >> 24) * 0x10001u;
+  uint32_t out[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t t = __builtin_amdgcn_perm(0u, j < 2 ? p.x : p.y, (j & 1) ? 0x0c030c02u : 0x0c010c00u);
+    const uint32_t d = (h >> (6 * j)) & 63u;
+    const uint32_t ex = base2 + (d & 7u) + ((d >> 3) << 16);
+    out[j] = ((t & 0x00800080u) << 8) | (t & 0x007F007Fu) | (ex << 7);
+  }
+  return make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+// dots_ring over lossless-encoded rows: plane rows (K bytes each) in `segp`, header rows (K/8 words)
+// in `segh`, the escaped chunks of the workgroup's rows (ordinals first, first+1, ...) in `segr`.
+// Each lane rebuilds exactly the 16-byte chunks dots_ring would read from a dense segment and
+// accumulates them in the same order, so the sums are bit-identical to the dense matrix's.
+template <class G, int K, int MAXR>
+__device__ __forceinline__ void dots_ring_lossless(const Consumer<G>& C, uint32_t segp, uint32_t segh,
+                                                   uint32_t segr, uint32_t first, const XChunks<K, 8>& x,
+                                                   float (&out)[MAXR]) {
+  constexpr int CPL = Chunks<K>::CPL, CH = Chunks<K>::CH;
+  uint4 w[MAXR][CPL];
+#pragma unroll
+  for (int r = 0; r < MAXR; ++r) {
+    const uint32_t row = uint32_t(C.cw + NCW * r);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const uint32_t ch = uint32_t(C.lane + 64 * c);
+      const uint32_t h = C.ring4(segh + (row * uint32_t(CH) + ch) * 4u);
+      w[r][c] = lossless_chunk(C.ring8(segp + row * uint32_t(K) + ch * 8u), h);
+      if ((h >> 24) == 255u) w[r][c] = C.ring16(segr + ((h & 0xFFFFFFu) - first) * 16u);
+    }
+  }
+  if (CH % 64 != 0) {
+    const bool tail_ok = C.lane + 64 * (CPL - 1) < CH;
+#pragma unroll
+    for (int r = 0; r < MAXR; ++r)
+      if (!tail_ok) w[r][CPL - 1] = make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int r = 0; r < MAXR; ++r) {
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      acc = dot2(w[r][c].x, x[c][0].x, acc);
+      acc = dot2(w[r][c].y, x[c][0].y, acc);
+      acc = dot2(w[r][c].z, x[c][0].z, acc);
+      acc = dot2(w[r][c].w, x[c][0].w, acc);
     }
     out[r] = acc;
   }
@@ -1330,11 +1427,16 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
     // ---------------- P4: RMSNorm(h1) + gate/up + SwiGLU ----------------
     C.refresh();
     {
+      const GUE& ge = sm.gue[l];
       const uint32_t segn = C.next_seg(seg_bytes(P, S_NORM2, 0, p.cs_fp32));
-      const uint32_t segg = C.next_seg(seg_bytes(P, S_GATE, 0, p.cs_fp32));
-      const uint32_t segg_s = C.next_seg(seg_bytes(P, S_GATE_S, 0, p.cs_fp32));
-      const uint32_t segu = C.next_seg(seg_bytes(P, S_UP, 0, p.cs_fp32));
-      const uint32_t segu_s = C.next_seg(seg_bytes(P, S_UP_S, 0, p.cs_fp32));
+      const uint32_t segg = C.next_seg(seg_bytes(P, S_GATE, 0, p.cs_fp32, &ge));
+      const uint32_t segg_s = C.next_seg(seg_bytes(P, S_GATE_S, 0, p.cs_fp32, &ge));
+      const uint32_t segg_h = C.next_seg(seg_bytes(P, S_GATE_H, 0, p.cs_fp32, &ge));
+      const uint32_t segg_r = C.next_seg(seg_bytes(P, S_GATE_R, 0, p.cs_fp32, &ge));
+      const uint32_t segu = C.next_seg(seg_bytes(P, S_UP, 0, p.cs_fp32, &ge));
+      const uint32_t segu_s = C.next_seg(seg_bytes(P, S_UP_S, 0, p.cs_fp32, &ge));
+      const uint32_t segu_h = C.next_seg(seg_bytes(P, S_UP_H, 0, p.cs_fp32, &ge));
+      const uint32_t segu_r = C.next_seg(seg_bytes(P, S_UP_R, 0, p.cs_fp32, &ge));
       const int na = P.a1 - P.a0;
       C.wait_filled(C.pos);
       XChunks<G::H, EW> nw;
@@ -1346,8 +1448,19 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       XChunks<G::H, EW> x;
       load_x<G::H, EW, true>(x, sm.xs, nw, rs, C.lane);
       float og[R::ACT], ou[R::ACT];
-      gemv<G, G::H, R::ACT>(C, segg, segg_s, na, x, og);
-      gemv<G, G::H, R::ACT>(C, segu, segu_s, na, x, ou);
+      if constexpr (G::WF == 0) {
+        if (ge.on) {
+          dots_ring_lossless<G, G::H, R::ACT>(C, segg, segg_h, segg_r, ge.first[0], x, og);
+          dots_ring_lossless<G, G::H, R::ACT>(C, segu, segu_h, segu_r, ge.first[1], x, ou);
+        } else {
+          gemv<G, G::H, R::ACT>(C, segg, segg_s, na, x, og);
+          gemv<G, G::H, R::ACT>(C, segu, segu_s, na, x, ou);
+        }
+      } else {
+        (void)segg_h; (void)segg_r; (void)segu_h; (void)segu_r;
+        gemv<G, G::H, R::ACT>(C, segg, segg_s, na, x, og);
+        gemv<G, G::H, R::ACT>(C, segu, segu_s, na, x, ou);
+      }
       C.release(C.pos);
       const int row = C.cw + NCW * C.lane;
       if (C.lane < R::ACT && row < na) {
@@ -1503,6 +1616,24 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel(Params p) {
     }
     sm.lw[i] = w;
     sm.kvp[i] = p.kv[i];
+    // lossless gate/up: this workgroup's row range of each matrix and its escapes
+    GUE e{};
+    if (G::WF == 0 && p.encoded_gu != nullptr) {
+      const EncodedGULayer d = p.encoded_gu[i];
+      if (*d.enabled != 0u) {
+        const int a0 = split_lo(G::I, NWG, blockIdx.x), a1 = split_lo(G::I, NWG, blockIdx.x + 1);
+        e.plane = d.plane;
+        e.hdr = d.headers;
+        e.raw = d.raw;
+        e.on = 1u;
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          e.first[m] = d.row_offsets[m * G::I + a0];
+          e.cnt[m] = d.row_offsets[m * G::I + a1] - e.first[m];
+        }
+      }
+    }
+    sm.gue[i] = e;
   }
   __syncthreads();
   Plan<G> P;
@@ -2667,8 +2798,10 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
                        long long v_off, long long block_stride, long long token_stride,
                        long long head_stride, int block_size, const void* cos_sin, int cs_fp32,
                        void* out_hidden, void* layer_outputs, void* out_ids, void* out_logits,
-                       void* scratch, size_t scratch_bytes, int max_seq_len) {
+                       void* scratch, size_t scratch_bytes, int max_seq_len, const void* encoded_gu = nullptr) {
   if (B < 1 || B > (G::WF ? 1 : BMAX)) return PK_ERR_BATCH;  // MXFP8 weights: batch 1 only
+  // the lossless gate/up codec has the 360M gate_up shape [5120, 960]
+  if (encoded_gu && (G::WF || G::H != 960 || G::I != 2560)) return PK_ERR_MODEL;
   if (n_layers < 1 || n_layers > G::L) return PK_ERR_MODEL;
   if (max_seq_len < 1 || max_seq_len > kMaxSeq) return PK_ERR_MAX_SEQ;
   if (!input_ids || !embed || !final_norm || !positions || !seq_lens || !block_table ||
@@ -2681,6 +2814,7 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
     return PK_ERR_ALIGN;
   auto mis = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) != 0; };
   if (mis(embed) || mis(final_norm) || mis(layers) || mis(kv) || mis(out_hidden) || mis(scratch) ||
+      (encoded_gu && mis(encoded_gu)) ||
       (layer_outputs && mis(layer_outputs)) || (out_logits && mis(out_logits)))
     return PK_ERR_ALIGN;
   Params p{};
@@ -2712,6 +2846,7 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
   p.lm_head = (out_ids || out_logits) ? 1 : 0;
   p.max_seq = max_seq_len;
   p.trace = g_trace;
+  p.encoded_gu = reinterpret_cast<const EncodedGULayer*>(encoded_gu);  // read by the batch-1 kernel
   static_assert((WSB<G>::TOTAL * 4) % 16 == 0, "workspace is zero-filled in 16-byte units");
   const int st = ensure_workspace(scratch, WSB<G>::TOTAL * 4, reinterpret_cast<hipStream_t>(stream));
   if (st != PK_OK) return st;
@@ -2805,6 +2940,21 @@ extern "C" int pk_decode(void* stream, int model, int B, int n_layers, const voi
   return PK_ERR_MODEL;
 }
 
+extern "C" int pk_decode_lossless(void* stream, int model, int B, int n_layers, const void* input_ids,
+                                  int ids_i64, const void* embed, const void* final_norm, const void* positions,
+                                  const void* seq_lens, const void* block_table, int bt_stride,
+                                  const void* slot_mapping, const void* layers, void* const* kv, long long k_off,
+                                  long long v_off, long long block_stride, long long token_stride,
+                                  long long head_stride, int block_size, const void* cos_sin, int cs_fp32,
+                                  void* out_hidden, void* layer_outputs, void* out_ids, void* out_logits,
+                                  void* scratch, size_t scratch_bytes, int max_seq_len, const void* encoded_gu_table) {
+  if (model != PK_MODEL_SMOLLM2_360M) return PK_ERR_MODEL;
+  return pk::decode_impl<pk::G360>(stream, B, n_layers, input_ids, ids_i64, embed, final_norm, positions, seq_lens,
+                                   block_table, bt_stride, slot_mapping, layers, kv, k_off, v_off, block_stride,
+                                   token_stride, head_stride, block_size, cos_sin, cs_fp32, out_hidden, layer_outputs,
+                                   out_ids, out_logits, scratch, scratch_bytes, max_seq_len, encoded_gu_table);
+}
+
 extern "C" int pk_decode_mxfp8(void* stream, int model, int B, int n_layers, const void* input_ids, int ids_i64,
                                const void* embed, const void* final_norm, const void* positions,
                                const void* seq_lens, const void* block_table, int bt_stride,
@@ -2884,6 +3034,23 @@ extern "C" int decode360(void* stream, int B, const void* input_ids, const void*
                    seq_lens, block_table, bt_stride, slot_mapping, layers, kv, k_off, v_off, block_stride,
                    token_stride, head_stride, block_size, cos_sin, cs_fp32, out_hidden, layer_outputs, nullptr,
                    nullptr, scratch, scratch_bytes, max_seq_len);
+}
+
+extern "C" int decode360_lossless(void* stream, int B, const void* input_ids, const void* embed,
+                                  const void* final_norm, const void* positions, const void* seq_lens,
+                                  const void* block_table, int bt_stride, const void* slot_mapping, const void* layers,
+                                  void* const* kv, long long k_off, long long v_off, long long block_stride,
+                                  long long token_stride, long long head_stride, int block_size, const void* cos_sin,
+                                  int cs_fp32, void* out_hidden, void* layer_outputs, void* scratch,
+                                  size_t scratch_bytes, void* debug, size_t debug_bytes, int max_seq_len,
+                                  int debug_layer_index, const void* encoded_gu_table) {
+  (void)debug_bytes;
+  if (debug_layer_index < -1 || debug_layer_index >= pk::G360::L) return PK_ERR_BLOCK;
+  if (debug) return PK_ERR_DEBUG;
+  return pk_decode_lossless(stream, PK_MODEL_SMOLLM2_360M, B, pk::G360::L, input_ids, 0, embed, final_norm,
+                            positions, seq_lens, block_table, bt_stride, slot_mapping, layers, kv, k_off, v_off,
+                            block_stride, token_stride, head_stride, block_size, cos_sin, cs_fp32, out_hidden,
+                            layer_outputs, nullptr, nullptr, scratch, scratch_bytes, max_seq_len, encoded_gu_table);
 }
 
 extern "C" size_t mk_workspace_bytes(int B, int max_seq_len) {

@@ -4,7 +4,8 @@ Drop-in for prime_kernels.decode_megakernel_360m (reference __init__.py:142-234)
 `decode_step(**kw)` contract.  The returned tensor is a view into a shared per-device output
 buffer and is overwritten by the next call on that device; consume or copy it before then.
 Extensions: `return_token_ids=True` (greedy ids from the fused tied LM head), `logits_out=`,
-`num_layers=`.  Batch 1; KV block size 16; contexts up to 12288 tokens.
+`num_layers=`.  Batch 1..16 (ragged contexts; B >= 2 runs the batched MFMA kernel); KV block
+size 16; contexts up to 12288 tokens.
 """
 
 from prime_kernels_amd import _ops  # registers torch.ops.prime_decode.*

@@ -12,11 +12,12 @@ import prime_kernels_amd as pk
 from prime_kernels_amd import _native, _spec
 
 ROOT = Path(__file__).resolve().parents[1]
-HEADER = ROOT / "include" / "prime_decode.h"
+HEADERS = (ROOT / "include" / "prime_decode.h", ROOT / "include" / "prime_lossless.h")
 
 
 def test_registry_surface():
-    assert pk.KERNELS == ("decode_megakernel_360m", "decode_megakernel", "decode_megakernel_360m_mxfp8")
+    assert pk.KERNELS == ("decode_megakernel_360m", "decode_megakernel", "decode_megakernel_360m_mxfp8",
+                          "decode_megakernel_360m_lossless", "lossless_bf16")
     s = pk.spec("decode_megakernel_360m")
     assert s.module == "prime_kernels_amd.decode_megakernel_360m"
     assert [str(a) for a in s.archs] == ["gfx950"] and s.ops == "prime_decode"
@@ -38,15 +39,18 @@ def test_arch_parse():
 
 
 def _header_functions():
-    text = HEADER.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b([a-z_0-9]+)\s*\(", text)) - {"defined"})
+    names = set()
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b([a-z_0-9]+)\s*\(", text))
+    return sorted(names - {"defined"})
 
 
 def test_library_exports_every_header_symbol():
     lib = _native.library()
     names = _header_functions()
     assert "decode360" in names and "mk_decode" in names and "pk_decode" in names
+    assert "lossless_encode_layer" in names and "decode360_lossless" in names
     for name in names:
         assert hasattr(lib, name), f"libprime_decode.so does not export {name}"
     assert set(names) <= set(_native.SIGNATURES), "ctypes signatures missing for a header function"
@@ -162,3 +166,46 @@ def test_torch_ops_schema_and_fake_kernels():
         assert i2.shape == (1,)
         with pytest.raises(ValueError):
             torch.ops.prime_decode.decode_step(360, *args[1:7], lw[:5], *args[8:])
+
+
+def test_lossless_abi_validation_without_gpu():
+    """Argument checks of the codec and the lossless decode entry return before any GPU call."""
+    lib = _native.library()
+    assert lib.lossless_scan_workspace_bytes() == 5120 * 4
+    ws = lib.lossless_scan_workspace_bytes()
+    def enc(**over):
+        a = dict(input=16, plane=16, headers=16, raw=16, row_offsets=16, flags=16, prefix=16, scan=16,
+                 scan_bytes=ws, enabled=16, capacity=8, stream=None)
+        a.update(over)
+        return lib.lossless_encode_layer(*a.values())
+    assert enc(input=None) == 9103
+    assert enc(raw=None) == 9103                   # capacity > 0 needs an escape table
+    assert enc(scan_bytes=ws - 4) == 9108
+    assert enc(plane=24) == 9107
+    assert lib.lossless_decode_layer(16, 16, None, 16, None) == 9103
+    assert lib.lossless_decode_layer(16, 16, 16, 8, None) == 9107
+    assert lib.lossless_write_descriptor(None, 0, 16, 16, 16, 16, 16, None) == 9103
+    a = _args()
+    assert lib.pk_decode_lossless(*_args(model=135), 16) == 9110      # the codec's shape is 360M's
+    assert lib.pk_decode_lossless(*a, 24) == 9107                      # misaligned table
+    assert lib.pk_decode_lossless(*_args(B=17), 16) == 9101
+    d = dict(stream=None, B=1, input_ids=16, embed=16, final_norm=16, positions=16, seq_lens=16, block_table=16,
+             bt_stride=64, slot_mapping=16, layers=16, kv=16, k_off=0, v_off=64, block_stride=10240,
+             token_stride=128, head_stride=2048, block_size=16, cos_sin=16, cs_fp32=0, out_hidden=16,
+             layer_outputs=None, scratch=16, scratch_bytes=1 << 40, debug=16, debug_bytes=1 << 20,
+             max_seq_len=1024, debug_layer_index=-1, table=16)
+    assert lib.decode360_lossless(*d.values()) == 9111                # per-stage capture not built
+    d.update(debug=None, debug_layer_index=32)
+    assert lib.decode360_lossless(*d.values()) == 9109
+
+
+def test_lossless_modules_on_cpu():
+    from prime_kernels_amd import decode_megakernel_360m_lossless as L
+    from prime_kernels_amd import lossless_bf16 as LB
+
+    assert (LB.LAYERS, LB.ROWS, LB.COLS, LB.CHUNKS) == (32, 5120, 960, 614400)
+    assert L.cache_statistics("cpu") is None
+    with pytest.raises(ValueError):
+        L.prepare_weights([()] * 3)
+    with pytest.raises(ValueError):
+        LB.EncodedGUCache([torch.zeros(5120, 960, dtype=torch.bfloat16)] * 2)
