@@ -85,11 +85,16 @@ def main() -> None:
                     help="sequences per step; above 1 each sequence's context is drawn uniformly from "
                          "128..4096 (BASELINE config 4 at 16; bf16 weights only)")
     ap.add_argument("--seed", type=int, default=4, help="seed of the ragged contexts and token ids")
+    ap.add_argument("--lossless", action="store_true",
+                    help="stream the gate/up weights through the lossless codec (batch 1, bf16)")
     args = ap.parse_args()
     context = args.context if args.context is not None else (CONTEXT if args.weights == "bf16" else 8192)
     B = args.batch
     if not 1 <= B <= 16 or (B > 1 and args.weights != "bf16"):
         print("--batch takes 1..16 sequences, with bf16 weights above 1", file=sys.stderr)
+        sys.exit(2)
+    if args.lossless and (B != 1 or args.weights != "bf16"):
+        print("--lossless runs batch 1 with bf16 weights", file=sys.stderr)
         sys.exit(2)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: every box in this setup has one MI355X and the decode "
@@ -116,6 +121,16 @@ def main() -> None:
     embed, final_norm, layers = WL.random_weights(pk.load("decode_megakernel_360m").MODEL, 1234, dev)
     if args.weights == "mxfp8":
         layers = mod.quantize_layers(layers)
+    cache = None
+    gu_bytes_saved = 0
+    if args.lossless:
+        from prime_kernels_amd.lossless_bf16 import EncodedGUCache, COLS, ROWS
+
+        cache = EncodedGUCache([layer[4] for layer in layers])
+        st = cache.statistics()
+        # encoded gate/up bytes a step streams: plane + headers + escaped chunks, per layer
+        enc = sum(ROWS * COLS + ROWS * (COLS // 8) * 4 + 16 * n for n in st["escape_chunks"])
+        gu_bytes_saved = len(layers) * ROWS * COLS * 2 - enc
     cap = max(contexts) + max(K, W) + 16
     kv = WL.PagedKV(model, B, cap, device=dev, seed=5, fill="randn")
     cos_sin = WL.rope_table(cap, device=dev)
@@ -123,7 +138,7 @@ def main() -> None:
 
     stream = torch.cuda.current_stream(dev)
     common = dict(embed=embed, layers=layers, final_norm=final_norm, kv_caches=kv.caches, block_table=kv.block_table,
-                  cos_sin_cache=cos_sin, first_id=first_ids, start_pos=contexts, batch=B)
+                  cos_sin_cache=cos_sin, first_id=first_ids, start_pos=contexts, batch=B, encoded_gu=cache)
     warm = StepLauncher(model, steps=max(W, 1), **common)
     for k in range(W):
         warm.launch(k, stream.cuda_stream)
@@ -145,19 +160,22 @@ def main() -> None:
     if not bool(((ids >= 0) & (ids < 49152)).all()):
         raise RuntimeError("greedy ids out of range")
 
-    total_bytes = sum(step_bytes([c + 1 + k for c in contexts], weights=args.weights) for k in range(K))
+    total_bytes = sum(step_bytes([c + 1 + k for c in contexts], weights=args.weights) - gu_bytes_saved
+                      for k in range(K))
     ms_per_step = ms / K
     achieved = total_bytes / (ms * 1e-3) / 1e9
     traffic = None
     tname = (f"decode360_b{B}_ragged" if B > 1 else
-             f"decode360_{'' if args.weights == 'bf16' else 'mxfp8_'}ctx{context}")
+             f"decode360_{'' if args.weights == 'bf16' else 'mxfp8_'}{'lossless_' if args.lossless else ''}"
+             f"ctx{context}")
     tfile = ROOT / "profiles" / f"{tname}_traffic.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
-    wname = "bf16" if args.weights == "bf16" else "MXFP8-weight"
+    wname = ("bf16 lossless-GU" if args.lossless else "bf16") if args.weights == "bf16" else "MXFP8-weight"
     ctx_name = f"ctx={context}" if B == 1 else "ragged ctx 128..4096"
     workload = (f"smollm2-360m greedy decode, batch 1, {context}-token context, K steps at context "
                 f"{context + 1}..{context}+K" + (", MXFP8 projection weights" if args.weights == "mxfp8" else "")
+                + (", gate/up streamed through the lossless codec" if args.lossless else "")
                 if B == 1 else
                 f"smollm2-360m greedy decode, batch {B}, contexts drawn uniformly from 128..4096 "
                 f"(seed {args.seed}, mean {sum(contexts) / B:.0f}), K steps per sequence")
@@ -178,6 +196,7 @@ def main() -> None:
                 ", KV context N(0,1) bf16, greedy ids fed back on device)",
         "config": {"workload": workload,
                    "batch": B, "context": context if B == 1 else contexts, "layers": 32, "weights": args.weights,
+                   "gate_up": "lossless codec" if args.lossless else "dense",
                    "lm_head": "tied, fused argmax", "launch": "one cooperative kernel per step, 256 workgroups"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,

@@ -278,7 +278,7 @@ class StepLauncher:
     """
 
     def __init__(self, model: Model, *, embed, layers, final_norm, kv_caches, block_table, cos_sin_cache,
-                 first_id, start_pos, steps: int, logits: bool = False, batch: int = 1):
+                 first_id, start_pos, steps: int, logits: bool = False, batch: int = 1, encoded_gu=None):
         dev = embed.device
         B = batch
         if not 1 <= B <= model.max_batch:
@@ -309,11 +309,17 @@ class StepLauncher:
         self.ids[0] = firsts.to(dev)
         self.logits = torch.empty((B, VOCAB), dtype=torch.bfloat16, device=dev) if logits else None
         self.steps = steps
+        self.encoded_gu = encoded_gu  # lossless_bf16.EncodedGUCache of these gate_up matrices, or None
 
     def launch(self, k: int, stream: int) -> None:
         m, rt, B = self.model, self.rt, self.batch
         embed, layers, final_norm, kv_caches, block_table, cos_sin = self.keep
-        launch = self.lib.pk_decode_mxfp8 if m.weight_format == "mxfp8" else self.lib.pk_decode
+        extra = ()
+        if self.encoded_gu is not None:
+            launch = self.lib.pk_decode_lossless
+            extra = (self.encoded_gu.table.data_ptr(),)
+        else:
+            launch = self.lib.pk_decode_mxfp8 if m.weight_format == "mxfp8" else self.lib.pk_decode
         rc = launch(
             stream, m.model_id, B, len(layers), self.ids.data_ptr() + 8 * B * k, 1, embed.data_ptr(),
             final_norm.data_ptr(), self.positions.data_ptr() + 8 * B * k, self.seq_lens.data_ptr() + 4 * B * k,
@@ -321,6 +327,6 @@ class StepLauncher:
             self.layers_t.data_ptr(), self.kv_t.data_ptr(), *self.kv_strides, BLOCK_SIZE,
             cos_sin.data_ptr(), int(cos_sin.dtype == torch.float32), rt.out.data_ptr(), None,
             self.ids.data_ptr() + 8 * B * (k + 1), self.logits.data_ptr() if self.logits is not None else None,
-            rt.scratch_ptr, rt.scratch_bytes, self.max_seq)
+            rt.scratch_ptr, rt.scratch_bytes, self.max_seq, *extra)
         if rc != 0:
             raise RuntimeError(f"{m.name} failed: {_native.status_string(rc)}")

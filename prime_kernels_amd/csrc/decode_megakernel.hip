@@ -914,62 +914,100 @@ __device__ __forceinline__ void dots_ring_q(const Consumer<G>& C, uint32_t segq,
 
 // The 8 bf16 words (4 packed pairs) of a lossless chunk: plane bytes p (sign | mantissa) and the
 // header's base exponent and 3-bit deltas give word_i = (p_i & 0x80) << 8 | (base + d_i) << 7 |
-// (p_i & 0x7f) (prime_kernels/lossless_bf16/csrc/lossless_bf16.cu:94-101).  A pair is built in one
-// register: v_perm places bytes 2j, 2j+1 in bits 0-7 / 16-23, both exponents are added at once.
+// (p_i & 0x7f) (prime_kernels/lossless_bf16/csrc/lossless_bf16.cu:94-101).  Per pair of words,
+// in one register: v_perm copies plane bytes 2j, 2j+1 into both bytes of the low / high half, so
+// one mask keeps each sign at bit 15 / 31 and each mantissa at bits 0-6 / 16-22; the pair's 6 delta
+// bits d times 0x100080 is d << 7 | d << 20, whose bits 7-9 and 23-25 are the two deltas in
+// exponent position; the base exponent is added to both halves at once.  No field overflows into
+// the next: every exponent of a plain chunk is at most 254 + 7 < 256.
 __device__ __forceinline__ uint4 lossless_chunk(uint2 p, uint32_t h) {
-  const uint32_t base2 = (h >> 24) * 0x10001u;
+  const uint32_t base7 = (h >> 24) * 0x00800080u;
   uint32_t out[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const uint32_t t = __builtin_amdgcn_perm(0u, j < 2 ? p.x : p.y, (j & 1) ? 0x0c030c02u : 0x0c010c00u);
-    const uint32_t d = (h >> (6 * j)) & 63u;
-    const uint32_t ex = base2 + (d & 7u) + ((d >> 3) << 16);
-    out[j] = ((t & 0x00800080u) << 8) | (t & 0x007F007Fu) | (ex << 7);
+    const uint32_t t = __builtin_amdgcn_perm(0u, j < 2 ? p.x : p.y, (j & 1) ? 0x03030202u : 0x01010000u);
+    const uint32_t d = __builtin_amdgcn_ubfe(h, 6 * j, 6);
+    const uint32_t e7 = (__umul24(d, 0x100080u) & 0x03800380u) + base7;
+    out[j] = (t & 0x807F807Fu) | e7;
   }
   return make_uint4(out[0], out[1], out[2], out[3]);
 }
 
-// dots_ring over lossless-encoded rows: plane rows (K bytes each) in `segp`, header rows (K/8 words)
-// in `segh`, the escaped chunks of the workgroup's rows (ordinals first, first+1, ...) in `segr`.
-// Each lane rebuilds exactly the 16-byte chunks dots_ring would read from a dense segment and
-// accumulates them in the same order, so the sums are bit-identical to the dense matrix's.
-template <class G, int K, int MAXR>
-__device__ __forceinline__ void dots_ring_lossless(const Consumer<G>& C, uint32_t segp, uint32_t segh,
-                                                   uint32_t segr, uint32_t first, const XChunks<K, 8>& x,
-                                                   float (&out)[MAXR]) {
+// The lossless-encoded gate and up rows of P4 as the 16-byte chunks dots_ring would read from a
+// dense segment (bit-identical words): for matrix m, plane rows (K bytes each) in `segp[m]`, header
+// rows (K/8 words) in `segh[m]`, the escaped chunks of the workgroup's rows (ordinals first[m],
+// first[m]+1, ...) in `segr[m]`.  All plane and header reads of both matrices issue back to back,
+// then all escape reads (branch-free: a plain chunk reads escape 0 and discards it), so the phase
+// pays two LDS round trips rather than one per chunk.
+template <class G, int K, int MAXR, int NM = 2>
+__device__ __forceinline__ void decode_lossless2(const Consumer<G>& C, const uint32_t (&segp)[NM],
+                                                 const uint32_t (&segh)[NM], const uint32_t (&segr)[NM],
+                                                 const uint32_t (&first)[NM],
+                                                 uint4 (&w)[NM][MAXR][Chunks<K>::CPL]) {
   constexpr int CPL = Chunks<K>::CPL, CH = Chunks<K>::CH;
-  uint4 w[MAXR][CPL];
+  uint2 pl[NM][MAXR][CPL];
+  uint32_t hd[NM][MAXR][CPL];
 #pragma unroll
-  for (int r = 0; r < MAXR; ++r) {
-    const uint32_t row = uint32_t(C.cw + NCW * r);
+  for (int m = 0; m < NM; ++m)
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      const uint32_t ch = uint32_t(C.lane + 64 * c);
-      const uint32_t h = C.ring4(segh + (row * uint32_t(CH) + ch) * 4u);
-      w[r][c] = lossless_chunk(C.ring8(segp + row * uint32_t(K) + ch * 8u), h);
-      if ((h >> 24) == 255u) w[r][c] = C.ring16(segr + ((h & 0xFFFFFFu) - first) * 16u);
+    for (int r = 0; r < MAXR; ++r) {
+      const uint32_t row = uint32_t(C.cw + NCW * r);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const uint32_t ch = uint32_t(C.lane + 64 * c);
+        hd[m][r][c] = C.ring4(segh[m] + (row * uint32_t(CH) + ch) * 4u);
+        pl[m][r][c] = C.ring8(segp[m] + row * uint32_t(K) + ch * 8u);
+      }
     }
-  }
-  if (CH % 64 != 0) {
-    const bool tail_ok = C.lane + 64 * (CPL - 1) < CH;
+  // Every chunk is rebuilt (an escaped chunk's result is discarded) and the results are made opaque
+  // before the escapes are merged: otherwise the compiler turns the merge into a branch per chunk
+  // around the rebuild, with an LDS wait and the plane read inside it, serialising the chunks.
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
 #pragma unroll
     for (int r = 0; r < MAXR; ++r)
-      if (!tail_ok) w[r][CPL - 1] = make_uint4(0, 0, 0, 0);
-  }
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        w[m][r][c] = lossless_chunk(pl[m][r][c], hd[m][r][c]);
+        asm volatile("" : "+v"(w[m][r][c].x), "+v"(w[m][r][c].y), "+v"(w[m][r][c].z), "+v"(w[m][r][c].w));
+      }
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int r = 0; r < MAXR; ++r)
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const uint32_t h = hd[m][r][c];
+        const bool esc = (h >> 24) == 255u;
+        const uint4 e = C.ring16(segr[m] + (esc ? (h & 0xFFFFFFu) - first[m] : 0u) * 16u);
+        w[m][r][c].x = esc ? e.x : w[m][r][c].x;
+        w[m][r][c].y = esc ? e.y : w[m][r][c].y;
+        w[m][r][c].z = esc ? e.z : w[m][r][c].z;
+        w[m][r][c].w = esc ? e.w : w[m][r][c].w;
+      }
+  if (CH % 64 != 0 && C.lane + 64 * (CPL - 1) >= CH)
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int r = 0; r < MAXR; ++r) w[m][r][CPL - 1] = make_uint4(0, 0, 0, 0);
+}
+
+// out[r] = w[r] . x for weight chunks already in registers (dots_ring's accumulation order).
+template <int K, int MAXR>
+__device__ __forceinline__ void dots_regs(const uint4 (&w)[MAXR][Chunks<K>::CPL], const XChunks<K, 8>& x,
+                                          float (&out)[MAXR]) {
 #pragma unroll
   for (int r = 0; r < MAXR; ++r) {
     float acc = 0.f;
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
+    for (int c = 0; c < Chunks<K>::CPL; ++c) {
       acc = dot2(w[r][c].x, x[c][0].x, acc);
       acc = dot2(w[r][c].y, x[c][0].y, acc);
       acc = dot2(w[r][c].z, x[c][0].z, acc);
       acc = dot2(w[r][c].w, x[c][0].w, acc);
     }
-    out[r] = acc;
+    out[r] = wave_sum(acc);
   }
-#pragma unroll
-  for (int r = 0; r < MAXR; ++r) out[r] = wave_sum(out[r]);
 }
 
 // Projection rows of a phase in the workgroup's weight format.
@@ -1441,6 +1479,15 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       C.wait_filled(C.pos);
       XChunks<G::H, EW> nw;
       load_normw<G, G::H, EW>(C, nw, segn);
+      // lossless layer: the gate chunks are rebuilt while the h1 exchange is in flight (the up
+      // chunks after it: both sets live across the poll would exceed the register budget)
+      uint4 wg[1][R::ACT][Chunks<G::H>::CPL];
+      if constexpr (G::WF == 0) {
+        if (ge.on) {
+          const uint32_t sp[1] = {segg}, sh[1] = {segg_h}, sr[1] = {segg_r}, fo[1] = {ge.first[0]};
+          decode_lossless2<G, G::H, R::ACT, 1>(C, sp, sh, sr, fo, wg);
+        }
+      }
       tr(l, 9);
       const float ss = C.template poll_split<GH>(X_H1, l, b, G::H, sm.xs, sm.h1keep);
       const float rs = rms_scale(C.block_total(ss), G::H);
@@ -1448,16 +1495,20 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       XChunks<G::H, EW> x;
       load_x<G::H, EW, true>(x, sm.xs, nw, rs, C.lane);
       float og[R::ACT], ou[R::ACT];
+      bool done = false;
       if constexpr (G::WF == 0) {
         if (ge.on) {
-          dots_ring_lossless<G, G::H, R::ACT>(C, segg, segg_h, segg_r, ge.first[0], x, og);
-          dots_ring_lossless<G, G::H, R::ACT>(C, segu, segu_h, segu_r, ge.first[1], x, ou);
-        } else {
-          gemv<G, G::H, R::ACT>(C, segg, segg_s, na, x, og);
-          gemv<G, G::H, R::ACT>(C, segu, segu_s, na, x, ou);
+          const uint32_t sp[1] = {segu}, sh[1] = {segu_h}, sr[1] = {segu_r}, fo[1] = {ge.first[1]};
+          uint4 wu[1][R::ACT][Chunks<G::H>::CPL];
+          decode_lossless2<G, G::H, R::ACT, 1>(C, sp, sh, sr, fo, wu);
+          dots_regs<G::H, R::ACT>(wg[0], x, og);
+          dots_regs<G::H, R::ACT>(wu[0], x, ou);
+          done = true;
         }
       } else {
         (void)segg_h; (void)segg_r; (void)segu_h; (void)segu_r;
+      }
+      if (!done) {
         gemv<G, G::H, R::ACT>(C, segg, segg_s, na, x, og);
         gemv<G, G::H, R::ACT>(C, segu, segu_s, na, x, ou);
       }
