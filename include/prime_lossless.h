@@ -52,7 +52,8 @@ int lossless_encode_layer(const void* input, void* plane, void* headers, void* r
                           void* flags, void* prefix, void* scan_workspace, size_t scan_workspace_bytes,
                           void* enabled, uint32_t capacity, void* stream);
 
-/* Decode one encoded matrix back to bf16 [5120, 960] (bit-exact). */
+/* Decode one encoded matrix back to bf16 [5120, 960] (bit-exact).  Only for a matrix whose enabled
+ * flag is 1: a disabled one has escape ordinals past its table. */
 int lossless_decode_layer(const void* plane, const void* headers, const void* raw, void* output, void* stream);
 
 /* Write entry `index` of a device table of EncodedGULayer (stream-ordered). */
