@@ -1716,6 +1716,9 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel(Params p) {
 constexpr int BMAX = 16;                  // sequences per launch (the MFMA N dimension)
 constexpr uint32_t RING_B = 64u * 1024u;  // ring bytes (the staged activations take the rest of LDS)
 constexpr int TCB = 256;                  // max cached tokens per attention item
+#ifndef PK_TC_CAP
+#define PK_TC_CAP TCB                     // preferred largest chunk (sequences past 64 * cap use more)
+#endif
 constexpr int IPW = 16;                   // max attention items per workgroup
 constexpr int MAX_ITEMS = NWG * IPW;
 
@@ -1739,15 +1742,24 @@ struct WSB {
   __device__ static size_t data(int kind, int l) { return DATA0 + (size_t(kind) * G::L + l) * DATA_WORDS; }
 };
 
+// An attention item: sequence b, KV head g, chunk c of C (the last one is the leader, which also owns
+// the new token), index of chunk 0 of (b, g) among all items, cached tokens [t0, t1).
+struct ItemB {
+  int b, g, c, C, base, t0, t1, pad;
+};
+
 template <class G>
 struct SmemB {
   static constexpr int XS = G::I > G::H ? G::I : G::H;
   struct Attn {
-    float qkvw[NCW][5 * 64];          // per-wave attention inputs of the current item
+    float qb[IPW][5 * 64];            // per item: 3 q heads, then (leader items) the new k and v
     uint16_t sc[IPW][3][TCB + 2];     // bf16 scores of every item of this workgroup
-    uint16_t pb[3][TCB + 4];          // bf16 probabilities of the current item
+    uint16_t pb[3][TCB + 4];          // bf16 probabilities (each wave its own token range)
     float own[IPW][3 * 64];           // leader items: this chunk's partial sums of p.v
+    float wml[IPW][NCW][2][3];        // per item and wave: softmax max / sum per head
     float cst[IPW][2][3];             // chunk softmax max / sum per item and head
+    float gml[IPW][2][3];             // global (all chunks) max / sum per item and head
+    float wo[2][NCW][3][64];          // per-wave P.V partials, double-buffered over items
     float csr[BMAX][64];              // rotary cos | sin of each sequence's position
   };
   uint8_t ring[RING_B];
@@ -1760,11 +1772,10 @@ struct SmemB {
   float hk[BMAX][8];                  // residual h1 of this workgroup's down rows
   float rsb[BMAX];                    // per-sequence RMS scale
   float red[NCW];
-  float wml[NCW][2][3];
-  float wo[NCW][3][64];
   LayerW lw[G::L];
   const void* kvp[G::L];
   int32_t blk[IPW][TCB / 16 + 2];     // block ids of each item's chunk
+  ItemB it[IPW];                      // this workgroup's attention items
   int32_t sS[BMAX], sPos[BMAX], sId[BMAX];
   long long sSlot[BMAX];
   float lm_val[NCW][BMAX];
@@ -1773,11 +1784,11 @@ struct SmemB {
   uint32_t consumed[NCW];
   uint32_t cbar;
 };
-static_assert(sizeof(typename SmemB<G135>::Attn) <= sizeof(uint16_t) * BMAX * SmemB<G135>::XS, "union sizing");
 // Attention items at the largest batch and context: each (sequence, KV head) has at most
 // ceil((kMaxSeq - 1) / TCB) chunks, and every workgroup holds at most IPW items.
 static_assert((G360::KVH > G135::KVH ? G360::KVH : G135::KVH) * BMAX * ((kMaxSeq - 1 + TCB - 1) / TCB) <= MAX_ITEMS,
               "item arrays hold every chunk");
+static_assert((kMaxSeq - 1 + TCB - 1) / TCB <= 64, "a (sequence, head) never has more than 64 chunks");
 
 template <class G>
 struct PlanB {
@@ -1801,12 +1812,18 @@ struct PlanB {
     if (p.lm_head) { v0 = split_lo(G::V, NWG, wg); v1 = split_lo(G::V, NWG, wg + 1); }
     else { v0 = v1 = 0; }
     n_lm = (v1 - v0 + LM_ROWS - 1) / LM_ROWS;
-    // chunks of about two items per workgroup, 64..TCB tokens, a multiple of 16
+    // chunks of about two items per workgroup, 64..TCB tokens, a multiple of 16, and long enough that
+    // no (sequence, head) has more than 64 chunks (one wave lane per chunk gathers their statistics)
     long long tot = 0;
-    for (int b = 0; b < B; ++b) tot += max(sS[b], 1) - 1;
+    int most = 0;
+    for (int b = 0; b < B; ++b) {
+      tot += max(sS[b], 1) - 1;
+      most = max(most, max(sS[b], 1) - 1);
+    }
     int t = int((tot * G::KVH + 2LL * NWG - 1) / (2LL * NWG));
-    t = (t + 15) / 16 * 16;
-    tc = min(max(t, 64), TCB);
+    t = min(max(t, 64), PK_TC_CAP);
+    t = max(t, (most + 63) / 64);
+    tc = min((t + 15) / 16 * 16, TCB);
     nitems = 0;
     for (int b = 0; b < B; ++b) nitems += G::KVH * chunks(sS[b]);
     ni = nitems > wg ? (nitems - wg + NWG - 1) / NWG : 0;
@@ -1845,16 +1862,12 @@ __device__ __forceinline__ uint32_t kvb_slot(int j, int part) {
 enum SegB { B_NORM1, B_QKV, B_CS, B_K, B_V, B_O, B_NORM2, B_GATE, B_UP, B_DOWN, B_FNORM, B_LM };
 
 template <class G>
-__device__ __forceinline__ uint32_t segb_bytes(const PlanB<G>& P, const int32_t* sS, int kind, int idx, int cs_fp32) {
+__device__ __forceinline__ uint32_t segb_bytes(const PlanB<G>& P, const ItemB* it, int kind, int idx, int cs_fp32) {
   switch (kind) {
     case B_NORM1: case B_NORM2: case B_FNORM: return G::H * 2;
     case B_QKV: return uint32_t(P.q1 - P.q0) * G::H * 2;
     case B_CS: return P.ni ? uint32_t(P.B) * (cs_fp32 ? 256u : 128u) : 0u;
-    case B_K: case B_V: {
-      int b, g, c, C, base, t0, t1;
-      P.item(sS, P.wg + idx * NWG, b, g, c, C, base, t0, t1);
-      return uint32_t(t1 - t0) * 128u;
-    }
+    case B_K: case B_V: return uint32_t(it[idx].t1 - it[idx].t0) * 128u;
     case B_O: return uint32_t(P.o1 - P.o0) * G::H * 2;
     case B_GATE: case B_UP: return uint32_t(P.a1 - P.a0) * G::H * 2;
     case B_DOWN: return uint32_t(P.d1 - P.d0) * G::I * 2;
@@ -1870,12 +1883,14 @@ __device__ __forceinline__ void producer_b(const Params& p, const PlanB<G>& P, S
   const int pw = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const uint32_t ring_base = uint32_t(reinterpret_cast<uintptr_t>(sm.ring));
-  if (pw == 0) {  // block ids of every item's chunk (the same for every layer)
+  if (pw == 0) {  // the item table and every item's block ids (the same for every layer)
     for (int k = 0; k < P.ni; ++k) {
-      int b, g, c, C, base, t0, t1;
-      P.item(sm.sS, P.wg + k * NWG, b, g, c, C, base, t0, t1);
-      const int nb = t1 > t0 ? (t1 - 1) / 16 - t0 / 16 + 1 : 0;
-      for (int i = lane; i < nb; i += 64) sm.blk[k][i] = p.block_table[size_t(b) * p.bt_stride + t0 / 16 + i];
+      ItemB e;
+      P.item(sm.sS, P.wg + k * NWG, e.b, e.g, e.c, e.C, e.base, e.t0, e.t1);
+      e.pad = 0;
+      if (lane == 0) sm.it[k] = e;
+      const int nb = e.t1 > e.t0 ? (e.t1 - 1) / 16 - e.t0 / 16 + 1 : 0;
+      for (int i = lane; i < nb; i += 64) sm.blk[k][i] = p.block_table[size_t(e.b) * p.bt_stride + e.t0 / 16 + i];
     }
   }
   wait_vmcnt<0>();
@@ -1893,7 +1908,7 @@ __device__ __forceinline__ void producer_b(const Params& p, const PlanB<G>& P, S
     if (lane == 0) st_lds(&sm.front[pw], first_pending_packet * PKT);
   };
   auto issue_segment = [&](int kind, int layer, int idx) {
-    const uint32_t bytes = segb_bytes(P, sm.sS, kind, idx, p.cs_fp32);
+    const uint32_t bytes = segb_bytes(P, sm.it, kind, idx, p.cs_fp32);
     const uint32_t npk = pad_pkt(bytes) / PKT;
     if (npk == 0) return;
     const uint8_t* base = nullptr;
@@ -1904,12 +1919,12 @@ __device__ __forceinline__ void producer_b(const Params& p, const PlanB<G>& P, S
     switch (kind) {
       case B_NORM1: base = u8(Lw.norm1); break;
       case B_QKV: base = u8(Lw.qkv) + size_t(P.q0) * G::H * 2; break;
-      case B_K: case B_V: {
-        int c, C, bs, t1;
-        P.item(sm.sS, P.wg + idx * NWG, ib, ig, c, C, bs, it0, t1);
+      case B_K: case B_V:
+        ib = sm.it[idx].b;
+        ig = sm.it[idx].g;
+        it0 = sm.it[idx].t0;
         cache = u8(sm.kvp[layer]);
         break;
-      }
       case B_O: base = u8(Lw.o) + size_t(P.o0) * G::H * 2; break;
       case B_NORM2: base = u8(Lw.norm2); break;
       case B_GATE: base = u8(Lw.gate_up) + size_t(P.a0) * G::H * 2; break;
@@ -2022,24 +2037,41 @@ __device__ __forceinline__ void put_bf16(const ConsumerB<G>& C, int kind, int l,
 
 // Per-sequence RMS scale of the staged rows, then the rows normalised in place with
 // LlamaRMSNorm rounding y = bf16(w * bf16(x * rs)) (modeling_llama.py:62-67); w from a ring segment.
+// Wave w sums the squares of sequences w, w + 4, ... (lane l: 8-value chunks l and l + 64); the
+// normalisation then runs over 8-value chunks of all rows, 16-byte LDS reads and writes.
 template <class G>
 __device__ __forceinline__ void norm_staged(ConsumerB<G>& C, uint32_t segw) {
   SmemB<G>& sm = C.sm;
+  constexpr int CH = G::H / 8;
   for (int b = C.cw; b < C.P.B; b += NCW) {
     float s = 0.f;
-    for (int k = C.lane; k < G::H; k += 64) {
-      const float v = bf2f(sm.xs[b * G::H + k]);
-      s += v * v;
+    for (int c = C.lane; c < CH; c += 64) {
+      const uint4 v = *reinterpret_cast<const uint4*>(sm.xs + b * G::H + c * 8);
+      const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = bf_lo(u[e]), hi = bf_hi(u[e]);
+        s += lo * lo + hi * hi;
+      }
     }
     s = wave_sum(s);
     if (C.lane == 0) sm.rsb[b] = rms_scale(s, G::H);
   }
   C.cbar();
-  const int n = C.P.B * G::H;
-  for (int i = C.ct; i < n; i += NCT) {
-    const int b = i / G::H, k = i - b * G::H;
-    const float w = bf2f(*reinterpret_cast<const uint16_t*>(sm.ring + ((segw + uint32_t(k) * 2u) & (RING_B - 1))));
-    sm.xs[i] = uint16_t(f2bf(w * rnd(bf2f(sm.xs[i]) * sm.rsb[b])));
+  for (int i = C.ct; i < C.P.B * CH; i += NCT) {
+    const int b = i / CH, c = i - b * CH;
+    uint4* px = reinterpret_cast<uint4*>(sm.xs + b * G::H + c * 8);
+    const uint4 v = *px;
+    const uint4 wv = C.ring16(segw + uint32_t(c) * 16u);
+    const float rs = sm.rsb[b];
+    const uint32_t u[4] = {v.x, v.y, v.z, v.w}, wu[4] = {wv.x, wv.y, wv.z, wv.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t t = pack2(bf_lo(u[e]) * rs, bf_hi(u[e]) * rs);
+      o[e] = pack2(bf_lo(wu[e]) * bf_lo(t), bf_hi(wu[e]) * bf_hi(t));
+    }
+    *px = make_uint4(o[0], o[1], o[2], o[3]);
   }
   C.cbar();
 }
@@ -2098,7 +2130,18 @@ __device__ __forceinline__ floatx4 mfma_tile(ConsumerB<G>& C, uint32_t seg, floa
 }
 
 // ------------------------------------------------------------------------------------------------
-// Batched attention: passes A / B / C over this workgroup's items (see the section comment).
+// Batched attention over this workgroup's items (sequence, KV head, chunk of cached tokens):
+//   Q  one block-wide poll brings every item's 3 query heads (and, for leader items, the new
+//      token's k and v) into LDS;
+//   A  per item: RoPE, the KV append (leader), bf16 scores of the chunk's tokens and the per-wave
+//      softmax statistics -- no barrier between items (every item has its own buffers); then one
+//      barrier and each wave merges the statistics of a quarter of the items and publishes the
+//      chunk (max, sum) records;
+//   G  one poll of every item's chunk records gives the global max and sum of its (sequence, head);
+//   B  per item: p = bf16(exp(s - M) / L) with the global statistics (HF's rounding), P.V over the
+//      chunk, the four waves' partials summed in wave order after one barrier; non-leader chunks
+//      publish their partial, leaders keep theirs;
+//   C  leaders add the other chunks' partials in chunk order and write attn.
 // Records and statistics are reused by every layer, so their tags carry the layer as well.
 // ------------------------------------------------------------------------------------------------
 template <class G>
@@ -2107,11 +2150,53 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
   const PlanB<G>& P = C.P;
   SmemB<G>& sm = C.sm;
   const int lane = C.lane, w = C.cw;
-  const int part = lane & 7, grp = lane >> 3;
   const uint32_t tagb = (C.tag32 << 5) | uint32_t(l);
   const uint64_t tg = uint64_t(tagb) << 32;
-  float* in = sm.at.qkvw[w];
+  auto tri = [&](int ev) { if (C.ct == 0) trace_at(p, l, ev, p.n_layers); };
+  auto trk = [&](int k, int ev) { if (C.ct == 0 && k < 4) trace_at(p, l, ev, p.n_layers); };
   C.cbar();  // P1's reads of xs (which shares storage with sm.at) are done
+  // ---- Q: every item's q (and new k / v) from the exchange words, one poll for all ----
+  {
+    constexpr int GPI = 5 * 64 / 4;                      // groups of 4 words per item
+    constexpr int MAXG = (IPW * GPI + NCT - 1) / NCT;
+    const __amdgpu_buffer_rsrc_t r = rsrc(p.ws);
+    auto word = [&](int gidx) -> int {                   // exchange word of group gidx, -1: none
+      const int k = gidx / GPI, e = (gidx - k * GPI) * 4;
+      const ItemB& it = sm.it[k];
+      if (e < 192) return int(WS<G>::xw(X_QKV, l, it.b, it.g * 192 + e));
+      if (it.c != it.C - 1) return -1;                   // only the leader needs the new token
+      if (e < 256) return int(WS<G>::xw(X_QKV, l, it.b, G::H + it.g * 64 + (e - 192)));
+      return int(WS<G>::xw(X_QKV, l, it.b, G::H + G::KVH * 64 + it.g * 64 + (e - 256)));
+    };
+    u32x4 v[MAXG];
+    int wd[MAXG];
+    uint32_t pend = 0;
+#pragma unroll
+    for (int gi = 0; gi < MAXG; ++gi) {
+      const int gidx = C.ct + gi * NCT;
+      wd[gi] = gidx < P.ni * GPI ? word(gidx) : -1;
+      if (wd[gi] >= 0) {
+        v[gi] = ld_dev128(r, uint32_t(wd[gi]) * 4u);
+        pend |= 1u << gi;
+      }
+    }
+    Spin spin(p.ws, 12);
+    while (true) {
+#pragma unroll
+      for (int gi = 0; gi < MAXG; ++gi)
+        if (((pend >> gi) & 1u) && C.ok4(v[gi])) {
+          const int gidx = C.ct + gi * NCT, k = gidx / GPI, e = (gidx - k * GPI) * 4;
+          *reinterpret_cast<float4*>(&sm.at.qb[k][e]) =
+              make_float4(bf_lo(v[gi].x), bf_lo(v[gi].y), bf_lo(v[gi].z), bf_lo(v[gi].w));
+          pend &= ~(1u << gi);
+        }
+      if (!pend) break;
+      if (C.dead || !spin.again()) { C.dead = true; break; }
+#pragma unroll
+      for (int gi = 0; gi < MAXG; ++gi)
+        if ((pend >> gi) & 1u) v[gi] = ld_dev128(r, uint32_t(wd[gi]) * 4u);
+    }
+  }
   if (P.ni) {  // every sequence's rotary row, out of the ring (its segment is released with item 0's K)
     C.wait_filled(C.pos);
     for (int i = C.ct; i < P.B * 64; i += NCT) {
@@ -2120,87 +2205,114 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
                                   : bf2f(*reinterpret_cast<const uint16_t*>(
                                         sm.ring + ((segcs + uint32_t(b) * 128u + uint32_t(f) * 2u) & (RING_B - 1))));
     }
-    C.cbar();
   }
-  if (C.ct == 0) trace_at(p, l, 4, p.n_layers);
-  const float sgn = part < 4 ? -1.f : 1.f;
-  // ---- pass A: scores and chunk statistics of every item ----
+  C.cbar();
+  tri(4);
+  // ---- A: scores and per-wave statistics of every item ----
+  // Scores on the matrix cores: D[token][head] = K[token][:] . q[head][:] as 16-token tiles,
+  // v_mfma_f32_16x16x32_bf16 over the 64 dimensions in two k-steps.  Lane l supplies row l%16 of A
+  // (token tile*16 + l%16, 8 dimensions of piece 4s + l/16 from the ring) and column l%16 of B (the
+  // roped q of head l%16 < 3, the same piece; zero for the padding heads) and receives
+  // D[4(l/16) + j][l%16], i.e. head l%16's scores of tokens 4(l/16) + j.  Each wave covers whole
+  // 16-token tiles; the rounding is bf16(q.k) * 1/8 as before.
+  const int hq = lane & 15, pq = lane >> 4;   // MFMA column (head) and piece of this lane
   for (int k = 0; k < P.ni; ++k) {
-    int b, g, c, Cc, base, t0, t1;
-    P.item(sm.sS, P.wg + k * NWG, b, g, c, Cc, base, t0, t1);
-    const bool leader = c == Cc - 1;
-    const int T_old = t1 - t0, T = T_old + (leader ? 1 : 0);
-    auto edge = [&](int q) { return q >= NCW ? T : ((T * q) / NCW) & ~1; };
+    const ItemB it = sm.it[k];
+    const int b = it.b, g = it.g;
+    const bool leader = it.c == it.C - 1;
+    const int T_old = it.t1 - it.t0, T = T_old + (leader ? 1 : 0);
+    auto edge = [&](int q) { return q >= NCW ? T : ((T * q) / NCW) & ~15; };
     const int j0 = edge(w), j1 = edge(w + 1);
     const bool has_new = leader && j1 == T && T > j0;
     const uint32_t segk = C.next_seg(uint32_t(T_old) * 128u);
-    C.poll_wave3(l, b, g * 192, 192, G::H + g * 64, has_new ? 64 : 0, G::H + G::KVH * 64 + g * 64,
-                 has_new ? 64 : 0, in);
+    const float* in = sm.at.qb[k];
+    trk(k, 18 + 3 * k);
     C.wait_filled(C.pos);
-    // cos/sin of this sequence's position, dims 8*part .. 8*part+7 (mod 32)
+    trk(k, 19 + 3 * k);
+    // RoPE of pieces pq (first half) and pq + 4 (second half) of a head: dims 8pq..8pq+7 and +32
     float cs8[8], sn8[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      cs8[e] = sm.at.csr[b][(part & 3) * 8 + e];
-      sn8[e] = sm.at.csr[b][32 + (part & 3) * 8 + e];
+      cs8[e] = sm.at.csr[b][pq * 8 + e];
+      sn8[e] = sm.at.csr[b][32 + pq * 8 + e];
     }
-    auto rope8 = [&](const float* head, uint32_t (&out)[4]) {
-      const float4 a0 = *reinterpret_cast<const float4*>(head + part * 8);
-      const float4 a1 = *reinterpret_cast<const float4*>(head + part * 8 + 4);
-      const float4 b0 = *reinterpret_cast<const float4*>(head + (part ^ 4) * 8);
-      const float4 b1 = *reinterpret_cast<const float4*>(head + (part ^ 4) * 8 + 4);
+    auto rope_pair = [&](const float* head, uint32_t (&lo)[4], uint32_t (&hi)[4]) {
+      const float4 a0 = *reinterpret_cast<const float4*>(head + pq * 8);
+      const float4 a1 = *reinterpret_cast<const float4*>(head + pq * 8 + 4);
+      const float4 b0 = *reinterpret_cast<const float4*>(head + 32 + pq * 8);
+      const float4 b1 = *reinterpret_cast<const float4*>(head + 32 + pq * 8 + 4);
       const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
       const float y[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-      float r[8];
+      float rl[8], rh[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) r[e] = rnd(rnd(x[e] * cs8[e]) + rnd((sgn * y[e]) * sn8[e]));
+      for (int e = 0; e < 8; ++e) {
+        rl[e] = rnd(rnd(x[e] * cs8[e]) + rnd((-y[e]) * sn8[e]));
+        rh[e] = rnd(rnd(y[e] * cs8[e]) + rnd(x[e] * sn8[e]));
+      }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) out[e] = pack2(r[2 * e], r[2 * e + 1]);
+      for (int e = 0; e < 4; ++e) {
+        lo[e] = pack2(rl[2 * e], rl[2 * e + 1]);
+        hi[e] = pack2(rh[2 * e], rh[2 * e + 1]);
+      }
     };
-    wait_lgkm0();
-    uint32_t q[3][4], kn[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int h = 0; h < 3; ++h) rope8(in + h * 64, q[h]);
-    if (has_new) rope8(in + 192, kn);
-    if (has_new && sm.sSlot[b] >= 0 && grp < 2) {  // KV append (block360_kernel.inc:124-135)
+    uint32_t qlo[4] = {0u, 0u, 0u, 0u}, qhi[4] = {0u, 0u, 0u, 0u};
+    if (hq < 3) rope_pair(in + hq * 64, qlo, qhi);
+    uint32_t klo[4] = {0u, 0u, 0u, 0u}, khi[4] = {0u, 0u, 0u, 0u};
+    if (has_new) rope_pair(in + 192, klo, khi);
+    if (has_new && sm.sSlot[b] >= 0 && hq < 2) {  // KV append (block360_kernel.inc:124-135)
+      // lane 16q (k) / 16q + 1 (v) writes pieces q and q + 4 of the new token
       const long long slot = sm.sSlot[b];
       uint16_t* cache = reinterpret_cast<uint16_t*>(const_cast<void*>(sm.kvp[l]));
       const long long e = (slot / 16) * p.block_stride + (slot % 16) * p.token_stride +
-                          (long long)g * p.head_stride + (grp ? p.v_off : p.k_off) + part * 8;
-      uint32_t val[4];
-      if (grp == 0) {
+                          (long long)g * p.head_stride + (hq ? p.v_off : p.k_off);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) val[i] = kn[i];
-      } else {
+      for (int hv = 0; hv < 2; ++hv) {
+        const int piece = pq + 4 * hv;
+        uint32_t val[4];
+        if (hq == 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) val[i] = pack2(in[256 + part * 8 + 2 * i], in[256 + part * 8 + 2 * i + 1]);
-      }
-      uint16_t* dst = cache + e;
-      if ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
-        *reinterpret_cast<uint4*>(dst) = make_uint4(val[0], val[1], val[2], val[3]);
-      } else {
+          for (int i = 0; i < 4; ++i) val[i] = hv ? khi[i] : klo[i];
+        } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) { dst[2 * i] = uint16_t(val[i] & 0xffffu); dst[2 * i + 1] = uint16_t(val[i] >> 16); }
+          for (int i = 0; i < 4; ++i) val[i] = pack2(in[256 + piece * 8 + 2 * i], in[256 + piece * 8 + 2 * i + 1]);
+        }
+        uint16_t* dst = cache + e + piece * 8;
+        if ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+          *reinterpret_cast<uint4*>(dst) = make_uint4(val[0], val[1], val[2], val[3]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) { dst[2 * i] = uint16_t(val[i] & 0xffffu); dst[2 * i + 1] = uint16_t(val[i] >> 16); }
+        }
       }
     }
-    for (int jb = j0; jb < j1; jb += 8) {
-      const int j = jb + grp;
-      const uint4 kk = j < T_old ? C.ring16(segk + kvb_slot(j, part)) : make_uint4(kn[0], kn[1], kn[2], kn[3]);
-      float s3[3];
+    const bf16x8 bq0 = __builtin_bit_cast(bf16x8, make_uint4(qlo[0], qlo[1], qlo[2], qlo[3]));
+    const bf16x8 bq1 = __builtin_bit_cast(bf16x8, make_uint4(qhi[0], qhi[1], qhi[2], qhi[3]));
+    const int ntiles = (j1 - j0 + 15) / 16;
 #pragma unroll
-      for (int h = 0; h < 3; ++h) {
-        float a = dot2(q[h][0], kk.x, 0.f);
-        a = dot2(q[h][1], kk.y, a);
-        a = dot2(q[h][2], kk.z, a);
-        a = dot2(q[h][3], kk.w, a);
-        s3[h] = group8_sum(a);
+    for (int ti = 0; ti < 5; ++ti) {
+      if (ti >= ntiles) break;
+      const int tok = j0 + ti * 16 + hq;       // A row of this lane
+      uint4 a0 = make_uint4(0u, 0u, 0u, 0u), a1 = make_uint4(0u, 0u, 0u, 0u);
+      if (tok < T_old) {
+        a0 = C.ring16(segk + kvb_slot(tok, pq));
+        a1 = C.ring16(segk + kvb_slot(tok, pq + 4));
+      } else if (tok == T_old && leader) {
+        a0 = make_uint4(klo[0], klo[1], klo[2], klo[3]);
+        a1 = make_uint4(khi[0], khi[1], khi[2], khi[3]);
       }
-      if (part == 0 && j < j1)
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a0), bq0, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1), bq1, acc, 0, 0, 0);
+      if (hq < 3)
 #pragma unroll
-        for (int h = 0; h < 3; ++h) sm.at.sc[k][h][j] = uint16_t(f2bf(rnd(s3[h]) * 0.125f));
+        for (int jj = 0; jj < 4; ++jj) {
+          const int t = j0 + ti * 16 + 4 * pq + jj;
+          if (t < j1) sm.at.sc[k][hq][t] = uint16_t(f2bf(rnd(acc[jj]) * 0.125f));
+        }
     }
     wait_lgkm0();
     C.release(C.pos);  // this item's K is no longer read
+    // per-wave (max, sum) of each head over the wave's tokens, two tokens per lane from LDS
 #pragma unroll
     for (int h = 0; h < 3; ++h) {
       float sv[2];
@@ -2214,93 +2326,109 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
 #pragma unroll
       for (int i = 0; i < 2; ++i) ls += sv[i] == -INFINITY ? 0.f : expf(sv[i] - m);
       ls = wave_sum(ls);
-      if (lane == 0) { sm.wml[w][0][h] = m; sm.wml[w][1][h] = ls; }
+      if (lane == 0) { sm.at.wml[k][w][0][h] = m; sm.at.wml[k][w][1][h] = ls; }
     }
-    C.cbar();
-    if (w == 0) {
-      float mq = -INFINITY, lq = 0.f;
-      if (lane < 12) { mq = sm.wml[lane & 3][0][lane >> 2]; lq = sm.wml[lane & 3][1][lane >> 2]; }
-      float mx = fmaxf(mq, dpp<0xb1>(mq, mq));
-      mx = fmaxf(mx, dpp<0x4e>(mx, mx));
-      float ex = mq == -INFINITY ? 0.f : lq * expf(mq - mx);
-      ex += dpp<0xb1>(0.f, ex);
-      ex += dpp<0x4e>(0.f, ex);
-      if (lane < 12 && (lane & 3) == 0) { sm.at.cst[k][0][lane >> 2] = mx; sm.at.cst[k][1][lane >> 2] = ex; }
-      if (Cc > 1 && lane < 12 && (lane & 3) == 0) {
-        uint64_t* st = reinterpret_cast<uint64_t*>(p.ws + WSB<G>::stat(P.wg + k * NWG));
-        st_dev64(st + 2 * (lane >> 2), tg | __float_as_uint(mx));
-        st_dev64(st + 2 * (lane >> 2) + 1, tg | __float_as_uint(ex));
+    trk(k, 20 + 3 * k);
+  }
+  C.cbar();
+  tri(5);
+  // ---- chunk statistics: wave w merges items w, w + 4, ... (lanes 0-11: wave lane&3, head lane>>2) ----
+  for (int k = w; k < P.ni; k += NCW) {
+    const ItemB it = sm.it[k];
+    float mq = -INFINITY, lq = 0.f;
+    if (lane < 12) { mq = sm.at.wml[k][lane & 3][0][lane >> 2]; lq = sm.at.wml[k][lane & 3][1][lane >> 2]; }
+    float mx = fmaxf(mq, dpp<0xb1>(mq, mq));
+    mx = fmaxf(mx, dpp<0x4e>(mx, mx));
+    float ex = mq == -INFINITY ? 0.f : lq * expf(mq - mx);
+    ex += dpp<0xb1>(0.f, ex);
+    ex += dpp<0x4e>(0.f, ex);
+    if (lane < 12 && (lane & 3) == 0) { sm.at.cst[k][0][lane >> 2] = mx; sm.at.cst[k][1][lane >> 2] = ex; }
+    if (it.C > 1 && lane < 12 && (lane & 3) == 0) {
+      uint64_t* st = reinterpret_cast<uint64_t*>(p.ws + WSB<G>::stat(P.wg + k * NWG));
+      st_dev64(st + 2 * (lane >> 2), tg | __float_as_uint(mx));
+      st_dev64(st + 2 * (lane >> 2) + 1, tg | __float_as_uint(ex));
+    }
+  }
+  C.cbar();
+  // ---- G: global statistics of every item (wave w: items w, w + 4, ...; lane kc reads chunk kc) ----
+  {
+    constexpr int MAXI = (IPW + NCW - 1) / NCW;
+    u32x4 v[MAXI][3];
+    uint32_t pend = 0;
+#pragma unroll
+    for (int i = 0; i < MAXI; ++i) {
+      const int k = w + NCW * i;
+      if (k < P.ni && sm.it[k].C > 1 && lane < sm.it[k].C) {
+        const __amdgpu_buffer_rsrc_t r = rsrc(p.ws + WSB<G>::stat(sm.it[k].base));
+#pragma unroll
+        for (int h = 0; h < 3; ++h) v[i][h] = ld_dev128(r, uint32_t(lane * STAT_WORDS + 2 * h) * 8u);
+        pend |= 1u << i;
       }
     }
-    C.cbar();  // wml is reused by the next item
-  }
-  if (C.ct == 0) trace_at(p, l, 5, p.n_layers);
-  // ---- pass B: global statistics, probabilities, P.V of every item ----
-  for (int k = 0; k < P.ni; ++k) {
-    int b, g, c, Cc, base, t0, t1;
-    P.item(sm.sS, P.wg + k * NWG, b, g, c, Cc, base, t0, t1);
-    const bool leader = c == Cc - 1;
-    const int T_old = t1 - t0, T = T_old + (leader ? 1 : 0);
-    auto edge = [&](int q) { return q >= NCW ? T : ((T * q) / NCW) & ~1; };
-    const int j0 = edge(w), j1 = edge(w + 1);
-    const bool has_new = leader && j1 == T && T > j0;
-    const uint32_t segv = C.next_seg(uint32_t(T_old) * 128u);
-    float Mh[3], Lh[3];
-    if (Cc > 1) {
-      // lane k2 (and k2 + 64, ...) reads chunk k2's (max, sum) of the three heads
-      const __amdgpu_buffer_rsrc_t r = rsrc(p.ws + WSB<G>::stat(base));
-      float mk[4][3], lk[4][3];
+    auto ok = [&](const u32x4 (&x)[3]) {
+      return x[0].y == tagb && x[0].w == tagb && x[1].y == tagb && x[1].w == tagb && x[2].y == tagb &&
+             x[2].w == tagb;
+    };
+    Spin spin(p.ws, 9);
+    while (true) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < MAXI; ++i)
+        if (((pend >> i) & 1u) && ok(v[i])) pend &= ~(1u << i);
+      if (!pend) break;
+      if (C.dead || !spin.again()) { C.dead = true; break; }
 #pragma unroll
-        for (int h = 0; h < 3; ++h) { mk[i][h] = -INFINITY; lk[i][h] = 0.f; }
+      for (int i = 0; i < MAXI; ++i)
+        if ((pend >> i) & 1u) {
+          const __amdgpu_buffer_rsrc_t r = rsrc(p.ws + WSB<G>::stat(sm.it[w + NCW * i].base));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kc = lane + 64 * i;
-        if (kc < Cc) {
-          Spin spin(p.ws, 9);
-          u32x4 v[3];
-          while (true) {
-#pragma unroll
-            for (int h = 0; h < 3; ++h) v[h] = ld_dev128(r, uint32_t(kc * STAT_WORDS + 2 * h) * 8u);
-            bool ok = true;
-#pragma unroll
-            for (int h = 0; h < 3; ++h) ok = ok && v[h].y == tagb && v[h].w == tagb;
-            if (ok) break;
-            if (C.dead || !spin.again()) { C.dead = true; break; }
-          }
-#pragma unroll
-          for (int h = 0; h < 3; ++h) { mk[i][h] = __uint_as_float(v[h].x); lk[i][h] = __uint_as_float(v[h].z); }
+          for (int h = 0; h < 3; ++h) v[i][h] = ld_dev128(r, uint32_t(lane * STAT_WORDS + 2 * h) * 8u);
         }
+    }
+#pragma unroll
+    for (int i = 0; i < MAXI; ++i) {
+      const int k = w + NCW * i;
+      if (k >= P.ni) continue;
+      const int Cc = sm.it[k].C;
+      if (Cc == 1) {
+        if (lane < 6) sm.at.gml[k][lane / 3][lane % 3] = sm.at.cst[k][lane / 3][lane % 3];
+        continue;
       }
 #pragma unroll
       for (int h = 0; h < 3; ++h) {
-        float m = fmaxf(fmaxf(mk[0][h], mk[1][h]), fmaxf(mk[2][h], mk[3][h]));
-        m = wave_max(m);
-        float ls = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ls += mk[i][h] == -INFINITY ? 0.f : lk[i][h] * expf(mk[i][h] - m);
-        Mh[h] = m;
-        Lh[h] = wave_sum(ls);
+        const bool mine = lane < Cc;
+        const float mk = mine ? __uint_as_float(v[i][h].x) : -INFINITY;
+        const float lk = mine ? __uint_as_float(v[i][h].z) : 0.f;
+        const float m = wave_max(mk);
+        const float ls = wave_sum(mk == -INFINITY ? 0.f : lk * expf(mk - m));
+        if (lane == 0) { sm.at.gml[k][0][h] = m; sm.at.gml[k][1][h] = ls; }
       }
-    } else {
-#pragma unroll
-      for (int h = 0; h < 3; ++h) { Mh[h] = sm.at.cst[k][0][h]; Lh[h] = sm.at.cst[k][1][h]; }
     }
+  }
+  C.cbar();
+  tri(6);
+  // ---- B: probabilities and P.V of every item ----
+  const int half = lane >> 5, d2 = lane & 31;
+  const uint32_t voff = uint32_t(d2 & 3) * 4u;
+  for (int k = 0; k < P.ni; ++k) {
+    const ItemB it = sm.it[k];
+    const bool leader = it.c == it.C - 1;
+    const int T_old = it.t1 - it.t0, T = T_old + (leader ? 1 : 0);
+    auto edge = [&](int q) { return q >= NCW ? T : ((T * q) / NCW) & ~15; };
+    const int j0 = edge(w), j1 = edge(w + 1);
+    const bool has_new = leader && j1 == T && T > j0;
+    const uint32_t segv = C.next_seg(uint32_t(T_old) * 128u);
+    const float* in = sm.at.qb[k];
 #pragma unroll
     for (int h = 0; h < 3; ++h) {
-      const float inv = 1.0f / Lh[h];
+      const float M = sm.at.gml[k][0][h], inv = 1.0f / sm.at.gml[k][1][h];
       for (int j = j0 + lane; j < j1; j += 64)
-        sm.at.pb[h][j] = uint16_t(f2bf(expf(bf2f(sm.at.sc[k][h][j]) - Mh[h]) * inv));
+        sm.at.pb[h][j] = uint16_t(f2bf(expf(bf2f(sm.at.sc[k][h][j]) - M) * inv));
     }
-    if (has_new)  // the new token's v (this wave's input buffer has since held other items)
-      C.poll_wave3(l, b, 0, 0, 0, 0, G::H + G::KVH * 64 + g * 64, 64, in + 256);
     wait_lgkm0();
+    trk(k, 30 + 2 * k);
     C.wait_filled(C.pos);  // this item's V
-    const int half = lane >> 5, d2 = lane & 31;
     const int jo1 = min(j1, T_old);
     const int npairs = jo1 > j0 ? (jo1 - j0) / 2 : 0;
-    const uint32_t voff = uint32_t(d2 & 3) * 4u;
     float acc[3][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
     for (int kp = half; kp < npairs; kp += 2) {
       const int j = j0 + 2 * kp;
@@ -2341,25 +2469,28 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
       acc[h][1] += __shfl_xor(acc[h][1], 32);
     }
     C.release(C.pos);  // this item's V is no longer read
+    float (*wo)[3][64] = sm.at.wo[k & 1];
     if (lane < 32)
 #pragma unroll
-      for (int h = 0; h < 3; ++h) { sm.wo[w][h][2 * d2] = acc[h][0]; sm.wo[w][h][2 * d2 + 1] = acc[h][1]; }
+      for (int h = 0; h < 3; ++h) { wo[w][h][2 * d2] = acc[h][0]; wo[w][h][2 * d2 + 1] = acc[h][1]; }
+    // one barrier per item: wo[k & 1] is next written by item k + 2, after the barrier of item k + 1,
+    // and pb is only read by the wave that wrote it, before this barrier
     C.cbar();
     if (w < 3) {
       float O = 0.f;
 #pragma unroll
-      for (int v = 0; v < NCW; ++v) O += sm.wo[v][w][lane];
+      for (int v = 0; v < NCW; ++v) O += wo[v][w][lane];
       if (leader) sm.at.own[k][w * 64 + lane] = O;
       else st_dev64(reinterpret_cast<uint64_t*>(p.ws + WSB<G>::rec(P.wg + k * NWG)) + w * 64 + lane, tg | __float_as_uint(O));
     }
-    C.cbar();  // wo and pb are reused by the next item
+    trk(k, 31 + 2 * k);
   }
-  if (C.ct == 0) trace_at(p, l, 6, p.n_layers);
-  // ---- pass C: leaders add their chunks' partials (chunk order) and publish attn ----
+  tri(7);
+  // ---- C: leaders add their chunks' partials (chunk order) and publish attn ----
   for (int k = 0; k < P.ni; ++k) {
-    int b, g, c, Cc, base, t0, t1;
-    P.item(sm.sS, P.wg + k * NWG, b, g, c, Cc, base, t0, t1);
-    if (c != Cc - 1 || w >= 3) continue;
+    const ItemB it = sm.it[k];
+    if (it.c != it.C - 1 || w >= 3) continue;
+    const int Cc = it.C, base = it.base;
     float O = 0.f;
     constexpr int MB = 8;
     for (int c0 = 0; c0 < Cc - 1; c0 += MB) {
@@ -2389,9 +2520,8 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
         if (kk < nc) O += __uint_as_float(uint32_t(ro[kk]));
     }
     O += sm.at.own[k][w * 64 + lane];
-    put_bf16<G>(C, X_ATTN, l, G::H, b, (g * 3 + w) * 64 + lane, O);
+    put_bf16<G>(C, X_ATTN, l, G::H, it.b, (it.g * 3 + w) * 64 + lane, O);
   }
-  if (C.ct == 0) trace_at(p, l, 7, p.n_layers);
   publish_flag<G>(C, X_ATTN, l);
 }
 
