@@ -33,7 +33,7 @@ extern "C" {
 #define PK_ERR_SCRATCH 9108      /* workspace or debug buffer too small */
 #define PK_ERR_BLOCK 9109        /* block_size != 16, bt_stride too small, or bad layer index */
 #define PK_ERR_MODEL 9110        /* unknown model id or layer count */
-#define PK_ERR_DEBUG 9111        /* per-stage debug capture is not available in this build */
+#define PK_ERR_DEBUG 9111        /* per-stage debug capture requested for a model/format without it */
 #define PK_ERR_CAPTURE 9112      /* a workspace's first use (its zero fill) happened under stream capture */
 
 /* Models. */
@@ -78,6 +78,23 @@ int pk_decode(void* stream, int model, int B, int n_layers, const void* input_id
               int cs_fp32, void* out_hidden, void* layer_outputs, void* out_ids, void* out_logits,
               void* scratch, size_t scratch_bytes, int max_seq_len);
 
+/* pk_decode with per-stage debug capture (SmolLM2-360M bf16, B <= 2) and, for 360M, an optional
+ * lossless gate/up table (prime_lossless.h; NULL: dense).  `debug` (16-byte aligned, at least
+ * decode360_debug_bytes() bytes, NULL: no capture) receives the reference's layout
+ * (block360_kernel.inc:1-20): for every layer the bf16 rows [2][N] of norm1, qkv, attn, o, h1,
+ * norm2, gate, up, silu, act, down, out (row b = sequence b); for layer `debug_layer_index`
+ * (-1: none) also the rotated queries [2][960], bf16(q.k), the scaled scores and the probabilities
+ * [2][15][8192] (positions from 8192 on are not recorded) and the P.V output [2][960].  Other
+ * models or MXFP8 weights return PK_ERR_DEBUG when `debug` is set. */
+int pk_decode_debug(void* stream, int model, int B, int n_layers, const void* input_ids, int ids_i64,
+                    const void* embed, const void* final_norm, const void* positions, const void* seq_lens,
+                    const void* block_table, int bt_stride, const void* slot_mapping, const void* layers,
+                    void* const* kv, long long k_off, long long v_off, long long block_stride,
+                    long long token_stride, long long head_stride, int block_size, const void* cos_sin,
+                    int cs_fp32, void* out_hidden, void* layer_outputs, void* out_ids, void* out_logits,
+                    void* scratch, size_t scratch_bytes, int max_seq_len, const void* encoded_gu_table,
+                    void* debug, size_t debug_bytes, int debug_layer_index);
+
 /* pk_decode with MXFP8 projection weights (SmolLM2-360M only): `layers` is a device table
  * [n_layers][10] of (norm1, qkv, qkv_scales, o, o_scales, norm2, gate_up, gate_up_scales, down,
  * down_scales): e4m3 bytes [rows, cols] and e8m0 scale codes [rows, pk_mxfp8_scale_stride(cols)],
@@ -115,7 +132,8 @@ const char* prime_decode_status_string(int status);
 /* ---- reference-compatible entry points -------------------------------------------------- */
 
 /* SmolLM2-360M, 32 layers, hidden state out (block360_kernel.inc:852-862, same argument list).
- * `debug` must be NULL (per-stage capture: PK_ERR_DEBUG); `debug_layer_index` must be -1..31. */
+ * `debug` (optional, B <= 2) receives the per-stage capture described at pk_decode_debug;
+ * `debug_layer_index` must be -1..31. */
 int decode360(void* stream, int B, const void* input_ids, const void* embed, const void* final_norm,
               const void* positions, const void* seq_lens, const void* block_table, int bt_stride,
               const void* slot_mapping, const void* layers, void* const* kv, long long k_off,
@@ -124,7 +142,7 @@ int decode360(void* stream, int B, const void* input_ids, const void* embed, con
               void* scratch, size_t scratch_bytes, void* debug, size_t debug_bytes, int max_seq_len,
               int debug_layer_index);
 size_t decode360_workspace_bytes(void);   /* block360_kernel.inc:849 */
-size_t decode360_debug_bytes(void);       /* block360_kernel.inc:850; 0: capture unavailable */
+size_t decode360_debug_bytes(void);       /* block360_kernel.inc:850 */
 const char* decode360_status_string(int status);  /* block360_kernel.inc:925-938 */
 
 /* SmolLM2-135M, 30 layers (megakernel.cu:844-851, same argument list). */

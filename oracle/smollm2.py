@@ -296,7 +296,10 @@ def decoder_layer(geom: Geometry, layer_w, x: torch.Tensor, pos: int, cos_sin: t
     d = F.linear(act, down)
     x = residual + d
     if stages is not None:
-        stages.update(norm1=h, q_rot=q_rot, k_rot=k_rot, v=v, attn=attn, probs=probs, o=o,
+        # bf16(q . k) before the 1/sqrt(D) scale and the scaled scores, by the op eager_attention uses
+        qk = torch.matmul(q_rot, repeat_kv(keys, NH // KVH).transpose(2, 3))
+        stages.update(norm1=h, qkv=torch.cat([q.reshape(-1), k.reshape(-1), v.reshape(-1)]), q_rot=q_rot,
+                      k_rot=k_rot, v=v, qk=qk, scores=qk * D ** -0.5, attn=attn, probs=probs, o=o,
                       h1=residual, norm2=h2, gate=g, up=u, silu=silu, act=act, down=d, out=x)
     return x, k_rot[0, :, 0, :], v[0, :, 0, :]
 

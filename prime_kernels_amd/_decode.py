@@ -177,7 +177,10 @@ def decode_step(model: Model, *, input_ids, positions, seq_lens, block_table, sl
     if debug_layer_index < -1 or debug_layer_index >= model.layers:
         raise ValueError(f"debug_layer_index must be -1 or a layer index 0..{model.layers - 1}")
     if debug is not None:
-        raise ValueError("per-stage debug capture is not available in this build")
+        if model.model_id != 360 or model.weight_format != "bf16":
+            raise ValueError("per-stage debug capture is available for SmolLM2-360M bf16 weights")
+        if batch > 2:
+            raise ValueError("per-stage debug capture holds at most 2 sequences")
 
     device = input_ids.device
     _check_tensor(input_ids, "input_ids", device=device)
@@ -231,6 +234,14 @@ def decode_step(model: Model, *, input_ids, positions, seq_lens, block_table, sl
         _check_tensor(logits_out, "logits_out", dtype=torch.bfloat16, device=device, shape=(batch, VOCAB))
         if not logits_out.is_contiguous():
             raise ValueError("logits_out must be contiguous")
+    if debug is not None:  # decode_megakernel_360m/__init__.py:198-213
+        _check_tensor(debug, "debug", dtype=torch.uint8, device=device)
+        if not debug.is_contiguous():
+            raise ValueError("debug must be contiguous raw byte storage")
+        if debug.numel() < _native.library().decode360_debug_bytes():
+            raise ValueError("debug buffer is too small")
+        if debug.data_ptr() % 16:
+            raise ValueError("debug buffer must be 16-byte aligned")
 
     extra = ()
     if encoded_gu is not None:
@@ -245,7 +256,11 @@ def decode_step(model: Model, *, input_ids, positions, seq_lens, block_table, sl
     layers_t, kv_t = _tables(rt, layers, kv_caches)
     stream = torch.cuda.current_stream(device).cuda_stream
     want_ids = return_token_ids or logits_out is not None
-    if encoded_gu is not None:
+    if debug is not None:
+        launch = rt.lib.pk_decode_debug
+        extra = (encoded_gu.table.data_ptr() if encoded_gu is not None else None, debug.data_ptr(),
+                 debug.numel(), debug_layer_index)
+    elif encoded_gu is not None:
         launch = rt.lib.pk_decode_lossless
         extra = (encoded_gu.table.data_ptr(),)
     else:

@@ -18,7 +18,7 @@ _lib = None
 
 vp, ci, ll, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_size_t
 
-# symbol -> (restype, argtypes); the list every test checks against include/prime_decode.h
+# symbol -> (restype, argtypes); the list every test checks against include/*.h
 SIGNATURES = {
     "pk_workspace_bytes": (sz, [ci]),
     "pk_workspace_alloc": (vp, [sz, ci]),
@@ -27,6 +27,8 @@ SIGNATURES = {
     "pk_workspace_read": (ci, [vp, sz, ctypes.POINTER(ctypes.c_uint), ci]),
     "pk_decode": (ci, [vp, ci, ci, ci, vp, ci, vp, vp, vp, vp, vp, ci, vp, vp, vp,
                        ll, ll, ll, ll, ll, ci, vp, ci, vp, vp, vp, vp, vp, sz, ci]),
+    "pk_decode_debug": (ci, [vp, ci, ci, ci, vp, ci, vp, vp, vp, vp, vp, ci, vp, vp, vp,
+                             ll, ll, ll, ll, ll, ci, vp, ci, vp, vp, vp, vp, vp, sz, ci, vp, vp, sz, ci]),
     "pk_decode_mxfp8": (ci, [vp, ci, ci, ci, vp, ci, vp, vp, vp, vp, vp, ci, vp, vp, vp,
                              ll, ll, ll, ll, ll, ci, vp, ci, vp, vp, vp, vp, vp, sz, ci]),
     "pk_mxfp8_scale_stride": (sz, [ci]),

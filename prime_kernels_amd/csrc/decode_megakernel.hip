@@ -135,6 +135,26 @@ struct Params {
   int ids_i64;
   unsigned long long* trace;   // optional per-phase timestamps (diagnostics)
   const EncodedGULayer* encoded_gu;  // optional [L] lossless gate/up encodings (batch-1 bf16 kernel)
+  uint16_t* debug;             // optional per-stage capture (Dbg layout), batch <= 2
+  int debug_layer;             // layer whose attention internals are captured (-1: none)
+};
+
+// Per-stage debug capture, the reference's layout (block360_kernel.inc:1-20), bf16 elements:
+// per layer [norm1, qkv, attn, o, h1, norm2, gate, up, silu, act, down, out], each [2][N] (rows for
+// sequences 0 and 1); then, for layer `debug_layer` only, the rotated queries [2][H], bf16(q.k)
+// [2][NH][8192], the scaled scores and the probabilities (same shape) and the P.V output [2][H].
+// Positions from 8192 on are not recorded.
+template <class G>
+struct Dbg {
+  static constexpr size_t MB = 2, SEQ = 8192;
+  static constexpr size_t NORM1 = 0, QKV = NORM1 + MB * G::H, ATTN = QKV + MB * G::QKV, O = ATTN + MB * G::H,
+                          H1 = O + MB * G::H, NORM2 = H1 + MB * G::H, GATE = NORM2 + MB * G::H,
+                          UP = GATE + MB * G::I, SILU = UP + MB * G::I, ACT = SILU + MB * G::I,
+                          DOWN = ACT + MB * G::I, OUT = DOWN + MB * G::H, LAYER = OUT + MB * G::H;
+  static constexpr size_t STAGES = size_t(G::L) * LAYER, AQ = STAGES, AQK = AQ + MB * G::H,
+                          ASC = AQK + MB * G::NH * SEQ, APR = ASC + MB * G::NH * SEQ, APV = APR + MB * G::NH * SEQ,
+                          TOTAL = APV + MB * G::H;
+  __device__ static size_t head_pos(int b, int head, int pos) { return (size_t(b) * G::NH + head) * SEQ + pos; }
 };
 
 // A layer's lossless gate/up encoding as this workgroup streams it (on = 0: dense gate/up): the
@@ -1052,7 +1072,7 @@ __device__ __forceinline__ float rms_scale(float sumsq, int n) {
 // and rounds once (leader).  The leader's wave 3 appends the new K/V (block360_kernel.inc:124-135).
 // ------------------------------------------------------------------------------------------------
 
-template <class G>
+template <class G, bool DBG>
 __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, uint32_t seg) {
   const Params& p = C.p;
   const Plan<G>& P = C.P;
@@ -1118,6 +1138,13 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
 #pragma unroll
   for (int h = 0; h < 3; ++h) rope8(in + h * 64, q[h]);
   if (has_new) rope8(in + 192, kn);
+  // debug capture of layer debug_layer: rotated queries (chunk 0 of each KV head, lanes 0-7)
+  const bool dbg_attn = DBG && p.debug != nullptr && l == p.debug_layer;
+  if (dbg_attn && P.c == 0 && w == 0 && grp == 0)
+#pragma unroll
+    for (int h = 0; h < 3; ++h)
+      *reinterpret_cast<uint4*>(p.debug + Dbg<G>::AQ + (g * 3 + h) * 64 + part * 8) =
+          make_uint4(q[h][0], q[h][1], q[h][2], q[h][3]);
   if (has_new && P.slot >= 0 && grp < 2) {
     // KV append at slot_mapping[b] (block360_kernel.inc:124-135; slot < 0 skips): lanes 0-7 store
     // the rotated new K, lanes 8-15 the new V, 8 dims (16 bytes) per lane
@@ -1159,7 +1186,13 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
     }
     if (part == 0 && j < j1)
 #pragma unroll
-      for (int h = 0; h < 3; ++h) sm.at.sc[h][j] = rnd(s3[h]) * 0.125f;
+      for (int h = 0; h < 3; ++h) {
+        sm.at.sc[h][j] = rnd(s3[h]) * 0.125f;
+        if (dbg_attn && P.t0 + j < int(Dbg<G>::SEQ)) {
+          p.debug[Dbg<G>::AQK + Dbg<G>::head_pos(b, g * 3 + h, P.t0 + j)] = uint16_t(f2bf(s3[h]));
+          p.debug[Dbg<G>::ASC + Dbg<G>::head_pos(b, g * 3 + h, P.t0 + j)] = uint16_t(f2bf(rnd(s3[h]) * 0.125f));
+        }
+      }
   }
   wait_lgkm0();
   if (w == 0 && lane == 0) trace_at(p, l, 17, p.n_layers);
@@ -1262,7 +1295,11 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int j = j0 + lane + 64 * i;
-      if (j < j1) sm.at.pb[h][j] = uint16_t(f2bf(expf(sv[h][i] - Mh[h]) * inv));
+      if (j < j1) {
+        sm.at.pb[h][j] = uint16_t(f2bf(expf(sv[h][i] - Mh[h]) * inv));
+        if (dbg_attn && P.t0 + j < int(Dbg<G>::SEQ))
+          p.debug[Dbg<G>::APR + Dbg<G>::head_pos(b, g * 3 + h, P.t0 + j)] = sm.at.pb[h][j];
+      }
     }
   }
   wait_lgkm0();
@@ -1364,6 +1401,11 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   if (w == 0 && lane == 0) trace_at(p, l, 20, p.n_layers);
   O += o_own;
   st_dev(p.ws + W::xw(X_ATTN, l, b, (g * 3 + hh) * 64 + d), C.w16(O));
+  if (DBG && p.debug) {
+    const uint16_t ob = uint16_t(f2bf(O));
+    p.debug[size_t(l) * Dbg<G>::LAYER + Dbg<G>::ATTN + (g * 3 + hh) * 64 + d] = ob;
+    if (l == p.debug_layer) p.debug[Dbg<G>::APV + (g * 3 + hh) * 64 + d] = ob;
+  }
   if (w == 0 && lane == 0) trace_at(p, l, 5, p.n_layers);
 }
 
@@ -1371,7 +1413,7 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
 // Consumer main loop
 // ------------------------------------------------------------------------------------------------
 
-template <class G>
+template <class G, bool DBG>
 __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem<G>& sm, uint32_t epoch) {
   Consumer<G> C(p, P, sm, epoch);
   __builtin_amdgcn_s_barrier();  // pairs with the producer's barrier (blk[] ready)
@@ -1382,6 +1424,15 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
   constexpr int EW = G::WF ? 16 : 8;                      // activations per 16-byte weight chunk
   const int b = 0;
   auto tr = [&](int l, int ev) { if (C.ct == 0) trace_at(p, l, ev, p.n_layers); };
+  // debug capture: this layer's stage rows (sequence 0), and a normalised vector from wave 0
+  auto dl = [&](int l) { return p.debug + size_t(l) * Dbg<G>::LAYER; };
+  auto dbg_vec = [&](uint16_t* dst, const XChunks<G::H, 8>& v) {
+#pragma unroll
+    for (int cc = 0; cc < Chunks<G::H>::CPL; ++cc) {
+      const int ch = C.lane + 64 * cc;
+      if (ch < Chunks<G::H>::CH) *reinterpret_cast<uint4*>(dst + ch * 8) = v[cc][0];
+    }
+  };
   if (C.ct == 0 && p.trace)
     p.trace[size_t(blockIdx.x) * (size_t(p.n_layers) * TR_EVENTS + TR_TAIL) + size_t(p.n_layers) * TR_EVENTS] =
         wall_clock64();
@@ -1418,13 +1469,18 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       tr(l, 1);
       XChunks<G::H, EW> x;
       load_x<G::H, EW, true>(x, sm.xs, nw, rs, C.lane);
+      if constexpr (EW == 8)
+        if (DBG && p.debug && P.q0 == 0 && C.cw == 0) dbg_vec(dl(l) + Dbg<G>::NORM1, x);
       tr(l, 21);
       float out[R::QKV];
       gemv<G, G::H, R::QKV>(C, seg, segs, P.q1 - P.q0, x, out);
       C.release(C.pos);
       tr(l, 22);
       const int row = C.cw + NCW * C.lane;
-      if (C.lane < R::QKV && row < P.q1 - P.q0) st_dev(p.ws + W::xw(X_QKV, l, b, P.q0 + row), C.w16(pick(out, C.lane)));
+      if (C.lane < R::QKV && row < P.q1 - P.q0) {
+        st_dev(p.ws + W::xw(X_QKV, l, b, P.q0 + row), C.w16(pick(out, C.lane)));
+        if (DBG && p.debug) dl(l)[Dbg<G>::QKV + P.q0 + row] = uint16_t(f2bf(pick(out, C.lane)));
+      }
       tr(l, 2);
     }
     // ---------------- P2: attention ----------------
@@ -1432,7 +1488,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
     {
       const uint32_t segc = C.next_seg(seg_bytes(P, S_CS, 0, p.cs_fp32));
       const uint32_t seg = C.next_seg(seg_bytes(P, S_KV, 0, p.cs_fp32));
-      if (P.att) attention(C, l, segc, seg);
+      if (P.att) attention<G, DBG>(C, l, segc, seg);
     }
     // ---------------- P3: O + residual ----------------
     C.refresh();
@@ -1455,7 +1511,12 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
         const int row = C.cw + NCW * C.lane;
         if (C.lane < R::O && row < nrows) {
           const int r = P.o0 + row;
-          st_dev(p.ws + W::xw(X_H1, l, b, r), C.w16(sm.xkeep[r] + rnd(pick(out, C.lane))));
+          const float o = rnd(pick(out, C.lane));
+          st_dev(p.ws + W::xw(X_H1, l, b, r), C.w16(sm.xkeep[r] + o));
+          if (DBG && p.debug) {
+            dl(l)[Dbg<G>::O + r] = uint16_t(f2bf(o));
+            dl(l)[Dbg<G>::H1 + r] = uint16_t(f2bf(sm.xkeep[r] + o));
+          }
         }
         tr(l, 8);
       } else {
@@ -1494,6 +1555,8 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       tr(l, 10);
       XChunks<G::H, EW> x;
       load_x<G::H, EW, true>(x, sm.xs, nw, rs, C.lane);
+      if constexpr (EW == 8)
+        if (DBG && p.debug && P.a0 == 0 && C.cw == 0) dbg_vec(dl(l) + Dbg<G>::NORM2, x);
       float og[R::ACT], ou[R::ACT];
       bool done = false;
       if constexpr (G::WF == 0) {
@@ -1518,6 +1581,13 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
         const float gv = rnd(pick(og, C.lane)), uv = rnd(pick(ou, C.lane));
         const float silu = rnd(gv / (1.0f + expf(-gv)));
         st_dev(p.ws + W::xw(X_ACT, l, b, P.a0 + row), C.w16(silu * uv));
+        if (DBG && p.debug) {
+          const int r = P.a0 + row;
+          dl(l)[Dbg<G>::GATE + r] = uint16_t(f2bf(gv));
+          dl(l)[Dbg<G>::UP + r] = uint16_t(f2bf(uv));
+          dl(l)[Dbg<G>::SILU + r] = uint16_t(f2bf(silu));
+          dl(l)[Dbg<G>::ACT + r] = uint16_t(f2bf(silu * uv));
+        }
       }
       tr(l, 11);
     }
@@ -1543,6 +1613,10 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
         const int r = P.d0 + row;
         const float y = rnd(sm.h1keep[r] + rnd(pick(out, C.lane)));
         st_dev(p.ws + W::xw(X_X, l, b, r), C.w16(y));
+        if (DBG && p.debug) {
+          dl(l)[Dbg<G>::DOWN + r] = uint16_t(f2bf(rnd(pick(out, C.lane))));
+          dl(l)[Dbg<G>::OUT + r] = uint16_t(f2bf(y));
+        }
         if (p.layer_outputs) p.layer_outputs[(size_t(l) * p.B + b) * G::H + r] = uint16_t(f2bf(y));
       }
       tr(l, 14);
@@ -1643,7 +1717,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
 // Kernel
 // ------------------------------------------------------------------------------------------------
 
-template <class G>
+template <class G, bool DBG = false>
 __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel(Params p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
   Smem<G>& sm = *reinterpret_cast<Smem<G>*>(smem_raw);
@@ -1692,7 +1766,7 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel(Params p) {
   uint32_t epoch = ld_dev(p.ws + HDR_EPOCH) + 1u;
   if (epoch == 0) epoch = 1;
   if (threadIdx.x < 64 * NPW) producer<G>(p, P, sm);
-  else consumer<G>(p, P, sm, epoch);
+  else consumer<G, DBG>(p, P, sm, epoch);
   __syncthreads();
   if (blockIdx.x == 0 && threadIdx.x == 0) st_dev(p.ws + HDR_EPOCH, epoch);
 }
@@ -2144,7 +2218,7 @@ __device__ __forceinline__ floatx4 mfma_tile(ConsumerB<G>& C, uint32_t seg, floa
 //   C  leaders add the other chunks' partials in chunk order and write attn.
 // Records and statistics are reused by every layer, so their tags carry the layer as well.
 // ------------------------------------------------------------------------------------------------
-template <class G>
+template <class G, bool DBG>
 __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t segcs) {
   const Params& p = C.p;
   const PlanB<G>& P = C.P;
@@ -2153,6 +2227,7 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
   const uint32_t tagb = (C.tag32 << 5) | uint32_t(l);
   const uint64_t tg = uint64_t(tagb) << 32;
   auto tri = [&](int ev) { if (C.ct == 0) trace_at(p, l, ev, p.n_layers); };
+  const bool dbg_attn = DBG && p.debug != nullptr && l == p.debug_layer;  // attention internals of this layer
   auto trk = [&](int k, int ev) { if (C.ct == 0 && k < 4) trace_at(p, l, ev, p.n_layers); };
   C.cbar();  // P1's reads of xs (which shares storage with sm.at) are done
   // ---- Q: every item's q (and new k / v) from the exchange words, one poll for all ----
@@ -2257,6 +2332,11 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
     };
     uint32_t qlo[4] = {0u, 0u, 0u, 0u}, qhi[4] = {0u, 0u, 0u, 0u};
     if (hq < 3) rope_pair(in + hq * 64, qlo, qhi);
+    if (dbg_attn && it.c == 0 && w == 0 && hq < 3) {
+      uint16_t* dq = p.debug + Dbg<G>::AQ + size_t(b) * G::H + (g * 3 + hq) * 64 + pq * 8;
+      *reinterpret_cast<uint4*>(dq) = make_uint4(qlo[0], qlo[1], qlo[2], qlo[3]);
+      *reinterpret_cast<uint4*>(dq + 32) = make_uint4(qhi[0], qhi[1], qhi[2], qhi[3]);
+    }
     uint32_t klo[4] = {0u, 0u, 0u, 0u}, khi[4] = {0u, 0u, 0u, 0u};
     if (has_new) rope_pair(in + 192, klo, khi);
     if (has_new && sm.sSlot[b] >= 0 && hq < 2) {  // KV append (block360_kernel.inc:124-135)
@@ -2307,7 +2387,14 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const int t = j0 + ti * 16 + 4 * pq + jj;
-          if (t < j1) sm.at.sc[k][hq][t] = uint16_t(f2bf(rnd(acc[jj]) * 0.125f));
+          if (t < j1) {
+            sm.at.sc[k][hq][t] = uint16_t(f2bf(rnd(acc[jj]) * 0.125f));
+            const int pos = it.t0 + t;
+            if (dbg_attn && pos < int(Dbg<G>::SEQ)) {
+              p.debug[Dbg<G>::AQK + Dbg<G>::head_pos(b, g * 3 + hq, pos)] = uint16_t(f2bf(acc[jj]));
+              p.debug[Dbg<G>::ASC + Dbg<G>::head_pos(b, g * 3 + hq, pos)] = sm.at.sc[k][hq][t];
+            }
+          }
         }
     }
     wait_lgkm0();
@@ -2421,8 +2508,11 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
 #pragma unroll
     for (int h = 0; h < 3; ++h) {
       const float M = sm.at.gml[k][0][h], inv = 1.0f / sm.at.gml[k][1][h];
-      for (int j = j0 + lane; j < j1; j += 64)
+      for (int j = j0 + lane; j < j1; j += 64) {
         sm.at.pb[h][j] = uint16_t(f2bf(expf(bf2f(sm.at.sc[k][h][j]) - M) * inv));
+        if (dbg_attn && it.t0 + j < int(Dbg<G>::SEQ))
+          p.debug[Dbg<G>::APR + Dbg<G>::head_pos(it.b, it.g * 3 + h, it.t0 + j)] = sm.at.pb[h][j];
+      }
     }
     wait_lgkm0();
     trk(k, 30 + 2 * k);
@@ -2521,6 +2611,11 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
     }
     O += sm.at.own[k][w * 64 + lane];
     put_bf16<G>(C, X_ATTN, l, G::H, it.b, (it.g * 3 + w) * 64 + lane, O);
+    if (DBG && p.debug) {
+      const size_t e = size_t(it.b) * G::H + (it.g * 3 + w) * 64 + lane;
+      p.debug[size_t(l) * Dbg<G>::LAYER + Dbg<G>::ATTN + e] = uint16_t(f2bf(O));
+      if (dbg_attn) p.debug[Dbg<G>::APV + e] = uint16_t(f2bf(O));
+    }
   }
   publish_flag<G>(C, X_ATTN, l);
 }
@@ -2528,7 +2623,7 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
 // ------------------------------------------------------------------------------------------------
 // Batched consumer
 // ------------------------------------------------------------------------------------------------
-template <class G>
+template <class G, bool DBG>
 __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, SmemB<G>& sm, uint32_t epoch) {
   ConsumerB<G> C(p, P, sm, epoch);
   __builtin_amdgcn_s_barrier();  // pairs with the producer's barrier (blk[] ready)
@@ -2536,6 +2631,12 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
   const int B = P.B;
   const int nq = P.q1 - P.q0, no = P.o1 - P.o0, na = P.a1 - P.a0, nd = P.d1 - P.d0;
   const int orow = 4 * (C.lane >> 4), tok = C.lane & 15;  // this lane's MFMA output rows / token
+  // debug capture (batch <= 2): stage rows of layer l; workgroup 0 copies the normalised vectors
+  auto dl = [&](int l) { return p.debug + size_t(l) * Dbg<G>::LAYER; };
+  auto dbg_xs = [&](uint16_t* dst) {
+    if (P.wg == 0)
+      for (int i = C.ct; i < B * G::H; i += NCT) dst[i] = sm.xs[i];
+  };
   // Diagnostic timestamps (events per layer: 0 P1 start, 1 staged, 2 weights in, 3 QKV stored,
   // 4 attention start, 5-7 passes A-C done, 8 attn published, 9-11 P3, 12-14 P4, 15-17 P5).
   auto tr = [&](int l, int ev) { if (C.ct == 0) trace_at(p, l, ev, p.n_layers); };
@@ -2567,19 +2668,23 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
       C.wait_filled(C.pos);
       tr(l, 2);
       norm_staged<G>(C, segn);
+      if (DBG && p.debug) dbg_xs(dl(l) + Dbg<G>::NORM1);
       const floatx4 acc = mfma_tile<G, G::H>(C, segq, sm.tile);
       C.release(C.pos);
       if (C.cw == 0 && tok < B)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          if (orow + j < nq) st_dev(p.ws + W::xw(X_QKV, l, tok, P.q0 + orow + j), C.w16(acc[j]));
+          if (orow + j < nq) {
+            st_dev(p.ws + W::xw(X_QKV, l, tok, P.q0 + orow + j), C.w16(acc[j]));
+            if (DBG && p.debug) dl(l)[Dbg<G>::QKV + size_t(tok) * G::QKV + P.q0 + orow + j] = uint16_t(f2bf(acc[j]));
+          }
       tr(l, 3);
     }
     // ---------------- P2: attention ----------------
     C.refresh();
     {
       const uint32_t segcs = C.next_seg(P.ni ? uint32_t(B) * (p.cs_fp32 ? 256u : 128u) : 0u);
-      attention_b<G>(C, l, segcs);
+      attention_b<G, DBG>(C, l, segcs);
       tr(l, 8);
     }
     // ---------------- P3: O + residual ----------------
@@ -2595,7 +2700,14 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
       if (C.cw == 0 && tok < B)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          if (orow + j < no) put_bf16<G>(C, X_H1, l, G::H, tok, P.o0 + orow + j, sm.xk[tok][orow + j] + rnd(acc[j]));
+          if (orow + j < no) {
+            put_bf16<G>(C, X_H1, l, G::H, tok, P.o0 + orow + j, sm.xk[tok][orow + j] + rnd(acc[j]));
+            if (DBG && p.debug) {
+              const size_t e = size_t(tok) * G::H + P.o0 + orow + j;
+              dl(l)[Dbg<G>::O + e] = uint16_t(f2bf(acc[j]));
+              dl(l)[Dbg<G>::H1 + e] = uint16_t(f2bf(sm.xk[tok][orow + j] + rnd(acc[j])));
+            }
+          }
       publish_flag<G>(C, X_H1, l);
       tr(l, 11);
     }
@@ -2614,6 +2726,7 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
       C.wait_filled(C.pos);
       tr(l, 13);
       norm_staged<G>(C, segn);
+      if (DBG && p.debug) dbg_xs(dl(l) + Dbg<G>::NORM2);
       floatx4 gt = {0.f, 0.f, 0.f, 0.f}, up = {0.f, 0.f, 0.f, 0.f};
       mfma_tile_pair<G, G::H>(C, segg, segu, sm.tile, gt, up);
       C.release(C.pos);
@@ -2624,6 +2737,13 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
             const float gv = rnd(gt[j]), uv = rnd(up[j]);
             const float silu = rnd(gv / (1.0f + expf(-gv)));
             put_bf16<G>(C, X_ACT, l, G::I, tok, P.a0 + orow + j, silu * uv);
+            if (DBG && p.debug) {
+              const size_t e = size_t(tok) * G::I + P.a0 + orow + j;
+              dl(l)[Dbg<G>::GATE + e] = uint16_t(f2bf(gv));
+              dl(l)[Dbg<G>::UP + e] = uint16_t(f2bf(uv));
+              dl(l)[Dbg<G>::SILU + e] = uint16_t(f2bf(silu));
+              dl(l)[Dbg<G>::ACT + e] = uint16_t(f2bf(silu * uv));
+            }
           }
       publish_flag<G>(C, X_ACT, l);
       tr(l, 14);
@@ -2644,6 +2764,11 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
           if (orow + j < nd) {
             const float y = rnd(sm.hk[tok][orow + j] + rnd(acc[j]));
             put_bf16<G>(C, X_X, l, G::H, tok, P.d0 + orow + j, y);
+            if (DBG && p.debug) {
+              const size_t e = size_t(tok) * G::H + P.d0 + orow + j;
+              dl(l)[Dbg<G>::DOWN + e] = uint16_t(f2bf(acc[j]));
+              dl(l)[Dbg<G>::OUT + e] = uint16_t(f2bf(y));
+            }
             if (p.layer_outputs) p.layer_outputs[(size_t(l) * B + tok) * G::H + P.d0 + orow + j] = uint16_t(f2bf(y));
           }
       publish_flag<G>(C, X_X, l);
@@ -2740,7 +2865,7 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
   }
 }
 
-template <class G>
+template <class G, bool DBG = false>
 __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel_b(Params p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
   SmemB<G>& sm = *reinterpret_cast<SmemB<G>*>(smem_raw);
@@ -2771,7 +2896,7 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel_b(Params p) {
   uint32_t epoch = ld_dev(p.ws + HDR_EPOCH) + 1u;
   if (epoch == 0) epoch = 1;
   if (threadIdx.x < 64 * NPW) producer_b<G>(p, P, sm);
-  else consumer_b<G>(p, P, sm, epoch);
+  else consumer_b<G, DBG>(p, P, sm, epoch);
   __syncthreads();
   if (blockIdx.x == 0 && threadIdx.x == 0) st_dev(p.ws + HDR_EPOCH, epoch);
 }
@@ -2933,16 +3058,16 @@ static int ensure_workspace(void* ws, size_t bytes, hipStream_t stream) {
   return PK_OK;
 }
 
-template <class G, bool BATCHED>
+template <class G, bool BATCHED, bool DBG = false>
 static int launch(const Params& p, hipStream_t stream) {
   static LaunchCache<G> cache;
   const void* fn;
   size_t lds;
   if constexpr (BATCHED) {
-    fn = reinterpret_cast<const void*>(decode_kernel_b<G>);
+    fn = reinterpret_cast<const void*>(decode_kernel_b<G, DBG>);
     lds = lds_bytes_b<G>();
   } else {
-    fn = reinterpret_cast<const void*>(decode_kernel<G>);
+    fn = reinterpret_cast<const void*>(decode_kernel<G, DBG>);
     lds = lds_bytes<G>();
   }
   int dev = 0;
@@ -2979,8 +3104,16 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
                        long long v_off, long long block_stride, long long token_stride,
                        long long head_stride, int block_size, const void* cos_sin, int cs_fp32,
                        void* out_hidden, void* layer_outputs, void* out_ids, void* out_logits,
-                       void* scratch, size_t scratch_bytes, int max_seq_len, const void* encoded_gu = nullptr) {
+                       void* scratch, size_t scratch_bytes, int max_seq_len, const void* encoded_gu = nullptr,
+                       void* debug = nullptr, size_t debug_bytes = 0, int debug_layer = -1) {
   if (B < 1 || B > (G::WF ? 1 : BMAX)) return PK_ERR_BATCH;  // MXFP8 weights: batch 1 only
+  if (debug_layer < -1 || debug_layer >= G::L) return PK_ERR_BLOCK;
+  if (debug) {  // per-stage capture: the reference's SmolLM2-360M bf16 layout, at most 2 sequences
+    if (G::WF || G::H != 960 || G::L != 32) return PK_ERR_DEBUG;
+    if (B > int(Dbg<G>::MB)) return PK_ERR_BATCH;
+    if (debug_bytes < Dbg<G>::TOTAL * 2) return PK_ERR_SCRATCH;
+    if (reinterpret_cast<uintptr_t>(debug) & 15u) return PK_ERR_ALIGN;
+  }
   // the lossless gate/up codec has the 360M gate_up shape [5120, 960]
   if (encoded_gu && (G::WF || G::H != 960 || G::I != 2560)) return PK_ERR_MODEL;
   if (n_layers < 1 || n_layers > G::L) return PK_ERR_MODEL;
@@ -3028,12 +3161,18 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
   p.max_seq = max_seq_len;
   p.trace = g_trace;
   p.encoded_gu = reinterpret_cast<const EncodedGULayer*>(encoded_gu);  // read by the batch-1 kernel
+  p.debug = reinterpret_cast<uint16_t*>(debug);
+  p.debug_layer = debug_layer;
   static_assert((WSB<G>::TOTAL * 4) % 16 == 0, "workspace is zero-filled in 16-byte units");
   const int st = ensure_workspace(scratch, WSB<G>::TOTAL * 4, reinterpret_cast<hipStream_t>(stream));
   if (st != PK_OK) return st;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if constexpr (G::WF == 0 && G::H == 960 && G::L == 32) {  // kernels with the capture compiled in
+    if (debug) return B > 1 ? launch<G, true, true>(p, s) : launch<G, false, true>(p, s);
+  }
   if constexpr (G::WF == 0)
-    if (B > 1) return launch<G, true>(p, reinterpret_cast<hipStream_t>(stream));
-  return launch<G, false>(p, reinterpret_cast<hipStream_t>(stream));
+    if (B > 1) return launch<G, true>(p, s);
+  return launch<G, false>(p, s);
 }
 
 }  // namespace pk
@@ -3136,6 +3275,30 @@ extern "C" int pk_decode_lossless(void* stream, int model, int B, int n_layers, 
                                    out_ids, out_logits, scratch, scratch_bytes, max_seq_len, encoded_gu_table);
 }
 
+extern "C" int pk_decode_debug(void* stream, int model, int B, int n_layers, const void* input_ids, int ids_i64,
+                               const void* embed, const void* final_norm, const void* positions,
+                               const void* seq_lens, const void* block_table, int bt_stride,
+                               const void* slot_mapping, const void* layers, void* const* kv, long long k_off,
+                               long long v_off, long long block_stride, long long token_stride,
+                               long long head_stride, int block_size, const void* cos_sin, int cs_fp32,
+                               void* out_hidden, void* layer_outputs, void* out_ids, void* out_logits,
+                               void* scratch, size_t scratch_bytes, int max_seq_len, const void* encoded_gu_table,
+                               void* debug, size_t debug_bytes, int debug_layer_index) {
+  if (model == PK_MODEL_SMOLLM2_360M)
+    return pk::decode_impl<pk::G360>(stream, B, n_layers, input_ids, ids_i64, embed, final_norm, positions,
+                                     seq_lens, block_table, bt_stride, slot_mapping, layers, kv, k_off, v_off,
+                                     block_stride, token_stride, head_stride, block_size, cos_sin, cs_fp32,
+                                     out_hidden, layer_outputs, out_ids, out_logits, scratch, scratch_bytes,
+                                     max_seq_len, encoded_gu_table, debug, debug_bytes, debug_layer_index);
+  if (model == PK_MODEL_SMOLLM2_135M)
+    return pk::decode_impl<pk::G135>(stream, B, n_layers, input_ids, ids_i64, embed, final_norm, positions,
+                                     seq_lens, block_table, bt_stride, slot_mapping, layers, kv, k_off, v_off,
+                                     block_stride, token_stride, head_stride, block_size, cos_sin, cs_fp32,
+                                     out_hidden, layer_outputs, out_ids, out_logits, scratch, scratch_bytes,
+                                     max_seq_len, encoded_gu_table, debug, debug_bytes, debug_layer_index);
+  return PK_ERR_MODEL;
+}
+
 extern "C" int pk_decode_mxfp8(void* stream, int model, int B, int n_layers, const void* input_ids, int ids_i64,
                                const void* embed, const void* final_norm, const void* positions,
                                const void* seq_lens, const void* block_table, int bt_stride,
@@ -3198,7 +3361,7 @@ extern "C" const char* prime_decode_status_string(int status) {
 }
 
 extern "C" size_t decode360_workspace_bytes(void) { return pk_workspace_bytes(PK_MODEL_SMOLLM2_360M); }
-extern "C" size_t decode360_debug_bytes(void) { return 0; }
+extern "C" size_t decode360_debug_bytes(void) { return pk::Dbg<pk::G360>::TOTAL * sizeof(uint16_t); }
 extern "C" const char* decode360_status_string(int status) { return prime_decode_status_string(status); }
 
 extern "C" int decode360(void* stream, int B, const void* input_ids, const void* embed, const void* final_norm,
@@ -3208,13 +3371,12 @@ extern "C" int decode360(void* stream, int B, const void* input_ids, const void*
                          int block_size, const void* cos_sin, int cs_fp32, void* out_hidden, void* layer_outputs,
                          void* scratch, size_t scratch_bytes, void* debug, size_t debug_bytes, int max_seq_len,
                          int debug_layer_index) {
-  (void)debug_bytes;
   if (debug_layer_index < -1 || debug_layer_index >= pk::G360::L) return PK_ERR_BLOCK;
-  if (debug) return PK_ERR_DEBUG;
-  return pk_decode(stream, PK_MODEL_SMOLLM2_360M, B, pk::G360::L, input_ids, 0, embed, final_norm, positions,
-                   seq_lens, block_table, bt_stride, slot_mapping, layers, kv, k_off, v_off, block_stride,
-                   token_stride, head_stride, block_size, cos_sin, cs_fp32, out_hidden, layer_outputs, nullptr,
-                   nullptr, scratch, scratch_bytes, max_seq_len);
+  return pk_decode_debug(stream, PK_MODEL_SMOLLM2_360M, B, pk::G360::L, input_ids, 0, embed, final_norm, positions,
+                         seq_lens, block_table, bt_stride, slot_mapping, layers, kv, k_off, v_off, block_stride,
+                         token_stride, head_stride, block_size, cos_sin, cs_fp32, out_hidden, layer_outputs, nullptr,
+                         nullptr, scratch, scratch_bytes, max_seq_len, nullptr, debug, debug_bytes,
+                         debug_layer_index);
 }
 
 extern "C" int decode360_lossless(void* stream, int B, const void* input_ids, const void* embed,
@@ -3225,13 +3387,12 @@ extern "C" int decode360_lossless(void* stream, int B, const void* input_ids, co
                                   int cs_fp32, void* out_hidden, void* layer_outputs, void* scratch,
                                   size_t scratch_bytes, void* debug, size_t debug_bytes, int max_seq_len,
                                   int debug_layer_index, const void* encoded_gu_table) {
-  (void)debug_bytes;
   if (debug_layer_index < -1 || debug_layer_index >= pk::G360::L) return PK_ERR_BLOCK;
-  if (debug) return PK_ERR_DEBUG;
-  return pk_decode_lossless(stream, PK_MODEL_SMOLLM2_360M, B, pk::G360::L, input_ids, 0, embed, final_norm,
-                            positions, seq_lens, block_table, bt_stride, slot_mapping, layers, kv, k_off, v_off,
-                            block_stride, token_stride, head_stride, block_size, cos_sin, cs_fp32, out_hidden,
-                            layer_outputs, nullptr, nullptr, scratch, scratch_bytes, max_seq_len, encoded_gu_table);
+  return pk_decode_debug(stream, PK_MODEL_SMOLLM2_360M, B, pk::G360::L, input_ids, 0, embed, final_norm, positions,
+                         seq_lens, block_table, bt_stride, slot_mapping, layers, kv, k_off, v_off, block_stride,
+                         token_stride, head_stride, block_size, cos_sin, cs_fp32, out_hidden, layer_outputs, nullptr,
+                         nullptr, scratch, scratch_bytes, max_seq_len, encoded_gu_table, debug, debug_bytes,
+                         debug_layer_index);
 }
 
 extern "C" size_t mk_workspace_bytes(int B, int max_seq_len) {

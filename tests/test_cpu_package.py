@@ -68,7 +68,9 @@ def test_status_strings_and_sizes():
     assert lib.decode360_workspace_bytes() == lib.pk_workspace_bytes(360) > 0
     assert lib.mk_workspace_bytes(1, 1024) == lib.pk_workspace_bytes(135) > 0
     assert lib.pk_workspace_bytes(7) == 0
-    assert lib.decode360_debug_bytes() == 0
+    # the reference's layout (block360_kernel.inc:1-20): 32 layers x 37,120 stage values, then the
+    # attention internals of one layer (2 x 960 + 3 x 2 x 15 x 8192 + 2 x 960), bf16
+    assert lib.decode360_debug_bytes() == 2 * (32 * 37120 + 2 * 960 + 3 * 2 * 15 * 8192 + 2 * 960)
 
 
 def _args(**over):
@@ -109,8 +111,15 @@ def test_reference_abi_validation():
     assert lib.decode360(*bad) == 9101
     bad = list(base); bad[-1] = 40
     assert lib.decode360(*bad) == 9109
-    bad = list(base); bad[24] = vp
-    assert lib.decode360(*bad) == 9111
+    dbg = lib.decode360_debug_bytes()
+    bad = list(base); bad[24] = vp                       # debug buffer too small
+    assert lib.decode360(*bad) == 9108
+    bad = list(base); bad[24] = 24; bad[25] = dbg        # misaligned debug buffer
+    assert lib.decode360(*bad) == 9107
+    bad = list(base); bad[1] = 3; bad[24] = vp; bad[25] = dbg  # capture holds 2 sequences
+    assert lib.decode360(*bad) == 9101
+    assert lib.pk_decode_debug(*_args(model=135), None, 16, dbg, -1) == 9111
+    assert lib.pk_decode_debug(*_args(), None, 16, dbg, 32) == 9109
     mk = [None, 17, vp, 1, vp, vp, vp, 64, vp, vp, vp, vp, vp, 0, 64, 10240, 128, 2048, 16, vp, 0, vp, vp, 1 << 40, 1024]
     assert lib.mk_decode(*mk) == 9101
 
@@ -194,7 +203,7 @@ def test_lossless_abi_validation_without_gpu():
              token_stride=128, head_stride=2048, block_size=16, cos_sin=16, cs_fp32=0, out_hidden=16,
              layer_outputs=None, scratch=16, scratch_bytes=1 << 40, debug=16, debug_bytes=1 << 20,
              max_seq_len=1024, debug_layer_index=-1, table=16)
-    assert lib.decode360_lossless(*d.values()) == 9111                # per-stage capture not built
+    assert lib.decode360_lossless(*d.values()) == 9108                # debug buffer too small
     d.update(debug=None, debug_layer_index=32)
     assert lib.decode360_lossless(*d.values()) == 9109
 
