@@ -9,6 +9,8 @@
  *       prime_kernels/decode_megakernel_360m/csrc/block360_kernel.inc:849-938
  *   mk_decode, mk_workspace_bytes, mk_status_string, mk_query
  *       prime_kernels/decode_megakernel/csrc/megakernel.cu:833-927
+ *   block360_decode, block360_workspace_bytes, block360_debug_bytes, block360_status_string
+ *       research/smollm2_360m_block/block360_kernel.inc:398-479
  * pk_decode / pk_workspace_bytes / pk_query are this library's superset of both (model choice,
  * layer count, LM head with greedy ids and optional logits); they have no single counterpart.
  */
@@ -144,6 +146,21 @@ int decode360(void* stream, int B, const void* input_ids, const void* embed, con
 size_t decode360_workspace_bytes(void);   /* block360_kernel.inc:849 */
 size_t decode360_debug_bytes(void);       /* block360_kernel.inc:850 */
 const char* decode360_status_string(int status);  /* block360_kernel.inc:925-938 */
+
+/* Research single-block ABI (research/smollm2_360m_block/block360_kernel.inc:399-470, same argument
+ * list): one SmolLM2-360M decoder block, hidden states [B, 960] in (B = 1, 2), the block output
+ * [B, 960] out (no final norm), `layer` a device table of the 6 layer pointers, `kv` that layer's
+ * paged cache.  `debug` (optional, block360_debug_bytes()) receives the block's stage layout
+ * (block360_kernel.inc:1-8): norm1, qkv, attn, h1, norm2, act, out, each [4][N] (row b = sequence
+ * b).  The scratch (block360_workspace_bytes()) follows pk_workspace_bytes' rules. */
+int block360_decode(void* stream, int B, const void* hidden, const void* positions, const void* seq_lens,
+                    const void* block_table, int bt_stride, const void* slot_mapping, const void* layer, void* kv,
+                    long long k_off, long long v_off, long long block_stride, long long token_stride,
+                    long long head_stride, int block_size, const void* cos_sin, int cs_fp32, void* out_hidden,
+                    void* scratch, size_t scratch_bytes, void* debug, size_t debug_bytes, int max_seq_len);
+size_t block360_workspace_bytes(void);        /* block360_kernel.inc:398 */
+size_t block360_debug_bytes(void);            /* block360_kernel.inc:399 */
+const char* block360_status_string(int status);
 
 /* SmolLM2-135M, 30 layers (megakernel.cu:844-851, same argument list). */
 int mk_decode(void* stream, int B, const void* input_ids, int ids_i64, const void* positions,

@@ -46,6 +46,11 @@ SIGNATURES = {
                        ci, vp, vp, sz, ci]),
     "mk_workspace_bytes": (sz, [ci, ci]),
     "mk_status_string": (ctypes.c_char_p, [ci]),
+    "block360_decode": (ci, [vp, ci, vp, vp, vp, vp, ci, vp, vp, vp, ll, ll, ll, ll, ll, ci, vp, ci, vp, vp, sz,
+                             vp, sz, ci]),
+    "block360_workspace_bytes": (sz, []),
+    "block360_debug_bytes": (sz, []),
+    "block360_status_string": (ctypes.c_char_p, [ci]),
     # include/prime_lossless.h
     "lossless_scan_workspace_bytes": (sz, []),
     "lossless_encode_layer": (ci, [vp, vp, vp, vp, vp, vp, vp, vp, sz, vp, ctypes.c_uint, vp]),

@@ -137,6 +137,7 @@ struct Params {
   const EncodedGULayer* encoded_gu;  // optional [L] lossless gate/up encodings (batch-1 bf16 kernel)
   uint16_t* debug;             // optional per-stage capture (Dbg layout), batch <= 2
   int debug_layer;             // layer whose attention internals are captured (-1: none)
+  const uint16_t* input_hidden;  // optional [B, H]: layer 0's input instead of the embedding rows
 };
 
 // Per-stage debug capture, the reference's layout (block360_kernel.inc:1-20), bf16 elements:
@@ -1453,7 +1454,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
         long long id = p.ids_i64 ? reinterpret_cast<const int64_t*>(p.input_ids)[b]
                                  : reinterpret_cast<const int32_t*>(p.input_ids)[b];
         id = min(max(id, 0LL), (long long)G::V - 1);  // an out-of-range id must not read past the table
-        const uint16_t* e = p.embed + size_t(id) * G::H;
+        const uint16_t* e = p.input_hidden ? p.input_hidden + size_t(b) * G::H : p.embed + size_t(id) * G::H;
         float s = 0.f;
         for (int i = C.ct; i < G::H; i += NCT) {
           const float v = bf2f(e[i]);
@@ -2654,7 +2655,8 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
         for (int i = C.ct; i < B * (G::H / 8); i += NCT) {
           const int b = i / (G::H / 8), c8 = i - b * (G::H / 8);
           *reinterpret_cast<uint4*>(sm.xs + b * G::H + c8 * 8) =
-              *reinterpret_cast<const uint4*>(p.embed + size_t(sm.sId[b]) * G::H + c8 * 8);
+              *reinterpret_cast<const uint4*>((p.input_hidden ? p.input_hidden + size_t(b) * G::H
+                                                              : p.embed + size_t(sm.sId[b]) * G::H) + c8 * 8);
         }
         C.cbar();
       } else {
@@ -3105,7 +3107,8 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
                        long long head_stride, int block_size, const void* cos_sin, int cs_fp32,
                        void* out_hidden, void* layer_outputs, void* out_ids, void* out_logits,
                        void* scratch, size_t scratch_bytes, int max_seq_len, const void* encoded_gu = nullptr,
-                       void* debug = nullptr, size_t debug_bytes = 0, int debug_layer = -1) {
+                       void* debug = nullptr, size_t debug_bytes = 0, int debug_layer = -1,
+                       const void* input_hidden = nullptr) {
   if (B < 1 || B > (G::WF ? 1 : BMAX)) return PK_ERR_BATCH;  // MXFP8 weights: batch 1 only
   if (debug_layer < -1 || debug_layer >= G::L) return PK_ERR_BLOCK;
   if (debug) {  // per-stage capture: the reference's SmolLM2-360M bf16 layout, at most 2 sequences
@@ -3128,7 +3131,7 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
     return PK_ERR_ALIGN;
   auto mis = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) != 0; };
   if (mis(embed) || mis(final_norm) || mis(layers) || mis(kv) || mis(out_hidden) || mis(scratch) ||
-      (encoded_gu && mis(encoded_gu)) ||
+      (encoded_gu && mis(encoded_gu)) || (input_hidden && mis(input_hidden)) ||
       (layer_outputs && mis(layer_outputs)) || (out_logits && mis(out_logits)))
     return PK_ERR_ALIGN;
   Params p{};
@@ -3163,6 +3166,7 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
   p.encoded_gu = reinterpret_cast<const EncodedGULayer*>(encoded_gu);  // read by the batch-1 kernel
   p.debug = reinterpret_cast<uint16_t*>(debug);
   p.debug_layer = debug_layer;
+  p.input_hidden = reinterpret_cast<const uint16_t*>(input_hidden);
   static_assert((WSB<G>::TOTAL * 4) % 16 == 0, "workspace is zero-filled in 16-byte units");
   const int st = ensure_workspace(scratch, WSB<G>::TOTAL * 4, reinterpret_cast<hipStream_t>(stream));
   if (st != PK_OK) return st;
@@ -3393,6 +3397,83 @@ extern "C" int decode360_lossless(void* stream, int B, const void* input_ids, co
                          token_stride, head_stride, block_size, cos_sin, cs_fp32, out_hidden, layer_outputs, nullptr,
                          nullptr, scratch, scratch_bytes, max_seq_len, encoded_gu_table, debug, debug_bytes,
                          debug_layer_index);
+}
+
+// ---- research single-block ABI (research/smollm2_360m_block/block360_kernel.inc:399-470) ----
+// One SmolLM2-360M decoder block from hidden states [B, H] to the block output [B, H] (B = 1, 2):
+// the decode kernels with the block's input in place of the embedding rows and the layer output
+// taken from their layer_outputs.  The scratch holds, after the decode workspace, the one-entry
+// cache table, a discarded final-normed hidden state and a capture area in the decode360 layout,
+// which a small kernel repacks into the block's own stage layout (block360_kernel.inc:1-8:
+// norm1, qkv, attn, h1, norm2, act, out, rows of 4 sequences).
+namespace pk {
+constexpr size_t BLK_MAXB = 4;
+constexpr size_t BLK_NORM1 = 0, BLK_QKV = BLK_NORM1 + BLK_MAXB * 960, BLK_ATTN = BLK_QKV + BLK_MAXB * 1600,
+                 BLK_H1 = BLK_ATTN + BLK_MAXB * 960, BLK_NORM2 = BLK_H1 + BLK_MAXB * 960,
+                 BLK_ACT = BLK_NORM2 + BLK_MAXB * 960, BLK_OUT = BLK_ACT + BLK_MAXB * 2560,
+                 BLK_DEBUG = BLK_OUT + BLK_MAXB * 960;
+constexpr size_t BLK_WS = (WSB<G360>::TOTAL * 4 + 255) / 256 * 256;    // decode workspace
+constexpr size_t BLK_KVT = BLK_WS;                                      // cache table (one pointer)
+constexpr size_t BLK_HID = BLK_KVT + 256;                               // discarded final hidden [2][960]
+constexpr size_t BLK_CAP = BLK_HID + 4096;                              // capture area (Dbg layout)
+constexpr size_t BLK_TOTAL = BLK_CAP + (Dbg<G360>::TOTAL * 2 + 255) / 256 * 256;
+
+__global__ void blk_table(void** slot, void* kv) {
+  if (threadIdx.x == 0) *slot = kv;
+}
+__global__ void __launch_bounds__(256) blk_repack(const uint16_t* cap, uint16_t* dbg, int B) {
+  using D = Dbg<G360>;
+  const size_t src[7] = {D::NORM1, D::QKV, D::ATTN, D::H1, D::NORM2, D::ACT, D::OUT};
+  const size_t dst[7] = {BLK_NORM1, BLK_QKV, BLK_ATTN, BLK_H1, BLK_NORM2, BLK_ACT, BLK_OUT};
+  const int n[7] = {960, 1600, 960, 960, 960, 2560, 960};
+  for (int st = 0; st < 7; ++st)
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < B * n[st]; i += gridDim.x * 256) {
+      const int b = i / n[st], e = i - b * n[st];
+      dbg[dst[st] + size_t(b) * n[st] + e] = cap[src[st] + size_t(b) * n[st] + e];
+    }
+}
+}  // namespace pk
+
+extern "C" size_t block360_workspace_bytes(void) { return pk::BLK_TOTAL; }
+extern "C" size_t block360_debug_bytes(void) { return pk::BLK_DEBUG * sizeof(uint16_t); }
+extern "C" const char* block360_status_string(int status) { return prime_decode_status_string(status); }
+
+extern "C" int block360_decode(void* stream, int B, const void* hidden, const void* positions, const void* seq_lens,
+                               const void* block_table, int bt_stride, const void* slot_mapping, const void* layer,
+                               void* kv, long long k_off, long long v_off, long long block_stride,
+                               long long token_stride, long long head_stride, int block_size, const void* cos_sin,
+                               int cs_fp32, void* out_hidden, void* scratch, size_t scratch_bytes, void* debug,
+                               size_t debug_bytes, int max_seq_len) {
+  if (B < 1 || B > 2) return PK_ERR_BATCH;
+  if (max_seq_len < 1 || max_seq_len > pk::kMaxSeq) return PK_ERR_MAX_SEQ;
+  if (!hidden || !positions || !seq_lens || !block_table || !slot_mapping || !layer || !kv || !cos_sin ||
+      !out_hidden || !scratch)
+    return PK_ERR_NULL;
+  if (scratch_bytes < pk::BLK_TOTAL || (debug && debug_bytes < block360_debug_bytes())) return PK_ERR_SCRATCH;
+  auto mis = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) != 0; };
+  if (mis(hidden) || mis(layer) || mis(kv) || mis(out_hidden) || mis(scratch) || (debug && mis(debug)))
+    return PK_ERR_ALIGN;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  uint8_t* ws = static_cast<uint8_t*>(scratch);
+  // first sight of the workspace (zero fill, or the capture refusal) before anything is launched
+  const int first = pk::ensure_workspace(scratch, pk::WSB<pk::G360>::TOTAL * 4, s);
+  if (first != PK_OK) return first;
+  void** kvt = reinterpret_cast<void**>(ws + pk::BLK_KVT);
+  pk::blk_table<<<1, 64, 0, s>>>(kvt, kv);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  // The block has no final norm: the decode kernel's final-normed output goes to a discarded area
+  // (its norm weights: any readable [960] bf16 array, here the input itself).
+  int st = pk::decode_impl<pk::G360>(stream, B, 1, hidden, 0, hidden, hidden, positions, seq_lens, block_table,
+                                      bt_stride, slot_mapping, layer, kvt, k_off, v_off, block_stride, token_stride,
+                                      head_stride, block_size, cos_sin, cs_fp32, ws + pk::BLK_HID, out_hidden,
+                                      nullptr, nullptr, ws, pk::BLK_WS, max_seq_len, nullptr,
+                                      debug ? ws + pk::BLK_CAP : nullptr, debug ? pk::Dbg<pk::G360>::TOTAL * 2 : 0,
+                                      debug ? 0 : -1, hidden);
+  if (st != PK_OK || !debug) return st;
+  pk::blk_repack<<<32, 256, 0, s>>>(reinterpret_cast<const uint16_t*>(ws + pk::BLK_CAP),
+                                    static_cast<uint16_t*>(debug), B);
+  return hipGetLastError();
 }
 
 extern "C" size_t mk_workspace_bytes(int B, int max_seq_len) {

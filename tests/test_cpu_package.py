@@ -218,3 +218,23 @@ def test_lossless_modules_on_cpu():
         L.prepare_weights([()] * 3)
     with pytest.raises(ValueError):
         LB.EncodedGUCache([torch.zeros(5120, 960, dtype=torch.bfloat16)] * 2)
+
+
+def test_block360_abi_validation_without_gpu():
+    """The research single-block ABI: sizes and the checks that return before any GPU call."""
+    lib = _native.library()
+    assert lib.block360_debug_bytes() == 2 * 4 * (5 * 960 + 1600 + 2560)
+    ws = lib.block360_workspace_bytes()
+    assert ws >= lib.pk_workspace_bytes(360) + lib.decode360_debug_bytes()
+    a = dict(stream=None, B=1, hidden=16, positions=16, seq_lens=16, block_table=16, bt_stride=64, slot_mapping=16,
+             layer=16, kv=16, k_off=0, v_off=64, block_stride=10240, token_stride=128, head_stride=2048,
+             block_size=16, cos_sin=16, cs_fp32=0, out_hidden=16, scratch=16, scratch_bytes=ws, debug=None,
+             debug_bytes=0, max_seq_len=1024)
+    call = lambda **o: lib.block360_decode(*dict(a, **o).values())
+    assert call(B=3) == 9101
+    assert call(max_seq_len=0) == 9102
+    assert call(hidden=None) == 9103
+    assert call(scratch_bytes=ws - 1) == 9108
+    assert call(debug=16, debug_bytes=16) == 9108
+    assert call(out_hidden=24) == 9107
+    assert lib.block360_status_string(9101).decode() == "batch_out_of_range"
