@@ -273,6 +273,16 @@ __device__ __forceinline__ void st_dev64(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// Stores into caller memory through a pointer read from LDS (the KV cache base): without the
+// explicit global address space the compiler emits a flat store, which also counts on the LDS
+// counter, so the wave's next wait for an LDS read would also wait for this store's completion.
+typedef __attribute__((address_space(1))) u32x4 g_u32x4;
+typedef __attribute__((address_space(1))) uint16_t g_u16;
+__device__ __forceinline__ void st_global16(uint16_t* dst, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  const u32x4 v = {a, b, c, d};
+  *(g_u32x4*)(dst) = v;
+}
+__device__ __forceinline__ void st_global2(uint16_t* dst, uint16_t v) { *(g_u16*)(dst) = v; }
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
 }
@@ -1162,12 +1172,12 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
     }
     uint16_t* dst = cache + e;
     if ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
-      *reinterpret_cast<uint4*>(dst) = make_uint4(val[0], val[1], val[2], val[3]);
+      st_global16(dst, val[0], val[1], val[2], val[3]);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        dst[2 * i] = uint16_t(val[i] & 0xffffu);
-        dst[2 * i + 1] = uint16_t(val[i] >> 16);
+        st_global2(dst + 2 * i, uint16_t(val[i] & 0xffffu));
+        st_global2(dst + 2 * i + 1, uint16_t(val[i] >> 16));
       }
     }
   }
@@ -2359,10 +2369,13 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
         }
         uint16_t* dst = cache + e + piece * 8;
         if ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
-          *reinterpret_cast<uint4*>(dst) = make_uint4(val[0], val[1], val[2], val[3]);
+          st_global16(dst, val[0], val[1], val[2], val[3]);
         } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) { dst[2 * i] = uint16_t(val[i] & 0xffffu); dst[2 * i + 1] = uint16_t(val[i] >> 16); }
+          for (int i = 0; i < 4; ++i) {
+            st_global2(dst + 2 * i, uint16_t(val[i] & 0xffffu));
+            st_global2(dst + 2 * i + 1, uint16_t(val[i] >> 16));
+          }
         }
       }
     }
