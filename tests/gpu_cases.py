@@ -178,9 +178,10 @@ def greedy_ok(kernel_id: int, ref_logits: torch.Tensor, tol: float = LOGIT_ATOL)
 
 
 def random_kv_case(geom: O.Geometry, seed: int, contexts, *, max_pos: int | None = None, norm_jitter=0.05,
-                   fill_seed: int | None = None, extra_blocks: int = 0) -> Case:
+                   fill_seed: int | None = None, extra_blocks: int = 0, capacity: int | None = None) -> Case:
+    """`capacity`: tokens the block table addresses (default: the longest context + 16)."""
     w = O.make_weights(geom, seed, norm_jitter=norm_jitter)
-    cap = max(contexts) + 16
+    cap = capacity if capacity is not None else max(contexts) + 16
     kv = O.make_paged_kv(geom, len(contexts), cap, seed=fill_seed if fill_seed is not None else seed + 3,
                          extra_blocks=extra_blocks)
     return Case(geom, w, kv, max_pos or cap + 16)

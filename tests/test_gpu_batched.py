@@ -151,3 +151,42 @@ def test_batched_full_360m_config4_teacher_forced_layers():
         c = GC.compare_logits(k["logits"][b][keep], r["logits"][b][keep])
         assert c["max_abs"] <= GC.LOGIT_ATOL and c["cos"] >= GC.COS_MIN, (b, c)
     print("config4 teacher-forced mean bit-identical fraction", round(sum(fracs) / len(fracs), 4))
+
+
+def test_batched_max_context_and_edges():
+    """Batch 3 with one sequence at the longest context (12288), one of 3 tokens and one of 700."""
+    _need_gpu()
+    geom = O.with_layers(O.SMOLLM2_360M, 2)
+    contexts = [12288, 3, 700]
+    case = GC.random_kv_case(geom, 303, contexts, capacity=12288)
+    ids = [5, 6, 7]
+    pos = [S - 1 for S in contexts]
+    k = case.kernel_step(ids, pos, layer_outputs=True)
+    f = case.eager_gpu_step(ids, pos)
+    r = case.oracle_step(ids, pos, layer_outputs=True)
+    GC.assert_within_floor(k, r, f, "batched max context")
+    _kv_appends_match(case, contexts, "max context")
+
+
+def test_batched_slot_minus_one_int32_ids_fp32_rope():
+    """Batched step: slot_mapping < 0 skips that sequence's K/V write and leaves its result unchanged;
+    int32 ids and an fp32 cos/sin table give the identical result."""
+    _need_gpu()
+    geom = O.with_layers(O.SMOLLM2_360M, 2)
+    contexts = [300, 41, 129]
+    case = GC.random_kv_case(geom, 305, contexts)
+    ids = [11, 12, 13]
+    pos = [S - 1 for S in contexts]
+    slots = [case.kv.slot(b, pos[b]) for b in range(3)]
+    before = [c.clone() for c in case.kvd]
+    k1 = case.kernel_step(ids, pos, slot_mapping=[slots[0], -1, slots[2]])
+    for li, (a, c) in enumerate(zip(before, case.kvd)):
+        s = slots[1]
+        assert torch.equal(a[s // 16, :, s % 16], c[s // 16, :, s % 16]), li
+        for b in (0, 2):
+            s = slots[b]
+            assert not torch.equal(a[s // 16, :, s % 16], c[s // 16, :, s % 16]), (li, b)
+    k2 = case.kernel_step(ids, pos)
+    assert torch.equal(k1["logits"], k2["logits"]) and torch.equal(k1["ids"], k2["ids"])
+    k3 = case.kernel_step(ids, pos, ids_dtype=torch.int32, cs_fp32=True)
+    assert torch.equal(k3["logits"], k2["logits"]) and torch.equal(k3["hidden"], k2["hidden"])
