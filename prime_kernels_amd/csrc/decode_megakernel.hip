@@ -1866,7 +1866,7 @@ struct SmemB {
   float lm_val[NCW][BMAX];
   int32_t lm_idx[NCW][BMAX];
   uint32_t front[NPW];
-  uint32_t consumed[NCW];
+  alignas(16) uint32_t consumed[NCW];
   uint32_t cbar;
 };
 // Attention items at the largest batch and context: each (sequence, KV head) has at most
@@ -1983,12 +1983,18 @@ __device__ __forceinline__ void producer_b(const Params& p, const PlanB<G>& P, S
   uint32_t n = 0;
   Spin spin(p.ws, 1);
   bool dead = false;
+  // Lowest stream position released by every consumer wave, in one 16-byte LDS read.  A stale value
+  // is a lower bound (each wave's position only grows), so the last one read is kept in `avail`
+  // and read again only when the next packet would pass it: the issue loop does no LDS round trip
+  // per packet.  The DMA that reuses released bytes is issued after the read returns, and the
+  // consumers' release stores follow their reads of those bytes.
+  static_assert(NCW == 4, "one 16-byte read of the consumer positions");
   auto cmin = [&]() -> uint32_t {
-    uint32_t c = ld_lds(&sm.consumed[0]);
-#pragma unroll
-    for (int w = 1; w < NCW; ++w) c = min(c, ld_lds(&sm.consumed[w]));
-    return c;
+    typedef __attribute__((address_space(3))) const volatile u32x4 lds_u32x4;
+    const u32x4 c = *(lds_u32x4*)(sm.consumed);
+    return min(min(c.x, c.y), min(c.z, c.w));
   };
+  uint32_t avail = 0;  // last cmin() + ring bytes: packets ending at or below it may be issued
   auto publish = [&](uint32_t first_pending_packet) {
     if (lane == 0) st_lds(&sm.front[pw], first_pending_packet * PKT);
   };
@@ -2022,10 +2028,10 @@ __device__ __forceinline__ void producer_b(const Params& p, const PlanB<G>& P, S
     const uint32_t cs_row = p.cs_fp32 ? 256u : 128u;
     for (uint32_t i = (uint32_t(pw) + NPW - n % NPW) % NPW; i < npk && !dead; i += NPW) {
       const uint32_t gn = n + i;
-      if ((gn + 1) * PKT > cmin() + RING_B) {
+      if ((gn + 1) * PKT > avail && (gn + 1) * PKT > (avail = cmin() + RING_B)) {
         wait_vmcnt<0>();
         publish(gn);
-        while ((gn + 1) * PKT > cmin() + RING_B)
+        while ((gn + 1) * PKT > (avail = cmin() + RING_B))
           if (!spin.again()) { dead = true; break; }
         if (dead) break;
       }
