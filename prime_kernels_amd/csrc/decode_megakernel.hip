@@ -483,7 +483,7 @@ struct Smem {
   int32_t blk[TC_MAX / 16 + 2];
   float lm_val[NCW];
   int32_t lm_idx[NCW];
-  uint32_t front[NPW];           // per producer wave: stream bytes below which its packets landed
+  alignas(16) uint32_t front[NPW];  // per producer wave: stream bytes below which its packets landed
   uint32_t consumed[NCW];
   uint32_t cbar;
 };
@@ -667,17 +667,23 @@ struct Consumer {
     pos += pad_pkt(bytes);
     return s;
   }
+  // Lowest stream position landed in the ring over the producer waves, in one 16-byte LDS read.
+  // The producers publish a position after their DMA into LDS completed, so every ring byte below
+  // a value read here is in place; the last value is kept in `seen` (positions only grow) and a
+  // wait for bytes below it needs no LDS read at all.
+  static_assert(NPW == 4, "one 16-byte read of the producer positions");
+  uint32_t seen = 0;
   __device__ __forceinline__ uint32_t filled() const {
-    uint32_t f = ld_lds(&sm.front[0]);
-#pragma unroll
-    for (int w = 1; w < NPW; ++w) f = min(f, ld_lds(&sm.front[w]));
-    return f;
+    typedef __attribute__((address_space(3))) const volatile u32x4 lds_u32x4;
+    const u32x4 f = *(lds_u32x4*)(sm.front);
+    return min(min(f.x, f.y), min(f.z, f.w));
   }
   __device__ __forceinline__ void wait_filled(uint32_t end) {
-    if (dead) return;
+    if (dead || end <= seen) return;
     Spin spin(p.ws, 2);
-    while (filled() < end)
+    while ((seen = filled()) < end)
       if (!spin.again()) { dead = true; return; }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the ring reads that follow stay after the wait
   }
   __device__ __forceinline__ void release(uint32_t end) {
     wait_lgkm0();  // ring reads of this wave have returned
@@ -1865,7 +1871,7 @@ struct SmemB {
   long long sSlot[BMAX];
   float lm_val[NCW][BMAX];
   int32_t lm_idx[NCW][BMAX];
-  uint32_t front[NPW];
+  alignas(16) uint32_t front[NPW];
   alignas(16) uint32_t consumed[NCW];
   uint32_t cbar;
 };
