@@ -1106,9 +1106,11 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   float* in = sm.at.qkvw[w];
 
   const int part = lane & 7, grp = lane >> 3;
-  // queries of the 3 heads -> in[0, 192); the new key -> in[192, 256) and value -> in[256, 320).
-  // The wave with the new token is the leader's last wave (edge(3) < T), which also appends K/V.
-  C.poll_wave3(l, b, g * 192, 192, G::H + g * 64, has_new ? 64 : 0, G::H + G::KVH * 64 + g * 64, has_new ? 64 : 0, in);
+  // queries of the 3 heads -> in[0, 192).  The wave with the new token (the leader's last wave,
+  // edge(3) < T) fetches the new key and value -> in[192, 320) only after the scores of its cached
+  // tokens: those words come from other writers than q and often land later, so the wait overlaps
+  // the scores instead of preceding them.
+  C.poll_wave3(l, b, g * 192, 192, 0, 0, 0, 0, in);
   C.wait_filled(C.pos);  // cos/sin row and KV chunk are in the ring
   // cos/sin of dims 8*part .. 8*part+7 (mod 32): contiguous in the table row of this position
   float cs8[8], sn8[8];
@@ -1150,11 +1152,10 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   };
   wait_lgkm0();
   if (w == 0 && lane == 0) trace_at(p, l, 3, p.n_layers);
-  // rotated queries and (for the wave with the new token) the rotated new key, packed bf16 pairs
+  // rotated queries (and, further down, the rotated new key), packed bf16 pairs
   uint32_t q[3][4], kn[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int h = 0; h < 3; ++h) rope8(in + h * 64, q[h]);
-  if (has_new) rope8(in + 192, kn);
   // debug capture of layer debug_layer: rotated queries (chunk 0 of each KV head, lanes 0-7)
   const bool dbg_attn = DBG && p.debug != nullptr && l == p.debug_layer;
   if (dbg_attn && P.c == 0 && w == 0 && grp == 0)
@@ -1162,36 +1163,9 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
     for (int h = 0; h < 3; ++h)
       *reinterpret_cast<uint4*>(p.debug + Dbg<G>::AQ + (g * 3 + h) * 64 + part * 8) =
           make_uint4(q[h][0], q[h][1], q[h][2], q[h][3]);
-  if (has_new && P.slot >= 0 && grp < 2) {
-    // KV append at slot_mapping[b] (block360_kernel.inc:124-135; slot < 0 skips): lanes 0-7 store
-    // the rotated new K, lanes 8-15 the new V, 8 dims (16 bytes) per lane
-    uint16_t* cache = reinterpret_cast<uint16_t*>(const_cast<void*>(sm.kvp[l]));
-    const long long e = (P.slot / 16) * p.block_stride + (P.slot % 16) * p.token_stride +
-                        (long long)g * p.head_stride + (grp ? p.v_off : p.k_off) + part * 8;
-    uint32_t val[4];
-    if (grp == 0) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) val[i] = kn[i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) val[i] = pack2(in[256 + part * 8 + 2 * i], in[256 + part * 8 + 2 * i + 1]);
-    }
-    uint16_t* dst = cache + e;
-    if ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
-      st_global16(dst, val[0], val[1], val[2], val[3]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        st_global2(dst + 2 * i, uint16_t(val[i] & 0xffffu));
-        st_global2(dst + 2 * i + 1, uint16_t(val[i] >> 16));
-      }
-    }
-  }
   if (w == 0 && lane == 0) trace_at(p, l, 16, p.n_layers);
   // scores: 8 lanes per token (8 dims each), 8 tokens per pass; s = bf16(q.k) * 1/8 (exact scale)
-  for (int jb = j0; jb < j1; jb += 8) {
-    const int j = jb + grp;
-    const uint4 k = j < T_old ? C.ring16(seg + kv_slot(j, 0, part)) : make_uint4(kn[0], kn[1], kn[2], kn[3]);
+  auto score = [&](int j, const uint4& k, bool keep) {
     float s3[3];
 #pragma unroll
     for (int h = 0; h < 3; ++h) {
@@ -1201,7 +1175,7 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
       a = dot2(q[h][3], k.w, a);
       s3[h] = group8_sum(a);
     }
-    if (part == 0 && j < j1)
+    if (part == 0 && keep)
 #pragma unroll
       for (int h = 0; h < 3; ++h) {
         sm.at.sc[h][j] = rnd(s3[h]) * 0.125f;
@@ -1210,6 +1184,18 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
           p.debug[Dbg<G>::ASC + Dbg<G>::head_pos(b, g * 3 + h, P.t0 + j)] = uint16_t(f2bf(rnd(s3[h]) * 0.125f));
         }
       }
+  };
+  const int jc = min(j1, T_old);  // this wave's cached tokens end here
+  for (int jb = j0; jb < jc; jb += 8) {
+    const int j = jb + grp;
+    score(j, j < jc ? C.ring16(seg + kv_slot(j, 0, part)) : make_uint4(0u, 0u, 0u, 0u), j < jc);
+  }
+  if (has_new) {
+    // the new key and value, RoPE on the key, and its score (every 8-lane group computes it; the
+    // first group keeps it)
+    C.poll_wave3(l, b, G::H + g * 64, 64, G::H + G::KVH * 64 + g * 64, 64, 0, 0, in + 192);
+    rope8(in + 192, kn);
+    score(T_old, make_uint4(kn[0], kn[1], kn[2], kn[3]), grp == 0);
   }
   wait_lgkm0();
   if (w == 0 && lane == 0) trace_at(p, l, 17, p.n_layers);
@@ -1366,6 +1352,33 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
     acc[h][1] += __shfl_xor(acc[h][1], 32);
   }
   C.release(C.pos);  // this wave no longer reads the K/V chunk
+  if (has_new && P.slot >= 0 && grp < 2) {
+    // KV append at slot_mapping[b] (block360_kernel.inc:124-135; slot < 0 skips): lanes 0-7 store
+    // the rotated new K, lanes 8-15 the new V, 8 dims (16 bytes) per lane.  Issued after the
+    // scores and P.V: a later wait on this wave's memory counter would otherwise hold those
+    // phases until the stores are acknowledged.
+    uint16_t* cache = reinterpret_cast<uint16_t*>(const_cast<void*>(sm.kvp[l]));
+    const long long e = (P.slot / 16) * p.block_stride + (P.slot % 16) * p.token_stride +
+                        (long long)g * p.head_stride + (grp ? p.v_off : p.k_off) + part * 8;
+    uint32_t val[4];
+    if (grp == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) val[i] = kn[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) val[i] = pack2(in[256 + part * 8 + 2 * i], in[256 + part * 8 + 2 * i + 1]);
+    }
+    uint16_t* dst = cache + e;
+    if ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+      st_global16(dst, val[0], val[1], val[2], val[3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        st_global2(dst + 2 * i, uint16_t(val[i] & 0xffffu));
+        st_global2(dst + 2 * i + 1, uint16_t(val[i] >> 16));
+      }
+    }
+  }
   if (lane < 32)
 #pragma unroll
     for (int h = 0; h < 3; ++h) {
