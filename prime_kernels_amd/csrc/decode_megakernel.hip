@@ -81,7 +81,13 @@ constexpr uint32_t RING = 128u * 1024u;  // LDS ring bytes (power of two)
 constexpr uint32_t PKT = 1024;           // one LDS-DMA instruction: 64 lanes x 16 B
 constexpr int DEPTH = PK_DMA_DEPTH;      // packets in flight per producer wave
 constexpr int TC_MAX = 256;              // max cached tokens per attention chunk (64 KB of K/V)
-constexpr int TC_TARGET = 64;            // preferred tokens per chunk
+// Batch-1 chunking of a KV head's cached tokens: chunks of up to TC_LONG tokens, but at least
+// C_SHORT chunks of at least TC_SHORT tokens while the context allows (measured at 360M batch 1:
+// short contexts gain from more chunks, long ones from fewer; the two exchanges between a head's
+// chunks cost more with every chunk)
+constexpr int TC_LONG = 128;
+constexpr int TC_SHORT = 64;
+constexpr int C_SHORT = 8;
 constexpr int LM_ROWS = 16;              // LM-head rows per ring segment
 constexpr int MAX_B = 16;                // exchange-buffer slots per layer
 constexpr int REC_WORDS = 3 * 64;        // attention partial: 3 heads x sum(p.v)[64], 64-bit words
@@ -351,7 +357,7 @@ struct Plan {
     pos = int(max(p.positions[0], (int64_t)0));
     slot = p.slot_mapping[0];
     const int old = S - 1;
-    int C0 = old <= 0 ? 1 : (old + TC_TARGET - 1) / TC_TARGET;
+    int C0 = old <= 0 ? 1 : max((old + TC_LONG - 1) / TC_LONG, min((old + TC_SHORT - 1) / TC_SHORT, C_SHORT));
     C0 = min(C0, NWG / G::KVH);
     const int tc = old <= 0 ? 16 : ((old + C0 - 1) / C0 + 15) / 16 * 16;
     C = old <= 0 ? 1 : (old + tc - 1) / tc;

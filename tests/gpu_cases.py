@@ -225,6 +225,38 @@ def assert_within_floor(kres: dict, rres: dict, floor: dict, label: str = "") ->
     return out if len(out) > 1 else out[0]
 
 
+SEED_SET_HARD_ATOL = 2 * LOGIT_ATOL   # no case of a seed set may exceed this
+SEED_SET_MEAN_FACTOR = 1.5            # mean error at most this multiple of eager-GPU's (or LOGIT_ATOL / 2)
+
+
+def assert_seed_set_parity(cases: list, label: str = "") -> dict:
+    """Parity of a shallow model over a set of seeds, each case a (kernel, eager_gpu, oracle) triple
+    of single-sequence step results.  At two random-init layers the north-star bound sits at the
+    noise level of accumulation order: one bf16 rounding that flips early in layer 0 spreads
+    one-ulp differences through the step and moves the logits by 0.015-0.025, and over 60 seeded
+    2-layer 360M steps (bf16 and MXFP8, contexts 1025..2049) PyTorch eager on the GPU exceeds
+    LOGIT_ATOL against the CPU oracle on 3 and the kernel on 2; which seeds do changes whenever
+    either side's summation order changes.  So every case must meet COS_MIN, pick the oracle's
+    greedy id (or a near-tie) and stay within SEED_SET_HARD_ATOL, and the mean logits error over
+    the set may be at most SEED_SET_MEAN_FACTOR times eager-GPU's mean on the same seeds (or
+    LOGIT_ATOL / 2, whichever is larger)."""
+    errs, floors = [], []
+    for i, (k, e, r) in enumerate(cases):
+        c = compare_logits(k["logits"][0], r["logits"][0])
+        f = compare_logits(e["logits"][0], r["logits"][0])
+        assert c["cos"] >= COS_MIN, f"{label} case {i}: logits cosine {c['cos']}"
+        assert c["max_abs"] <= SEED_SET_HARD_ATOL, f"{label} case {i}: logits max abs err {c['max_abs']}"
+        assert greedy_ok(int(k["ids"][0]), r["logits"][0]), \
+            f"{label} case {i}: greedy id {int(k['ids'][0])} vs oracle {int(r['ids'][0])}"
+        errs.append(c["max_abs"])
+        floors.append(f["max_abs"])
+    mean, floor = sum(errs) / len(errs), sum(floors) / len(floors)
+    bar = max(LOGIT_ATOL / 2, SEED_SET_MEAN_FACTOR * floor)
+    assert mean <= bar, f"{label}: mean logits max abs err {mean} > {bar} (eager GPU mean {floor})"
+    return {"cases": len(cases), "mean": mean, "eager_mean": floor, "worst": max(errs),
+            "over_atol": sum(x > LOGIT_ATOL for x in errs), "eager_over_atol": sum(x > LOGIT_ATOL for x in floors)}
+
+
 def identical_fraction(a: torch.Tensor, b: torch.Tensor) -> float:
     return float((a.to(BF16).view(torch.int16) == b.to(BF16).view(torch.int16)).float().mean().item())
 

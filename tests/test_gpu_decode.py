@@ -82,7 +82,7 @@ def test_golden_greedy_teacher_forced(golden, key):
             case.kvd[li][slot // 16, :, slot % 16, geom.head_dim:] = from_bits(g["step_v"][step][li]).to(case.dev)
 
 
-@pytest.mark.parametrize("S", [1, 2, 3, 17, 64, 65, 129, 1025, 4097, 8448])
+@pytest.mark.parametrize("S", [1, 2, 3, 17, 64, 65, 129, 600, 1025, 1157, 2049, 4097, 8448])
 def test_context_lengths_two_layers(S):
     """Chunking edge cases of the split-KV attention (one chunk, partial chunks, many chunks,
     the BASELINE config-5 context) on a 2-layer 360M model with random N(0,1) cached K/V."""
