@@ -140,6 +140,7 @@ struct Params {
   int max_seq;                 // block_table capacity in tokens (seq_lens are clamped to it)
   int ids_i64;
   unsigned long long* trace;   // optional per-phase timestamps (diagnostics)
+  uint32_t trace_lds;          // LDS byte offset of the launch's timestamp buffer (when tracing)
   const EncodedGULayer* encoded_gu;  // optional [L] lossless gate/up encodings (batch-1 bf16 kernel)
   uint16_t* debug;             // optional per-stage capture (Dbg layout), batch <= 2
   int debug_layer;             // layer whose attention internals are captured (-1: none)
@@ -319,13 +320,42 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
-// Diagnostic timestamps: TR_EVENTS per layer per workgroup, plus TR_TAIL at the end.
+// Diagnostic timestamps: TR_EVENTS per layer per workgroup, plus TR_TAIL at the end.  During the
+// launch they are kept in LDS, past the kernel's own shared memory, as the low 32 bits of the
+// 100 MHz clock, and written out as full 64-bit values when the workgroup ends: a global store
+// per event would add its acknowledgement to the next wait on the wave's memory counter, and so
+// stretch the phases being timed.
 constexpr int TR_EVENTS = 40;
 constexpr int TR_TAIL = 4;
+constexpr int TR_LAYERS = 32;
+constexpr uint32_t TRACE_LDS_BYTES = uint32_t(TR_LAYERS * TR_EVENTS + TR_TAIL) * 4u;
+__device__ __forceinline__ uint32_t* trace_lds(const Params& p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
+  return reinterpret_cast<uint32_t*>(smem_raw + p.trace_lds);
+}
 __device__ __forceinline__ void trace_at(const Params& p, int layer, int ev, int n_layers) {
+  if (p.trace) trace_lds(p)[layer * TR_EVENTS + ev] = uint32_t(wall_clock64());
+}
+__device__ __forceinline__ void trace_tail(const Params& p, int k) {
+  if (p.trace) trace_lds(p)[p.n_layers * TR_EVENTS + k] = uint32_t(wall_clock64());
+}
+// Before the workgroup's first barrier: clear the buffer (0 = event not reached).
+__device__ __forceinline__ void trace_begin(const Params& p) {
   if (p.trace)
-    p.trace[size_t(blockIdx.x) * (size_t(n_layers) * TR_EVENTS + TR_TAIL) + size_t(layer) * TR_EVENTS + ev] =
-        wall_clock64();
+    for (int i = threadIdx.x; i < p.n_layers * TR_EVENTS + TR_TAIL; i += blockDim.x) trace_lds(p)[i] = 0u;
+}
+// After the workgroup's last barrier: full timestamps, each the latest clock value with its low bits
+// (the launch is far shorter than the 43 s the low 32 bits cover).
+__device__ __forceinline__ void trace_end(const Params& p) {
+  if (!p.trace) return;
+  const uint64_t now = wall_clock64();
+  const int n = p.n_layers * TR_EVENTS + TR_TAIL;
+  const uint32_t* t = trace_lds(p);
+  unsigned long long* out = p.trace + size_t(blockIdx.x) * size_t(n);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const uint32_t lo = t[i];
+    out[i] = lo ? now - uint64_t(uint32_t(uint32_t(now) - lo)) : 0ull;
+  }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1119,8 +1149,7 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   C.poll_wave3(l, b, g * 192, 192, 0, 0, 0, 0, in);
   C.wait_filled(C.pos);  // cos/sin row and KV chunk are in the ring
   // cos/sin of dims 8*part .. 8*part+7 (mod 32): contiguous in the table row of this position
-  float cs8[8], sn8[8];
-  {
+  auto load_cs = [&](float (&cs8)[8], float (&sn8)[8]) {
     const uint32_t f0 = uint32_t(part & 3) * 8u;
     if (p.cs_fp32) {
       const uint4 c0 = C.ring16(segc + f0 * 4u), c1 = C.ring16(segc + f0 * 4u + 16u);
@@ -1138,12 +1167,12 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
         sn8[2 * e] = bf_lo(su[e]); sn8[2 * e + 1] = bf_hi(su[e]);
       }
     }
-  }
+  };
   // RoPE with HF rounding, bf16(bf16(x*cos) + bf16(rotate_half(x)*sin)) (modeling_llama.py:138-160):
   // this lane's dims 8*part..+7 of a head and their rotation partners 8*(part^4)..+7, as float4s;
   // rotate_half negates the partner for the first half (dims < 32).
   const float sgn = part < 4 ? -1.f : 1.f;
-  auto rope8 = [&](const float* head, uint32_t (&out)[4]) {
+  auto rope8 = [&](const float* head, const float (&cs8)[8], const float (&sn8)[8], uint32_t (&out)[4]) {
     const float4 a0 = *reinterpret_cast<const float4*>(head + part * 8);
     const float4 a1 = *reinterpret_cast<const float4*>(head + part * 8 + 4);
     const float4 b0 = *reinterpret_cast<const float4*>(head + (part ^ 4) * 8);
@@ -1160,8 +1189,12 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   if (w == 0 && lane == 0) trace_at(p, l, 3, p.n_layers);
   // rotated queries (and, further down, the rotated new key), packed bf16 pairs
   uint32_t q[3][4], kn[4] = {0u, 0u, 0u, 0u};
+  {
+    float cs8[8], sn8[8];
+    load_cs(cs8, sn8);
 #pragma unroll
-  for (int h = 0; h < 3; ++h) rope8(in + h * 64, q[h]);
+    for (int h = 0; h < 3; ++h) rope8(in + h * 64, cs8, sn8, q[h]);
+  }
   // debug capture of layer debug_layer: rotated queries (chunk 0 of each KV head, lanes 0-7)
   const bool dbg_attn = DBG && p.debug != nullptr && l == p.debug_layer;
   if (dbg_attn && P.c == 0 && w == 0 && grp == 0)
@@ -1200,7 +1233,12 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
     // the new key and value, RoPE on the key, and its score (every 8-lane group computes it; the
     // first group keeps it)
     C.poll_wave3(l, b, G::H + g * 64, 64, G::H + G::KVH * 64 + g * 64, 64, 0, 0, in + 192);
-    rope8(in + 192, kn);
+    // the cos/sin row is read again (still in the ring): held in registers across the scores it
+    // would take 16 of them where the kernel has none to spare
+    asm volatile("" ::: "memory");
+    float cs8[8], sn8[8];
+    load_cs(cs8, sn8);
+    rope8(in + 192, cs8, sn8, kn);
     score(T_old, make_uint4(kn[0], kn[1], kn[2], kn[3]), grp == 0);
   }
   wait_lgkm0();
@@ -1469,9 +1507,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       if (ch < Chunks<G::H>::CH) *reinterpret_cast<uint4*>(dst + ch * 8) = v[cc][0];
     }
   };
-  if (C.ct == 0 && p.trace)
-    p.trace[size_t(blockIdx.x) * (size_t(p.n_layers) * TR_EVENTS + TR_TAIL) + size_t(p.n_layers) * TR_EVENTS] =
-        wall_clock64();
+  if (C.ct == 0) trace_tail(p, 0);
 
   for (int l = 0; l < p.n_layers; ++l) {
     // ---------------- P1: RMSNorm(x) + QKV ----------------
@@ -1705,9 +1741,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
   }
   if (C.lane == 0) { sm.lm_val[C.cw] = best; sm.lm_idx[C.cw] = best_i; }
   C.cbar();
-  if (C.ct == 0 && p.trace)
-    p.trace[size_t(blockIdx.x) * (size_t(p.n_layers) * TR_EVENTS + TR_TAIL) + size_t(p.n_layers) * TR_EVENTS + 1] =
-        wall_clock64();
+  if (C.ct == 0) trace_tail(p, 1);
   if (C.ct == 0) {
     float bv = sm.lm_val[0];
     int bi = sm.lm_idx[0];
@@ -1796,6 +1830,7 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel(Params p) {
     }
     sm.gue[i] = e;
   }
+  trace_begin(p);
   __syncthreads();
   Plan<G> P;
   P.init(p, blockIdx.x);
@@ -1805,6 +1840,7 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel(Params p) {
   else consumer<G, DBG>(p, P, sm, epoch);
   __syncthreads();
   if (blockIdx.x == 0 && threadIdx.x == 0) st_dev(p.ws + HDR_EPOCH, epoch);
+  trace_end(p);
 }
 
 // ================================================================================================
@@ -2685,9 +2721,7 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
   // Diagnostic timestamps (events per layer: 0 P1 start, 1 staged, 2 weights in, 3 QKV stored,
   // 4 attention start, 5-7 passes A-C done, 8 attn published, 9-11 P3, 12-14 P4, 15-17 P5).
   auto tr = [&](int l, int ev) { if (C.ct == 0) trace_at(p, l, ev, p.n_layers); };
-  if (C.ct == 0 && p.trace)
-    p.trace[size_t(blockIdx.x) * (size_t(p.n_layers) * TR_EVENTS + TR_TAIL) + size_t(p.n_layers) * TR_EVENTS] =
-        wall_clock64();
+  if (C.ct == 0) trace_tail(p, 0);
   for (int l = 0; l < p.n_layers; ++l) {
     // ---------------- P1: RMSNorm(x) + QKV ----------------
     C.refresh();
@@ -2863,9 +2897,7 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
   }
   if (C.lane < BMAX) { sm.lm_val[C.cw][C.lane] = best; sm.lm_idx[C.cw][C.lane] = bidx; }
   C.cbar();
-  if (C.ct == 0 && p.trace)
-    p.trace[size_t(blockIdx.x) * (size_t(p.n_layers) * TR_EVENTS + TR_TAIL) + size_t(p.n_layers) * TR_EVENTS + 1] =
-        wall_clock64();
+  if (C.ct == 0) trace_tail(p, 1);
   if (C.ct < B) {
     float bv = sm.lm_val[0][C.ct];
     int bi = sm.lm_idx[0][C.ct];
@@ -2936,6 +2968,7 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel_b(Params p) {
                                    : reinterpret_cast<const int32_t*>(p.input_ids)[t];
     sm.sId[t] = int(min(max(id, 0LL), (long long)G::V - 1));
   }
+  trace_begin(p);
   __syncthreads();
   PlanB<G> P;
   P.init(p, sm.sS, blockIdx.x);
@@ -2945,10 +2978,12 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel_b(Params p) {
   else consumer_b<G, DBG>(p, P, sm, epoch);
   __syncthreads();
   if (blockIdx.x == 0 && threadIdx.x == 0) st_dev(p.ws + HDR_EPOCH, epoch);
+  trace_end(p);
 }
 
 template <class G>
 constexpr size_t lds_bytes() { return sizeof(Smem<G>); }
+constexpr size_t trace_offset(size_t lds) { return (lds + 15) & ~size_t(15); }
 template <class G>
 constexpr size_t lds_bytes_b() { return sizeof(SmemB<G>); }
 static_assert(sizeof(SmemB<G360>) <= 160 * 1024, "LDS budget of one gfx950 workgroup");
@@ -2956,6 +2991,12 @@ static_assert(sizeof(SmemB<G135>) <= 160 * 1024, "LDS budget of one gfx950 workg
 static_assert(sizeof(Smem<G360>) <= 160 * 1024, "LDS budget of one gfx950 workgroup");
 static_assert(sizeof(Smem<G135>) <= 160 * 1024, "LDS budget of one gfx950 workgroup");
 static_assert(sizeof(Smem<G360Q>) <= 160 * 1024, "LDS budget of one gfx950 workgroup");
+static_assert(trace_offset(sizeof(SmemB<G360>)) + TRACE_LDS_BYTES <= 160 * 1024 &&
+                  trace_offset(sizeof(SmemB<G135>)) + TRACE_LDS_BYTES <= 160 * 1024 &&
+                  trace_offset(sizeof(Smem<G360>)) + TRACE_LDS_BYTES <= 160 * 1024 &&
+                  trace_offset(sizeof(Smem<G135>)) + TRACE_LDS_BYTES <= 160 * 1024 &&
+                  trace_offset(sizeof(Smem<G360Q>)) + TRACE_LDS_BYTES <= 160 * 1024,
+              "room for the diagnostic timestamp buffer");
 
 // ------------------------------------------------------------------------------------------------
 // MXFP8 quantisation of bf16 weights: per 32 consecutive elements of a row, scale code
@@ -3116,6 +3157,7 @@ static int launch(const Params& p, hipStream_t stream) {
     fn = reinterpret_cast<const void*>(decode_kernel<G, DBG>);
     lds = lds_bytes<G>();
   }
+  const size_t lds_traced = trace_offset(lds) + TRACE_LDS_BYTES;  // with the timestamp buffer
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
@@ -3126,9 +3168,9 @@ static int launch(const Params& p, hipStream_t stream) {
     if (!d.ok) st = d.status;
     else if (!d.gfx950) st = PK_ERR_ARCH;
     else if (!d.coop) st = PK_ERR_COOP;
-    else if (d.cus < NWG || size_t(d.max_lds) < lds) st = PK_ERR_RESIDENCY;
+    else if (d.cus < NWG || size_t(d.max_lds) < lds_traced) st = PK_ERR_RESIDENCY;
     else {
-      e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+      e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_traced));
       if (e != hipSuccess) st = e;
     }
     cache.status[dev] = st;
@@ -3136,6 +3178,11 @@ static int launch(const Params& p, hipStream_t stream) {
   }
   if (cache.status[dev]) return cache.status[dev];
   Params q = p;
+  if (q.trace) {
+    if (q.n_layers > TR_LAYERS) return PK_ERR_MODEL;
+    q.trace_lds = uint32_t(trace_offset(lds));
+    lds = lds_traced;
+  }
   void* args[] = {&q};
   e = hipLaunchCooperativeKernel(fn, dim3(NWG), dim3(WG_THREADS), args, lds, stream);
   if (e != hipSuccess) return e;
