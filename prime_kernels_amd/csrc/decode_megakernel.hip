@@ -182,7 +182,14 @@ struct GUE {
 // (b * XLINES + k) * XSLOTS + layer * NKIND + kind, so the consecutive lines of one vector are
 // XSLOTS * 64 bytes apart (10 KB for 32 layers) and spread over the HBM channels instead of
 // concentrating every reader's polls on the one or two channels a contiguous vector would hit.
+// The batch-1 kernel writes each exchange word to XREP copies, in the sequence slots 0..XREP-1 of
+// the vector (unused at batch 1), and workgroup i polls copy i mod XREP: every 64-byte line is then
+// polled by NWG / XREP workgroups instead of all of them.  A line polled by every workgroup queues
+// NWG requests at its memory channel each polling round, which made one round of uncached loads
+// take ~0.75 us inside the step.
 enum XKind { X_QKV, X_ATTN, X_H1, X_ACT, X_X, NKIND };
+constexpr int XREP = 8;
+static_assert(XREP <= MAX_B && NWG % XREP == 0, "copies live in the sequence slots");
 template <class G>
 struct WS {
   static constexpr int XSLOTS = G::L * NKIND;
@@ -683,9 +690,11 @@ struct Consumer {
   uint32_t bar_gen = 0;
   uint32_t tag16, tag32;
   bool dead = false;
+  int xr;                    // the copy of the batch-1 exchange vectors this workgroup polls
 
   __device__ __forceinline__ Consumer(const Params& p_, const PL& P_, SM& sm_, uint32_t ep)
       : p(p_), P(P_), sm(sm_) {
+    xr = P.wg % XREP;
     cw = (threadIdx.x >> 6) - NPW;
     lane = threadIdx.x & 63;
     ct = cw * 64 + lane;
@@ -696,6 +705,12 @@ struct Consumer {
   // Makes the lane ids opaque at a phase boundary, so per-lane addresses are recomputed inside the
   // layer loop instead of being hoisted out of it and kept live in registers.
   __device__ __forceinline__ void refresh() { asm volatile("" : "+v"(lane), "+v"(ct)); }
+
+  // Batch-1 exchange word: element i of vector (kind, layer l), written to every copy.
+  __device__ __forceinline__ void st_x(int kind, int l, int i, uint32_t v) const {
+#pragma unroll
+    for (int r = 0; r < XREP; ++r) st_dev(p.ws + WS<G>::xw(kind, l, r, i), v);
+  }
 
   // Claims the next segment of the stream; returns its start position.
   __device__ __forceinline__ uint32_t next_seg(uint32_t bytes) {
@@ -1146,7 +1161,7 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   // edge(3) < T) fetches the new key and value -> in[192, 320) only after the scores of its cached
   // tokens: those words come from other writers than q and often land later, so the wait overlaps
   // the scores instead of preceding them.
-  C.poll_wave3(l, b, g * 192, 192, 0, 0, 0, 0, in);
+  C.poll_wave3(l, C.xr, g * 192, 192, 0, 0, 0, 0, in);
   C.wait_filled(C.pos);  // cos/sin row and KV chunk are in the ring
   // cos/sin of dims 8*part .. 8*part+7 (mod 32): contiguous in the table row of this position
   auto load_cs = [&](float (&cs8)[8], float (&sn8)[8]) {
@@ -1232,7 +1247,7 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   if (has_new) {
     // the new key and value, RoPE on the key, and its score (every 8-lane group computes it; the
     // first group keeps it)
-    C.poll_wave3(l, b, G::H + g * 64, 64, G::H + G::KVH * 64 + g * 64, 64, 0, 0, in + 192);
+    C.poll_wave3(l, C.xr, G::H + g * 64, 64, G::H + G::KVH * 64 + g * 64, 64, 0, 0, in + 192);
     // the cos/sin row is read again (still in the ring): held in registers across the scores it
     // would take 16 of them where the kernel has none to spare
     asm volatile("" ::: "memory");
@@ -1474,7 +1489,7 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   }
   if (w == 0 && lane == 0) trace_at(p, l, 20, p.n_layers);
   O += o_own;
-  st_dev(p.ws + W::xw(X_ATTN, l, b, (g * 3 + hh) * 64 + d), C.w16(O));
+  C.st_x(X_ATTN, l, (g * 3 + hh) * 64 + d, C.w16(O));
   if (DBG && p.debug) {
     const uint16_t ob = uint16_t(f2bf(O));
     p.debug[size_t(l) * Dbg<G>::LAYER + Dbg<G>::ATTN + (g * 3 + hh) * 64 + d] = ob;
@@ -1535,7 +1550,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
         }
         ss = wave_sum(s);
       } else {
-        ss = C.template poll_split<GH>(X_X, l - 1, b, G::H, sm.xs, sm.xkeep);
+        ss = C.template poll_split<GH>(X_X, l - 1, C.xr, G::H, sm.xs, sm.xkeep);
       }
       const float rs = rms_scale(C.block_total(ss), G::H);
       tr(l, 1);
@@ -1550,7 +1565,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       tr(l, 22);
       const int row = C.cw + NCW * C.lane;
       if (C.lane < R::QKV && row < P.q1 - P.q0) {
-        st_dev(p.ws + W::xw(X_QKV, l, b, P.q0 + row), C.w16(pick(out, C.lane)));
+        C.st_x(X_QKV, l, P.q0 + row, C.w16(pick(out, C.lane)));
         if (DBG && p.debug) dl(l)[Dbg<G>::QKV + P.q0 + row] = uint16_t(f2bf(pick(out, C.lane)));
       }
       tr(l, 2);
@@ -1571,7 +1586,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       if (nrows > 0) {
         C.wait_filled(C.pos);
         tr(l, 6);
-        C.template poll_split<GH>(X_ATTN, l, b, G::H, sm.xs, nullptr);
+        C.template poll_split<GH>(X_ATTN, l, C.xr, G::H, sm.xs, nullptr);
         C.cbar();
         tr(l, 7);
         XChunks<G::H, EW> x;
@@ -1584,7 +1599,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
         if (C.lane < R::O && row < nrows) {
           const int r = P.o0 + row;
           const float o = rnd(pick(out, C.lane));
-          st_dev(p.ws + W::xw(X_H1, l, b, r), C.w16(sm.xkeep[r] + o));
+          C.st_x(X_H1, l, r, C.w16(sm.xkeep[r] + o));
           if (DBG && p.debug) {
             dl(l)[Dbg<G>::O + r] = uint16_t(f2bf(o));
             dl(l)[Dbg<G>::H1 + r] = uint16_t(f2bf(sm.xkeep[r] + o));
@@ -1622,7 +1637,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
         }
       }
       tr(l, 9);
-      const float ss = C.template poll_split<GH>(X_H1, l, b, G::H, sm.xs, sm.h1keep);
+      const float ss = C.template poll_split<GH>(X_H1, l, C.xr, G::H, sm.xs, sm.h1keep);
       const float rs = rms_scale(C.block_total(ss), G::H);
       tr(l, 10);
       XChunks<G::H, EW> x;
@@ -1652,7 +1667,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       if (C.lane < R::ACT && row < na) {
         const float gv = rnd(pick(og, C.lane)), uv = rnd(pick(ou, C.lane));
         const float silu = rnd(gv / (1.0f + expf(-gv)));
-        st_dev(p.ws + W::xw(X_ACT, l, b, P.a0 + row), C.w16(silu * uv));
+        C.st_x(X_ACT, l, P.a0 + row, C.w16(silu * uv));
         if (DBG && p.debug) {
           const int r = P.a0 + row;
           dl(l)[Dbg<G>::GATE + r] = uint16_t(f2bf(gv));
@@ -1671,7 +1686,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       const int nrows = P.d1 - P.d0;
       C.wait_filled(C.pos);
       tr(l, 12);
-      C.template poll_split<GI>(X_ACT, l, b, G::I, sm.xs, nullptr);
+      C.template poll_split<GI>(X_ACT, l, C.xr, G::I, sm.xs, nullptr);
       C.cbar();
       tr(l, 13);
       XChunks<G::I, EW> x;
@@ -1684,7 +1699,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       if (C.lane < R::DOWN && row < nrows) {
         const int r = P.d0 + row;
         const float y = rnd(sm.h1keep[r] + rnd(pick(out, C.lane)));
-        st_dev(p.ws + W::xw(X_X, l, b, r), C.w16(y));
+        C.st_x(X_X, l, r, C.w16(y));
         if (DBG && p.debug) {
           dl(l)[Dbg<G>::DOWN + r] = uint16_t(f2bf(rnd(pick(out, C.lane))));
           dl(l)[Dbg<G>::OUT + r] = uint16_t(f2bf(y));
@@ -1700,7 +1715,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
   XChunks<G::H> nw;  // the final norm and the tied LM head stay bf16
   load_normw<G, G::H, 8>(C, nw, segf);
   C.release(C.pos);
-  const float ss = C.template poll_split<GH>(X_X, p.n_layers - 1, b, G::H, sm.xs, nullptr);
+  const float ss = C.template poll_split<GH>(X_X, p.n_layers - 1, C.xr, G::H, sm.xs, nullptr);
   const float rs = rms_scale(C.block_total(ss), G::H);
   XChunks<G::H> x;
   load_x<G::H, 8, true>(x, sm.xs, nw, rs, C.lane);
