@@ -264,6 +264,42 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<0x143, 0xc>(v, v));
   return lane63(v);
 }
+// wave_max / wave_sum of N values at once: the same steps per value, the N chains interleaved so
+// that each DPP step's wait states are filled by the other chains instead of s_nop.
+template <int N>
+__device__ __forceinline__ void wave_max_n(float (&v)[N]) {
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] = fmaxf(v[k], dpp<0x111>(v[k], v[k]));
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] = fmaxf(v[k], dpp<0x112>(v[k], v[k]));
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] = fmaxf(v[k], dpp<0x114, 0xf, 0xe>(v[k], v[k]));
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] = fmaxf(v[k], dpp<0x118, 0xf, 0xc>(v[k], v[k]));
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] = fmaxf(v[k], dpp<0x142, 0xa>(v[k], v[k]));
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] = fmaxf(v[k], dpp<0x143, 0xc>(v[k], v[k]));
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] = lane63(v[k]);
+}
+template <int N>
+__device__ __forceinline__ void wave_sum_n(float (&v)[N]) {
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] += dpp<0x111>(0.f, v[k]);
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] += dpp<0x112>(0.f, v[k]);
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] += dpp<0x114, 0xf, 0xe>(0.f, v[k]);
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] += dpp<0x118, 0xf, 0xc>(0.f, v[k]);
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] += dpp<0x142, 0xa>(0.f, v[k]);
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] += dpp<0x143, 0xc>(0.f, v[k]);
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] = lane63(v[k]);
+}
 // Sum over each aligned group of 8 lanes; every lane of the group gets the group sum.
 __device__ __forceinline__ float group8_sum(float v) {
   v += dpp<0xb1>(0.f, v);                  // quad_perm [1,0,3,2]
@@ -1158,10 +1194,18 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
 
   const int part = lane & 7, grp = lane >> 3;
   // queries of the 3 heads -> in[0, 192).  The wave with the new token (the leader's last wave,
-  // edge(3) < T) fetches the new key and value -> in[192, 320) only after the scores of its cached
-  // tokens: those words come from other writers than q and often land later, so the wait overlaps
-  // the scores instead of preceding them.
+  // edge(3) < T) also needs the new key and value -> in[192, 320): it issues their loads after q
+  // has arrived and looks at them only after the scores of its cached tokens, so the load's round
+  // trip (most of a microsecond inside the step) overlaps that work; words not yet current then
+  // are polled again.
   C.poll_wave3(l, C.xr, g * 192, 192, 0, 0, 0, 0, in);
+  // the new key (lanes 0-15) and value (lanes 16-31) words: loaded now, checked after the scores
+  const __amdgpu_buffer_rsrc_t rkv = rsrc(p.ws);
+  auto kv_at = [&](int i) {
+    return uint32_t(W::xw(X_QKV, l, C.xr, i < 64 ? G::H + g * 64 + i : G::H + G::KVH * 64 + g * 64 + i - 64)) * 4u;
+  };
+  u32x4 kvw = {0u, 0u, 0u, 0u};
+  if (has_new && lane < 32) kvw = ld_dev128(rkv, kv_at(lane * 4));
   C.wait_filled(C.pos);  // cos/sin row and KV chunk are in the ring
   // cos/sin of dims 8*part .. 8*part+7 (mod 32): contiguous in the table row of this position
   auto load_cs = [&](float (&cs8)[8], float (&sn8)[8]) {
@@ -1247,7 +1291,14 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   if (has_new) {
     // the new key and value, RoPE on the key, and its score (every 8-lane group computes it; the
     // first group keeps it)
-    C.poll_wave3(l, C.xr, G::H + g * 64, 64, G::H + G::KVH * 64 + g * 64, 64, 0, 0, in + 192);
+    if (lane < 32) {
+      Spin spin(p.ws, 7);
+      while (!C.ok4(kvw)) {
+        if (C.dead || !spin.again()) { C.dead = true; break; }
+        kvw = ld_dev128(rkv, kv_at(lane * 4));
+      }
+      *reinterpret_cast<float4*>(in + 192 + lane * 4) = make_float4(bf_lo(kvw.x), bf_lo(kvw.y), bf_lo(kvw.z), bf_lo(kvw.w));
+    }
     // the cos/sin row is read again (still in the ring): held in registers across the scores it
     // would take 16 of them where the kernel has none to spare
     asm volatile("" ::: "memory");
@@ -1271,14 +1322,21 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
       const int j = j0 + lane + 64 * i;
       sv[h][i] = j < j1 ? sm.at.sc[h][j] : -INFINITY;
     }
+  {
+    float m3[3], l3[3];
 #pragma unroll
-  for (int h = 0; h < 3; ++h) {
-    const float m = wave_max(fmaxf(sv[h][0], sv[h][1]));
-    float ls = 0.f;
+    for (int h = 0; h < 3; ++h) m3[h] = fmaxf(sv[h][0], sv[h][1]);
+    wave_max_n<3>(m3);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) ls += sv[h][i] == -INFINITY ? 0.f : expf(sv[h][i] - m);
-    ls = wave_sum(ls);
-    if (lane == 0) { sm.wml[w][0][h] = m; sm.wml[w][1][h] = ls; }
+    for (int h = 0; h < 3; ++h) {
+      l3[h] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) l3[h] += sv[h][i] == -INFINITY ? 0.f : expf(sv[h][i] - m3[h]);
+    }
+    wave_sum_n<3>(l3);
+    if (lane == 0)
+#pragma unroll
+      for (int h = 0; h < 3; ++h) { sm.wml[w][0][h] = m3[h]; sm.wml[w][1][h] = l3[h]; }
   }
   C.cbar();
   // lane 4h + v holds wave v's (max, sum) of head h; max and rescaled sum over each quad of lanes
@@ -1335,18 +1393,20 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
     }
 #pragma unroll
     for (int h = 0; h < 3; ++h) {
-      float m = -INFINITY;
+      Mh[h] = -INFINITY;
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        if (lane + 64 * i < P.C) m = fmaxf(m, __uint_as_float(s[i][h].x));
-      m = wave_max(m);
-      float ls = 0.f;
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        if (lane + 64 * i < P.C) ls += __uint_as_float(s[i][h].z) * expf(__uint_as_float(s[i][h].x) - m);
-      Mh[h] = m;
-      Lh[h] = wave_sum(ls);
+        if (lane + 64 * i < P.C) Mh[h] = fmaxf(Mh[h], __uint_as_float(s[i][h].x));
     }
+    wave_max_n<3>(Mh);
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      Lh[h] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        if (lane + 64 * i < P.C) Lh[h] += __uint_as_float(s[i][h].z) * expf(__uint_as_float(s[i][h].x) - Mh[h]);
+    }
+    wave_sum_n<3>(Lh);
   }
   if (w == 0 && lane == 0) trace_at(p, l, 18, p.n_layers);
   // probabilities with the softmax's global max and sum, rounded to bf16 before P.V as HF does
