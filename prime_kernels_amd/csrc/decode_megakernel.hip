@@ -141,6 +141,7 @@ struct Params {
   int ids_i64;
   unsigned long long* trace;   // optional per-phase timestamps (diagnostics)
   uint32_t trace_lds;          // LDS byte offset of the launch's timestamp buffer (when tracing)
+  uint32_t* xws;               // optional: batch-1 attention records in ordinary device memory
   const EncodedGULayer* encoded_gu;  // optional [L] lossless gate/up encodings (batch-1 bf16 kernel)
   uint16_t* debug;             // optional per-stage capture (Dbg layout), batch <= 2
   int debug_layer;             // layer whose attention internals are captured (-1: none)
@@ -210,6 +211,9 @@ struct WS {
     return X0 + ((size_t(b) * XLINES + size_t(i >> 4)) * XSLOTS + size_t(l) * NKIND + kind) * 16 + size_t(i & 15);
   }
   __device__ static size_t rec(int l, int item) { return REC0 + l * REC_LAYER + size_t(item) * REC_WORDS * 2; }
+  // The batch-1 attention records (partials and statistics, REC0 .. LM0) can live in a separate
+  // buffer of XREC_WORDS words at the same relative offsets.
+  static constexpr size_t XREC_WORDS = LM0 - REC0;
   __device__ static size_t stat(int l, size_t item) { return STAT0 + l * STAT_LAYER + item * STAT_WORDS * 2; }
   __device__ static size_t lm(int b, int wg) { return LM0 + (size_t(b) * NWG + wg) * 2; }
 };
@@ -322,6 +326,12 @@ __device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
 __device__ __forceinline__ void st_dev64(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Plain 64-bit store (no cache-policy bits): through the write-through L1 into the XCD's L2, where
+// device-scope loads from the same XCD see it.
+__device__ __forceinline__ void st_l2(uint64_t* p, uint64_t v) {
+  typedef __attribute__((address_space(1))) uint64_t g_u64;
+  *(g_u64*)(p) = v;
+}
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // Stores into caller memory through a pointer read from LDS (the KV cache base): without the
 // explicit global address space the compiler emits a flat store, which also counts on the LDS
@@ -423,6 +433,8 @@ struct Plan {
   int S, pos;   // tokens attended (incl. new) and the new token's position
   long long slot;  // KV slot of the new token (slot_mapping[0]; < 0: no append)
   int leader;   // owns the new token, merges the chunk partials and appends K/V
+  int xcd;      // chunk c of KV head g on workgroup g + 8c: a head's chunks share one XCD and
+                // exchange their records through its L2 (p.xws, ordinary memory)
 
   __device__ __forceinline__ void init(const Params& p, int wg_) {
     wg = wg_;
@@ -435,11 +447,22 @@ struct Plan {
     const int tc = old <= 0 ? 16 : ((old + C0 - 1) / C0 + 15) / 16 * 16;
     C = old <= 0 ? 1 : (old + tc - 1) / tc;
     natt = G::KVH * C;
-    att = wg < natt;
+    // Workgroups are dispatched to the 8 XCDs round-robin (workgroup i on XCC (i + s) mod 8, where
+    // the start s carries over from earlier dispatches), so with chunk c of head g on workgroup
+    // g + 8c every chunk of a head shares an XCD and its L2.  Were that ever not so, the record
+    // polls would run into their bound and the launch would end with its abort word set.
+    xcd = p.xws != nullptr && C <= NWG / 8 && G::KVH <= 8;
+    att = xcd ? ((wg % 8) < G::KVH && (wg / 8) < C) : wg < natt;
+    int below = 0;  // attention workgroups with a lower index
+    if (xcd) {
+      for (int r = 0; r < G::KVH; ++r) below += r < wg ? min(C, (wg - r + 7) / 8) : 0;
+    } else {
+      below = min(wg, natt);
+    }
     g = c = t0 = t1 = leader = 0;
     if (att) {
-      g = wg / C;
-      c = wg % C;
+      g = xcd ? wg % 8 : wg / C;
+      c = xcd ? wg / 8 : wg % C;
       t0 = min(c * tc, old);
       t1 = min((c + 1) * tc, old);
       leader = c == C - 1;
@@ -447,7 +470,7 @@ struct Plan {
     // QKV and O rows go to the workgroups without an attention chunk when those are at least
     // half: attention workgroups also stream their KV chunk, and their P2 precedes P3.
     if (natt <= NWG / 2) {
-      const int nw = NWG - natt, i = wg - natt;
+      const int nw = NWG - natt, i = wg - below;
       q0 = att ? 0 : split_lo(G::QKV, nw, i);
       q1 = att ? 0 : split_lo(G::QKV, nw, i + 1);
       o0 = att ? 0 : split_lo(G::H, nw, i);
@@ -1358,11 +1381,14 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   }
   const uint64_t tg = uint64_t(C.tag32) << 32;
   if (P.C > 1) {
-    uint64_t* stat_base = reinterpret_cast<uint64_t*>(p.ws + W::stat(l, size_t(g) * P.C));
+    // same-XCD records: plain stores reach the shared L2, the (sc1) polls read it there
+    uint64_t* stat_base = reinterpret_cast<uint64_t*>(P.xcd ? p.xws + (W::stat(l, size_t(g) * P.C) - W::REC0)
+                                                            : p.ws + W::stat(l, size_t(g) * P.C));
     if (w == 0 && lane < 6) {
       const int h = lane >> 1;
       const float v = (lane & 1) ? (h == 0 ? Lh[0] : h == 1 ? Lh[1] : Lh[2]) : (h == 0 ? Mh[0] : h == 1 ? Mh[1] : Mh[2]);
-      st_dev64(stat_base + size_t(P.c) * STAT_WORDS + lane, tg | __float_as_uint(v));
+      if (P.xcd) st_l2(stat_base + size_t(P.c) * STAT_WORDS + lane, tg | __float_as_uint(v));
+      else st_dev64(stat_base + size_t(P.c) * STAT_WORDS + lane, tg | __float_as_uint(v));
     }
     // lane k polls chunk k (and k + 64): 3 x 16 bytes = (m, l) of the 3 heads
     const __amdgpu_buffer_rsrc_t r = rsrc(stat_base);
@@ -1513,9 +1539,11 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
 #pragma unroll
   for (int v = 0; v < NCW; ++v) O += sm.wo[v][hh][d];
   if (w == 0 && lane == 0) trace_at(p, l, 4, p.n_layers);
-  uint64_t* rec_base = reinterpret_cast<uint64_t*>(p.ws + W::rec(l, 0));
+  uint64_t* rec_base = reinterpret_cast<uint64_t*>(P.xcd ? p.xws + (W::rec(l, 0) - W::REC0) : p.ws + W::rec(l, 0));
   if (!P.leader) {
-    st_dev64(rec_base + size_t(P.wg) * REC_WORDS + hh * 64 + d, tg | __float_as_uint(O));
+    uint64_t* dst = rec_base + size_t(g * P.C + P.c) * REC_WORDS + hh * 64 + d;
+    if (P.xcd) st_l2(dst, tg | __float_as_uint(O));
+    else st_dev64(dst, tg | __float_as_uint(O));
     return;
   }
   // leader: sum the chunk partials 0..C-1 in chunk order (this chunk is C-1), round once
@@ -3175,6 +3203,22 @@ struct WsEntry {
 };
 static std::mutex g_ws_mu;
 static std::vector<WsEntry> g_ws;
+// Companion buffers (ordinary device memory) for the batch-1 attention records, made by
+// pk_workspace_alloc together with its workspace and dropped with it.
+struct RecEntry {
+  const void* ws;
+  void* rec;
+};
+static std::vector<RecEntry> g_rec;
+static constexpr size_t rec_bytes() {
+  return (WS<G360>::XREC_WORDS > WS<G135>::XREC_WORDS ? WS<G360>::XREC_WORDS : WS<G135>::XREC_WORDS) * 4;
+}
+static uint32_t* rec_lookup(const void* ws) {
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  for (const RecEntry& r : g_rec)
+    if (r.ws == ws) return reinterpret_cast<uint32_t*>(r.rec);
+  return nullptr;
+}
 
 __global__ void __launch_bounds__(256) zero_fill(uint4* p, size_t n) {
   for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
@@ -3196,6 +3240,15 @@ static void ws_forget(const void* ptr) {
   for (size_t i = 0; i < g_ws.size();)
     if (g_ws[i].ptr == ptr) g_ws.erase(g_ws.begin() + long(i));
     else ++i;
+  // the companion goes too: its records carry epochs of the workspace it was made with, which a
+  // re-zeroed workspace would count again
+  for (size_t i = 0; i < g_rec.size();)
+    if (g_rec[i].ws == ptr) {
+      (void)hipFree(g_rec[i].rec);
+      g_rec.erase(g_rec.begin() + long(i));
+    } else {
+      ++i;
+    }
 }
 
 static int ensure_workspace(void* ws, size_t bytes, hipStream_t stream) {
@@ -3253,6 +3306,7 @@ static int launch(const Params& p, hipStream_t stream) {
   }
   if (cache.status[dev]) return cache.status[dev];
   Params q = p;
+  q.xws = BATCHED ? nullptr : rec_lookup(p.ws);
   if (q.trace) {
     if (q.n_layers > TR_LAYERS) return PK_ERR_MODEL;
     q.trace_lds = uint32_t(trace_offset(lds));
@@ -3380,6 +3434,16 @@ extern "C" void* pk_workspace_alloc(size_t bytes, int kind) {
   }
   int dev = 0;
   if (hipGetDevice(&dev) == hipSuccess) pk::ws_register(dev, ptr, bytes);
+  // companion for the batch-1 attention records (optional: without it they stay in the workspace)
+  void* rec = nullptr;
+  if (hipMalloc(&rec, pk::rec_bytes()) == hipSuccess) {
+    if (hipMemset(rec, 0, pk::rec_bytes()) == hipSuccess && hipDeviceSynchronize() == hipSuccess) {
+      std::lock_guard<std::mutex> lk(pk::g_ws_mu);
+      pk::g_rec.push_back(pk::RecEntry{ptr, rec});
+    } else {
+      (void)hipFree(rec);
+    }
+  }
   return ptr;
 }
 extern "C" int pk_workspace_forget(const void* ptr) {
