@@ -187,9 +187,10 @@ struct GUE {
 // the vector (unused at batch 1), and workgroup i polls copy i mod XREP: every 64-byte line is then
 // polled by NWG / XREP workgroups instead of all of them.  A line polled by every workgroup queues
 // NWG requests at its memory channel each polling round, which made one round of uncached loads
-// take ~0.75 us inside the step.
+// take ~0.75 us inside the step.  Measured at 360M batch 1: 4 copies slightly ahead of 8, 16
+// behind (the extra stores cost more than the shorter queues save).
 enum XKind { X_QKV, X_ATTN, X_H1, X_ACT, X_X, NKIND };
-constexpr int XREP = 8;
+constexpr int XREP = 4;
 static_assert(XREP <= MAX_B && NWG % XREP == 0, "copies live in the sequence slots");
 template <class G>
 struct WS {
@@ -1981,13 +1982,18 @@ struct WSB {
   static constexpr size_t REC0 = WS<G>::TOTAL;                       // P.V partials, 3 x 64 tagged fp32
   static constexpr size_t STAT0 = REC0 + size_t(MAX_ITEMS) * REC_WORDS * 2;
   static constexpr size_t FLAG0 = STAT0 + size_t(MAX_ITEMS) * STAT_WORDS * 2;
-  static constexpr size_t DATA0 = FLAG0 + size_t(NKIND) * G::L * NWG;  // 64-byte aligned below
+  // FREP copies of each (kind, layer) flag row; workgroup i polls copy i mod FREP (a row that
+  // every workgroup polls queues NWG requests per line and polling round)
+  static constexpr int FREP = 8;
+  static constexpr size_t DATA0 = FLAG0 + size_t(NKIND) * G::L * FREP * NWG;  // 64-byte aligned below
   static constexpr size_t DATA_WORDS = size_t(BMAX) * XMAX / 2;        // one [B][K] bf16 array
   static constexpr size_t TOTAL = DATA0 + size_t(NKIND) * G::L * DATA_WORDS;
   static_assert(DATA0 % 16 == 0 && DATA_WORDS % 256 == 0, "bf16 arrays start on 64-byte lines");
   __device__ static size_t rec(int item) { return REC0 + size_t(item) * REC_WORDS * 2; }
   __device__ static size_t stat(int item) { return STAT0 + size_t(item) * STAT_WORDS * 2; }
-  __device__ static size_t flag(int kind, int l, int wg) { return FLAG0 + (size_t(kind) * G::L + l) * NWG + wg; }
+  __device__ static size_t flag(int kind, int l, int wg, int r) {
+    return FLAG0 + ((size_t(kind) * G::L + l) * FREP + r) * NWG + wg;
+  }
   __device__ static size_t data(int kind, int l) { return DATA0 + (size_t(kind) * G::L + l) * DATA_WORDS; }
 };
 
@@ -2258,13 +2264,13 @@ template <class G>
 __device__ __forceinline__ void publish_flag(ConsumerB<G>& C, int kind, int l) {
   wait_vmcnt<0>();
   C.cbar();
-  if (C.ct == 0) st_dev(C.p.ws + WSB<G>::flag(kind, l, C.P.wg), C.tag32);
+  if (C.ct < WSB<G>::FREP) st_dev(C.p.ws + WSB<G>::flag(kind, l, C.P.wg, C.ct), C.tag32);
 }
 
 // Wait until all workgroups have published (kind, l), then copy the [B][K] bf16 array into xs.
 template <class G>
 __device__ __forceinline__ void stage_flagged(ConsumerB<G>& C, int kind, int l, int K) {
-  const uint32_t* flags = C.p.ws + WSB<G>::flag(kind, l, 0);
+  const uint32_t* flags = C.p.ws + WSB<G>::flag(kind, l, 0, C.P.wg % WSB<G>::FREP);
   {
     Spin spin(C.p.ws, 8);
     for (int w = C.ct; w < NWG; w += NCT)
