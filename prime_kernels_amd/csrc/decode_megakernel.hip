@@ -79,7 +79,11 @@ constexpr int NCT = 64 * NCW;            // consumer threads
 constexpr int WG_THREADS = 64 * (NPW + NCW);
 constexpr uint32_t RING = 128u * 1024u;  // LDS ring bytes (power of two)
 constexpr uint32_t PKT = 1024;           // one LDS-DMA instruction: 64 lanes x 16 B
-constexpr int DEPTH = PK_DMA_DEPTH;      // packets in flight per producer wave
+constexpr int DEPTH = PK_DMA_DEPTH;      // packets in flight per producer wave (batch 1)
+// The batched kernel streams 1.4-2.5 GB of paged K/V per step and gains from more packets in
+// flight (32: -0.8% at config 4); at batch 1 more in flight lengthens the memory queues the
+// exchanges wait in (24: +11%, 32: +19%).
+constexpr int DEPTH_B = 32;
 constexpr int TC_MAX = 256;              // max cached tokens per attention chunk (64 KB of K/V)
 // Batch-1 chunking of a KV head's cached tokens: chunks of up to TC_LONG tokens, but at least
 // C_SHORT chunks of at least TC_SHORT tokens while the context allows (measured at 360M batch 1:
@@ -2224,8 +2228,8 @@ __device__ __forceinline__ void producer_b(const Params& p, const PlanB<G>& P, S
         }
         dma16(src, __builtin_amdgcn_readfirstlane(ring_base + ((gn * PKT) & (RING_B - 1))));
       }
-      wait_vmcnt<DEPTH>();
-      if (gn >= uint32_t(DEPTH - 1) * NPW) publish(gn - uint32_t(DEPTH - 1) * NPW);
+      wait_vmcnt<DEPTH_B>();
+      if (gn >= uint32_t(DEPTH_B - 1) * NPW) publish(gn - uint32_t(DEPTH_B - 1) * NPW);
     }
     n += npk;
   };
