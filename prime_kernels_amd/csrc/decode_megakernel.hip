@@ -68,7 +68,7 @@ constexpr int NWG = 256;                 // persistent workgroups (one per CU)
 #define PK_PRODUCER_WAVES 4
 #endif
 #ifndef PK_DMA_DEPTH
-#define PK_DMA_DEPTH 16
+#define PK_DMA_DEPTH 8
 #endif
 #ifndef PK_POLL_SLEEP
 #define PK_POLL_SLEEP 1                  // s_sleep units (64 clocks) between polls of an exchange
@@ -82,7 +82,8 @@ constexpr uint32_t PKT = 1024;           // one LDS-DMA instruction: 64 lanes x 
 constexpr int DEPTH = PK_DMA_DEPTH;      // packets in flight per producer wave (batch 1)
 // The batched kernel streams 1.4-2.5 GB of paged K/V per step and gains from more packets in
 // flight (32: -0.8% at config 4); at batch 1 more in flight lengthens the memory queues the
-// exchanges wait in (24: +11%, 32: +19%).
+// exchanges wait in (16 -> 24: +11%, 32: +19%; 8 is 0.3-0.4% faster than 16 at contexts 1024 to
+// 8192, also with a depth of 32 for the LM-head segments alone, which is slower).
 constexpr int DEPTH_B = 32;
 constexpr int TC_MAX = 256;              // max cached tokens per attention chunk (64 KB of K/V)
 // Batch-1 chunking of a KV head's cached tokens: chunks of up to TC_LONG tokens, but at least
