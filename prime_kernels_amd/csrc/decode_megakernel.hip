@@ -88,11 +88,12 @@ constexpr int DEPTH_B = 32;
 constexpr int TC_MAX = 256;              // max cached tokens per attention chunk (64 KB of K/V)
 // Batch-1 chunking of a KV head's cached tokens: chunks of up to TC_LONG tokens, but at least
 // C_SHORT chunks of at least TC_SHORT tokens while the context allows (measured at 360M batch 1:
-// short contexts gain from more chunks, long ones from fewer; the two exchanges between a head's
-// chunks cost more with every chunk)
+// more chunks shorten each chunk's work, and the exchanges between a head's chunks, through its
+// XCD's L2, cost little more with every chunk as long as the leader polls all partial records
+// in one batch)
 constexpr int TC_LONG = 128;
 constexpr int TC_SHORT = 64;
-constexpr int C_SHORT = 8;
+constexpr int C_SHORT = 16;
 constexpr int LM_ROWS = 16;              // LM-head rows per ring segment
 constexpr int MAX_B = 16;                // exchange-buffer slots per layer
 constexpr int REC_WORDS = 3 * 64;        // attention partial: 3 heads x sum(p.v)[64], 64-bit words
@@ -1555,7 +1556,7 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   // leader: sum the chunk partials 0..C-1 in chunk order (this chunk is C-1), round once
   const float o_own = O;
   O = 0.f;
-  constexpr int MB = 8;  // chunk records polled at once
+  constexpr int MB = 16;  // chunk records polled at once
   for (int c0 = 0; c0 < P.C - 1; c0 += MB) {
     const int nc = min(MB, P.C - 1 - c0);
     uint64_t ro[MB];
