@@ -345,6 +345,43 @@ def test_reference_abi_uninitialised_scratch():
     assert _native.status_string(rc) == "workspace_first_use_under_stream_capture"
 
 
+@pytest.mark.parametrize("S", [300, 1100])
+def test_caller_workspace_equals_library_workspace(S):
+    """A workspace from pk_workspace_alloc (the module's) has a companion buffer, so a KV head's
+    chunks exchange their softmax statistics and partials through their XCD's L2; a caller's
+    buffer has none and keeps them in the workspace.  The chunks and the order in which their
+    partials are added are the same, so the two give the same bits (S = 1100: 16 chunks of 80
+    tokens per KV head, the leader adding 15 partial records)."""
+    _need_gpu()
+    from prime_kernels_amd import _native
+    geom = O.SMOLLM2_360M  # decode360 (the reference ABI) always runs all 32 layers
+    case = GC.random_kv_case(geom, 29 + S, [S], norm_jitter=0.0)
+    lib = _native.library()
+    layers_t = torch.tensor([[t.data_ptr() for t in layer] for layer in case.wd.layers], dtype=torch.int64,
+                            device=case.dev)
+    kv_t = torch.tensor([c.data_ptr() for c in case.kvd], dtype=torch.int64, device=case.dev)
+    ids32 = torch.tensor([91], dtype=torch.int32, device=case.dev)
+    pos = torch.tensor([S - 1], dtype=torch.int64, device=case.dev)
+    sl = torch.tensor([S], dtype=torch.int32, device=case.dev)
+    slot = torch.tensor([case.kv.slot(0, S - 1)], dtype=torch.int64, device=case.dev)
+    rt = case.mod.workspace(case.dev)
+    lib_out = torch.empty((1, 960), dtype=BF16, device=case.dev)
+    rc = lib.decode360(*_decode360_args(case, lib_out, rt.scratch_ptr, rt.scratch_bytes, ids32, pos, sl, slot,
+                                        layers_t, kv_t))
+    assert rc == 0, _native.status_string(rc)
+    torch.cuda.synchronize()
+    nbytes = lib.decode360_workspace_bytes()
+    mine = torch.empty(nbytes // 4, dtype=torch.int32, device=case.dev)
+    case.sync_kv_from_oracle()
+    out = torch.empty((1, 960), dtype=BF16, device=case.dev)
+    rc = lib.decode360(*_decode360_args(case, out, mine.data_ptr(), nbytes, ids32, pos, sl, slot, layers_t, kv_t))
+    assert rc == 0, _native.status_string(rc)
+    torch.cuda.synchronize()
+    assert lib.pk_workspace_forget(mine.data_ptr()) == 0
+    assert rt.abort_word() == 0
+    assert torch.equal(out.view(torch.int16), lib_out.view(torch.int16))
+
+
 def test_torch_op_matches_decode_step():
     """torch.ops.prime_decode.decode_step / decode_logits give the same hidden state, ids and
     logits as decode_step(**kw), as fresh tensors."""
