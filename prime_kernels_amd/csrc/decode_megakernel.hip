@@ -71,7 +71,7 @@ constexpr int NWG = 256;                 // persistent workgroups (one per CU)
 #define PK_DMA_DEPTH 8
 #endif
 #ifndef PK_POLL_SLEEP
-#define PK_POLL_SLEEP 1                  // s_sleep units (64 clocks) between polls of an exchange
+#define PK_POLL_SLEEP 0                  // s_sleep units (64 clocks) between polls (0: -0.2% at batch 1, -0.9% at 16, against 1)
 #endif
 constexpr int NPW = PK_PRODUCER_WAVES;   // producer waves per workgroup (LDS-DMA issue is per-wave bound)
 constexpr int NCW = 4;                   // consumer waves per workgroup
