@@ -153,9 +153,9 @@ def main() -> None:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1)
-    abort = timed.rt.abort_word()
-    if abort:
-        raise RuntimeError("kernel reported an abandoned wait (abort word set)")
+    epoch, site = timed.rt.pending_failure()
+    if epoch:
+        raise RuntimeError(f"a timed step gave up a bounded wait (epoch {epoch}, wait site {site})")
     ids = timed.ids.cpu()
     if not bool(((ids >= 0) & (ids < 49152)).all()):
         raise RuntimeError("greedy ids out of range")

@@ -36,31 +36,45 @@ extern "C" {
 #define PK_ERR_BLOCK 9109        /* block_size != 16, bt_stride too small, or bad layer index */
 #define PK_ERR_MODEL 9110        /* unknown model id or layer count */
 #define PK_ERR_DEBUG 9111        /* per-stage debug capture requested for a model/format without it */
-#define PK_ERR_CAPTURE 9112      /* a workspace's first use (its zero fill) happened under stream capture */
+#define PK_ERR_CAPTURE 9112      /* the first use of a device (its state's allocation) happened under stream capture */
+#define PK_ERR_ABORTED 9113      /* a previous step on this device gave up a bounded wait; its outputs were poisoned */
+#define PK_ERR_STATE 9114        /* the library's per-device state could not be allocated */
+
+/* Options for pk_set_option. */
+#define PK_OPT_COOPERATIVE 1     /* 1: launch with hipLaunchCooperativeKernel (default 0, or PK_LAUNCH=cooperative) */
+#define PK_OPT_SPLIT_ROLE 2      /* 0: batch-1 steps stay on the general kernel (default 1, or PK_SPLIT_ROLE=0) */
 
 /* Models. */
 #define PK_MODEL_SMOLLM2_360M 360
 #define PK_MODEL_SMOLLM2_135M 135
 
-/* Workspace bytes for `model`.  The workspace carries the step epoch and tagged exchange words, so
- * it must start zeroed: pk_workspace_alloc returns a zeroed one, and any other buffer passed as
- * `scratch` is zero-filled on the launch stream the first time it is seen on a device (refused
- * with PK_ERR_CAPTURE if that first use is under stream capture).  A workspace stays dedicated
- * to the library until pk_workspace_forget / pk_workspace_free. */
+/* Bytes of the `scratch` argument the decode entry points require (present and at least this large).
+ * The scratch carries nothing between calls, as in the reference, where it is plain torch memory
+ * (decode_megakernel_360m/__init__.py:40-48): every word the kernels exchange lives in state the
+ * library allocates per device (uncached device memory for the exchange words, ordinary device memory
+ * for records that stay in one XCD's L2, a pinned host status word pair) on pk_init or the first
+ * decode call on the device, and keeps until the process ends.  As with the reference's per-device
+ * scratch, steps on one device must not run concurrently from two streams. */
 size_t pk_workspace_bytes(int model);
 
-/* Allocate a zeroed workspace on the current device: kind 0 ordinary device memory, 1 fine-grained
- * (lower cross-XCD latency for the exchange words), 2 uncached.  NULL on failure.  No reference
- * counterpart: the reference's wrapper allocates its scratch with torch
- * (decode_megakernel_360m/__init__.py:63). */
-void* pk_workspace_alloc(size_t bytes, int kind);
-/* Free a workspace; an uncached one (kind 2) is only forgotten and stays allocated until the
- * process ends, because uncached memory a kernel has read must not be reused. */
-int pk_workspace_free(void* ptr);
-/* The caller is reusing `ptr` for other data: it is zero-filled again at its next use. */
-int pk_workspace_forget(const void* ptr);
-/* Synchronous copy of n header words of a workspace to the host (0 epoch, 1 abort, 2 abort site). */
-int pk_workspace_read(const void* ws, size_t word, unsigned* out, int n);
+/* Allocate and zero the current device's state now, outside any stream capture (a first use under
+ * capture returns PK_ERR_CAPTURE).  Returns 0 or a status code.  No reference counterpart. */
+int pk_init(void);
+
+/* Library options (PK_OPT_*).  Returns the previous value, or -1 for an unknown option.  No reference
+ * counterpart. */
+int pk_set_option(int option, int value);
+
+/* Diagnostics (no reference counterpart).  pk_state_read synchronises `stream` and copies n header
+ * words of the current device's state (0 step epoch, 1 epoch of the last step that gave up a bounded
+ * wait, 2 its wait site).  pk_state_status reads the pending failure report {epoch, wait site}
+ * without clearing it; the next decode call on the device returns PK_ERR_ABORTED and clears it. */
+int pk_state_read(void* stream, size_t word, unsigned* out, int n);
+int pk_state_status(void* stream, unsigned* out);
+/* Test hooks (synchronous; no reference counterpart): set the step epoch of the current device's
+ * state, or mark the next step as failed so that each of its bounded waits gives up at once. */
+int pk_test_set_epoch(void* stream, unsigned epoch);
+int pk_test_abort_next(void* stream);
 
 /* One greedy decode step for B = 1..16 sequences (vLLM FLASH_ATTN metadata, paged KV
  * [blocks, KVH, 16, 128]; contexts may differ per sequence).  B = 1 runs the GEMV kernel; B >= 2

@@ -71,28 +71,23 @@ MODELS = {m.model_id: m for m in (SMOLLM2_360M, SMOLLM2_135M)}
 
 
 class _Runtime:
-    """Per-device state (reference: decode_megakernel_360m/__init__.py:60-70).
-
-    The workspace (exchange words + step epoch) is module-owned and lives for the process.  It is
-    uncached device memory (the fastest kind for the cross-XCD exchange words: 0.93 ms against
-    1.03 ms per 360M step for fine-grained or ordinary memory), unless PK_WORKSPACE selects "fine"
-    or "coarse"."""
+    """Per-device state (reference: decode_megakernel_360m/__init__.py:60-70): the scratch the C ABI
+    requires, the output and greedy-id buffers and the pointer tables.  The scratch carries nothing
+    between calls -- the library keeps every exchanged word in state of its own per device
+    (include/prime_decode.h, pk_workspace_bytes), created here, before any graph capture -- so it is
+    plain torch memory, as in the reference."""
 
     def __init__(self, model: Model, device: torch.device):
         lib = _native.library()
         self.lib = lib
         self.device = device
-        nbytes = lib.pk_workspace_bytes(model.model_id)
-        kinds = {"coarse": 0, "fine": 1, "uncached": 2}
-        choice = os.environ.get("PK_WORKSPACE", "uncached")
-        if choice not in kinds:
-            raise ValueError(f"PK_WORKSPACE must be one of {', '.join(kinds)}, got {choice!r}")
-        kind = kinds[choice]
         with torch.cuda.device(device):
-            ptr = lib.pk_workspace_alloc(nbytes, kind)
-        if not ptr:
-            raise RuntimeError(f"could not allocate a {nbytes}-byte decode workspace on {device}")
-        self.scratch_ptr = ptr
+            rc = lib.pk_init()
+        if rc != 0:
+            raise RuntimeError(f"{model.name}: library state for {device}: {_native.status_string(rc)}")
+        nbytes = lib.pk_workspace_bytes(model.model_id)
+        self.scratch = torch.empty((nbytes,), dtype=torch.uint8, device=device)
+        self.scratch_ptr = self.scratch.data_ptr()
         self.scratch_bytes = nbytes
         self.out = torch.empty((model.max_batch, model.hidden), dtype=torch.bfloat16, device=device)
         self.ids = torch.empty((model.max_batch,), dtype=torch.int64, device=device)
@@ -100,17 +95,28 @@ class _Runtime:
         self.kv_t = None
         self.table_key = None
 
-    def header(self, n: int = 3) -> list:
+    def _stream(self, stream):
+        return torch.cuda.current_stream(self.device).cuda_stream if stream is None else stream
+
+    def header(self, n: int = 3, stream=None) -> list:
+        """Header words of the device's library state: step epoch, the epoch of the last step that
+        gave up a bounded wait, its wait site.  Synchronises `stream` (default: the current one)."""
         buf = (ctypes.c_uint * n)()
         with torch.cuda.device(self.device):
-            rc = self.lib.pk_workspace_read(self.scratch_ptr, 0, buf, n)
+            rc = self.lib.pk_state_read(self._stream(stream), 0, buf, n)
         if rc != 0:
-            raise RuntimeError(f"workspace read failed: {_native.status_string(rc)}")
+            raise RuntimeError(f"state read failed: {_native.status_string(rc)}")
         return list(buf)
 
-    def abort_word(self) -> int:
-        """Non-zero when a bounded wait inside the kernel gave up (a failed step)."""
-        return self.header(2)[1]
+    def pending_failure(self, stream=None) -> tuple:
+        """(epoch, wait site) of a step on the device that gave up a bounded wait and has not been
+        reported by a decode call yet; (0, 0) when there is none.  Does not synchronise."""
+        buf = (ctypes.c_uint * 2)()
+        with torch.cuda.device(self.device):
+            rc = self.lib.pk_state_status(self._stream(stream), buf)
+        if rc != 0:
+            raise RuntimeError(f"state read failed: {_native.status_string(rc)}")
+        return buf[0], buf[1]
 
 
 _runtimes: dict = {}
@@ -149,6 +155,25 @@ def _tables(rt: _Runtime, layers, kv_caches):
             rt.kv_t.copy_(kv_table)
         rt.table_key = key
     return rt.layers_t, rt.kv_t
+
+
+def _failure_message(model: Model, rc: int) -> str:
+    if rc == _native.PK_ERR_ABORTED:
+        return (f"{model.name} failed: {_native.status_string(rc)} (an earlier step on this device could not "
+                f"complete; its hidden state and logits were set to NaN and its token ids to -1)")
+    return f"{model.name} failed: {_native.status_string(rc)}"
+
+
+def check_failures(model: Model, device: torch.device, stream=None) -> None:
+    """Synchronise `device` and raise RuntimeError if a decode step on it gave up a bounded wait
+    since the last report (decode calls report such a step at the next call; this reports it now)."""
+    rt = runtime(model, device)
+    s = rt._stream(stream)
+    torch.cuda.synchronize(device)
+    epoch, site = rt.pending_failure(s)
+    if epoch:
+        raise RuntimeError(f"{model.name}: the step with epoch {epoch} gave up a bounded wait (site {site}); "
+                           f"its outputs were poisoned")
 
 
 def decode_step(model: Model, *, input_ids, positions, seq_lens, block_table, slot_mapping, embed, layers,
@@ -276,7 +301,7 @@ def decode_step(model: Model, *, input_ids, positions, seq_lens, block_table, sl
         logits_out.data_ptr() if logits_out is not None else None,
         rt.scratch_ptr, rt.scratch_bytes, block_table.shape[1] * BLOCK_SIZE, *extra)
     if rc != 0:
-        raise RuntimeError(f"{model.name} failed: {_native.status_string(rc)}")
+        raise RuntimeError(_failure_message(model, rc))
     if return_token_ids:
         return rt.out[:batch], rt.ids[:batch]
     return rt.out[:batch]
@@ -344,4 +369,4 @@ class StepLauncher:
             self.ids.data_ptr() + 8 * B * (k + 1), self.logits.data_ptr() if self.logits is not None else None,
             rt.scratch_ptr, rt.scratch_bytes, self.max_seq, *extra)
         if rc != 0:
-            raise RuntimeError(f"{m.name} failed: {_native.status_string(rc)}")
+            raise RuntimeError(_failure_message(m, rc))

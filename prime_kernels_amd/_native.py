@@ -14,6 +14,12 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libprime_decode.so"
 MODEL_360M = 360
 MODEL_135M = 135
 
+# status codes of include/prime_decode.h that callers act on
+PK_ERR_ABORTED = 9113
+# pk_set_option options
+PK_OPT_COOPERATIVE = 1
+PK_OPT_SPLIT_ROLE = 2
+
 _lib = None
 
 vp, ci, ll, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_size_t
@@ -21,10 +27,12 @@ vp, ci, ll, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_size
 # symbol -> (restype, argtypes); the list every test checks against include/*.h
 SIGNATURES = {
     "pk_workspace_bytes": (sz, [ci]),
-    "pk_workspace_alloc": (vp, [sz, ci]),
-    "pk_workspace_free": (ci, [vp]),
-    "pk_workspace_forget": (ci, [vp]),
-    "pk_workspace_read": (ci, [vp, sz, ctypes.POINTER(ctypes.c_uint), ci]),
+    "pk_init": (ci, []),
+    "pk_set_option": (ci, [ci, ci]),
+    "pk_state_read": (ci, [vp, sz, ctypes.POINTER(ctypes.c_uint), ci]),
+    "pk_state_status": (ci, [vp, ctypes.POINTER(ctypes.c_uint)]),
+    "pk_test_set_epoch": (ci, [vp, ctypes.c_uint]),
+    "pk_test_abort_next": (ci, [vp]),
     "pk_decode": (ci, [vp, ci, ci, ci, vp, ci, vp, vp, vp, vp, vp, ci, vp, vp, vp,
                        ll, ll, ll, ll, ll, ci, vp, ci, vp, vp, vp, vp, vp, sz, ci]),
     "pk_decode_debug": (ci, [vp, ci, ci, ci, vp, ci, vp, vp, vp, vp, vp, ci, vp, vp, vp,

@@ -17,7 +17,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 LIB_DIR = PKG / "_lib"
 LIB = LIB_DIR / "libprime_decode.so"
-SOURCES = [PKG / "csrc" / "decode_megakernel.hip", PKG / "csrc" / "lossless_bf16.hip"]
+SOURCES = [PKG / "csrc" / "decode_megakernel.hip", PKG / "csrc" / "decode_sr.hip", PKG / "csrc" / "lossless_bf16.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -25,6 +25,8 @@ HIPCC_FLAGS = [
     # packed-fp32 ops are kept out of generated code on this target (known-unstable forms)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-inline-asm", f"-I{ROOT / 'include'}",
+    # every symbol the library uses must be defined in it
+    "-Wl,--no-undefined",
 ]
 
 

@@ -20,7 +20,7 @@
 //   then final RMSNorm + tied LM head GEMV with per-workgroup argmax, and a 256-way argmax.
 //
 // Inter-workgroup exchange: no counters, no fences.  Every exchanged value is written as a
-// 32-bit word {tag16, bf16} (or a 64-bit word {tag32, fp32}) with device-scope relaxed atomic
+// 64-bit word {bf16 or fp32 value, tag32} with device-scope relaxed atomic
 // stores, into a buffer owned by one (layer, phase, sequence).  Readers poll those words with
 // device-scope (sc1) loads until every tag equals this step's epoch, so the data arrives with
 // the "ready" signal in one round trip.  The epoch is a device counter bumped by workgroup 0 at
@@ -33,126 +33,15 @@
 #include <cstddef>
 #include <cstdint>
 
-#include "../../include/prime_decode.h"
-#include "../../include/prime_lossless.h"
+
+#include "pk_common.h"
 
 namespace pk {
 
-static unsigned long long* g_trace = nullptr;
 
 // ------------------------------------------------------------------------------------------------
 // Geometry and launch constants
 // ------------------------------------------------------------------------------------------------
-
-template <int H_, int NH_, int KVH_, int I_, int L_>
-struct Geom {
-  static constexpr int H = H_, NH = NH_, KVH = KVH_, D = 64, I = I_, L = L_, V = 49152;
-  static constexpr int QKV = (NH + 2 * KVH) * D;
-  static constexpr int GQA = NH / KVH;
-  static constexpr int WF = 0;  // projection weights: 0 bf16, 1 MXFP8 (e4m3 + e8m0 scale per 32)
-  static_assert(GQA == 3, "SmolLM2 uses 3 query heads per KV head");
-};
-using G360 = Geom<960, 15, 5, 2560, 32>;   // decode_megakernel_360m/__init__.py:27-35
-using G135 = Geom<576, 9, 3, 1536, 30>;    // decode_megakernel/__init__.py:37-43
-// SmolLM2-360M with MXFP8 projection weights (embedding / LM head and norms stay bf16).
-struct G360Q : G360 {
-  static constexpr int WF = 1;
-};
-
-// MXFP8 scales are stored one byte per 32 weights, each row padded to a multiple of 16 bytes so
-// that every row segment a workgroup streams starts and ends on a 16-byte boundary.
-__host__ __device__ constexpr int scale_stride(int K) { return ((K / 32 + 15) / 16) * 16; }
-
-constexpr int NWG = 256;                 // persistent workgroups (one per CU)
-#ifndef PK_PRODUCER_WAVES
-#define PK_PRODUCER_WAVES 4
-#endif
-#ifndef PK_DMA_DEPTH
-#define PK_DMA_DEPTH 8
-#endif
-#ifndef PK_POLL_SLEEP
-#define PK_POLL_SLEEP 0                  // s_sleep units (64 clocks) between polls (0: -0.2% at batch 1, -0.9% at 16, against 1)
-#endif
-constexpr int NPW = PK_PRODUCER_WAVES;   // producer waves per workgroup (LDS-DMA issue is per-wave bound)
-constexpr int NCW = 4;                   // consumer waves per workgroup
-constexpr int NCT = 64 * NCW;            // consumer threads
-constexpr int WG_THREADS = 64 * (NPW + NCW);
-constexpr uint32_t RING = 128u * 1024u;  // LDS ring bytes (power of two)
-constexpr uint32_t PKT = 1024;           // one LDS-DMA instruction: 64 lanes x 16 B
-constexpr int DEPTH = PK_DMA_DEPTH;      // packets in flight per producer wave (batch 1)
-// The batched kernel streams 1.4-2.5 GB of paged K/V per step and gains from more packets in
-// flight (32: -0.8% at config 4); at batch 1 more in flight lengthens the memory queues the
-// exchanges wait in (16 -> 24: +11%, 32: +19%; 8 is 0.3-0.4% faster than 16 at contexts 1024 to
-// 8192, also with a depth of 32 for the LM-head segments alone, which is slower).
-constexpr int DEPTH_B = 32;
-constexpr int TC_MAX = 256;              // max cached tokens per attention chunk (64 KB of K/V)
-// Batch-1 chunking of a KV head's cached tokens: chunks of up to TC_LONG tokens, but at least
-// C_SHORT chunks of at least TC_SHORT tokens while the context allows (measured at 360M batch 1:
-// more chunks shorten each chunk's work, and the exchanges between a head's chunks, through its
-// XCD's L2, cost little more with every chunk as long as the leader polls all partial records
-// in one batch)
-constexpr int TC_LONG = 128;
-constexpr int TC_SHORT = 64;
-constexpr int C_SHORT = 16;
-constexpr int LM_ROWS = 16;              // LM-head rows per ring segment
-constexpr int MAX_B = 16;                // exchange-buffer slots per layer
-constexpr int REC_WORDS = 3 * 64;        // attention partial: 3 heads x sum(p.v)[64], 64-bit words
-constexpr int STAT_WORDS = 6;            // chunk softmax statistics: 3 heads x (max, sum), 64-bit words
-constexpr uint32_t SPIN_LIMIT = 1u << 22;
-constexpr int kMaxSeq = 12288;          // tokens per sequence (block_table capacity)
-
-// Workspace header words.
-constexpr int HDR_EPOCH = 0;
-constexpr int HDR_ABORT = 1;
-constexpr int HDR_ABORT_WHERE = 2;
-constexpr size_t HDR_WORDS = 64;
-
-struct LayerW {
-  const void* norm1;        // [H] bf16
-  const void* qkv;          // [(NH+2KVH)*D, H]: q rows, then k rows, then v rows (bf16 or e4m3)
-  const void* o;            // [H, H]
-  const void* norm2;        // [H] bf16
-  const void* gate_up;      // [2I, H]: gate rows, then up rows
-  const void* down;         // [H, I]
-  const uint8_t* qkv_s;     // MXFP8 only: e8m0 scales [rows, scale_stride(K)] of the matrix above
-  const uint8_t* o_s;
-  const uint8_t* gate_up_s;
-  const uint8_t* down_s;
-};
-
-struct Params {
-  const void* const* layers;   // [L][6] bf16 (norm1, qkv, o, norm2, gate_up, down) or [L][10] MXFP8
-                               // (norm1, qkv, qkv_s, o, o_s, norm2, gate_up, gate_up_s, down, down_s)
-  const uint16_t* embed;       // [V, H]
-  const uint16_t* final_norm;  // [H]
-  const void* input_ids;       // [B] int32 or int64 (ids_i64)
-  void* const* kv;             // [L] paged caches
-  const int64_t* positions;    // [B]
-  const int32_t* seq_lens;     // [B] tokens attended, including the new one
-  const int32_t* block_table;  // [B, bt_stride]
-  const int64_t* slot_mapping; // [B]
-  const void* cos_sin;         // [max_pos, D]: cos [0, D/2), sin [D/2, D)
-  uint16_t* out_hidden;        // [B, H] final-normed hidden
-  uint16_t* layer_outputs;     // optional [L, B, H]
-  uint16_t* out_logits;        // optional [B, V]
-  int64_t* out_ids;            // optional [B] greedy ids
-  uint32_t* ws;                // workspace (header + exchange buffers), zero-initialised once
-  long long k_off, v_off, block_stride, token_stride, head_stride;  // elements
-  int bt_stride;
-  int cs_fp32;
-  int B;
-  int n_layers;
-  int lm_head;                 // 1: run the LM head + argmax
-  int max_seq;                 // block_table capacity in tokens (seq_lens are clamped to it)
-  int ids_i64;
-  unsigned long long* trace;   // optional per-phase timestamps (diagnostics)
-  uint32_t trace_lds;          // LDS byte offset of the launch's timestamp buffer (when tracing)
-  uint32_t* xws;               // optional: batch-1 attention records in ordinary device memory
-  const EncodedGULayer* encoded_gu;  // optional [L] lossless gate/up encodings (batch-1 bf16 kernel)
-  uint16_t* debug;             // optional per-stage capture (Dbg layout), batch <= 2
-  int debug_layer;             // layer whose attention internals are captured (-1: none)
-  const uint16_t* input_hidden;  // optional [B, H]: layer 0's input instead of the embedding rows
-};
 
 // Per-stage debug capture, the reference's layout (block360_kernel.inc:1-20), bf16 elements:
 // per layer [norm1, qkv, attn, o, h1, norm2, gate, up, silu, act, down, out], each [2][N] (rows for
@@ -202,8 +91,8 @@ template <class G>
 struct WS {
   static constexpr int XSLOTS = G::L * NKIND;
   static constexpr int XMAX = G::QKV > G::I ? (G::QKV > G::H ? G::QKV : G::H) : (G::I > G::H ? G::I : G::H);
-  static constexpr int XLINES = XMAX / 16;
-  static_assert(G::QKV % 16 == 0 && G::H % 16 == 0 && G::I % 16 == 0 && (G::H + G::KVH * 64) % 16 == 0,
+  static constexpr int XLINES = XMAX / 8;  // 64-byte lines of 8 words {bf16 value, tag32}
+  static_assert(G::QKV % 8 == 0 && G::H % 8 == 0 && G::I % 8 == 0 && (G::H + G::KVH * 64) % 8 == 0,
                 "vector segments start on 64-byte lines");
   static constexpr size_t X0 = HDR_WORDS;
   static constexpr size_t XWORDS = size_t(MAX_B) * XLINES * XSLOTS * 16;
@@ -213,9 +102,9 @@ struct WS {
   static constexpr size_t STAT_LAYER = size_t(NWG) * STAT_WORDS * 2;
   static constexpr size_t LM0 = STAT0 + STAT_LAYER * G::L;
   static constexpr size_t TOTAL = LM0 + size_t(MAX_B) * NWG * 2;
-  // word offset of element i of vector (kind, layer l, sequence b)
+  // 32-bit word offset of the 64-bit word {bf16 value, tag32} of element i of vector (kind, layer l, sequence b)
   __device__ static size_t xw(int kind, int l, int b, int i) {
-    return X0 + ((size_t(b) * XLINES + size_t(i >> 4)) * XSLOTS + size_t(l) * NKIND + kind) * 16 + size_t(i & 15);
+    return X0 + (((size_t(b) * XLINES + size_t(i >> 3)) * XSLOTS + size_t(l) * NKIND + kind) * 8 + size_t(i & 7)) * 2;
   }
   __device__ static size_t rec(int l, int item) { return REC0 + l * REC_LAYER + size_t(item) * REC_WORDS * 2; }
   // The batch-1 attention records (partials and statistics, REC0 .. LM0) can live in a separate
@@ -226,203 +115,9 @@ struct WS {
 };
 
 // ------------------------------------------------------------------------------------------------
-// Scalar and cross-lane helpers
-// ------------------------------------------------------------------------------------------------
-
-__device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
-__device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
-__device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
-
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-// fp32 -> bf16, round to nearest even (v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
-__device__ __forceinline__ float rnd(float f) { return float((__bf16)f); }
-// Two fp32 -> packed bf16 pair {lo = a, hi = b}, one instruction.
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-  const bf16x2 v = {(__bf16)a, (__bf16)b};
-  return __builtin_bit_cast(uint32_t, v);
-}
-// acc + a.lo*b.lo + a.hi*b.hi over packed bf16 pairs (v_dot2_f32_bf16).
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), acc, false);
-}
-
-// DPP move: lanes whose source is outside the row, or that the row/bank masks disable, get `old`.
-template <int CTRL, int RM = 0xf, int BM = 0xf>
-__device__ __forceinline__ float dpp(float old, float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
-                                                               __builtin_bit_cast(int, v), CTRL, RM, BM, false));
-}
-__device__ __forceinline__ float lane63(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-// Wave64 sum / max through DPP row shifts and row broadcasts; the result is uniform.
-__device__ __forceinline__ float wave_sum(float v) {
-  v += dpp<0x111>(0.f, v);            // row_shr:1
-  v += dpp<0x112>(0.f, v);            // row_shr:2
-  v += dpp<0x114, 0xf, 0xe>(0.f, v);  // row_shr:4, banks 1-3
-  v += dpp<0x118, 0xf, 0xc>(0.f, v);  // row_shr:8, banks 2-3
-  v += dpp<0x142, 0xa>(0.f, v);       // row_bcast:15 into rows 1, 3
-  v += dpp<0x143, 0xc>(0.f, v);       // row_bcast:31 into rows 2, 3
-  return lane63(v);
-}
-__device__ __forceinline__ float wave_max(float v) {
-  v = fmaxf(v, dpp<0x111>(v, v));
-  v = fmaxf(v, dpp<0x112>(v, v));
-  v = fmaxf(v, dpp<0x114, 0xf, 0xe>(v, v));
-  v = fmaxf(v, dpp<0x118, 0xf, 0xc>(v, v));
-  v = fmaxf(v, dpp<0x142, 0xa>(v, v));
-  v = fmaxf(v, dpp<0x143, 0xc>(v, v));
-  return lane63(v);
-}
-// wave_max / wave_sum of N values at once: the same steps per value, the N chains interleaved so
-// that each DPP step's wait states are filled by the other chains instead of s_nop.
-template <int N>
-__device__ __forceinline__ void wave_max_n(float (&v)[N]) {
-#pragma unroll
-  for (int k = 0; k < N; ++k) v[k] = fmaxf(v[k], dpp<0x111>(v[k], v[k]));
-#pragma unroll
-  for (int k = 0; k < N; ++k) v[k] = fmaxf(v[k], dpp<0x112>(v[k], v[k]));
-#pragma unroll
-  for (int k = 0; k < N; ++k) v[k] = fmaxf(v[k], dpp<0x114, 0xf, 0xe>(v[k], v[k]));
-#pragma unroll
-  for (int k = 0; k < N; ++k) v[k] = fmaxf(v[k], dpp<0x118, 0xf, 0xc>(v[k], v[k]));
-#pragma unroll
-  for (int k = 0; k < N; ++k) v[k] = fmaxf(v[k], dpp<0x142, 0xa>(v[k], v[k]));
-#pragma unroll
-  for (int k = 0; k < N; ++k) v[k] = fmaxf(v[k], dpp<0x143, 0xc>(v[k], v[k]));
-#pragma unroll
-  for (int k = 0; k < N; ++k) v[k] = lane63(v[k]);
-}
-template <int N>
-__device__ __forceinline__ void wave_sum_n(float (&v)[N]) {
-#pragma unroll
-  for (int k = 0; k < N; ++k) v[k] += dpp<0x111>(0.f, v[k]);
-#pragma unroll
-  for (int k = 0; k < N; ++k) v[k] += dpp<0x112>(0.f, v[k]);
-#pragma unroll
-  for (int k = 0; k < N; ++k) v[k] += dpp<0x114, 0xf, 0xe>(0.f, v[k]);
-#pragma unroll
-  for (int k = 0; k < N; ++k) v[k] += dpp<0x118, 0xf, 0xc>(0.f, v[k]);
-#pragma unroll
-  for (int k = 0; k < N; ++k) v[k] += dpp<0x142, 0xa>(0.f, v[k]);
-#pragma unroll
-  for (int k = 0; k < N; ++k) v[k] += dpp<0x143, 0xc>(0.f, v[k]);
-#pragma unroll
-  for (int k = 0; k < N; ++k) v[k] = lane63(v[k]);
-}
-// Sum over each aligned group of 8 lanes; every lane of the group gets the group sum.
-__device__ __forceinline__ float group8_sum(float v) {
-  v += dpp<0xb1>(0.f, v);                  // quad_perm [1,0,3,2]
-  v += dpp<0x4e>(0.f, v);                  // quad_perm [2,3,0,1]
-  float t = dpp<0x104, 0xf, 0x5>(0.f, v);  // row_shl:4 into banks 0, 2
-  t = dpp<0x114, 0xf, 0xa>(t, v);          // row_shr:4 into banks 1, 3
-  return v + t;
-}
-
-// Device-scope (coherent across XCDs) accesses for exchange words.
-__device__ __forceinline__ uint32_t ld_dev(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t ld_dev64(const uint64_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev64(uint64_t* p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Plain 64-bit store (no cache-policy bits): through the write-through L1 into the XCD's L2, where
-// device-scope loads from the same XCD see it.
-__device__ __forceinline__ void st_l2(uint64_t* p, uint64_t v) {
-  typedef __attribute__((address_space(1))) uint64_t g_u64;
-  *(g_u64*)(p) = v;
-}
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-// Stores into caller memory through a pointer read from LDS (the KV cache base): without the
-// explicit global address space the compiler emits a flat store, which also counts on the LDS
-// counter, so the wave's next wait for an LDS read would also wait for this store's completion.
-typedef __attribute__((address_space(1))) u32x4 g_u32x4;
-typedef __attribute__((address_space(1))) uint16_t g_u16;
-__device__ __forceinline__ void st_global16(uint16_t* dst, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-  const u32x4 v = {a, b, c, d};
-  *(g_u32x4*)(dst) = v;
-}
-__device__ __forceinline__ void st_global2(uint16_t* dst, uint16_t v) { *(g_u16*)(dst) = v; }
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
-}
-// 16-byte device-scope load (sc1); each 32-bit word is read atomically.
-__device__ __forceinline__ u32x4 ld_dev128(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, int(byte_off), 0, 16);
-}
-
-// LDS words shared between the waves of one workgroup.
-__device__ __forceinline__ uint32_t ld_lds(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-__device__ __forceinline__ void st_lds(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-
-// One LDS-DMA packet: lane i copies 16 bytes from `g` to LDS byte address m0 + 16*i.  Written as
-// inline asm so the compiler does not force vmcnt(0) before the producer's LDS counter writes;
-// the producer waits on vmcnt itself.
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_addr), "v"(g)
-               : "memory", "m0");
-}
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
-
-// Diagnostic timestamps: TR_EVENTS per layer per workgroup, plus TR_TAIL at the end.  During the
-// launch they are kept in LDS, past the kernel's own shared memory, as the low 32 bits of the
-// 100 MHz clock, and written out as full 64-bit values when the workgroup ends: a global store
-// per event would add its acknowledgement to the next wait on the wave's memory counter, and so
-// stretch the phases being timed.
-constexpr int TR_EVENTS = 40;
-constexpr int TR_TAIL = 4;
-constexpr int TR_LAYERS = 32;
-constexpr uint32_t TRACE_LDS_BYTES = uint32_t(TR_LAYERS * TR_EVENTS + TR_TAIL) * 4u;
-__device__ __forceinline__ uint32_t* trace_lds(const Params& p) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
-  return reinterpret_cast<uint32_t*>(smem_raw + p.trace_lds);
-}
-__device__ __forceinline__ void trace_at(const Params& p, int layer, int ev, int n_layers) {
-  if (p.trace) trace_lds(p)[layer * TR_EVENTS + ev] = uint32_t(wall_clock64());
-}
-__device__ __forceinline__ void trace_tail(const Params& p, int k) {
-  if (p.trace) trace_lds(p)[p.n_layers * TR_EVENTS + k] = uint32_t(wall_clock64());
-}
-// Before the workgroup's first barrier: clear the buffer (0 = event not reached).
-__device__ __forceinline__ void trace_begin(const Params& p) {
-  if (p.trace)
-    for (int i = threadIdx.x; i < p.n_layers * TR_EVENTS + TR_TAIL; i += blockDim.x) trace_lds(p)[i] = 0u;
-}
-// After the workgroup's last barrier: full timestamps, each the latest clock value with its low bits
-// (the launch is far shorter than the 43 s the low 32 bits cover).
-__device__ __forceinline__ void trace_end(const Params& p) {
-  if (!p.trace) return;
-  const uint64_t now = wall_clock64();
-  const int n = p.n_layers * TR_EVENTS + TR_TAIL;
-  const uint32_t* t = trace_lds(p);
-  unsigned long long* out = p.trace + size_t(blockIdx.x) * size_t(n);
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const uint32_t lo = t[i];
-    out[i] = lo ? now - uint64_t(uint32_t(uint32_t(now) - lo)) : 0ull;
-  }
-}
-
-// ------------------------------------------------------------------------------------------------
 // Per-workgroup plan: which rows / chunk this workgroup owns.  Computed identically by all waves.
 // ------------------------------------------------------------------------------------------------
 
-__device__ __forceinline__ int split_lo(int n, int parts, int i) { return int((long long)n * i / parts); }
 
 template <class G>
 struct Plan {
@@ -554,7 +249,6 @@ __device__ __forceinline__ uint32_t seg_bytes(const Plan<G>& P, int kind, int lm
   }
 }
 
-__device__ __forceinline__ uint32_t pad_pkt(uint32_t b) { return (b + PKT - 1) & ~(PKT - 1); }
 
 // Ring byte offset (within a KV segment) of 16-byte piece `part` of K (v=0) or V (v=1) of token j.
 __device__ __forceinline__ uint32_t kv_slot(int j, int v, int part) {
@@ -598,31 +292,6 @@ struct Smem {
 };
 
 // ------------------------------------------------------------------------------------------------
-// Spin helper with a bound and a global abort word, so a logic error cannot hang the GPU.
-// ------------------------------------------------------------------------------------------------
-
-struct Spin {
-  uint32_t n = 0;
-  uint32_t* abort_word;
-  int where;
-  __device__ __forceinline__ Spin(uint32_t* ws, int w) : abort_word(ws + HDR_ABORT), where(w) {}
-  // Returns false when the wait must be abandoned.
-  __device__ __forceinline__ bool again() {
-    ++n;
-    if ((n & 127u) == 0) {
-      if (ld_dev(abort_word)) return false;
-      if (n >= SPIN_LIMIT) {
-        st_dev(abort_word, 1u);
-        st_dev(abort_word + 1, uint32_t(where));
-        return false;
-      }
-    }
-    __builtin_amdgcn_s_sleep(PK_POLL_SLEEP);
-    return true;
-  }
-};
-
-// ------------------------------------------------------------------------------------------------
 // Producer wave
 // ------------------------------------------------------------------------------------------------
 
@@ -632,7 +301,7 @@ struct Spin {
 // minimum over the waves.  Nothing here waits on a compiler-visible vector-memory load: the
 // pointer tables and block ids come from LDS, so the only vmcnt waits are the explicit ones.
 template <class G>
-__device__ __forceinline__ void producer(const Params& p, const Plan<G>& P, Smem<G>& sm) {
+__device__ __forceinline__ void producer(const Params& p, const Plan<G>& P, Smem<G>& sm, uint32_t epoch) {
   const int pw = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const uint32_t ring_base = uint32_t(reinterpret_cast<uintptr_t>(sm.ring));
@@ -645,7 +314,7 @@ __device__ __forceinline__ void producer(const Params& p, const Plan<G>& P, Smem
   __builtin_amdgcn_s_barrier();  // consumers may read blk[] after this
 
   uint32_t n = 0;  // global packet index at the start of the current segment
-  Spin spin(p.ws, 1);
+  Spin spin(p.ws, epoch, 1);
   bool dead = false;
   auto cmin = [&]() -> uint32_t {
     uint32_t c = ld_lds(&sm.consumed[0]);
@@ -754,7 +423,7 @@ struct Consumer {
   int cw, lane, ct;          // consumer wave, lane, consumer thread id
   uint32_t pos = 0;          // stream cursor (mirrors the producer)
   uint32_t bar_gen = 0;
-  uint32_t tag16, tag32;
+  uint32_t tag32;
   bool dead = false;
   int xr;                    // the copy of the batch-1 exchange vectors this workgroup polls
 
@@ -765,7 +434,6 @@ struct Consumer {
     lane = threadIdx.x & 63;
     ct = cw * 64 + lane;
     tag32 = ep;
-    tag16 = ((ep - 1u) % 65535u) + 1u;
   }
 
   // Makes the lane ids opaque at a phase boundary, so per-lane addresses are recomputed inside the
@@ -773,9 +441,9 @@ struct Consumer {
   __device__ __forceinline__ void refresh() { asm volatile("" : "+v"(lane), "+v"(ct)); }
 
   // Batch-1 exchange word: element i of vector (kind, layer l), written to every copy.
-  __device__ __forceinline__ void st_x(int kind, int l, int i, uint32_t v) const {
+  __device__ __forceinline__ void st_x(int kind, int l, int i, uint64_t v) const {
 #pragma unroll
-    for (int r = 0; r < XREP; ++r) st_dev(p.ws + WS<G>::xw(kind, l, r, i), v);
+    for (int r = 0; r < XREP; ++r) st_dev64(reinterpret_cast<uint64_t*>(p.ws + WS<G>::xw(kind, l, r, i)), v);
   }
 
   // Claims the next segment of the stream; returns its start position.
@@ -797,7 +465,7 @@ struct Consumer {
   }
   __device__ __forceinline__ void wait_filled(uint32_t end) {
     if (dead || end <= seen) return;
-    Spin spin(p.ws, 2);
+    Spin spin(p.ws, tag32, 2);
     while ((seen = filled()) < end)
       if (!spin.again()) { dead = true; return; }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the ring reads that follow stay after the wait
@@ -810,7 +478,7 @@ struct Consumer {
   __device__ __forceinline__ void cbar() {
     bar_gen += NCW;
     if (lane == 0) __hip_atomic_fetch_add(&sm.cbar, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-    Spin spin(p.ws, 3);
+    Spin spin(p.ws, tag32, 3);
     while (ld_lds(&sm.cbar) < bar_gen)
       if (!spin.again()) { dead = true; break; }
   }
@@ -823,14 +491,13 @@ struct Consumer {
   __device__ __forceinline__ uint2 ring8(uint32_t at) const {
     return *reinterpret_cast<const uint2*>(sm.ring + (at & (RB - 1)));
   }
-  __device__ __forceinline__ uint32_t w16(float v) const { return (tag16 << 16) | f2bf(v); }
-  __device__ __forceinline__ bool ok4(u32x4 v) const {
-    return (v.x >> 16) == tag16 && (v.y >> 16) == tag16 && (v.z >> 16) == tag16 && (v.w >> 16) == tag16;
-  }
+  // an exchange word {bf16 value, tag32}; a 16-byte load holds two of them
+  __device__ __forceinline__ uint64_t w64(float v) const { return (uint64_t(tag32) << 32) | f2bf(v); }
+  __device__ __forceinline__ bool ok2(u32x4 v) const { return v.y == tag32 && v.w == tag32; }
 
-  // Poll `n` (multiple of 4) tagged bf16 words at ws+off, split over all consumer threads; writes
-  // the values (fp32) to dst[] (and keep[] when given).  Every load of a thread is in flight at
-  // once; only groups whose tags are stale are polled again.  Returns this wave's sum of squares.
+  // Poll `n` (even) tagged exchange words, two per 16-byte load, split over all consumer threads;
+  // writes the values (fp32) to dst[] (and keep[] when given).  Every load of a thread is in flight
+  // at once; only pairs whose tags are stale are polled again.  Returns this wave's sum of squares.
   template <int MAXG>
   __device__ __forceinline__ float poll_split(int kind, int l, int b, int n, float* dst, float* keep) {
     const __amdgpu_buffer_rsrc_t r = rsrc(p.ws);
@@ -839,21 +506,21 @@ struct Consumer {
     uint32_t pend = 0;
 #pragma unroll
     for (int g = 0; g < MAXG; ++g) {
-      const int i = (ct + g * NCT) * 4;
+      const int i = (ct + g * NCT) * 2;
       if (i < n) { v[g] = ld_dev128(r, at(i)); pend |= 1u << g; }
     }
     float ss = 0.f;
-    Spin spin(p.ws, 4);
+    Spin spin(p.ws, tag32, 4);
     while (true) {
 #pragma unroll
       for (int g = 0; g < MAXG; ++g) {
         if ((pend >> g) & 1u) {
-          if (ok4(v[g])) {
-            const int i = (ct + g * NCT) * 4;
-            const float f0 = bf_lo(v[g].x), f1 = bf_lo(v[g].y), f2 = bf_lo(v[g].z), f3 = bf_lo(v[g].w);
-            *reinterpret_cast<float4*>(dst + i) = make_float4(f0, f1, f2, f3);
-            if (keep) *reinterpret_cast<float4*>(keep + i) = make_float4(f0, f1, f2, f3);
-            ss += f0 * f0 + f1 * f1 + f2 * f2 + f3 * f3;
+          if (ok2(v[g])) {
+            const int i = (ct + g * NCT) * 2;
+            const float f0 = bf_lo(v[g].x), f1 = bf_lo(v[g].z);
+            *reinterpret_cast<float2*>(dst + i) = make_float2(f0, f1);
+            if (keep) *reinterpret_cast<float2*>(keep + i) = make_float2(f0, f1);
+            ss += f0 * f0 + f1 * f1;
             pend &= ~(1u << g);
           }
         }
@@ -862,14 +529,14 @@ struct Consumer {
       if (dead || !spin.again()) { dead = true; break; }
 #pragma unroll
       for (int g = 0; g < MAXG; ++g)
-        if ((pend >> g) & 1u) v[g] = ld_dev128(r, at((ct + g * NCT) * 4));
+        if ((pend >> g) & 1u) v[g] = ld_dev128(r, at((ct + g * NCT) * 2));
     }
     return wave_sum(ss);
   }
 
   // Poll three element ranges [e0, e0+n0), [e1, e1+n1), [e2, e2+n2) of the qkv vector of layer l
-  // (each a multiple of 4 elements starting on a 4-element boundary, total <= 512) with this wave
-  // alone (no barrier); values -> dst[0 .. n0 + n1 + n2).  Both loads of a lane are in flight at once.
+  // (each an even number of elements starting on an even element, total <= 512) with this wave
+  // alone (no barrier); values -> dst[0 .. n0 + n1 + n2).  All loads of a lane are in flight at once.
   __device__ __forceinline__ void poll_wave3(int l, int b, int e0, int n0, int e1, int n1, int e2, int n2,
                                              float* dst) {
     const __amdgpu_buffer_rsrc_t r = rsrc(p.ws);
@@ -878,25 +545,27 @@ struct Consumer {
       return ld_dev128(r, uint32_t(WS<G>::xw(X_QKV, l, b, e)) * 4u);
     };
     const int n = n0 + n1 + n2;
-    const int i0 = lane * 4, i1 = (lane + 64) * 4;
-    u32x4 v0, v1;
+    constexpr int NL = 4;  // 16-byte loads per lane: 2 values each
+    u32x4 v[NL];
     uint32_t pend = 0;
-    if (i0 < n) { v0 = load(i0); pend |= 1u; }
-    if (i1 < n) { v1 = load(i1); pend |= 2u; }
-    Spin spin(p.ws, 7);
+#pragma unroll
+    for (int k = 0; k < NL; ++k) {
+      const int i = (lane + 64 * k) * 2;
+      if (i < n) { v[k] = load(i); pend |= 1u << k; }
+    }
+    Spin spin(p.ws, tag32, 7);
     while (true) {
-      if ((pend & 1u) && ok4(v0)) {
-        *reinterpret_cast<float4*>(dst + i0) = make_float4(bf_lo(v0.x), bf_lo(v0.y), bf_lo(v0.z), bf_lo(v0.w));
-        pend &= ~1u;
-      }
-      if ((pend & 2u) && ok4(v1)) {
-        *reinterpret_cast<float4*>(dst + i1) = make_float4(bf_lo(v1.x), bf_lo(v1.y), bf_lo(v1.z), bf_lo(v1.w));
-        pend &= ~2u;
-      }
+#pragma unroll
+      for (int k = 0; k < NL; ++k)
+        if (((pend >> k) & 1u) && ok2(v[k])) {
+          *reinterpret_cast<float2*>(dst + (lane + 64 * k) * 2) = make_float2(bf_lo(v[k].x), bf_lo(v[k].z));
+          pend &= ~(1u << k);
+        }
       if (!pend) break;
       if (dead || !spin.again()) { dead = true; break; }
-      if (pend & 1u) v0 = load(i0);
-      if (pend & 2u) v1 = load(i1);
+#pragma unroll
+      for (int k = 0; k < NL; ++k)
+        if ((pend >> k) & 1u) v[k] = load((lane + 64 * k) * 2);
     }
   }
 
@@ -911,18 +580,6 @@ struct Consumer {
   }
 };
 
-// A lane owns the 16-byte weight chunks j = lane + 64*c of every row; a chunk holds EPC weights
-// (8 bf16, or 16 e4m3 values), i.e. EPC/8 blocks of 8 activations.
-template <int K, int EPC = 8>
-struct Chunks {
-  static constexpr int CH = K / EPC;
-  static constexpr int CPL = (CH + 63) / 64;
-  static constexpr int SUB = EPC / 8;
-};
-// A lane's activation (or norm-weight) operand for K-long rows of chunk size EPC: 8 values per uint4.
-template <int K, int EPC = 8>
-using XChunks = uint4[Chunks<K, EPC>::CPL][EPC / 8];
-
 // Norm weights of a lane's chunks (8-element blocks), from the ring segment that carries them.
 template <class G, int K, int EPC>
 __device__ __forceinline__ void load_normw(const Consumer<G>& C, XChunks<K, EPC>& nw,
@@ -933,41 +590,6 @@ __device__ __forceinline__ void load_normw(const Consumer<G>& C, XChunks<K, EPC>
 #pragma unroll
     for (int i = 0; i < EPC / 8; ++i)
       nw[c][i] = ch < Chunks<K, EPC>::CH ? C.ring16(seg + uint32_t(ch * EPC + 8 * i) * 2u) : make_uint4(0, 0, 0, 0);
-  }
-}
-
-// Activation chunks of a lane from LDS as packed bf16 pairs: plain (the values are bf16 already),
-// or RMS-normalised with LlamaRMSNorm rounding y = bf16(w * bf16(x * rs)) (modeling_llama.py:62-67).
-template <int K, int EPC, bool NORM>
-__device__ __forceinline__ void load_x(XChunks<K, EPC>& x, const float* xs,
-                                       const XChunks<K, EPC>& nw, float rs, int lane) {
-#pragma unroll
-  for (int c = 0; c < Chunks<K, EPC>::CPL; ++c) {
-    const int ch = lane + 64 * c;
-#pragma unroll
-    for (int i = 0; i < EPC / 8; ++i) {
-      if (ch < Chunks<K, EPC>::CH) {
-        const float* src = xs + ch * EPC + 8 * i;
-        const float4 a = *reinterpret_cast<const float4*>(src);
-        const float4 b = *reinterpret_cast<const float4*>(src + 4);
-        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        uint32_t o[4];
-        if (NORM) {
-          const uint32_t u[4] = {nw[c][i].x, nw[c][i].y, nw[c][i].z, nw[c][i].w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t t = pack2(v[2 * e] * rs, v[2 * e + 1] * rs);
-            o[e] = pack2(bf_lo(u[e]) * bf_lo(t), bf_hi(u[e]) * bf_hi(t));
-          }
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = pack2(v[2 * e], v[2 * e + 1]);
-        }
-        x[c][i] = make_uint4(o[0], o[1], o[2], o[3]);
-      } else {
-        x[c][i] = make_uint4(0, 0, 0, 0);
-      }
-    }
   }
 }
 
@@ -1189,10 +811,6 @@ __device__ __forceinline__ float pick(const float (&out)[MAXR], int lane) {
   return v;
 }
 
-__device__ __forceinline__ float rms_scale(float sumsq, int n) {
-  const float mean = sumsq / float(n);
-  return 1.0f / sqrtf(mean + 1e-5f);
-}
 
 // ------------------------------------------------------------------------------------------------
 // P2: attention for one chunk (batch 1).  The chunk's tokens (cached ones, plus the new one for the
@@ -1235,7 +853,7 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
     return uint32_t(W::xw(X_QKV, l, C.xr, i < 64 ? G::H + g * 64 + i : G::H + G::KVH * 64 + g * 64 + i - 64)) * 4u;
   };
   u32x4 kvw = {0u, 0u, 0u, 0u};
-  if (has_new && lane < 32) kvw = ld_dev128(rkv, kv_at(lane * 4));
+  if (has_new) kvw = ld_dev128(rkv, kv_at(lane * 2));
   C.wait_filled(C.pos);  // cos/sin row and KV chunk are in the ring
   // cos/sin of dims 8*part .. 8*part+7 (mod 32): contiguous in the table row of this position
   auto load_cs = [&](float (&cs8)[8], float (&sn8)[8]) {
@@ -1321,13 +939,13 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   if (has_new) {
     // the new key and value, RoPE on the key, and its score (every 8-lane group computes it; the
     // first group keeps it)
-    if (lane < 32) {
-      Spin spin(p.ws, 7);
-      while (!C.ok4(kvw)) {
+    {
+      Spin spin(p.ws, C.tag32, 7);
+      while (!C.ok2(kvw)) {
         if (C.dead || !spin.again()) { C.dead = true; break; }
-        kvw = ld_dev128(rkv, kv_at(lane * 4));
+        kvw = ld_dev128(rkv, kv_at(lane * 2));
       }
-      *reinterpret_cast<float4*>(in + 192 + lane * 4) = make_float4(bf_lo(kvw.x), bf_lo(kvw.y), bf_lo(kvw.z), bf_lo(kvw.w));
+      *reinterpret_cast<float2*>(in + 192 + lane * 2) = make_float2(bf_lo(kvw.x), bf_lo(kvw.z));
     }
     // the cos/sin row is read again (still in the ring): held in registers across the scores it
     // would take 16 of them where the kernel has none to spare
@@ -1411,7 +1029,7 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
       }
     }
     auto fresh = [&](const u32x4& v) { return v.y == C.tag32 && v.w == C.tag32; };
-    Spin spin(p.ws, 6);
+    Spin spin(p.ws, C.tag32, 6);
     while (true) {
 #pragma unroll
       for (int i = 0; i < 2; ++i)
@@ -1567,7 +1185,7 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
         ro[k] = ld_dev64(rec_base + size_t(g * P.C + c0 + k) * REC_WORDS + hh * 64 + d);
         pend |= 1u << k;
       }
-    Spin spin(p.ws, 5);
+    Spin spin(p.ws, C.tag32, 5);
     while (true) {
 #pragma unroll
       for (int k = 0; k < MB; ++k)
@@ -1584,7 +1202,7 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   }
   if (w == 0 && lane == 0) trace_at(p, l, 20, p.n_layers);
   O += o_own;
-  C.st_x(X_ATTN, l, (g * 3 + hh) * 64 + d, C.w16(O));
+  C.st_x(X_ATTN, l, (g * 3 + hh) * 64 + d, C.w64(O));
   if (DBG && p.debug) {
     const uint16_t ob = uint16_t(f2bf(O));
     p.debug[size_t(l) * Dbg<G>::LAYER + Dbg<G>::ATTN + (g * 3 + hh) * 64 + d] = ob;
@@ -1603,8 +1221,8 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
   __builtin_amdgcn_s_barrier();  // pairs with the producer's barrier (blk[] ready)
   using W = WS<G>;
   using R = Rows<G>;
-  constexpr int GH = (G::H + NCT * 4 - 1) / (NCT * 4);   // poll groups per thread, H words
-  constexpr int GI = (G::I + NCT * 4 - 1) / (NCT * 4);   // ... I words
+  constexpr int GH = (G::H + NCT * 2 - 1) / (NCT * 2);   // poll loads per thread, H words
+  constexpr int GI = (G::I + NCT * 2 - 1) / (NCT * 2);   // ... I words
   constexpr int EW = G::WF ? 16 : 8;                      // activations per 16-byte weight chunk
   const int b = 0;
   auto tr = [&](int l, int ev) { if (C.ct == 0) trace_at(p, l, ev, p.n_layers); };
@@ -1660,7 +1278,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       tr(l, 22);
       const int row = C.cw + NCW * C.lane;
       if (C.lane < R::QKV && row < P.q1 - P.q0) {
-        C.st_x(X_QKV, l, P.q0 + row, C.w16(pick(out, C.lane)));
+        C.st_x(X_QKV, l, P.q0 + row, C.w64(pick(out, C.lane)));
         if (DBG && p.debug) dl(l)[Dbg<G>::QKV + P.q0 + row] = uint16_t(f2bf(pick(out, C.lane)));
       }
       tr(l, 2);
@@ -1694,7 +1312,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
         if (C.lane < R::O && row < nrows) {
           const int r = P.o0 + row;
           const float o = rnd(pick(out, C.lane));
-          C.st_x(X_H1, l, r, C.w16(sm.xkeep[r] + o));
+          C.st_x(X_H1, l, r, C.w64(sm.xkeep[r] + o));
           if (DBG && p.debug) {
             dl(l)[Dbg<G>::O + r] = uint16_t(f2bf(o));
             dl(l)[Dbg<G>::H1 + r] = uint16_t(f2bf(sm.xkeep[r] + o));
@@ -1762,7 +1380,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       if (C.lane < R::ACT && row < na) {
         const float gv = rnd(pick(og, C.lane)), uv = rnd(pick(ou, C.lane));
         const float silu = rnd(gv / (1.0f + expf(-gv)));
-        C.st_x(X_ACT, l, P.a0 + row, C.w16(silu * uv));
+        C.st_x(X_ACT, l, P.a0 + row, C.w64(silu * uv));
         if (DBG && p.debug) {
           const int r = P.a0 + row;
           dl(l)[Dbg<G>::GATE + r] = uint16_t(f2bf(gv));
@@ -1794,7 +1412,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       if (C.lane < R::DOWN && row < nrows) {
         const int r = P.d0 + row;
         const float y = rnd(sm.h1keep[r] + rnd(pick(out, C.lane)));
-        C.st_x(X_X, l, r, C.w16(y));
+        C.st_x(X_X, l, r, C.w64(y));
         if (DBG && p.debug) {
           dl(l)[Dbg<G>::DOWN + r] = uint16_t(f2bf(rnd(pick(out, C.lane))));
           dl(l)[Dbg<G>::OUT + r] = uint16_t(f2bf(y));
@@ -1823,10 +1441,9 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
         *reinterpret_cast<uint4*>(p.out_hidden + size_t(b) * G::H + ch * 8) = x[c][0];
     }
   }
-  if (!p.lm_head) return;
   float best = -INFINITY;
   int best_i = 0x7fffffff;
-  for (int j = 0; j < P.n_lm; ++j) {
+  for (int j = 0; j < P.n_lm; ++j) {  // no segments without the LM head
     const uint32_t seg = C.next_seg(seg_bytes(P, S_LM, j, p.cs_fp32));
     const int r0 = P.v0 + j * LM_ROWS;
     const int nrows = min(LM_ROWS, P.v1 - r0);
@@ -1852,44 +1469,61 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
   if (C.lane == 0) { sm.lm_val[C.cw] = best; sm.lm_idx[C.cw] = best_i; }
   C.cbar();
   if (C.ct == 0) trace_tail(p, 1);
+  // every workgroup's end record {bf16 best value, 16-bit index, tag32}: index LM_DEAD when one of
+  // its waits gave up, LM_NONE without an LM head; workgroup 0 gathers them all
   if (C.ct == 0) {
     float bv = sm.lm_val[0];
     int bi = sm.lm_idx[0];
     for (int w = 1; w < NCW; ++w)
       if (sm.lm_val[w] > bv || (sm.lm_val[w] == bv && sm.lm_idx[w] < bi)) { bv = sm.lm_val[w]; bi = sm.lm_idx[w]; }
-    const uint64_t rec = (uint64_t(C.tag32) << 32) | (uint64_t(uint32_t(bi) & 0xffffu) << 16) | f2bf(bv);
+    const uint32_t idx = C.dead ? LM_DEAD : p.lm_head ? uint32_t(bi) & 0xffffu : LM_NONE;
+    const uint64_t rec = (uint64_t(C.tag32) << 32) | (uint64_t(idx) << 16) | f2bf(bv);
     st_dev64(reinterpret_cast<uint64_t*>(p.ws + W::lm(b, P.wg)), rec);
   }
-  if (P.wg != 0) return;
+  if (P.wg != 0) {
+    if (p.out_logits && (C.dead || aborted(p.ws, C.tag32)))  // this workgroup's logits rows are not valid
+      for (int i = P.v0 + C.ct; i < P.v1; i += NCT) p.out_logits[size_t(b) * G::V + i] = 0x7fc0;
+    return;
+  }
   // workgroup 0: argmax over the NWG candidates (first index on ties, as torch.argmax)
   float bv = -INFINITY;
   int bi = 0x7fffffff;
+  uint32_t bad = 0;
   for (int q = C.ct; q < NWG; q += NCT) {
     const uint64_t* src = reinterpret_cast<const uint64_t*>(p.ws + W::lm(b, q));
-    Spin spin(p.ws, 6);
+    Spin spin(p.ws, C.tag32, 6);
     uint64_t r = ld_dev64(src);
     while (uint32_t(r >> 32) != C.tag32) {
-      if (C.dead || !spin.again()) { C.dead = true; break; }
+      if (!spin.again()) { bad = 1; break; }
       r = ld_dev64(src);
     }
     const float v = bf2f(uint32_t(r) & 0xffffu);
     const int i = int((uint32_t(r) >> 16) & 0xffffu);
+    bad |= (i == int(LM_DEAD)) ? 1u : 0u;
     if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
   }
+  const bool any_bad = __builtin_amdgcn_ballot_w64(bad != 0u) != 0ull;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(bv, o);
     const int oi = __shfl_xor(bi, o);
     if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
   }
-  if (C.lane == 0) { sm.lm_val[C.cw] = bv; sm.lm_idx[C.cw] = bi; }
+  if (C.lane == 0) { sm.lm_val[C.cw] = bv; sm.lm_idx[C.cw] = bi; sm.red[C.cw] = any_bad ? 1.f : 0.f; }
   C.cbar();
+  bool fail = C.dead || aborted(p.ws, C.tag32);
+  for (int w = 0; w < NCW; ++w) fail = fail || sm.red[w] != 0.f;
   if (C.ct == 0) {
     bv = sm.lm_val[0];
     bi = sm.lm_idx[0];
     for (int w = 1; w < NCW; ++w)
       if (sm.lm_val[w] > bv || (sm.lm_val[w] == bv && sm.lm_idx[w] < bi)) { bv = sm.lm_val[w]; bi = sm.lm_idx[w]; }
-    if (p.out_ids) p.out_ids[b] = bi;
+    if (p.out_ids) p.out_ids[b] = fail ? -1 : bi;
+  }
+  if (fail) {
+    step_failed(p, C.tag32, C.ct, b);
+    if (p.out_logits)  // workgroup 0's own logits rows
+      for (int i = P.v0 + C.ct; i < P.v1; i += NCT) p.out_logits[size_t(b) * G::V + i] = 0x7fc0;
   }
 }
 
@@ -1899,6 +1533,8 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
 
 template <class G, bool DBG = false>
 __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel(Params p) {
+  // the split-role kernel, launched before this one, did the step when the context is within its limit
+  if (p.sr_max_s > 0 && min(max(p.seq_lens[0], 1), p.max_seq) <= p.sr_max_s) return;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
   Smem<G>& sm = *reinterpret_cast<Smem<G>*>(smem_raw);
   if (threadIdx.x == 0) {
@@ -1944,9 +1580,8 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel(Params p) {
   __syncthreads();
   Plan<G> P;
   P.init(p, blockIdx.x);
-  uint32_t epoch = ld_dev(p.ws + HDR_EPOCH) + 1u;
-  if (epoch == 0) epoch = 1;
-  if (threadIdx.x < 64 * NPW) producer<G>(p, P, sm);
+  const uint32_t epoch = step_epoch(p.ws);
+  if (threadIdx.x < 64 * NPW) producer<G>(p, P, sm, epoch);
   else consumer<G, DBG>(p, P, sm, epoch);
   __syncthreads();
   if (blockIdx.x == 0 && threadIdx.x == 0) st_dev(p.ws + HDR_EPOCH, epoch);
@@ -2140,7 +1775,7 @@ __device__ __forceinline__ uint32_t segb_bytes(const PlanB<G>& P, const ItemB* i
 }
 
 template <class G>
-__device__ __forceinline__ void producer_b(const Params& p, const PlanB<G>& P, SmemB<G>& sm) {
+__device__ __forceinline__ void producer_b(const Params& p, const PlanB<G>& P, SmemB<G>& sm, uint32_t epoch) {
   const int pw = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const uint32_t ring_base = uint32_t(reinterpret_cast<uintptr_t>(sm.ring));
@@ -2157,7 +1792,7 @@ __device__ __forceinline__ void producer_b(const Params& p, const PlanB<G>& P, S
   wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
   uint32_t n = 0;
-  Spin spin(p.ws, 1);
+  Spin spin(p.ws, epoch, 1);
   bool dead = false;
   // Lowest stream position released by every consumer wave, in one 16-byte LDS read.  A stale value
   // is a lower bound (each wave's position only grows), so the last one read is kept in `avail`
@@ -2278,7 +1913,7 @@ template <class G>
 __device__ __forceinline__ void stage_flagged(ConsumerB<G>& C, int kind, int l, int K) {
   const uint32_t* flags = C.p.ws + WSB<G>::flag(kind, l, 0, C.P.wg % WSB<G>::FREP);
   {
-    Spin spin(C.p.ws, 8);
+    Spin spin(C.p.ws, C.tag32, 8);
     for (int w = C.ct; w < NWG; w += NCT)
       while (ld_dev(flags + w) != C.tag32)
         if (C.dead || !spin.again()) { C.dead = true; break; }
@@ -2425,11 +2060,11 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
   C.cbar();  // P1's reads of xs (which shares storage with sm.at) are done
   // ---- Q: every item's q (and new k / v) from the exchange words, one poll for all ----
   {
-    constexpr int GPI = 5 * 64 / 4;                      // groups of 4 words per item
+    constexpr int GPI = 5 * 64 / 2;                      // 16-byte loads (2 words) per item
     constexpr int MAXG = (IPW * GPI + NCT - 1) / NCT;
     const __amdgpu_buffer_rsrc_t r = rsrc(p.ws);
     auto word = [&](int gidx) -> int {                   // exchange word of group gidx, -1: none
-      const int k = gidx / GPI, e = (gidx - k * GPI) * 4;
+      const int k = gidx / GPI, e = (gidx - k * GPI) * 2;
       const ItemB& it = sm.it[k];
       if (e < 192) return int(WS<G>::xw(X_QKV, l, it.b, it.g * 192 + e));
       if (it.c != it.C - 1) return -1;                   // only the leader needs the new token
@@ -2448,14 +2083,13 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
         pend |= 1u << gi;
       }
     }
-    Spin spin(p.ws, 12);
+    Spin spin(p.ws, C.tag32, 12);
     while (true) {
 #pragma unroll
       for (int gi = 0; gi < MAXG; ++gi)
-        if (((pend >> gi) & 1u) && C.ok4(v[gi])) {
-          const int gidx = C.ct + gi * NCT, k = gidx / GPI, e = (gidx - k * GPI) * 4;
-          *reinterpret_cast<float4*>(&sm.at.qb[k][e]) =
-              make_float4(bf_lo(v[gi].x), bf_lo(v[gi].y), bf_lo(v[gi].z), bf_lo(v[gi].w));
+        if (((pend >> gi) & 1u) && C.ok2(v[gi])) {
+          const int gidx = C.ct + gi * NCT, k = gidx / GPI, e = (gidx - k * GPI) * 2;
+          *reinterpret_cast<float2*>(&sm.at.qb[k][e]) = make_float2(bf_lo(v[gi].x), bf_lo(v[gi].z));
           pend &= ~(1u << gi);
         }
       if (!pend) break;
@@ -2652,7 +2286,7 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
       return x[0].y == tagb && x[0].w == tagb && x[1].y == tagb && x[1].w == tagb && x[2].y == tagb &&
              x[2].w == tagb;
     };
-    Spin spin(p.ws, 9);
+    Spin spin(p.ws, C.tag32, 9);
     while (true) {
 #pragma unroll
       for (int i = 0; i < MAXI; ++i)
@@ -2789,7 +2423,7 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
           ro[kk] = ld_dev64(reinterpret_cast<const uint64_t*>(p.ws + WSB<G>::rec(base + c0 + kk)) + w * 64 + lane);
           pend |= 1u << kk;
         }
-      Spin spin(p.ws, 10);
+      Spin spin(p.ws, C.tag32, 10);
       while (true) {
 #pragma unroll
         for (int kk = 0; kk < MB; ++kk)
@@ -2870,7 +2504,7 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           if (orow + j < nq) {
-            st_dev(p.ws + W::xw(X_QKV, l, tok, P.q0 + orow + j), C.w16(acc[j]));
+            st_dev64(reinterpret_cast<uint64_t*>(p.ws + W::xw(X_QKV, l, tok, P.q0 + orow + j)), C.w64(acc[j]));
             if (DBG && p.debug) dl(l)[Dbg<G>::QKV + size_t(tok) * G::QKV + P.q0 + orow + j] = uint16_t(f2bf(acc[j]));
           }
       tr(l, 3);
@@ -2978,8 +2612,8 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
   C.release(C.pos);
   if (P.wg == 0)
     for (int i = C.ct; i < B * G::H; i += NCT) p.out_hidden[i] = sm.xs[i];
-  if (!p.lm_head) return;
-  // LM segment j (16 rows, one MFMA tile over the full K) is computed by wave j % NCW
+  // LM segment j (16 rows, one MFMA tile over the full K) is computed by wave j % NCW (none
+  // without the LM head)
   float best = -INFINITY;
   int bidx = 0x7fffffff;
   for (int j = 0; j < P.n_lm; ++j) {
@@ -3021,22 +2655,30 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
         bv = sm.lm_val[v][C.ct];
         bi = sm.lm_idx[v][C.ct];
       }
-    const uint64_t rec = (uint64_t(C.tag32) << 32) | (uint64_t(uint32_t(bi) & 0xffffu) << 16) | f2bf(bv);
+    const uint32_t idx = C.dead ? LM_DEAD : p.lm_head ? uint32_t(bi) & 0xffffu : LM_NONE;
+    const uint64_t rec = (uint64_t(C.tag32) << 32) | (uint64_t(idx) << 16) | f2bf(bv);
     st_dev64(reinterpret_cast<uint64_t*>(p.ws + W::lm(C.ct, P.wg)), rec);
   }
-  if (P.wg != 0) return;
+  if (P.wg != 0) {
+    if (p.out_logits && (C.dead || aborted(p.ws, C.tag32)))  // this workgroup's logits rows are not valid
+      for (int b = 0; b < B; ++b)
+        for (int i = P.v0 + C.ct; i < P.v1; i += NCT) p.out_logits[size_t(b) * G::V + i] = 0x7fc0;
+    return;
+  }
   C.cbar();  // lm_val is reused below
+  uint32_t bad = 0;
   // workgroup 0: per sequence, argmax over the NWG candidates (first index on ties, as torch.argmax)
   for (int b = 0; b < B; ++b) {
     const uint64_t* src = reinterpret_cast<const uint64_t*>(p.ws + W::lm(b, C.ct));
-    Spin spin(p.ws, 11);
+    Spin spin(p.ws, C.tag32, 11);
     uint64_t r = ld_dev64(src);
     while (uint32_t(r >> 32) != C.tag32) {
-      if (C.dead || !spin.again()) { C.dead = true; break; }
+      if (!spin.again()) { bad = 1; break; }
       r = ld_dev64(src);
     }
     float bv = bf2f(uint32_t(r) & 0xffffu);
     int bi = int((uint32_t(r) >> 16) & 0xffffu);
+    bad |= (bi == int(LM_DEAD)) ? 1u : 0u;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       const float ov = __shfl_xor(bv, o);
@@ -3045,7 +2687,11 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
     }
     if (C.lane == 0) { sm.lm_val[C.cw][b] = bv; sm.lm_idx[C.cw][b] = bi; }
   }
+  const bool any_bad = __builtin_amdgcn_ballot_w64(bad != 0u) != 0ull;
+  if (C.lane == 0) sm.red[C.cw] = any_bad ? 1.f : 0.f;
   C.cbar();
+  bool fail = C.dead || aborted(p.ws, C.tag32);
+  for (int w = 0; w < NCW; ++w) fail = fail || sm.red[w] != 0.f;
   if (C.ct < B) {
     float bv = sm.lm_val[0][C.ct];
     int bi = sm.lm_idx[0][C.ct];
@@ -3054,8 +2700,14 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
         bv = sm.lm_val[v][C.ct];
         bi = sm.lm_idx[v][C.ct];
       }
-    if (p.out_ids) p.out_ids[C.ct] = bi;
+    if (p.out_ids) p.out_ids[C.ct] = fail ? -1 : bi;
   }
+  if (fail)
+    for (int b = 0; b < B; ++b) {
+      step_failed(p, C.tag32, C.ct, b);
+      if (p.out_logits)  // workgroup 0's own logits rows
+        for (int i = P.v0 + C.ct; i < P.v1; i += NCT) p.out_logits[size_t(b) * G::V + i] = 0x7fc0;
+    }
 }
 
 template <class G, bool DBG = false>
@@ -3087,9 +2739,8 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel_b(Params p) {
   __syncthreads();
   PlanB<G> P;
   P.init(p, sm.sS, blockIdx.x);
-  uint32_t epoch = ld_dev(p.ws + HDR_EPOCH) + 1u;
-  if (epoch == 0) epoch = 1;
-  if (threadIdx.x < 64 * NPW) producer_b<G>(p, P, sm);
+  const uint32_t epoch = step_epoch(p.ws);
+  if (threadIdx.x < 64 * NPW) producer_b<G>(p, P, sm, epoch);
   else consumer_b<G, DBG>(p, P, sm, epoch);
   __syncthreads();
   if (blockIdx.x == 0 && threadIdx.x == 0) st_dev(p.ws + HDR_EPOCH, epoch);
@@ -3199,90 +2850,109 @@ struct LaunchCache {
   int status[MAX_DEV] = {};
 };
 
+// Library options (pk_set_option), initialised from the environment: PK_LAUNCH=cooperative makes
+// every decode launch cooperative (hipLaunchCooperativeKernel, which costs ~17 us more per launch
+// on this part than an ordinary launch of the same grid; the grid is one workgroup per CU either
+// way), PK_SPLIT_ROLE=0 keeps batch-1 steps on the general kernel.
+struct Options {
+  int cooperative = -1;
+  int split_role = -1;
+};
+static Options g_opt;
+static int opt_cooperative() {
+  if (g_opt.cooperative < 0) {
+    const char* e = getenv("PK_LAUNCH");
+    g_opt.cooperative = (e && __builtin_strcmp(e, "cooperative") == 0) ? 1 : 0;
+  }
+  return g_opt.cooperative;
+}
+static int opt_split_role() {
+  if (g_opt.split_role < 0) {
+    const char* e = getenv("PK_SPLIT_ROLE");
+    g_opt.split_role = (e && e[0] == '0') ? 0 : 1;
+  }
+  return g_opt.split_role;
+}
+
 // ------------------------------------------------------------------------------------------------
-// Workspace registry.  A step tells its exchange words apart from older contents only by their
-// tags, so a workspace must start zeroed.  Buffers from pk_workspace_alloc are zeroed there; a
-// buffer a caller passes in (the reference ABI takes plain scratch memory) is zero-filled on the
-// launch stream the first time it is seen on a device, by a fill kernel (graph-safe, no memset
-// node).  A first sight under stream capture is refused: the fill would be replayed with every
-// step and reset the epoch.  The library cannot see a caller reuse the memory for other data
-// between calls, so a workspace stays dedicated to it until pk_workspace_forget / _free.
+// Library-owned exchange state.  Every exchange word carries the step epoch, so the memory the
+// kernels exchange through must hold nothing the library did not write.  The library allocates it
+// per device on first use (pk_init, or the first decode call) -- uncached device memory for the
+// exchange words (header: epoch, abort word, wait site), ordinary device memory for the batch-1
+// records that stay in one XCD's L2, and a pinned host word pair the kernels set when a step gave up
+// a bounded wait -- zeroes it once and keeps it until the process ends (uncached memory that a kernel
+// has read is never returned to the allocator).  A caller's scratch buffer (the reference ABI's
+// `scratch`) is checked for presence and size only and carries nothing between calls.  As with the
+// reference's per-device scratch, steps on one device must not run concurrently from two streams.
 // ------------------------------------------------------------------------------------------------
-struct WsEntry {
+struct DevState {
   int dev;
-  const void* ptr;
-  size_t bytes;
+  uint32_t* ws;     // uncached: general layout, then the split-role region
+  uint32_t* rec;    // ordinary: general batch-1 records, then the split-role group-A records
+  uint32_t* host;   // pinned host memory: [0] epoch of the last step that gave up a wait, [1] its wait site
+  uint32_t* host_dev;
 };
-static std::mutex g_ws_mu;
-static std::vector<WsEntry> g_ws;
-// Companion buffers (ordinary device memory) for the batch-1 attention records, made by
-// pk_workspace_alloc together with its workspace and dropped with it.
-struct RecEntry {
-  const void* ws;
-  void* rec;
-};
-static std::vector<RecEntry> g_rec;
-static constexpr size_t rec_bytes() {
-  return (WS<G360>::XREC_WORDS > WS<G135>::XREC_WORDS ? WS<G360>::XREC_WORDS : WS<G135>::XREC_WORDS) * 4;
+constexpr int MAX_STATES = 64;
+static std::mutex g_state_mu;
+static DevState g_states[MAX_STATES];
+static int g_nstates = 0;
+
+static constexpr size_t round_up(size_t n, size_t a) { return (n + a - 1) / a * a; }
+static constexpr size_t ws_general_bytes() {
+  return round_up((WSB<G360>::TOTAL > WSB<G135>::TOTAL ? WSB<G360>::TOTAL : WSB<G135>::TOTAL) * 4, 4096);
 }
-static uint32_t* rec_lookup(const void* ws) {
-  std::lock_guard<std::mutex> lk(g_ws_mu);
-  for (const RecEntry& r : g_rec)
-    if (r.ws == ws) return reinterpret_cast<uint32_t*>(r.rec);
-  return nullptr;
+static constexpr size_t rec_general_bytes() {
+  return round_up((WS<G360>::XREC_WORDS > WS<G135>::XREC_WORDS ? WS<G360>::XREC_WORDS : WS<G135>::XREC_WORDS) * 4, 4096);
 }
+static size_t ws_bytes() { return ws_general_bytes() + round_up(sr_region_bytes(), 4096); }
+static size_t rec_bytes() { return rec_general_bytes() + round_up(sr_local_bytes(), 4096); }
 
 __global__ void __launch_bounds__(256) zero_fill(uint4* p, size_t n) {
   for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
     p[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
-static void ws_register(int dev, const void* ptr, size_t bytes) {
-  std::lock_guard<std::mutex> lk(g_ws_mu);
-  for (WsEntry& w : g_ws)
-    if (w.dev == dev && w.ptr == ptr) {
-      w.bytes = bytes > w.bytes ? bytes : w.bytes;
-      return;
-    }
-  g_ws.push_back(WsEntry{dev, ptr, bytes});
-}
-
-static void ws_forget(const void* ptr) {
-  std::lock_guard<std::mutex> lk(g_ws_mu);
-  for (size_t i = 0; i < g_ws.size();)
-    if (g_ws[i].ptr == ptr) g_ws.erase(g_ws.begin() + long(i));
-    else ++i;
-  // the companion goes too: its records carry epochs of the workspace it was made with, which a
-  // re-zeroed workspace would count again
-  for (size_t i = 0; i < g_rec.size();)
-    if (g_rec[i].ws == ptr) {
-      (void)hipFree(g_rec[i].rec);
-      g_rec.erase(g_rec.begin() + long(i));
-    } else {
-      ++i;
-    }
-}
-
-static int ensure_workspace(void* ws, size_t bytes, hipStream_t stream) {
+static int get_state(const void* stream, DevState** out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
-  {
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    for (const WsEntry& w : g_ws)
-      if (w.dev == dev && w.ptr == ws && w.bytes >= bytes) return PK_OK;
+  std::lock_guard<std::mutex> lk(g_state_mu);
+  for (int i = 0; i < g_nstates; ++i)
+    if (g_states[i].dev == dev) {
+      *out = &g_states[i];
+      return PK_OK;
+    }
+  if (g_nstates == MAX_STATES) return PK_ERR_STATE;
+  // the allocation and zero fill cannot be captured: a first use under capture is refused
+  if (stream) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(reinterpret_cast<hipStream_t>(const_cast<void*>(stream)), &cs);
+    if (e != hipSuccess) return e;
+    if (cs != hipStreamCaptureStatusNone) return PK_ERR_CAPTURE;
   }
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  e = hipStreamIsCapturing(stream, &cs);
-  if (e != hipSuccess) return e;
-  if (cs != hipStreamCaptureStatusNone) return PK_ERR_CAPTURE;
-  const size_t n16 = bytes / 16;
-  const size_t blocks = (n16 + 255) / 256 < 2048 ? (n16 + 255) / 256 : 2048;
-  hipLaunchKernelGGL(zero_fill, dim3(unsigned(blocks)), dim3(256), 0, stream, reinterpret_cast<uint4*>(ws), n16);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  ws_register(dev, ws, bytes);
+  DevState st{};
+  st.dev = dev;
+  if (hipExtMallocWithFlags(reinterpret_cast<void**>(&st.ws), ws_bytes(), hipDeviceMallocUncached) != hipSuccess)
+    return PK_ERR_STATE;
+  if (hipMalloc(reinterpret_cast<void**>(&st.rec), rec_bytes()) != hipSuccess) return PK_ERR_STATE;
+  if (hipHostMalloc(reinterpret_cast<void**>(&st.host), 64, hipHostMallocMapped) != hipSuccess) return PK_ERR_STATE;
+  if (hipHostGetDevicePointer(reinterpret_cast<void**>(&st.host_dev), st.host, 0) != hipSuccess) return PK_ERR_STATE;
+  for (int i = 0; i < 16; ++i) st.host[i] = 0u;
+  hipLaunchKernelGGL(zero_fill, dim3(2048), dim3(256), 0, nullptr, reinterpret_cast<uint4*>(st.ws), ws_bytes() / 16);
+  hipLaunchKernelGGL(zero_fill, dim3(2048), dim3(256), 0, nullptr, reinterpret_cast<uint4*>(st.rec), rec_bytes() / 16);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+  g_states[g_nstates] = st;
+  *out = &g_states[g_nstates++];
   return PK_OK;
+}
+
+// A step on this state gave up a bounded wait since the last call: report it once.
+static int take_abort(DevState* st) {
+  const uint32_t ep = __atomic_load_n(&st->host[0], __ATOMIC_ACQUIRE);
+  if (ep == 0u) return PK_OK;
+  __atomic_store_n(&st->host[0], 0u, __ATOMIC_RELEASE);
+  return PK_ERR_ABORTED;
 }
 
 template <class G, bool BATCHED, bool DBG = false>
@@ -3318,14 +2988,15 @@ static int launch(const Params& p, hipStream_t stream) {
   }
   if (cache.status[dev]) return cache.status[dev];
   Params q = p;
-  q.xws = BATCHED ? nullptr : rec_lookup(p.ws);
+  if (BATCHED) q.xws = nullptr;
   if (q.trace) {
     if (q.n_layers > TR_LAYERS) return PK_ERR_MODEL;
     q.trace_lds = uint32_t(trace_offset(lds));
     lds = lds_traced;
   }
   void* args[] = {&q};
-  e = hipLaunchCooperativeKernel(fn, dim3(NWG), dim3(WG_THREADS), args, lds, stream);
+  if (opt_cooperative()) e = hipLaunchCooperativeKernel(fn, dim3(NWG), dim3(WG_THREADS), args, lds, stream);
+  else e = hipLaunchKernel(fn, dim3(NWG), dim3(WG_THREADS), args, lds, stream);
   if (e != hipSuccess) return e;
   return hipGetLastError();
 }
@@ -3356,7 +3027,7 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
   if (!input_ids || !embed || !final_norm || !positions || !seq_lens || !block_table ||
       !slot_mapping || !layers || !kv || !cos_sin || !out_hidden || !scratch)
     return PK_ERR_NULL;
-  if (scratch_bytes < WSB<G>::TOTAL * 4) return PK_ERR_SCRATCH;
+  if (scratch_bytes < SCRATCH_BYTES) return PK_ERR_SCRATCH;
   if (block_size != 16 || bt_stride < 1 || (long long)bt_stride * block_size < max_seq_len) return PK_ERR_BLOCK;
   if (k_off % 8 || v_off % 8 || block_stride % 8 || token_stride % 8 || head_stride % 8 || k_off < 0 ||
       v_off < 0 || block_stride < 0 || token_stride < 0 || head_stride < 0)
@@ -3381,6 +3052,7 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
   p.cos_sin = cos_sin;
   p.cs_fp32 = cs_fp32 ? 1 : 0;
   p.out_hidden = reinterpret_cast<uint16_t*>(out_hidden);
+  p.h_dim = G::H;
   p.layer_outputs = reinterpret_cast<uint16_t*>(layer_outputs);
   p.out_logits = reinterpret_cast<uint16_t*>(out_logits);
   p.out_ids = reinterpret_cast<int64_t*>(out_ids);
@@ -3399,15 +3071,34 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
   p.debug = reinterpret_cast<uint16_t*>(debug);
   p.debug_layer = debug_layer;
   p.input_hidden = reinterpret_cast<const uint16_t*>(input_hidden);
-  static_assert((WSB<G>::TOTAL * 4) % 16 == 0, "workspace is zero-filled in 16-byte units");
-  const int st = ensure_workspace(scratch, WSB<G>::TOTAL * 4, reinterpret_cast<hipStream_t>(stream));
-  if (st != PK_OK) return st;
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  DevState* state = nullptr;
+  const int st = get_state(stream, &state);
+  if (st != PK_OK) return st;
+  const int ab = take_abort(state);
+  if (ab != PK_OK) return ab;
+  p.ws = state->ws;
+  p.xws = state->rec;
+  p.host_status = state->host_dev;
   if constexpr (G::WF == 0 && G::H == 960 && G::L == 32) {  // kernels with the capture compiled in
     if (debug) return B > 1 ? launch<G, true, true>(p, s) : launch<G, false, true>(p, s);
   }
   if constexpr (G::WF == 0)
     if (B > 1) return launch<G, true>(p, s);
+  // Batch 1: the split-role kernel takes contexts up to its limit, the general kernel the rest.
+  // Both are launched; each reads the context length on the device and exactly one does the step,
+  // so the host never has to read it (no synchronisation, and the pair can be captured in a graph).
+  if constexpr (G::WF == 0) {
+    const int model = G::H == 960 ? PK_MODEL_SMOLLM2_360M : PK_MODEL_SMOLLM2_135M;
+    if (opt_split_role() && !encoded_gu && !input_hidden) {
+      p.sr_max_s = sr_max_seq(model);
+      const int e = sr_launch(model, p, reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(state->ws) + ws_general_bytes()),
+                              reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(state->rec) + rec_general_bytes()), s,
+                              opt_cooperative());
+      if (e != PK_OK) return e;
+      if (max_seq_len <= p.sr_max_s) return PK_OK;  // no context can reach the general kernel
+    }
+  }
   return launch<G, false>(p, s);
 }
 
@@ -3421,65 +3112,81 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
 // Layout: [256 workgroups][n_layers * 16 + 4] uint64.
 extern "C" void pk_set_trace(void* buf) { pk::g_trace = reinterpret_cast<unsigned long long*>(buf); }
 
-// Workspace in fine-grained device memory (lower cross-XCD round trip for the exchange words).
-// Zero-initialised.  kind 0: ordinary (coarse-grained) device memory, 1: fine-grained.
-// Uncached allocations are never returned to the allocator: memory of this kind that a kernel has
-// read must stay allocated until the process ends (later allocations placed in freed uncached
-// memory have been seen to hold wrong values), so pk_workspace_free only forgets them.
-static std::mutex g_uncached_mu;
-static std::vector<void*> g_uncached;
-
-extern "C" void* pk_workspace_alloc(size_t bytes, int kind) {
-  void* ptr = nullptr;
-  hipError_t e;
-  if (kind == 1) e = hipExtMallocWithFlags(&ptr, bytes, hipDeviceMallocFinegrained);
-  else if (kind == 2) e = hipExtMallocWithFlags(&ptr, bytes, hipDeviceMallocUncached);
-  else e = hipMalloc(&ptr, bytes);
-  if (e != hipSuccess) return nullptr;
-  if (hipMemset(ptr, 0, bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
-    if (kind != 2) (void)hipFree(ptr);
-    return nullptr;
-  }
-  if (kind == 2) {
-    std::lock_guard<std::mutex> lk(g_uncached_mu);
-    g_uncached.push_back(ptr);
-  }
-  int dev = 0;
-  if (hipGetDevice(&dev) == hipSuccess) pk::ws_register(dev, ptr, bytes);
-  // companion for the batch-1 attention records (optional: without it they stay in the workspace)
-  void* rec = nullptr;
-  if (hipMalloc(&rec, pk::rec_bytes()) == hipSuccess) {
-    if (hipMemset(rec, 0, pk::rec_bytes()) == hipSuccess && hipDeviceSynchronize() == hipSuccess) {
-      std::lock_guard<std::mutex> lk(pk::g_ws_mu);
-      pk::g_rec.push_back(pk::RecEntry{ptr, rec});
-    } else {
-      (void)hipFree(rec);
-    }
-  }
-  return ptr;
+// Allocate and zero the current device's state now (outside any stream capture); later calls on
+// the device use it.  Returns 0 or a status code.
+extern "C" int pk_init(void) {
+  pk::DevState* st = nullptr;
+  return pk::get_state(nullptr, &st);
 }
-extern "C" int pk_workspace_forget(const void* ptr) {
-  pk::ws_forget(ptr);
+
+// Options (initially from PK_LAUNCH / PK_SPLIT_ROLE): PK_OPT_COOPERATIVE 1 launches the decode
+// kernels with hipLaunchCooperativeKernel, PK_OPT_SPLIT_ROLE 0 keeps batch-1 steps on the general
+// kernel.  Returns the previous value, or -1 for an unknown option.
+extern "C" int pk_set_option(int option, int value) {
+  if (option == PK_OPT_COOPERATIVE) {
+    const int old = pk::opt_cooperative();
+    pk::g_opt.cooperative = value ? 1 : 0;
+    return old;
+  }
+  if (option == PK_OPT_SPLIT_ROLE) {
+    const int old = pk::opt_split_role();
+    pk::g_opt.split_role = value ? 1 : 0;
+    return old;
+  }
+  return -1;
+}
+
+// Synchronous copy (after synchronising `stream`) of n header words of the current device's state
+// (0 epoch, 1 the epoch of the last step that gave up a wait, 2 its wait site).
+extern "C" int pk_state_read(void* stream, size_t word, unsigned* out, int n) {
+  pk::DevState* st = nullptr;
+  const int rc = pk::get_state(stream, &st);
+  if (rc != PK_OK) return rc;
+  if (n < 0 || word + size_t(n) > 64) return PK_ERR_BLOCK;
+  hipError_t e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return e;
+  return hipMemcpy(out, st->ws + word, size_t(n) * 4, hipMemcpyDeviceToHost);
+}
+
+// The pending failure report of the current device without clearing it: out[0] the epoch of the
+// last step that gave up a wait (0: none since the last report), out[1] its wait site.
+extern "C" int pk_state_status(void* stream, unsigned* out) {
+  pk::DevState* st = nullptr;
+  const int rc = pk::get_state(stream, &st);
+  if (rc != PK_OK) return rc;
+  out[0] = __atomic_load_n(&st->host[0], __ATOMIC_ACQUIRE);
+  out[1] = __atomic_load_n(&st->host[1], __ATOMIC_ACQUIRE);
   return PK_OK;
 }
-extern "C" int pk_workspace_free(void* ptr) {
-  pk::ws_forget(ptr);
-  {
-    std::lock_guard<std::mutex> lk(g_uncached_mu);
-    for (void* q : g_uncached)
-      if (q == ptr) return PK_OK;  // retained until the process ends
-  }
-  return hipFree(ptr);
+
+// Test hooks (synchronous).  pk_test_set_epoch sets the step epoch of the current device's state
+// (for tests that cross the 32-bit wrap); pk_test_abort_next marks the next step as already failed,
+// so every bounded wait of that step gives up at its first check and the kernels end normally
+// with poisoned outputs.
+extern "C" int pk_test_set_epoch(void* stream, unsigned epoch) {
+  pk::DevState* st = nullptr;
+  const int rc = pk::get_state(stream, &st);
+  if (rc != PK_OK) return rc;
+  hipError_t e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return e;
+  return hipMemcpy(st->ws + pk::HDR_EPOCH, &epoch, 4, hipMemcpyHostToDevice);
 }
-// Copy n 32-bit words of a workspace (header words: 0 epoch, 1 abort flag, 2 abort site) to host.
-extern "C" int pk_workspace_read(const void* ws, size_t word, unsigned* out, int n) {
-  const hipError_t e = hipMemcpy(out, reinterpret_cast<const unsigned*>(ws) + word, size_t(n) * 4, hipMemcpyDeviceToHost);
-  return e;
+extern "C" int pk_test_abort_next(void* stream) {
+  pk::DevState* st = nullptr;
+  const int rc = pk::get_state(stream, &st);
+  if (rc != PK_OK) return rc;
+  hipError_t e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return e;
+  unsigned ep = 0;
+  if ((e = hipMemcpy(&ep, st->ws + pk::HDR_EPOCH, 4, hipMemcpyDeviceToHost)) != hipSuccess) return e;
+  ep = ep + 1u == 0u ? 1u : ep + 1u;
+  return hipMemcpy(st->ws + pk::HDR_ABORT, &ep, 4, hipMemcpyHostToDevice);
 }
 
+// The scratch the decode entry points require.  It carries nothing between calls (all exchange
+// state is the library's own), so only its presence and this size are checked.
 extern "C" size_t pk_workspace_bytes(int model) {
-  if (model == PK_MODEL_SMOLLM2_360M) return pk::WSB<pk::G360>::TOTAL * 4;
-  if (model == PK_MODEL_SMOLLM2_135M) return pk::WSB<pk::G135>::TOTAL * 4;
+  if (model == PK_MODEL_SMOLLM2_360M || model == PK_MODEL_SMOLLM2_135M) return pk::SCRATCH_BYTES;
   return 0;
 }
 
@@ -3601,7 +3308,9 @@ extern "C" const char* prime_decode_status_string(int status) {
     case PK_ERR_BLOCK: return "block_size_or_stride_invalid";
     case PK_ERR_MODEL: return "unknown_model_or_layer_count";
     case PK_ERR_DEBUG: return "debug_capture_unavailable";
-    case PK_ERR_CAPTURE: return "workspace_first_use_under_stream_capture";
+    case PK_ERR_CAPTURE: return "first_use_of_the_device_under_stream_capture";
+    case PK_ERR_ABORTED: return "a_previous_step_on_this_device_gave_up_a_bounded_wait";
+    case PK_ERR_STATE: return "library_state_allocation_failed";
     default: return hipGetErrorString(static_cast<hipError_t>(status));
   }
 }
@@ -3654,7 +3363,7 @@ constexpr size_t BLK_NORM1 = 0, BLK_QKV = BLK_NORM1 + BLK_MAXB * 960, BLK_ATTN =
                  BLK_H1 = BLK_ATTN + BLK_MAXB * 960, BLK_NORM2 = BLK_H1 + BLK_MAXB * 960,
                  BLK_ACT = BLK_NORM2 + BLK_MAXB * 960, BLK_OUT = BLK_ACT + BLK_MAXB * 2560,
                  BLK_DEBUG = BLK_OUT + BLK_MAXB * 960;
-constexpr size_t BLK_WS = (WSB<G360>::TOTAL * 4 + 255) / 256 * 256;    // decode workspace
+constexpr size_t BLK_WS = (SCRATCH_BYTES + 255) / 256 * 256;              // the decode entry's scratch
 constexpr size_t BLK_KVT = BLK_WS;                                      // cache table (one pointer)
 constexpr size_t BLK_HID = BLK_KVT + 256;                               // discarded final hidden [2][960]
 constexpr size_t BLK_CAP = BLK_HID + 4096;                              // capture area (Dbg layout)
@@ -3697,9 +3406,6 @@ extern "C" int block360_decode(void* stream, int B, const void* hidden, const vo
     return PK_ERR_ALIGN;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   uint8_t* ws = static_cast<uint8_t*>(scratch);
-  // first sight of the workspace (zero fill, or the capture refusal) before anything is launched
-  const int first = pk::ensure_workspace(scratch, pk::WSB<pk::G360>::TOTAL * 4, s);
-  if (first != PK_OK) return first;
   void** kvt = reinterpret_cast<void**>(ws + pk::BLK_KVT);
   pk::blk_table<<<1, 64, 0, s>>>(kvt, kv);
   hipError_t e = hipGetLastError();

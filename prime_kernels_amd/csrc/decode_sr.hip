@@ -1,0 +1,1355 @@
+// SmolLM2 batch-1 decode step, split-role persistent kernel for gfx950 (MI355X).
+//
+// The 256 workgroups (one per CU, dispatched to the 8 XCDs round-robin) take one of two roles:
+//   group A, the 32 workgroups wg % 8 == 0 (one XCD): attention over the KV cache (C chunks per
+//           KV head), the merge of the chunk partials and the O projection + residual -> h1;
+//   group F, the other 224 workgroups (seven XCDs): RMSNorm + gate/up + SwiGLU, down + residual
+//           -> x, RMSNorm + the QKV projection.
+// Per layer the data cross XCDs four times (h1 A->F, act F->F, x F->F, q/k/v F->A); the three
+// exchanges inside attention (softmax statistics, P.V partials, the merged attention vector) stay
+// inside group A's XCD and go through its L2.  The two groups alternate: while one works, the other
+// streams its next layer's weights (or KV chunk) into its LDS ring, so no workgroup has DMA in
+// flight when it polls for data (an exchange poll issued behind outstanding DMA on the same CU
+// waits for that DMA; measured, a hop costs 0.3-1.2 us more with the CU's own DMA in flight).
+//
+// Exchange format: 16-byte units {three 32-bit payload words, 32-bit step tag}, written with one
+// 16-byte store and read with one 16-byte load (a payload of 6 bf16 or 3 fp32).  A reader polls a
+// unit until its tag equals the step epoch.  Cross-XCD units live in uncached device memory
+// (device-scope stores and loads); group A's records live in ordinary device memory written with
+// plain stores into the XCD's L2 and read with device-scope loads.  At the start of a launch the
+// group-A workgroups check that they really share one XCC (hardware register XCC_ID); if not, the
+// records go through the uncached workspace instead.
+//
+// Rounding points are those of HF eager Llama (modeling_llama.py), as in the general kernel:
+// RMSNorm bf16(w * bf16(x * rsqrt(mean(x^2) + eps))), every projection bf16(W.x) with fp32
+// accumulation, RoPE bf16(bf16(x cos) +- bf16(rot(x) sin)), scores bf16(q.k) / 8, softmax in fp32
+// with p rounded to bf16 using the global max and sum of the head, bf16(sum p.v), residuals
+// bf16(x + bf16(o)), silu bf16(g / (1 + exp(-g))), act bf16(silu * u).
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "pk_common.h"
+
+namespace pk {
+namespace sr {
+
+constexpr int AG = 32;                   // group A workgroups (wg % 8 == 0)
+constexpr int FG = NWG - AG;             // group F workgroups
+constexpr int VPU = 6;                   // bf16 values per 16-byte unit
+constexpr int REP = 1;                   // copies of each cross-XCD unit
+constexpr int TCS = 256;                 // max cached tokens per attention chunk
+constexpr int DEPTH_SR = 8;              // DMA packets in flight per producer wave
+constexpr int LM_ROWS_SR = 16;           // LM-head rows per ring segment
+
+__device__ __forceinline__ bool in_a(int wg) { return (wg & 7) == 0; }
+
+template <class G>
+struct SG {
+  static constexpr int HU = (G::H + VPU - 1) / VPU;     // units of an H-vector
+  static constexpr int IU = (G::I + VPU - 1) / VPU;     // units of the act vector
+  static constexpr int QU = (G::QKV + VPU - 1) / VPU;   // units of the qkv vector
+  static constexpr int C = AG / G::KVH;                 // attention chunks per KV head
+  static constexpr int NATT = C * G::KVH;
+  static constexpr int PU = 22;                         // units of one head's 64 fp32 partial sums
+  static constexpr int OU = (HU + AG - 1) / AG;         // most O units per group-A workgroup
+  static_assert(G::GQA == 3 && (3 * 64) % VPU == 0 && G::H % VPU == 0, "head groups are whole units");
+  static_assert(C >= 1 && C <= 16, "chunks per KV head");
+};
+
+// Workspace (uncached, 32-bit words), placed after the general kernels' layout (base word SR0) so
+// that no word is ever read in a format it was not written in; the header (epoch, abort) is shared.
+enum SKind { K_H1, K_ACT, K_X, K_XQ, NK };
+template <class G>
+struct SWS {
+  using S = SG<G>;
+  static constexpr int LINES = (S::IU + 3) / 4;
+  static constexpr int SLOTS = (G::L + 1) * NK;
+  static constexpr size_t XCC_TAB = 0;                        // 32 units: the group-A XCC ids
+  static constexpr size_t X0 = XCC_TAB + size_t(AG) * 16;     // cross-XCD vectors (bytes from the region base)
+  static constexpr size_t XBYTES = size_t(REP) * LINES * SLOTS * 64;
+  static constexpr size_t LMR = X0 + XBYTES;                  // per-workgroup end records: NWG units
+  static constexpr size_t LOC = LMR + size_t(NWG) * 16;      // group-A records when they cannot stay in L2
+  // group-A records per layer, in units: statistics (2 per chunk), partials (3 heads x PU per chunk),
+  // the merged attention vector (HU)
+  static constexpr size_t STAT_U = 0, PART_U = size_t(AG) * 2, ATTN_U = PART_U + size_t(AG) * 3 * S::PU;
+  static constexpr size_t LOC_LAYER = (ATTN_U + S::HU) * 16;
+  static constexpr size_t LOC_BYTES = LOC_LAYER * G::L;
+  static constexpr size_t BYTES = LOC + LOC_BYTES;
+  // unit u of vector (kind, layer l, copy r): consecutive lines of a vector are SLOTS lines apart,
+  // so one vector's lines spread over the memory channels
+  __device__ static uint32_t xoff(int kind, int l, int r, int u) {
+    return uint32_t(X0 + ((size_t(r) * LINES + size_t(u >> 2)) * SLOTS + size_t(l) * NK + kind) * 64 + size_t(u & 3) * 16);
+  }
+  __device__ static uint32_t loc(int l, size_t unit) { return uint32_t(size_t(l) * LOC_LAYER + unit * 16); }
+};
+
+typedef __attribute__((address_space(1))) u32x4 g_u32x4_t;
+
+template <int AUX>
+__device__ __forceinline__ void st_unit(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, int(off), 0, AUX);
+}
+__device__ __forceinline__ u32x4 ld_unit(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, int(off), 0, 16);  // device scope (sc1)
+}
+
+// ------------------------------------------------------------------------------------------------
+// Per-workgroup plan
+// ------------------------------------------------------------------------------------------------
+
+template <class G>
+struct PlanSR {
+  using GG = SG<G>;
+  int wg, a, rank;
+  // group F: act units [au0, au1), x units [xu0, xu1), qkv units [qu0, qu1) and their row ranges
+  int au0, au1, xu0, xu1, qu0, qu1;
+  int a0, a1, d0, d1, q0, q1;
+  // group A: attention chunk (KV head g, chunk c of C), cached tokens [t0, t1); O units [ou0, ou1)
+  int att, g, c, leader, t0, t1, S, pos;
+  long long slot;
+  int ou0, ou1, o0, o1;
+  // LM head rows [v0, v1) in n_lm segments, the first lm_pre of them streamed with the last bracket
+  int v0, v1, n_lm, lm_pre;
+
+  __device__ __forceinline__ void init(const Params& p, int wg_) {
+    wg = wg_;
+    a = in_a(wg);
+    rank = a ? wg >> 3 : (wg >> 3) * 7 + (wg & 7) - 1;
+    au0 = au1 = xu0 = xu1 = qu0 = qu1 = a0 = a1 = d0 = d1 = q0 = q1 = 0;
+    att = g = c = leader = t0 = t1 = ou0 = ou1 = o0 = o1 = 0;
+    S = min(max(p.seq_lens[0], 1), p.max_seq);
+    pos = int(max(p.positions[0], (int64_t)0));
+    slot = p.slot_mapping[0];
+    if (a) {
+      att = rank < GG::NATT;
+      g = rank % G::KVH;
+      c = rank / G::KVH;
+      leader = att && c == GG::C - 1;
+      const int old = S - 1;
+      const int tc = old <= 0 ? 16 : ((old + GG::C - 1) / GG::C + 15) / 16 * 16;
+      t0 = att ? min(c * tc, old) : 0;
+      t1 = att ? min((c + 1) * tc, old) : 0;
+      ou0 = split_lo(GG::HU, AG, rank);
+      ou1 = split_lo(GG::HU, AG, rank + 1);
+      o0 = ou0 * VPU;
+      o1 = min(ou1 * VPU, G::H);
+    } else {
+      au0 = split_lo(GG::IU, FG, rank); au1 = split_lo(GG::IU, FG, rank + 1);
+      xu0 = split_lo(GG::HU, FG, rank); xu1 = split_lo(GG::HU, FG, rank + 1);
+      qu0 = split_lo(GG::QU, FG, rank); qu1 = split_lo(GG::QU, FG, rank + 1);
+      a0 = au0 * VPU; a1 = min(au1 * VPU, G::I);
+      d0 = xu0 * VPU; d1 = min(xu1 * VPU, G::H);
+      q0 = qu0 * VPU; q1 = min(qu1 * VPU, G::QKV);
+    }
+    if (p.lm_head) {
+      v0 = split_lo(G::V, NWG, wg);
+      v1 = split_lo(G::V, NWG, wg + 1);
+    } else {
+      v0 = v1 = 0;
+    }
+    n_lm = (v1 - v0 + LM_ROWS_SR - 1) / LM_ROWS_SR;
+    // the last bracket: what it streams before the LM-head segments (F: the last layer's MLP)
+    const uint32_t last = a ? pad_pkt(G::H * 2)
+                            : 2 * pad_pkt(G::H * 2) + 2 * pad_pkt(uint32_t(a1 - a0) * G::H * 2) +
+                                  pad_pkt(uint32_t(d1 - d0) * G::I * 2);
+    const uint32_t lmseg = pad_pkt(uint32_t(LM_ROWS_SR) * G::H * 2);
+    lm_pre = min(n_lm, int((RING - last) / lmseg));
+  }
+};
+
+// Segments in stream order.  Group F, bracket k (0 <= k <= L): the MLP of layer k-1 (norm2, gate
+// rows, up rows, down rows; k >= 1) then norm1 and the QKV rows of layer k (k < L); bracket L ends
+// with the final-norm weights and the LM-head segments.  Group A, bracket k < L: the KV chunk and
+// the O rows of layer k; bracket L: the final-norm weights and the LM-head segments.
+enum SRSeg { R_NORM2, R_GATE, R_UP, R_DOWN, R_NORM1, R_QKV, R_KV, R_O, R_FNORM, R_LM };
+
+template <class G>
+__device__ __forceinline__ uint32_t sr_bytes(const PlanSR<G>& P, int kind, int lm_index) {
+  switch (kind) {
+    case R_NORM2:
+    case R_NORM1:
+    case R_FNORM: return G::H * 2;
+    case R_GATE:
+    case R_UP: return uint32_t(P.a1 - P.a0) * G::H * 2;
+    case R_DOWN: return uint32_t(P.d1 - P.d0) * G::I * 2;
+    case R_QKV: return uint32_t(P.q1 - P.q0) * G::H * 2;
+    case R_KV: return uint32_t(P.t1 - P.t0) * 256u;
+    case R_O: return uint32_t(P.o1 - P.o0) * G::H * 2;
+    default: {
+      const int r0 = P.v0 + lm_index * LM_ROWS_SR;
+      return uint32_t(min(LM_ROWS_SR, P.v1 - r0)) * G::H * 2;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Shared memory
+// ------------------------------------------------------------------------------------------------
+
+template <class G>
+struct SmemSR {
+  static constexpr int XS = G::I > G::H ? G::I : G::H;
+  struct Attn {
+    float qkvw[NCW][5 * 64];     // per-wave attention inputs (3 q heads, k_new, v_new; pre-RoPE)
+    float sc[3][TCS + 4];        // per-head scores
+    uint16_t pb[3][TCS + 4];     // per-head probabilities (bf16)
+  };
+  uint8_t ring[RING];
+  union {
+    float xs[XS];                // the phase input vector (bf16 values as fp32)
+    Attn at;
+  };
+  float keep[G::H];              // F: h1 (residual of down); A: x (residual of O, its own rows)
+  float wo[NCW][3][64];          // per-wave P.V partials
+  float ao[3][64];               // leader: the merged attention output of its 3 heads
+  float wml[NCW][2][3];          // per-wave softmax max / sum per head
+  float cs[128];                 // cos [0, 32), sin [32, 64) of this position (fp32 values)
+  float red[NCW];
+  LayerW lw[G::L];
+  const void* kvp[G::L];
+  int32_t blk[TCS / 16 + 2];
+  float lm_val[NCW];
+  int32_t lm_idx[NCW];
+  alignas(16) uint32_t front[NPW];
+  uint32_t consumed[NCW];
+  uint32_t cbar;
+  uint32_t go;                   // brackets the consumers have finished
+  uint32_t loc_l2;               // group A: 1 when its records go through the XCD's L2
+};
+
+// ------------------------------------------------------------------------------------------------
+// Producer waves: bracket k is issued once the consumers have finished bracket k-1, so the DMA of a
+// bracket runs while this workgroup waits for the other group, never during its own exchanges.
+// ------------------------------------------------------------------------------------------------
+
+template <class G>
+__device__ __forceinline__ void producer_sr(const Params& p, const PlanSR<G>& P, SmemSR<G>& sm, uint32_t epoch) {
+  const int pw = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const uint32_t ring_base = uint32_t(reinterpret_cast<uintptr_t>(sm.ring));
+  uint32_t n = 0;  // global packet index at the start of the current segment
+  Spin spin(p.ws, epoch, 21);
+  bool dead = false;
+  auto cmin = [&]() -> uint32_t {
+    uint32_t c = ld_lds(&sm.consumed[0]);
+#pragma unroll
+    for (int w = 1; w < NCW; ++w) c = min(c, ld_lds(&sm.consumed[w]));
+    return c;
+  };
+  auto publish = [&](uint32_t first_pending_packet) {
+    if (lane == 0) st_lds(&sm.front[pw], first_pending_packet * PKT);
+  };
+  auto issue = [&](int kind, int layer, int lm_index) {
+    const uint32_t bytes = sr_bytes(P, kind, lm_index);
+    const uint32_t npk = pad_pkt(bytes) / PKT;
+    if (npk == 0 || dead) return;
+    const uint8_t* base = nullptr;
+    const uint8_t* cache = nullptr;
+    auto u8 = [](const void* q) { return reinterpret_cast<const uint8_t*>(q); };
+    const LayerW& Lw = sm.lw[layer];
+    switch (kind) {
+      case R_NORM2: base = u8(Lw.norm2); break;
+      case R_GATE: base = u8(Lw.gate_up) + size_t(P.a0) * G::H * 2; break;
+      case R_UP: base = u8(Lw.gate_up) + size_t(G::I + P.a0) * G::H * 2; break;
+      case R_DOWN: base = u8(Lw.down) + size_t(P.d0) * G::I * 2; break;
+      case R_NORM1: base = u8(Lw.norm1); break;
+      case R_QKV: base = u8(Lw.qkv) + size_t(P.q0) * G::H * 2; break;
+      case R_KV: cache = u8(sm.kvp[layer]); break;
+      case R_O: base = u8(Lw.o) + size_t(P.o0) * G::H * 2; break;
+      case R_FNORM: base = u8(p.final_norm); break;
+      default: base = u8(p.embed) + size_t(P.v0 + lm_index * LM_ROWS_SR) * G::H * 2; break;
+    }
+    for (uint32_t i = (uint32_t(pw) + NPW - n % NPW) % NPW; i < npk && !dead; i += NPW) {
+      const uint32_t gn = n + i;
+      if ((gn + 1) * PKT > cmin() + RING) {
+        wait_vmcnt<0>();
+        publish(gn);
+        while ((gn + 1) * PKT > cmin() + RING)
+          if (!spin.again()) { dead = true; break; }
+        if (dead) break;
+      }
+      const uint32_t off = i * PKT + uint32_t(lane) * 16u;
+      const uint8_t* src;
+      if (kind == R_KV) {
+        // 4 tokens per packet, 256 B each: 8 K slots then 8 V slots of 16 B, slot s of token j
+        // holding piece (s - j) mod 8 so that 8 consecutive tokens spread over 8 LDS banks
+        const int jt = int(i) * 4 + (lane >> 4);
+        const int t = P.t0 + jt;
+        const int piece = (lane >> 3) & 1;
+        const int part = ((lane & 7) - jt) & 7;
+        const int blk = off < bytes ? sm.blk[t / 16 - P.t0 / 16] : 0;
+        const long long e = (long long)blk * p.block_stride + (long long)(t & 15) * p.token_stride +
+                            (long long)P.g * p.head_stride + (piece ? p.v_off : p.k_off) + part * 8;
+        src = cache + e * 2;
+      } else {
+        src = base + off;
+      }
+      if (off < bytes) dma16(src, __builtin_amdgcn_readfirstlane(ring_base + ((gn * PKT) & (RING - 1))));
+      wait_vmcnt<DEPTH_SR>();
+      if (gn >= uint32_t(DEPTH_SR - 1) * NPW) publish(gn - uint32_t(DEPTH_SR - 1) * NPW);
+    }
+    n += npk;
+  };
+  auto wait_go = [&](uint32_t k) {
+    wait_vmcnt<0>();
+    publish(n);
+    while (!dead && ld_lds(&sm.go) < k) {
+      if (!spin.again()) dead = true;
+      __builtin_amdgcn_s_sleep(2);
+    }
+  };
+  const int L = p.n_layers;
+  for (int k = 0; k <= L && !dead; ++k) {
+    if (k > 0) wait_go(uint32_t(k));
+    if (P.a) {
+      if (k < L) {
+        issue(R_KV, k, 0);
+        issue(R_O, k, 0);
+      } else {
+        issue(R_FNORM, 0, 0);
+      }
+    } else {
+      if (k > 0) {
+        issue(R_NORM2, k - 1, 0);
+        issue(R_GATE, k - 1, 0);
+        issue(R_UP, k - 1, 0);
+        issue(R_DOWN, k - 1, 0);
+      }
+      if (k < L) {
+        issue(R_NORM1, k, 0);
+        issue(R_QKV, k, 0);
+      } else {
+        issue(R_FNORM, 0, 0);
+      }
+    }
+  }
+  // LM head: the segments that fit with the last bracket now, the rest once the final hidden
+  // state has arrived (the consumers set go = L + 1)
+  for (int j = 0; j < P.lm_pre && !dead; ++j) issue(R_LM, 0, j);
+  if (P.lm_pre < P.n_lm) wait_go(uint32_t(L + 1));
+  for (int j = P.lm_pre; j < P.n_lm && !dead; ++j) issue(R_LM, 0, j);
+  wait_vmcnt<0>();
+  publish(dead ? 0x3fffffu : n);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Consumer waves
+// ------------------------------------------------------------------------------------------------
+
+template <class G>
+struct CSR {
+  static constexpr uint32_t RB = RING;
+  using W = SWS<G>;
+  const Params& p;
+  const PlanSR<G>& P;
+  SmemSR<G>& sm;
+  int cw, lane, ct;
+  uint32_t pos = 0, bar_gen = 0, seen = 0, tag;
+  bool dead = false;
+  uint32_t* region;             // the split-role region of the uncached workspace
+  __amdgpu_buffer_rsrc_t rx;    // ... as a buffer resource
+  __amdgpu_buffer_rsrc_t rl;    // group-A records (the XCD's L2, or the region's fallback area)
+  int xr;                       // the copy of the cross-XCD vectors this workgroup polls
+  uint32_t pos_kv_end = 0;      // group A: stream position after this layer's KV chunk
+
+  __device__ __forceinline__ CSR(const Params& p_, const PlanSR<G>& P_, SmemSR<G>& sm_, uint32_t ep,
+                                 uint32_t* region_)
+      : p(p_), P(P_), sm(sm_), tag(ep), region(region_) {
+    cw = (threadIdx.x >> 6) - NPW;
+    lane = threadIdx.x & 63;
+    ct = cw * 64 + lane;
+    rx = rsrc(region_);
+    rl = rx;
+    xr = P.wg % REP;
+  }
+  __device__ __forceinline__ void refresh() { asm volatile("" : "+v"(lane), "+v"(ct)); }
+  __device__ __forceinline__ uint32_t next_seg(uint32_t bytes) {
+    const uint32_t s = pos;
+    pos += pad_pkt(bytes);
+    return s;
+  }
+  __device__ __forceinline__ uint32_t filled() const {
+    typedef __attribute__((address_space(3))) const volatile u32x4 lds_u32x4;
+    const u32x4 f = *(lds_u32x4*)(sm.front);
+    return min(min(f.x, f.y), min(f.z, f.w));
+  }
+  __device__ __forceinline__ void wait_filled(uint32_t end) {
+    if (dead || end <= seen) return;
+    Spin spin(p.ws, tag, 22);
+    while ((seen = filled()) < end)
+      if (!spin.again()) { dead = true; return; }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  }
+  __device__ __forceinline__ void release(uint32_t end) {
+    wait_lgkm0();
+    if (lane == 0) st_lds(&sm.consumed[cw], end);
+  }
+  __device__ __forceinline__ void cbar() {
+    bar_gen += NCW;
+    if (lane == 0) __hip_atomic_fetch_add(&sm.cbar, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    Spin spin(p.ws, tag, 23);
+    while (ld_lds(&sm.cbar) < bar_gen)
+      if (!spin.again()) { dead = true; break; }
+  }
+  __device__ __forceinline__ float block_total(float wave_value) {
+    if (lane == 0) sm.red[cw] = wave_value;
+    cbar();
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < NCW; ++w) t += sm.red[w];
+    return t;
+  }
+  __device__ __forceinline__ uint4 ring16(uint32_t at) const {
+    return *reinterpret_cast<const uint4*>(sm.ring + (at & (RB - 1)));
+  }
+  // the consumers have finished bracket k: the producers may stream the next one
+  __device__ __forceinline__ void bracket_done(uint32_t k) {
+    if (ct == 0) st_lds(&sm.go, k);
+  }
+  __device__ __forceinline__ u32x4 unit6(const float (&v)[VPU]) const {
+    return u32x4{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), tag};
+  }
+  // one unit of cross-XCD vector (kind, l), to every copy
+  __device__ __forceinline__ void put_x(int kind, int l, int u, u32x4 v) const {
+#pragma unroll
+    for (int r = 0; r < REP; ++r) st_unit<16>(rx, W::xoff(kind, l, r, u), v);
+  }
+  // one unit of the group-A records (layer l, unit index)
+  __device__ __forceinline__ void put_loc(int l, size_t unit, u32x4 v) const {
+    if (sm.loc_l2) st_unit<0>(rl, W::loc(l, unit), v);
+    else st_unit<16>(rl, W::loc(l, unit), v);
+  }
+
+  // Poll n units, unit i at byte offset off(i) of resource r, spread over `nthr` threads starting
+  // at thread `tid` (at most MAXU per thread); use(i, unit) for each once its tag is current.
+  template <int MAXU, class OFF, class USE>
+  __device__ __forceinline__ void poll(__amdgpu_buffer_rsrc_t r, int n, int tid, int nthr, OFF off, USE use, int site) {
+    u32x4 v[MAXU];
+    uint32_t pend = 0;
+#pragma unroll
+    for (int k = 0; k < MAXU; ++k) {
+      const int i = tid + k * nthr;
+      if (i < n) { v[k] = ld_unit(r, off(i)); pend |= 1u << k; }
+    }
+    Spin spin(p.ws, tag, site);
+    while (true) {
+#pragma unroll
+      for (int k = 0; k < MAXU; ++k)
+        if (((pend >> k) & 1u) && v[k].w == tag) {
+          use(tid + k * nthr, v[k]);
+          pend &= ~(1u << k);
+        }
+      if (!pend) break;
+      if (dead || !spin.again()) { dead = true; break; }
+#pragma unroll
+      for (int k = 0; k < MAXU; ++k)
+        if ((pend >> k) & 1u) v[k] = ld_unit(r, off(tid + k * nthr));
+    }
+  }
+  // Poll all units of cross-XCD vector (kind, l) with n values into xs[] (and keep[] when given),
+  // split over the consumer threads; returns this wave's sum of squares of the values.
+  template <int MAXU>
+  __device__ __forceinline__ float poll_vec(int kind, int l, int n, float* dst, float* keep, int site) {
+    const int nu = (n + VPU - 1) / VPU;
+    float ss = 0.f;
+    poll<MAXU>(rx, nu, ct, NCT, [&](int u) { return W::xoff(kind, l, xr, u); },
+               [&](int u, const u32x4& v) {
+                 const float f[VPU] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y), bf_lo(v.z), bf_hi(v.z)};
+#pragma unroll
+                 for (int e = 0; e < VPU; ++e) {
+                   const int i = u * VPU + e;
+                   if (i < n) {
+                     dst[i] = f[e];
+                     if (keep) keep[i] = f[e];
+                     ss += f[e] * f[e];
+                   }
+                 }
+               },
+               site);
+    return wave_sum(ss);
+  }
+};
+
+// Rows r0 .. r0 + N - 1 of a ring segment of K-long bf16 rows, dotted with a lane's activation
+// chunks; the N sums are returned wave-uniform (the reductions interleaved).  Rows past the
+// segment read stale ring bytes whose sums the caller discards.
+template <int K, int N, class CT>
+__device__ __forceinline__ void dots_n(const CT& C, uint32_t seg, int r0, const XChunks<K, 8>& x, float (&out)[N]);
+
+// Long rows (down, K = I): the rows in two halves, so that a half's weights fit the registers.
+template <int K, int N, class CT>
+__device__ __forceinline__ void dots_split(const CT& C, uint32_t seg, int r0, const XChunks<K, 8>& x, float (&out)[N]) {
+  static_assert(N % 2 == 0, "two halves");
+  float a[N / 2], b[N / 2];
+  dots_n<K, N / 2>(C, seg, r0, x, a);
+  dots_n<K, N / 2>(C, seg, r0 + N / 2, x, b);
+#pragma unroll
+  for (int r = 0; r < N / 2; ++r) { out[r] = a[r]; out[N / 2 + r] = b[r]; }
+}
+
+template <int K, int N, class CT>
+__device__ __forceinline__ void dots_n(const CT& C, uint32_t seg, int r0, const XChunks<K, 8>& x, float (&out)[N]) {
+  constexpr int CPL = Chunks<K>::CPL, CH = Chunks<K>::CH;
+  uint4 w[N][CPL];
+#pragma unroll
+  for (int r = 0; r < N; ++r)
+#pragma unroll
+    for (int c = 0; c < CPL; ++c)
+      w[r][c] = C.ring16(seg + uint32_t(r0 + r) * uint32_t(K * 2) + uint32_t(C.lane + 64 * c) * 16u);
+  if (CH % 64 != 0) {
+    const bool tail_ok = C.lane + 64 * (CPL - 1) < CH;
+#pragma unroll
+    for (int r = 0; r < N; ++r)
+      if (!tail_ok) w[r][CPL - 1] = make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int r = 0; r < N; ++r) {
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      acc = dot2(w[r][c].x, x[c][0].x, acc);
+      acc = dot2(w[r][c].y, x[c][0].y, acc);
+      acc = dot2(w[r][c].z, x[c][0].z, acc);
+      acc = dot2(w[r][c].w, x[c][0].w, acc);
+    }
+    out[r] = acc;
+  }
+  wave_sum_n<N>(out);
+}
+
+// Norm weights of a lane's chunks from the ring segment that carries them.
+template <int K, class CT>
+__device__ __forceinline__ void normw(const CT& C, XChunks<K, 8>& nw, uint32_t seg) {
+#pragma unroll
+  for (int c = 0; c < Chunks<K>::CPL; ++c) {
+    const int ch = C.lane + 64 * c;
+    nw[c][0] = ch < Chunks<K>::CH ? C.ring16(seg + uint32_t(ch * 16)) : make_uint4(0, 0, 0, 0);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Group A: attention for one chunk (KV head g, chunk c), then the merge, O and h1
+// ------------------------------------------------------------------------------------------------
+
+template <class G>
+__device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg) {
+  using S = SG<G>;
+  using W = SWS<G>;
+  const Params& p = C.p;
+  const PlanSR<G>& P = C.P;
+  SmemSR<G>& sm = C.sm;
+  const int g = P.g, lane = C.lane, w = C.cw;
+  const int T_old = P.t1 - P.t0;
+  const int T = T_old + (P.leader ? 1 : 0);
+  auto edge = [&](int k) { return k >= NCW ? T : ((T * k) / NCW) & ~1; };
+  const int j0 = edge(w), j1 = edge(w + 1);
+  const bool has_new = P.leader && j1 == T && T > j0;
+  float* in = sm.at.qkvw[w];
+  const int part = lane & 7, grp = lane >> 3;
+  // q of the 3 heads of KV head g (units 32g .. 32g + 31), and for the wave with the new token the
+  // units holding its k and v rows
+  {
+    const int kb = G::H + 64 * g, vb = G::H + G::KVH * 64 + 64 * g;
+    const int ku0 = kb / VPU, kn = (kb + 63) / VPU - ku0 + 1;
+    const int vu0 = vb / VPU, vn = (vb + 63) / VPU - vu0 + 1;
+    const int nq = 32, nu = has_new ? nq + kn + vn : nq;
+    C.template poll<1>(C.rx, nu, lane, 64,
+                       [&](int i) {
+                         const int u = i < nq ? 32 * g + i : (i < nq + kn ? ku0 + i - nq : vu0 + i - nq - kn);
+                         return W::xoff(K_XQ, l, C.xr, u);
+                       },
+                       [&](int i, const u32x4& v) {
+                         const float f[VPU] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y), bf_lo(v.z), bf_hi(v.z)};
+                         if (i < nq) {
+#pragma unroll
+                           for (int e = 0; e < VPU; ++e) in[i * VPU + e] = f[e];
+                         } else {
+                           const int kv = i < nq + kn ? 0 : 1;
+                           const int u = kv ? vu0 + i - nq - kn : ku0 + i - nq;
+                           const int base = kv ? vb : kb;
+#pragma unroll
+                           for (int e = 0; e < VPU; ++e) {
+                             const int row = u * VPU + e - base;
+                             if (row >= 0 && row < 64) in[192 + 64 * kv + row] = f[e];
+                           }
+                         }
+                       },
+                       30);
+  }
+  if (w == 0 && lane == 0) trace_at(p, l, 34, p.n_layers);
+  C.wait_filled(C.pos);  // the KV chunk is in the ring (streamed long before)
+  wait_lgkm0();
+  if (w == 0 && lane == 0) trace_at(p, l, 3, p.n_layers);
+  const float sgn = part < 4 ? -1.f : 1.f;
+  auto rope8 = [&](const float* head, uint32_t (&out)[4]) {
+    const float4 a0 = *reinterpret_cast<const float4*>(head + part * 8);
+    const float4 a1 = *reinterpret_cast<const float4*>(head + part * 8 + 4);
+    const float4 b0 = *reinterpret_cast<const float4*>(head + (part ^ 4) * 8);
+    const float4 b1 = *reinterpret_cast<const float4*>(head + (part ^ 4) * 8 + 4);
+    const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const float y[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    const int f0 = (part & 3) * 8;
+    float r[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = rnd(rnd(x[e] * sm.cs[f0 + e]) + rnd((sgn * y[e]) * sm.cs[32 + f0 + e]));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[e] = pack2(r[2 * e], r[2 * e + 1]);
+  };
+  uint32_t q[3][4], kn[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int h = 0; h < 3; ++h) rope8(in + h * 64, q[h]);
+  if (w == 0 && lane == 0) trace_at(p, l, 35, p.n_layers);
+  auto score = [&](int j, const uint4& k, bool keep) {
+    float s3[3];
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      float a = dot2(q[h][0], k.x, 0.f);
+      a = dot2(q[h][1], k.y, a);
+      a = dot2(q[h][2], k.z, a);
+      a = dot2(q[h][3], k.w, a);
+      s3[h] = group8_sum(a);
+    }
+    if (part == 0 && keep)
+#pragma unroll
+      for (int h = 0; h < 3; ++h) sm.at.sc[h][j] = rnd(s3[h]) * 0.125f;
+  };
+  const int jc = min(j1, T_old);
+  for (int jb = j0; jb < jc; jb += 8) {
+    const int j = jb + grp;
+    score(j, j < jc ? C.ring16(seg + uint32_t(j) * 256u + uint32_t((part + j) & 7) * 16u) : make_uint4(0u, 0u, 0u, 0u),
+          j < jc);
+  }
+  if (has_new) {
+    rope8(in + 192, kn);
+    score(T_old, make_uint4(kn[0], kn[1], kn[2], kn[3]), grp == 0);
+  }
+  wait_lgkm0();
+  if (w == 0 && lane == 0) trace_at(p, l, 36, p.n_layers);
+  // chunk softmax statistics per head, over this wave's tokens, then over the chunk
+  float sv[3][2];
+#pragma unroll
+  for (int h = 0; h < 3; ++h)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int j = j0 + lane + 64 * i;
+      sv[h][i] = j < j1 ? sm.at.sc[h][j] : -INFINITY;
+    }
+  {
+    float m3[3], l3[3];
+#pragma unroll
+    for (int h = 0; h < 3; ++h) m3[h] = fmaxf(sv[h][0], sv[h][1]);
+    wave_max_n<3>(m3);
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      l3[h] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) l3[h] += sv[h][i] == -INFINITY ? 0.f : expf(sv[h][i] - m3[h]);
+    }
+    wave_sum_n<3>(l3);
+    if (lane == 0)
+#pragma unroll
+      for (int h = 0; h < 3; ++h) { sm.wml[w][0][h] = m3[h]; sm.wml[w][1][h] = l3[h]; }
+  }
+  if (w == 0 && lane == 0) trace_at(p, l, 37, p.n_layers);
+  C.cbar();
+  float mq = -INFINITY, lq = 0.f;
+  if (lane < 4 * 3) {
+    mq = sm.wml[lane & 3][0][lane >> 2];
+    lq = sm.wml[lane & 3][1][lane >> 2];
+  }
+  float mx = fmaxf(mq, dpp<0xb1>(mq, mq));
+  mx = fmaxf(mx, dpp<0x4e>(mx, mx));
+  float ex = mq == -INFINITY ? 0.f : lq * expf(mq - mx);
+  ex += dpp<0xb1>(0.f, ex);
+  ex += dpp<0x4e>(0.f, ex);
+  float Mh[3], Lh[3];
+#pragma unroll
+  for (int h = 0; h < 3; ++h) {
+    Mh[h] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx), 4 * h));
+    Lh[h] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), 4 * h));
+  }
+  if (w == 0 && lane == 0) trace_at(p, l, 17, p.n_layers);
+  // exchange (max, sum) with the other chunks of KV head g: chunk c' of head g is group-A rank
+  // g + KVH c'; its record is 2 units {max x3, tag}, {sum x3, tag}
+  if (w == 0 && lane < 2)
+    C.put_loc(l, W::STAT_U + size_t(P.rank) * 2 + lane,
+              lane ? u32x4{__float_as_uint(Lh[0]), __float_as_uint(Lh[1]), __float_as_uint(Lh[2]), C.tag}
+                   : u32x4{__float_as_uint(Mh[0]), __float_as_uint(Mh[1]), __float_as_uint(Mh[2]), C.tag});
+  {
+    // lane 2k + s polls unit s of chunk k: lane 2k the maxima of chunk k, lane 2k+1 its sums
+    float st[3] = {(lane & 1) ? 0.f : -INFINITY, (lane & 1) ? 0.f : -INFINITY, (lane & 1) ? 0.f : -INFINITY};
+    C.template poll<1>(C.rl, 2 * S::C, lane, 64,
+                       [&](int i) { return W::loc(l, W::STAT_U + size_t(g + G::KVH * (i >> 1)) * 2 + (i & 1)); },
+                       [&](int, const u32x4& v) {
+                         st[0] = __uint_as_float(v.x);
+                         st[1] = __uint_as_float(v.y);
+                         st[2] = __uint_as_float(v.z);
+                       },
+                       31);
+    // combine in one pass: the odd lane of each pair takes its chunk's maxima from the even lane
+    float m[3], s[3];
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      const float mo = __shfl_xor(st[h], 1);
+      m[h] = (lane & 1) ? mo : st[h];
+    }
+    float M[3] = {m[0], m[1], m[2]};
+    wave_max_n<3>(M);
+#pragma unroll
+    for (int h = 0; h < 3; ++h) s[h] = ((lane & 1) && lane < 2 * S::C && m[h] != -INFINITY) ? st[h] * expf(m[h] - M[h]) : 0.f;
+    wave_sum_n<3>(s);
+#pragma unroll
+    for (int h = 0; h < 3; ++h) { Mh[h] = M[h]; Lh[h] = s[h]; }
+  }
+  if (w == 0 && lane == 0) trace_at(p, l, 18, p.n_layers);
+  // probabilities with the global max and sum, rounded to bf16 before P.V as HF does
+#pragma unroll
+  for (int h = 0; h < 3; ++h) {
+    const float inv = 1.0f / Lh[h];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int j = j0 + lane + 64 * i;
+      if (j < j1) sm.at.pb[h][j] = uint16_t(f2bf(expf(sv[h][i] - Mh[h]) * inv));
+    }
+  }
+  wait_lgkm0();
+  // P.V: lane = (half, d2) owns dims 2*d2, 2*d2+1; token pairs alternate between the halves
+  const int half = lane >> 5, d2 = lane & 31;
+  const int jo1 = min(j1, T_old);
+  const int npairs = jo1 > j0 ? (jo1 - j0) / 2 : 0;
+  const uint32_t voff = uint32_t(d2 & 3) * 4u;
+  float acc[3][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
+  auto vslot = [&](int j) { return seg + uint32_t(j) * 256u + 128u + uint32_t(((d2 >> 2) + j) & 7) * 16u + voff; };
+#pragma unroll 4
+  for (int k = half; k < npairs; k += 2) {
+    const int j = j0 + 2 * k;
+    const uint32_t va = *reinterpret_cast<const uint32_t*>(sm.ring + (vslot(j) & (RING - 1)));
+    const uint32_t vb = *reinterpret_cast<const uint32_t*>(sm.ring + (vslot(j + 1) & (RING - 1)));
+    const uint32_t lo = __builtin_amdgcn_perm(vb, va, 0x05040100u);
+    const uint32_t hi = __builtin_amdgcn_perm(vb, va, 0x07060302u);
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      const uint32_t pp = *reinterpret_cast<const uint32_t*>(&sm.at.pb[h][j]);
+      acc[h][0] = dot2(pp, lo, acc[h][0]);
+      acc[h][1] = dot2(pp, hi, acc[h][1]);
+    }
+  }
+  if (half == 0) {
+    if (jo1 > j0 && ((jo1 - j0) & 1)) {
+      const int j = jo1 - 1;
+      const uint32_t v = *reinterpret_cast<const uint32_t*>(sm.ring + (vslot(j) & (RING - 1)));
+#pragma unroll
+      for (int h = 0; h < 3; ++h) {
+        const float pj = bf2f(sm.at.pb[h][j]);
+        acc[h][0] = fmaf(pj, bf_lo(v), acc[h][0]);
+        acc[h][1] = fmaf(pj, bf_hi(v), acc[h][1]);
+      }
+    }
+    if (has_new) {
+#pragma unroll
+      for (int h = 0; h < 3; ++h) {
+        const float pj = bf2f(sm.at.pb[h][T_old]);
+        acc[h][0] = fmaf(pj, in[256 + 2 * d2], acc[h][0]);
+        acc[h][1] = fmaf(pj, in[256 + 2 * d2 + 1], acc[h][1]);
+      }
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < 3; ++h) {
+    acc[h][0] += __shfl_xor(acc[h][0], 32);
+    acc[h][1] += __shfl_xor(acc[h][1], 32);
+  }
+  C.release(C.pos_kv_end);
+  if (has_new && P.slot >= 0 && grp < 2) {
+    // KV append at slot_mapping[0] (block360_kernel.inc:124-135; slot < 0 skips): lanes 0-7 store
+    // the rotated new K, lanes 8-15 the new V, 8 dims (16 bytes) per lane
+    uint16_t* cache = reinterpret_cast<uint16_t*>(const_cast<void*>(sm.kvp[l]));
+    const long long e = (P.slot / 16) * p.block_stride + (P.slot % 16) * p.token_stride +
+                        (long long)g * p.head_stride + (grp ? p.v_off : p.k_off) + part * 8;
+    uint32_t val[4];
+    if (grp == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) val[i] = kn[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) val[i] = pack2(in[256 + part * 8 + 2 * i], in[256 + part * 8 + 2 * i + 1]);
+    }
+    uint16_t* dst = cache + e;
+    if ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+      st_global16(dst, val[0], val[1], val[2], val[3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        st_global2(dst + 2 * i, uint16_t(val[i] & 0xffffu));
+        st_global2(dst + 2 * i + 1, uint16_t(val[i] >> 16));
+      }
+    }
+  }
+  if (lane < 32)
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      sm.wo[w][h][2 * d2] = acc[h][0];
+      sm.wo[w][h][2 * d2 + 1] = acc[h][1];
+    }
+  C.cbar();
+  if (w == 0 && lane == 0) trace_at(p, l, 19, p.n_layers);
+  // wave h < 3: head 3g + h.  The chunk's partial sum of p.v in fixed wave order, fp32.
+  float O = 0.f;
+  if (w < 3) {
+#pragma unroll
+    for (int v = 0; v < NCW; ++v) O += sm.wo[v][w][lane];
+  }
+  if (!P.leader) {
+    if (w < 3) {
+      // 22 units of 3 floats; lane 3u + s holds float s of unit u: lane 3u writes the unit
+      const float f1 = __shfl_down(O, 1), f2 = __shfl_down(O, 2);
+      if (lane % 3 == 0)
+        C.put_loc(l, W::PART_U + (size_t(P.rank) * 3 + w) * S::PU + lane / 3,
+                  u32x4{__float_as_uint(O), __float_as_uint(lane + 1 < 64 ? f1 : 0.f),
+                        __float_as_uint(lane + 2 < 64 ? f2 : 0.f), C.tag});
+    }
+    return;
+  }
+  // leader: add the partials of chunks 0 .. C-2 in chunk order (this chunk is C-1), round once
+  if (w < 3) {
+    float part_sum[S::C];
+#pragma unroll
+    for (int k = 0; k < S::C; ++k) part_sum[k] = 0.f;
+    C.template poll<S::C - 1 < 1 ? 1 : S::C - 1>(
+        C.rl, S::C - 1, 0, 1,
+        [&](int k) { return W::loc(l, W::PART_U + (size_t(g + G::KVH * k) * 3 + w) * S::PU + lane / 3); },
+        [&](int k, const u32x4& v) {
+          const uint32_t s = lane % 3;
+          part_sum[k] = __uint_as_float(s == 0 ? v.x : s == 1 ? v.y : v.z);
+        },
+        32);
+    float tot = 0.f;
+#pragma unroll
+    for (int k = 0; k < S::C - 1; ++k) tot += part_sum[k];
+    tot += O;
+    sm.ao[w][lane] = rnd(tot);
+  }
+  C.cbar();
+  if (w == 0 && lane < 32) {
+    // the head group's 192 values are units 32g .. 32g+31 of the attention vector
+    float v[VPU];
+#pragma unroll
+    for (int e = 0; e < VPU; ++e) {
+      const int i = lane * VPU + e;
+      v[e] = sm.ao[i >> 6][i & 63];
+    }
+    C.put_loc(l, W::ATTN_U + size_t(32 * g + lane), C.unit6(v));
+  }
+  if (w == 0 && lane == 0) trace_at(p, l, 20, p.n_layers);
+}
+
+// ------------------------------------------------------------------------------------------------
+// The LM head (both groups): final RMSNorm of x_L, this workgroup's rows of the tied embedding,
+// its greedy candidate; then the end record every workgroup writes, gathered by workgroup 0
+// ------------------------------------------------------------------------------------------------
+
+template <class G>
+__device__ __forceinline__ void lm_head_sr(CSR<G>& C) {
+  using S = SG<G>;
+  using W = SWS<G>;
+  const Params& p = C.p;
+  const PlanSR<G>& P = C.P;
+  SmemSR<G>& sm = C.sm;
+  const int L = p.n_layers;
+  const uint32_t segf = C.next_seg(sr_bytes(P, R_FNORM, 0));
+  C.wait_filled(C.pos);
+  XChunks<G::H, 8> nw;
+  normw<G::H>(C, nw, segf);
+  C.release(C.pos);
+  C.refresh();
+  const float ss = C.template poll_vec<1>(K_X, L, G::H, sm.xs, nullptr, 33);
+  const float rs = rms_scale(C.block_total(ss), G::H);
+  C.bracket_done(uint32_t(L + 1));
+  XChunks<G::H, 8> x;
+  load_x<G::H, 8, true>(x, sm.xs, nw, rs, C.lane);
+  if (P.wg == 0 && C.cw == 0) {
+#pragma unroll
+    for (int c = 0; c < Chunks<G::H>::CPL; ++c) {
+      const int ch = C.lane + 64 * c;
+      if (ch < Chunks<G::H>::CH) *reinterpret_cast<uint4*>(p.out_hidden + ch * 8) = x[c][0];
+    }
+  }
+  float best = -INFINITY;
+  int best_i = 0x7fffffff;
+  for (int j = 0; j < P.n_lm; ++j) {
+    const uint32_t seg = C.next_seg(sr_bytes(P, R_LM, j));
+    const int r0 = P.v0 + j * LM_ROWS_SR;
+    const int nrows = min(LM_ROWS_SR, P.v1 - r0);
+    C.wait_filled(C.pos);
+    constexpr int RW = LM_ROWS_SR / NCW;  // rows cw, cw + 4, ... of the segment
+    float out[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) out[r] = 0.f;
+    {
+      constexpr int CPL = Chunks<G::H>::CPL, CH = Chunks<G::H>::CH;
+      uint4 wr[RW][CPL];
+#pragma unroll
+      for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int c = 0; c < CPL; ++c)
+          wr[r][c] = C.ring16(seg + uint32_t(C.cw + NCW * r) * uint32_t(G::H * 2) + uint32_t(C.lane + 64 * c) * 16u);
+      if (CH % 64 != 0 && C.lane + 64 * (CPL - 1) >= CH)
+#pragma unroll
+        for (int r = 0; r < RW; ++r) wr[r][CPL - 1] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          acc = dot2(wr[r][c].x, x[c][0].x, acc);
+          acc = dot2(wr[r][c].y, x[c][0].y, acc);
+          acc = dot2(wr[r][c].z, x[c][0].z, acc);
+          acc = dot2(wr[r][c].w, x[c][0].w, acc);
+        }
+        out[r] = acc;
+      }
+      wave_sum_n<RW>(out);
+    }
+    C.release(C.pos);
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int row = C.cw + NCW * r;
+      if (row < nrows) {
+        const float v = rnd(out[r]);
+        const int idx = r0 + row;
+        if (v > best || (v == best && idx < best_i)) { best = v; best_i = idx; }
+        if (p.out_logits && C.lane == 0) p.out_logits[r0 + row] = uint16_t(f2bf(out[r]));
+      }
+    }
+  }
+  if (C.lane == 0) { sm.lm_val[C.cw] = best; sm.lm_idx[C.cw] = best_i; }
+  C.cbar();
+  if (C.ct == 0) trace_tail(p, 1);
+  if (p.out_logits && (C.dead || aborted(p.ws, C.tag)))
+    for (int i = P.v0 + C.ct; i < P.v1; i += NCT) p.out_logits[i] = 0x7fc0;
+  // the end record of this workgroup: {best value, its index, dead flag, tag}
+  if (C.ct == 0) {
+    float bv = sm.lm_val[0];
+    int bi = sm.lm_idx[0];
+    for (int w = 1; w < NCW; ++w)
+      if (sm.lm_val[w] > bv || (sm.lm_val[w] == bv && sm.lm_idx[w] < bi)) { bv = sm.lm_val[w]; bi = sm.lm_idx[w]; }
+    st_unit<16>(C.rx, uint32_t(W::LMR + size_t(P.wg) * 16), u32x4{__float_as_uint(bv), uint32_t(bi), C.dead ? 1u : 0u, C.tag});
+  }
+  (void)S::HU;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Consumer main loops
+// ------------------------------------------------------------------------------------------------
+
+template <class G>
+__device__ __forceinline__ void consumer_f(CSR<G>& C) {
+  using S = SG<G>;
+  using W = SWS<G>;
+  const Params& p = C.p;
+  const PlanSR<G>& P = C.P;
+  SmemSR<G>& sm = C.sm;
+  const int L = p.n_layers;
+  auto tr = [&](int l, int ev) { if (C.ct == 0) trace_at(p, l, ev, p.n_layers); };
+  for (int k = 0; k <= L; ++k) {
+    if (k > 0) {
+      const int l = k - 1;
+      // ---- RMSNorm(h1) + gate/up + SwiGLU of layer l ----
+      C.refresh();
+      const uint32_t segn = C.next_seg(sr_bytes(P, R_NORM2, 0));
+      const uint32_t segg = C.next_seg(sr_bytes(P, R_GATE, 0));
+      const uint32_t segu = C.next_seg(sr_bytes(P, R_UP, 0));
+      C.wait_filled(C.pos);
+      XChunks<G::H, 8> nw;
+      normw<G::H>(C, nw, segn);
+      tr(l, 9);
+      const float ss = C.template poll_vec<1>(K_H1, l, G::H, sm.xs, sm.keep, 40);
+      const float rs = rms_scale(C.block_total(ss), G::H);
+      tr(l, 10);
+      {
+        XChunks<G::H, 8> x;
+        load_x<G::H, 8, true>(x, sm.xs, nw, rs, C.lane);
+        tr(l, 21);
+        const int nunits = P.au1 - P.au0;
+        for (int j = C.cw; j < nunits; j += NCW) {
+          float og[VPU], ou[VPU];
+          dots_n<G::H, VPU>(C, segg, j * VPU, x, og);
+          tr(l, 22);
+          dots_n<G::H, VPU>(C, segu, j * VPU, x, ou);
+          tr(l, 23);
+          float a[VPU];
+#pragma unroll
+          for (int e = 0; e < VPU; ++e) {
+            const float gv = rnd(og[e]), uv = rnd(ou[e]);
+            const float silu = rnd(gv / (1.0f + expf(-gv)));
+            a[e] = silu * uv;
+          }
+          if (C.lane == 0) C.put_x(K_ACT, l, P.au0 + j, C.unit6(a));
+          tr(l, 24);
+        }
+      }
+      C.release(C.pos);
+      tr(l, 11);
+      // ---- down + residual of layer l -> x_{l+1} ----
+      C.refresh();
+      const uint32_t segd = C.next_seg(sr_bytes(P, R_DOWN, 0));
+      C.wait_filled(C.pos);
+      C.template poll_vec<2>(K_ACT, l, G::I, sm.xs, nullptr, 41);
+      C.cbar();
+      tr(l, 13);
+      if (P.xu1 > P.xu0 && C.cw == 0) {
+        XChunks<G::I, 8> x;
+        const XChunks<G::I, 8> none = {};
+        load_x<G::I, 8, false>(x, sm.xs, none, 1.f, C.lane);
+        tr(l, 28);
+        float od[VPU];
+        dots_split<G::I, VPU>(C, segd, 0, x, od);
+        tr(l, 29);
+        float y[VPU];
+#pragma unroll
+        for (int e = 0; e < VPU; ++e) {
+          const int r = min(P.d0 + e, G::H - 1);
+          y[e] = rnd(sm.keep[r] + rnd(od[e]));
+        }
+        if (C.lane == 0) C.put_x(K_X, l + 1, P.xu0, C.unit6(y));
+        if (p.layer_outputs && C.lane < VPU && P.d0 + C.lane < G::H) {
+          float yl = y[0];
+#pragma unroll
+          for (int e = 1; e < VPU; ++e) yl = C.lane == e ? y[e] : yl;
+          p.layer_outputs[size_t(l) * G::H + P.d0 + C.lane] = uint16_t(f2bf(yl));
+        }
+      }
+      C.release(C.pos);
+      tr(l, 14);
+    }
+    if (k == L) break;
+    // ---- RMSNorm(x) + QKV of layer k ----
+    const int l = k;
+    C.refresh();
+    const uint32_t segn = C.next_seg(sr_bytes(P, R_NORM1, 0));
+    const uint32_t segq = C.next_seg(sr_bytes(P, R_QKV, 0));
+    C.wait_filled(C.pos);
+    XChunks<G::H, 8> nw;
+    normw<G::H>(C, nw, segn);
+    tr(l, 0);
+    float ss;
+    if (l == 0) {
+      long long id = p.ids_i64 ? reinterpret_cast<const int64_t*>(p.input_ids)[0]
+                               : reinterpret_cast<const int32_t*>(p.input_ids)[0];
+      id = min(max(id, 0LL), (long long)G::V - 1);
+      const uint16_t* e = p.embed + size_t(id) * G::H;
+      float s = 0.f;
+      for (int i = C.ct; i < G::H; i += NCT) {
+        const float v = bf2f(e[i]);
+        sm.xs[i] = v;
+        s += v * v;
+      }
+      ss = wave_sum(s);
+    } else {
+      ss = C.template poll_vec<1>(K_X, l, G::H, sm.xs, nullptr, 42);
+    }
+    const float rs = rms_scale(C.block_total(ss), G::H);
+    tr(l, 1);
+    {
+      XChunks<G::H, 8> x;
+      load_x<G::H, 8, true>(x, sm.xs, nw, rs, C.lane);
+      tr(l, 25);
+      const int nunits = P.qu1 - P.qu0;
+      for (int j = C.cw; j < nunits; j += NCW) {
+        float o[VPU];
+        dots_n<G::H, VPU>(C, segq, j * VPU, x, o);
+        tr(l, 26);
+        if (C.lane == 0) C.put_x(K_XQ, l, P.qu0 + j, C.unit6(o));
+        tr(l, 27);
+      }
+    }
+    C.release(C.pos);
+    tr(l, 2);
+    C.bracket_done(uint32_t(k + 1));
+  }
+  lm_head_sr<G>(C);
+  (void)S::HU;
+  (void)sizeof(W);
+}
+
+template <class G>
+__device__ __forceinline__ void consumer_a(CSR<G>& C) {
+  using S = SG<G>;
+  using W = SWS<G>;
+  const Params& p = C.p;
+  const PlanSR<G>& P = C.P;
+  SmemSR<G>& sm = C.sm;
+  const int L = p.n_layers;
+  auto tr = [&](int l, int ev) { if (C.ct == 0) trace_at(p, l, ev, p.n_layers); };
+  // this position's cos/sin row (fp32 values) and layer 0's input rows
+  for (int i = C.ct; i < 64; i += NCT)
+    sm.cs[i] = p.cs_fp32 ? reinterpret_cast<const float*>(p.cos_sin)[size_t(P.pos) * 64 + i]
+                         : bf2f(reinterpret_cast<const uint16_t*>(p.cos_sin)[size_t(P.pos) * 64 + i]);
+  {
+    long long id = p.ids_i64 ? reinterpret_cast<const int64_t*>(p.input_ids)[0]
+                             : reinterpret_cast<const int32_t*>(p.input_ids)[0];
+    id = min(max(id, 0LL), (long long)G::V - 1);
+    for (int r = P.o0 + C.ct; r < P.o1; r += NCT) sm.keep[r] = bf2f(p.embed[size_t(id) * G::H + r]);
+  }
+  // are the group-A workgroups on one XCC?  Each publishes its XCC_ID, each reads all 32.
+  {
+    const uint32_t xcc = __builtin_amdgcn_s_getreg((15 << 11) | (0 << 6) | 20) & 15u;
+    if (C.ct == 0) st_unit<16>(C.rx, uint32_t(W::XCC_TAB + size_t(P.rank) * 16), u32x4{xcc, 0u, 0u, C.tag});
+    uint32_t mismatch = 0;
+    C.template poll<1>(C.rx, AG, C.lane, 64, [&](int i) { return uint32_t(W::XCC_TAB + size_t(i) * 16); },
+                       [&](int, const u32x4& v) { mismatch |= v.x != xcc ? 1u : 0u; }, 34);
+    mismatch = __builtin_amdgcn_ballot_w64(mismatch != 0u) != 0ull ? 1u : 0u;
+    if (C.ct == 0) sm.loc_l2 = (mismatch == 0u && p.xws != nullptr) ? 1u : 0u;
+    C.cbar();
+    C.rl = sm.loc_l2 ? rsrc(p.xws) : rsrc(reinterpret_cast<uint8_t*>(C.region) + W::LOC);
+  }
+  for (int l = 0; l < L; ++l) {
+    C.refresh();
+    const uint32_t segkv = C.next_seg(sr_bytes(P, R_KV, 0));
+    C.pos_kv_end = C.pos;
+    const uint32_t sego = C.next_seg(sr_bytes(P, R_O, 0));
+    // x_l rows of this workgroup's O rows (the residual): layer 0 read the embedding above
+    if (l > 0) {
+      const int nu = P.ou1 - P.ou0;
+      C.template poll<1>(C.rx, nu, C.ct, NCT, [&](int i) { return W::xoff(K_X, l, C.xr, P.ou0 + i); },
+                         [&](int i, const u32x4& v) {
+                           const float f[VPU] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y), bf_lo(v.z), bf_hi(v.z)};
+#pragma unroll
+                           for (int e = 0; e < VPU; ++e) {
+                             const int r = (P.ou0 + i) * VPU + e;
+                             if (r < G::H) sm.keep[r] = f[e];
+                           }
+                         },
+                         35);
+    }
+    tr(l, 6);
+    if (P.att) attention_sr<G>(C, l, segkv);
+    else C.release(C.pos_kv_end);
+    // every group-A workgroup: the merged attention vector, then its O rows + residual -> h1
+    C.cbar();  // the attention scratch shares storage with xs
+    C.wait_filled(C.pos);
+    C.template poll<1>(C.rl, S::HU, C.ct, NCT, [&](int u) { return W::loc(l, W::ATTN_U + size_t(u)); },
+                       [&](int u, const u32x4& v) {
+                         const float f[VPU] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y), bf_lo(v.z), bf_hi(v.z)};
+#pragma unroll
+                         for (int e = 0; e < VPU; ++e) sm.xs[u * VPU + e] = f[e];
+                       },
+                       36);
+    tr(l, 30);
+    C.cbar();
+    tr(l, 7);
+    {
+      XChunks<G::H, 8> x;
+      const XChunks<G::H, 8> none = {};
+      load_x<G::H, 8, false>(x, sm.xs, none, 1.f, C.lane);
+      tr(l, 31);
+      const int nunits = P.ou1 - P.ou0;
+      for (int j = C.cw; j < nunits; j += NCW) {
+        float o[VPU];
+        dots_n<G::H, VPU>(C, sego, j * VPU, x, o);
+        tr(l, 32);
+        float h[VPU];
+#pragma unroll
+        for (int e = 0; e < VPU; ++e) {
+          const int r = min((P.ou0 + j) * VPU + e, G::H - 1);
+          h[e] = rnd(sm.keep[r] + rnd(o[e]));
+        }
+        if (C.lane == 0) C.put_x(K_H1, l, P.ou0 + j, C.unit6(h));
+        tr(l, 33);
+      }
+    }
+    C.release(C.pos);
+    tr(l, 8);
+    C.bracket_done(uint32_t(l + 1));
+  }
+  lm_head_sr<G>(C);
+}
+
+
+// Workgroup 0: every workgroup's end record; the step's greedy id, or, when any workgroup gave up a
+// wait, poisoned outputs (ids -1, NaN hidden state) and the host-visible status.  Then the epoch.
+template <class G>
+__device__ __forceinline__ void final_gather(CSR<G>& C) {
+  using W = SWS<G>;
+  const Params& p = C.p;
+  SmemSR<G>& sm = C.sm;
+  const uint32_t epoch = C.tag;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  uint32_t bad = 0;
+  static_assert(NWG == NCT, "one end record per consumer thread");
+  {
+    Spin spin(p.ws, epoch, 24);
+    const uint32_t off = uint32_t(W::LMR + size_t(C.ct) * 16);
+    u32x4 v = ld_unit(C.rx, off);
+    while (v.w != epoch) {
+      if (!spin.again()) { bad = 1; break; }
+      v = ld_unit(C.rx, off);
+    }
+    if (!bad) {
+      bv = __uint_as_float(v.x);
+      bi = int(v.y);
+      bad = v.z;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int oi = __shfl_xor(bi, o);
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+  }
+  const bool any_bad = __builtin_amdgcn_ballot_w64(bad != 0u) != 0ull;
+  C.cbar();  // the LM phase's reads of lm_val / lm_idx / red are over
+  if (C.lane == 0) { sm.lm_val[C.cw] = bv; sm.lm_idx[C.cw] = bi; sm.red[C.cw] = any_bad ? 1.f : 0.f; }
+  C.cbar();
+  bool fail = C.dead || aborted(p.ws, epoch);
+  for (int w = 0; w < NCW; ++w) fail = fail || sm.red[w] != 0.f;
+  if (fail) {
+    if (C.ct == 0 && !aborted(p.ws, epoch)) raise_abort(p.ws, epoch, 25);
+    for (int i = C.ct; i < G::H; i += NCT) p.out_hidden[i] = 0x7fc0;
+  }
+  if (C.ct == 0) {
+    bv = sm.lm_val[0];
+    bi = sm.lm_idx[0];
+    for (int w = 1; w < NCW; ++w)
+      if (sm.lm_val[w] > bv || (sm.lm_val[w] == bv && sm.lm_idx[w] < bi)) { bv = sm.lm_val[w]; bi = sm.lm_idx[w]; }
+    if (p.out_ids) p.out_ids[0] = fail ? -1 : bi;
+    if (fail && p.host_status) {
+      __hip_atomic_store(p.host_status + 1, ld_dev(p.ws + HDR_ABORT_WHERE), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(p.host_status, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    st_dev(p.ws + HDR_EPOCH, epoch);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Kernel
+// ------------------------------------------------------------------------------------------------
+
+template <class G>
+__global__ void __launch_bounds__(WG_THREADS, 1) decode_sr(Params p, uint32_t* region) {
+  // the general kernel takes contexts beyond this kernel's limit (both are launched, exactly one runs)
+  if (min(max(p.seq_lens[0], 1), p.max_seq) > p.sr_max_s) return;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
+  SmemSR<G>& sm = *reinterpret_cast<SmemSR<G>*>(smem_raw);
+  if (threadIdx.x == 0) {
+    for (int w = 0; w < NPW; ++w) sm.front[w] = 0;
+    for (int w = 0; w < NCW; ++w) sm.consumed[w] = 0;
+    sm.cbar = 0;
+    sm.go = 0;
+    sm.loc_l2 = 0;
+  }
+  for (int i = threadIdx.x; i < p.n_layers; i += WG_THREADS) {
+    const void* const* t = p.layers + size_t(i) * 6;
+    LayerW w{};
+    w.norm1 = t[0]; w.qkv = t[1]; w.o = t[2]; w.norm2 = t[3]; w.gate_up = t[4]; w.down = t[5];
+    sm.lw[i] = w;
+    sm.kvp[i] = p.kv[i];
+  }
+  PlanSR<G> P;
+  P.init(p, blockIdx.x);
+  if (P.att) {
+    const int nb = (P.t1 > P.t0) ? ((P.t1 - 1) / 16 - P.t0 / 16 + 1) : 0;
+    for (int i = threadIdx.x; i < nb; i += WG_THREADS) sm.blk[i] = p.block_table[P.t0 / 16 + i];
+  }
+  trace_begin(p);
+  __syncthreads();
+  const uint32_t epoch = step_epoch(p.ws);
+  if (threadIdx.x < 64 * NPW) {
+    producer_sr<G>(p, P, sm, epoch);
+  } else {
+    CSR<G> C(p, P, sm, epoch, region);
+    if (P.a) consumer_a<G>(C);
+    else consumer_f<G>(C);
+    if (blockIdx.x == 0) final_gather<G>(C);
+  }
+  __syncthreads();
+  trace_end(p);
+}
+
+}  // namespace sr
+}  // namespace pk
+
+// ------------------------------------------------------------------------------------------------
+// Host side
+// ------------------------------------------------------------------------------------------------
+
+namespace pk {
+namespace sr {
+
+// Longest context (tokens attended, the new one included) the kernel takes: C chunks of at most TCS
+// cached tokens per KV head, and a chunk's K/V plus the workgroup's O rows within the LDS ring.
+template <class G>
+constexpr int max_seq() {
+  using S = SG<G>;
+  constexpr uint32_t o_bytes = uint32_t(S::OU) * VPU * G::H * 2;
+  constexpr int tc_ring = int((RING - pad_pkt(o_bytes) - 2 * PKT) / 256u) / 16 * 16;
+  constexpr int tc = tc_ring < TCS ? tc_ring : TCS;
+  return S::C * tc + 1;
+}
+static_assert(max_seq<G360>() >= 1281 && max_seq<G135>() >= 769, "the split-role kernel covers configs 2 and 3");
+
+template <class G>
+constexpr size_t lds_bytes() { return sizeof(SmemSR<G>); }
+static_assert((sizeof(SmemSR<G360>) + 15) / 16 * 16 + TRACE_LDS_BYTES <= 160 * 1024 &&
+                  (sizeof(SmemSR<G135>) + 15) / 16 * 16 + TRACE_LDS_BYTES <= 160 * 1024,
+              "LDS budget of one gfx950 workgroup, with the diagnostic timestamps");
+
+template <class G>
+static int launch(const Params& p, uint32_t* region, uint32_t* local, hipStream_t stream, int cooperative) {
+  static int ready[64] = {};
+  static int status[64] = {};
+  const void* fn = reinterpret_cast<const void*>(decode_sr<G>);
+  size_t lds = lds_bytes<G>();
+  const size_t trace_off = (lds + 15) / 16 * 16;
+  const size_t lds_traced = trace_off + TRACE_LDS_BYTES;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return PK_ERR_RESIDENCY;
+  if (!ready[dev]) {
+    hipDeviceProp_t prop;
+    int st = 0, max_lds = 0;
+    if ((e = hipGetDeviceProperties(&prop, dev)) != hipSuccess) st = e;
+    else if ((e = hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev)) != hipSuccess) st = e;
+    else if (__builtin_strncmp(prop.gcnArchName, "gfx950", 6) != 0) st = PK_ERR_ARCH;
+    else if (prop.multiProcessorCount < NWG || size_t(max_lds) < lds_traced) st = PK_ERR_RESIDENCY;
+    else if ((e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_traced))) != hipSuccess) st = e;
+    status[dev] = st;
+    ready[dev] = 1;
+  }
+  if (status[dev]) return status[dev];
+  Params q = p;
+  q.xws = local;
+  if (q.trace) {
+    if (q.n_layers > TR_LAYERS) return PK_ERR_MODEL;
+    q.trace_lds = uint32_t(trace_off);
+    lds = lds_traced;
+  }
+  void* args[] = {&q, &region};
+  if (cooperative) e = hipLaunchCooperativeKernel(fn, dim3(NWG), dim3(WG_THREADS), args, lds, stream);
+  else e = hipLaunchKernel(fn, dim3(NWG), dim3(WG_THREADS), args, lds, stream);
+  if (e != hipSuccess) return e;
+  return hipGetLastError();
+}
+
+}  // namespace sr
+
+int sr_launch(int model, const Params& p, uint32_t* region, uint32_t* local, hipStream_t stream, int cooperative) {
+  if (model == PK_MODEL_SMOLLM2_360M) return sr::launch<G360>(p, region, local, stream, cooperative);
+  if (model == PK_MODEL_SMOLLM2_135M) return sr::launch<G135>(p, region, local, stream, cooperative);
+  return PK_ERR_MODEL;
+}
+size_t sr_region_bytes() { return sr::SWS<G360>::BYTES > sr::SWS<G135>::BYTES ? sr::SWS<G360>::BYTES : sr::SWS<G135>::BYTES; }
+size_t sr_local_bytes() {
+  return sr::SWS<G360>::LOC_BYTES > sr::SWS<G135>::LOC_BYTES ? sr::SWS<G360>::LOC_BYTES : sr::SWS<G135>::LOC_BYTES;
+}
+int sr_max_seq(int model) {
+  if (model == PK_MODEL_SMOLLM2_360M) return sr::max_seq<G360>();
+  if (model == PK_MODEL_SMOLLM2_135M) return sr::max_seq<G135>();
+  return 0;
+}
+
+}  // namespace pk

@@ -62,8 +62,8 @@ class Case:
             num_layers=self.geom.layers, return_token_ids=True, logits_out=lg, layer_outputs=lo)
         torch.cuda.synchronize()
         rt = self.mod.workspace(dev)
-        hdr = rt.header(3)
-        assert hdr[1] == 0, f"kernel abandoned a bounded wait (wait site {hdr[2]}, epoch {hdr[0]})"
+        ep, site = rt.pending_failure()
+        assert ep == 0, f"kernel abandoned a bounded wait (wait site {site}, epoch {ep})"
         res = {"hidden": hid.clone().cpu(), "ids": out_ids.clone().cpu()}
         if logits:
             res["logits"] = lg.cpu()

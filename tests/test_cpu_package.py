@@ -61,7 +61,8 @@ def test_status_strings_and_sizes():
     want = {9101: "batch_out_of_range", 9103: "null_device_pointer", 9104: "cooperative_launch_unsupported",
             9106: "kernel_requires_gfx950", 9107: "kv_offsets_or_pointers_not_16_byte_aligned",
             9108: "scratch_or_debug_buffer_too_small", 9109: "block_size_or_stride_invalid",
-            9112: "workspace_first_use_under_stream_capture"}
+            9112: "first_use_of_the_device_under_stream_capture",
+            9113: "a_previous_step_on_this_device_gave_up_a_bounded_wait", 9114: "library_state_allocation_failed"}
     for code, s in want.items():
         assert lib.decode360_status_string(code).decode() == s
         assert lib.mk_status_string(code).decode() == s
@@ -87,7 +88,7 @@ def _args(**over):
 @pytest.mark.parametrize("over,code", [
     (dict(B=0), 9101), (dict(B=17), 9101), (dict(n_layers=0), 9110), (dict(n_layers=33), 9110),
     (dict(model=7), 9110), (dict(max_seq_len=0), 9102), (dict(max_seq_len=1 << 20), 9102),
-    (dict(embed=None), 9103), (dict(scratch=None), 9103), (dict(scratch_bytes=1024), 9108),
+    (dict(embed=None), 9103), (dict(scratch=None), 9103), (dict(scratch_bytes=16), 9108),
     (dict(block_size=32), 9109), (dict(bt_stride=1), 9109), (dict(k_off=4), 9107),
     (dict(embed=24), 9107), (dict(out_logits=8), 9107),
 ])

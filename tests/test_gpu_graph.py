@@ -1,6 +1,5 @@
 """The decode step under HIP graph capture (the reference's steady-state contract,
-validation-summary.json:186-205): after one eager call has initialised the workspace, the step
-is captured into a graph and replayed with new inputs written in place; every replay must equal
+validation-summary.json:186-205): after one eager call, the step is captured into a graph and replayed with new inputs written in place; every replay must equal
 the eager step on the same inputs bit for bit.  Eager work and synchronisations run between the
 replays."""
 
@@ -53,7 +52,7 @@ def test_decode_step_replays_from_a_graph(batch):
     mod, kv, st, logits, kw = _setup(batch, ctxs)
     kv0 = [c.clone() for c in kv.caches]
     _fill(kv, st, [5] * batch, ctxs)
-    mod.decode_step(**kw)                       # first use of the workspace: outside capture
+    mod.decode_step(**kw)                       # first use of the device: outside capture
     torch.cuda.synchronize()
 
     g = torch.cuda.CUDAGraph()
@@ -83,4 +82,4 @@ def test_decode_step_replays_from_a_graph(batch):
         assert torch.equal(ids_g, ie) and torch.equal(logits.view(torch.int16), le.view(torch.int16)), step
         assert all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(kv.caches, kv_e)), step
         _ = (torch.randn(1024, device=hid_g.device) * 2).sum().item()   # unrelated eager work between replays
-    assert mod.workspace(hid_g.device).abort_word() == 0
+    assert mod.workspace(hid_g.device).pending_failure() == (0, 0)

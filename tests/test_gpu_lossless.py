@@ -16,6 +16,20 @@ pytestmark = pytest.mark.gpu
 ROWS, COLS = 5120, 960
 
 
+@pytest.fixture(autouse=True)
+def _general_kernel_for_dense_steps():
+    """The lossless gate/up stream is read by the general batch-1 kernel; the dense steps these tests
+    compare it with run on the same kernel (split-role steps sum in another order)."""
+    if not torch.cuda.is_available():
+        yield
+        return
+    from prime_kernels_amd import _native
+    lib = _native.library()
+    old = lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, 0)
+    yield
+    lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, old)
+
+
 def _need_gpu():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
