@@ -39,6 +39,7 @@ extern "C" {
 #define PK_ERR_CAPTURE 9112      /* the first use of a device (its state's allocation) happened under stream capture */
 #define PK_ERR_ABORTED 9113      /* a previous step on this device gave up a bounded wait; its outputs were poisoned */
 #define PK_ERR_STATE 9114        /* the library's per-device state could not be allocated */
+#define PK_ERR_NOALLOC 9115      /* pk_decode_noalloc: batch, weights or context beyond what its fixed array holds */
 
 /* Options for pk_set_option. */
 #define PK_OPT_COOPERATIVE 1     /* 1: launch with hipLaunchCooperativeKernel (default 0, or PK_LAUNCH=cooperative) */
@@ -58,7 +59,8 @@ extern "C" {
 size_t pk_workspace_bytes(int model);
 
 /* Allocate and zero the current device's state now, outside any stream capture (a first use under
- * capture returns PK_ERR_CAPTURE).  Returns 0 or a status code.  No reference counterpart. */
+ * capture returns PK_ERR_CAPTURE), and clear pk_decode_noalloc's array on the device.  Returns 0 or a
+ * status code.  No reference counterpart. */
 int pk_init(void);
 
 /* Library options (PK_OPT_*).  Returns the previous value, or -1 for an unknown option.  No reference
@@ -93,6 +95,32 @@ int pk_decode(void* stream, int model, int B, int n_layers, const void* input_id
               long long token_stride, long long head_stride, int block_size, const void* cos_sin,
               int cs_fp32, void* out_hidden, void* layer_outputs, void* out_ids, void* out_logits,
               void* scratch, size_t scratch_bytes, int max_seq_len);
+
+/* Limits of pk_decode_noalloc: its fixed per-device array, and the largest max_seq_len per model. */
+#define PK_NOALLOC_SCRATCH_BYTES 4194304
+#define PK_NOALLOC_MAX_SEQ_360M 1537
+#define PK_NOALLOC_MAX_SEQ_135M 2561
+
+/* pk_decode that allocates nothing, for callers that cannot allocate device memory: code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc.  It has no counterpart in
+ * the reference.  Arguments are pk_decode's without `scratch`/`scratch_bytes`.  Every word its
+ * kernel exchanges lives in one array of PK_NOALLOC_SCRATCH_BYTES per device that is compiled into
+ * the library (a device global each GPU holds until the process ends); it calls no hipMalloc,
+ * hipFree or other allocating routine.  It runs the split-role batch-1 kernel only: B must be 1,
+ * the weights bf16, and max_seq_len (the block table's capacity) at most PK_NOALLOC_MAX_SEQ_360M or
+ * PK_NOALLOC_MAX_SEQ_135M; anything else returns PK_ERR_NOALLOC and launches nothing.  The first call
+ * on a device clears the array with a fill kernel on `stream` (pk_init also clears it; when the first
+ * call is captured, every replay of the graph clears it).  All calls on one device share the array
+ * and each leaves its contents for the next: calls that overlap on one device (from two streams, or
+ * beside another decode step) race.  A step that gives up a bounded wait is reported through its
+ * outputs only (token ids -1, NaN hidden state and logits); pk_state_status does not see it. */
+int pk_decode_noalloc(void* stream, int model, int B, int n_layers, const void* input_ids, int ids_i64,
+                      const void* embed, const void* final_norm, const void* positions, const void* seq_lens,
+                      const void* block_table, int bt_stride, const void* slot_mapping, const void* layers,
+                      void* const* kv, long long k_off, long long v_off, long long block_stride,
+                      long long token_stride, long long head_stride, int block_size, const void* cos_sin,
+                      int cs_fp32, void* out_hidden, void* layer_outputs, void* out_ids, void* out_logits,
+                      int max_seq_len);
 
 /* pk_decode with per-stage debug capture (SmolLM2-360M bf16, B <= 2) and, for 360M, an optional
  * lossless gate/up table (prime_lossless.h; NULL: dense).  `debug` (16-byte aligned, at least

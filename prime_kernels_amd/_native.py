@@ -16,6 +16,7 @@ MODEL_135M = 135
 
 # status codes of include/prime_decode.h that callers act on
 PK_ERR_ABORTED = 9113
+PK_ERR_NOALLOC = 9115
 # pk_set_option options
 PK_OPT_COOPERATIVE = 1
 PK_OPT_SPLIT_ROLE = 2
@@ -35,6 +36,8 @@ SIGNATURES = {
     "pk_test_abort_next": (ci, [vp]),
     "pk_decode": (ci, [vp, ci, ci, ci, vp, ci, vp, vp, vp, vp, vp, ci, vp, vp, vp,
                        ll, ll, ll, ll, ll, ci, vp, ci, vp, vp, vp, vp, vp, sz, ci]),
+    "pk_decode_noalloc": (ci, [vp, ci, ci, ci, vp, ci, vp, vp, vp, vp, vp, ci, vp, vp, vp,
+                               ll, ll, ll, ll, ll, ci, vp, ci, vp, vp, vp, vp, ci]),
     "pk_decode_debug": (ci, [vp, ci, ci, ci, vp, ci, vp, vp, vp, vp, vp, ci, vp, vp, vp,
                              ll, ll, ll, ll, ll, ci, vp, ci, vp, vp, vp, vp, vp, sz, ci, vp, vp, sz, ci]),
     "pk_decode_mxfp8": (ci, [vp, ci, ci, ci, vp, ci, vp, vp, vp, vp, vp, ci, vp, vp, vp,

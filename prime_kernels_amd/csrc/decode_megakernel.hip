@@ -2955,6 +2955,61 @@ static int take_abort(DevState* st) {
   return PK_ERR_ABORTED;
 }
 
+// ------------------------------------------------------------------------------------------------
+// State of pk_decode_noalloc: one fixed array per device, compiled into the library, holding the
+// split-role kernel's header words, exchange region and group-A records.  In host code `scratch`
+// only names the variable for the runtime: its device address, which differs per device, comes
+// from hipGetSymbolAddress once per device (with that device current) and only that address is
+// used.  Nothing here allocates.
+// ------------------------------------------------------------------------------------------------
+namespace noalloc {
+constexpr size_t HDR_BYTES = 4096;  // header words: step epoch, abort word, wait site
+static __device__ __align__(256) uint8_t scratch[PK_NOALLOC_SCRATCH_BYTES];
+struct Dev {
+  uint8_t* ptr;  // device address of this device's `scratch`
+  int cleared;   // a fill outside any capture has been issued
+};
+static std::mutex mu;
+static Dev devs[MAX_STATES];  // by device ordinal
+static size_t region_off() { return HDR_BYTES; }
+static size_t local_off() { return HDR_BYTES + round_up(sr_region_bytes(), 4096); }
+static size_t used_bytes() { return local_off() + round_up(sr_local_bytes(), 4096); }
+
+// The current device's array, cleared before its first use by a fill on `stream` (under capture
+// the fill is recorded, so every replay of the graph clears the array before its own step).  With
+// `sync`, the fill is waited for.  Called with `mu` held.
+static int base_locked(hipStream_t stream, bool sync, uint8_t** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= MAX_STATES) return PK_ERR_STATE;
+  Dev& d = devs[dev];
+  if (!d.ptr) {
+    void* q = nullptr;
+    if ((e = hipGetSymbolAddress(&q, HIP_SYMBOL(scratch))) != hipSuccess) return e;
+    if (!q || used_bytes() > PK_NOALLOC_SCRATCH_BYTES) return PK_ERR_STATE;
+    d.ptr = static_cast<uint8_t*>(q);
+  }
+  if (!d.cleared) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if ((e = hipStreamIsCapturing(stream, &cs)) != hipSuccess) return e;
+    hipLaunchKernelGGL(zero_fill, dim3(1024), dim3(256), 0, stream, reinterpret_cast<uint4*>(d.ptr),
+                       used_bytes() / 16);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (cs == hipStreamCaptureStatusNone) {
+      if (sync && (e = hipStreamSynchronize(stream)) != hipSuccess) return e;
+      d.cleared = 1;
+    }
+  }
+  *out = d.ptr;
+  return PK_OK;
+}
+static int base(hipStream_t stream, bool sync, uint8_t** out) {
+  std::lock_guard<std::mutex> lk(mu);
+  return base_locked(stream, sync, out);
+}
+}  // namespace noalloc
+
 template <class G, bool BATCHED, bool DBG = false>
 static int launch(const Params& p, hipStream_t stream) {
   static LaunchCache<G> cache;
@@ -3011,7 +3066,7 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
                        void* out_hidden, void* layer_outputs, void* out_ids, void* out_logits,
                        void* scratch, size_t scratch_bytes, int max_seq_len, const void* encoded_gu = nullptr,
                        void* debug = nullptr, size_t debug_bytes = 0, int debug_layer = -1,
-                       const void* input_hidden = nullptr) {
+                       const void* input_hidden = nullptr, bool noalloc = false) {
   if (B < 1 || B > (G::WF ? 1 : BMAX)) return PK_ERR_BATCH;  // MXFP8 weights: batch 1 only
   if (debug_layer < -1 || debug_layer >= G::L) return PK_ERR_BLOCK;
   if (debug) {  // per-stage capture: the reference's SmolLM2-360M bf16 layout, at most 2 sequences
@@ -3025,9 +3080,9 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
   if (n_layers < 1 || n_layers > G::L) return PK_ERR_MODEL;
   if (max_seq_len < 1 || max_seq_len > kMaxSeq) return PK_ERR_MAX_SEQ;
   if (!input_ids || !embed || !final_norm || !positions || !seq_lens || !block_table ||
-      !slot_mapping || !layers || !kv || !cos_sin || !out_hidden || !scratch)
+      !slot_mapping || !layers || !kv || !cos_sin || !out_hidden || (!scratch && !noalloc))
     return PK_ERR_NULL;
-  if (scratch_bytes < SCRATCH_BYTES) return PK_ERR_SCRATCH;
+  if (!noalloc && scratch_bytes < SCRATCH_BYTES) return PK_ERR_SCRATCH;
   if (block_size != 16 || bt_stride < 1 || (long long)bt_stride * block_size < max_seq_len) return PK_ERR_BLOCK;
   if (k_off % 8 || v_off % 8 || block_stride % 8 || token_stride % 8 || head_stride % 8 || k_off < 0 ||
       v_off < 0 || block_stride < 0 || token_stride < 0 || head_stride < 0)
@@ -3072,6 +3127,24 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
   p.debug_layer = debug_layer;
   p.input_hidden = reinterpret_cast<const uint16_t*>(input_hidden);
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (noalloc) {  // the split-role kernel on the fixed array; no library state is touched
+    if constexpr (G::WF == 0) {
+      const int model = G::H == 960 ? PK_MODEL_SMOLLM2_360M : PK_MODEL_SMOLLM2_135M;
+      const int lim = sr_max_seq(model);
+      if (B != 1 || debug || encoded_gu || input_hidden || max_seq_len > lim) return PK_ERR_NOALLOC;
+      uint8_t* base = nullptr;
+      const int rc = noalloc::base(s, false, &base);
+      if (rc != PK_OK) return rc;
+      p.ws = reinterpret_cast<uint32_t*>(base);
+      p.xws = nullptr;
+      p.host_status = nullptr;
+      p.sr_max_s = lim;
+      return sr_launch(model, p, reinterpret_cast<uint32_t*>(base + noalloc::region_off()),
+                       reinterpret_cast<uint32_t*>(base + noalloc::local_off()), s, opt_cooperative());
+    } else {
+      return PK_ERR_NOALLOC;
+    }
+  }
   DevState* state = nullptr;
   const int st = get_state(stream, &state);
   if (st != PK_OK) return st;
@@ -3116,7 +3189,10 @@ extern "C" void pk_set_trace(void* buf) { pk::g_trace = reinterpret_cast<unsigne
 // the device use it.  Returns 0 or a status code.
 extern "C" int pk_init(void) {
   pk::DevState* st = nullptr;
-  return pk::get_state(nullptr, &st);
+  const int rc = pk::get_state(nullptr, &st);
+  if (rc != PK_OK) return rc;
+  uint8_t* base = nullptr;
+  return pk::noalloc::base(nullptr, true, &base);
 }
 
 // Options (initially from PK_LAUNCH / PK_SPLIT_ROLE): PK_OPT_COOPERATIVE 1 launches the decode
@@ -3210,6 +3286,29 @@ extern "C" int pk_decode(void* stream, int model, int B, int n_layers, const voi
                                      block_stride, token_stride, head_stride, block_size, cos_sin, cs_fp32,
                                      out_hidden, layer_outputs, out_ids, out_logits, scratch, scratch_bytes,
                                      max_seq_len);
+  return PK_ERR_MODEL;
+}
+
+extern "C" int pk_decode_noalloc(void* stream, int model, int B, int n_layers, const void* input_ids, int ids_i64,
+                                 const void* embed, const void* final_norm, const void* positions,
+                                 const void* seq_lens, const void* block_table, int bt_stride,
+                                 const void* slot_mapping, const void* layers, void* const* kv, long long k_off,
+                                 long long v_off, long long block_stride, long long token_stride,
+                                 long long head_stride, int block_size, const void* cos_sin, int cs_fp32,
+                                 void* out_hidden, void* layer_outputs, void* out_ids, void* out_logits,
+                                 int max_seq_len) {
+  if (model == PK_MODEL_SMOLLM2_360M)
+    return pk::decode_impl<pk::G360>(stream, B, n_layers, input_ids, ids_i64, embed, final_norm, positions,
+                                     seq_lens, block_table, bt_stride, slot_mapping, layers, kv, k_off, v_off,
+                                     block_stride, token_stride, head_stride, block_size, cos_sin, cs_fp32,
+                                     out_hidden, layer_outputs, out_ids, out_logits, nullptr, 0, max_seq_len,
+                                     nullptr, nullptr, 0, -1, nullptr, true);
+  if (model == PK_MODEL_SMOLLM2_135M)
+    return pk::decode_impl<pk::G135>(stream, B, n_layers, input_ids, ids_i64, embed, final_norm, positions,
+                                     seq_lens, block_table, bt_stride, slot_mapping, layers, kv, k_off, v_off,
+                                     block_stride, token_stride, head_stride, block_size, cos_sin, cs_fp32,
+                                     out_hidden, layer_outputs, out_ids, out_logits, nullptr, 0, max_seq_len,
+                                     nullptr, nullptr, 0, -1, nullptr, true);
   return PK_ERR_MODEL;
 }
 
@@ -3311,6 +3410,7 @@ extern "C" const char* prime_decode_status_string(int status) {
     case PK_ERR_CAPTURE: return "first_use_of_the_device_under_stream_capture";
     case PK_ERR_ABORTED: return "a_previous_step_on_this_device_gave_up_a_bounded_wait";
     case PK_ERR_STATE: return "library_state_allocation_failed";
+    case PK_ERR_NOALLOC: return "no_alloc_entry_point_takes_batch_1_bf16_weights_and_max_seq_len_up_to_its_limit";
     default: return hipGetErrorString(static_cast<hipError_t>(status));
   }
 }

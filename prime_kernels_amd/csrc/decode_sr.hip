@@ -1290,6 +1290,12 @@ constexpr int max_seq() {
   return S::C * tc + 1;
 }
 static_assert(max_seq<G360>() >= 1281 && max_seq<G135>() >= 769, "the split-role kernel covers configs 2 and 3");
+static_assert(max_seq<G360>() == PK_NOALLOC_MAX_SEQ_360M && max_seq<G135>() == PK_NOALLOC_MAX_SEQ_135M,
+              "the context limits pk_decode_noalloc documents");
+constexpr size_t pages(size_t n) { return (n + 4095) / 4096 * 4096; }
+static_assert(4096 + pages(SWS<G360>::BYTES) + pages(SWS<G360>::LOC_BYTES) <= PK_NOALLOC_SCRATCH_BYTES &&
+                  4096 + pages(SWS<G135>::BYTES) + pages(SWS<G135>::LOC_BYTES) <= PK_NOALLOC_SCRATCH_BYTES,
+              "header, region and group-A records fit pk_decode_noalloc's array");
 
 template <class G>
 constexpr size_t lds_bytes() { return sizeof(SmemSR<G>); }
