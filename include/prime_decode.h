@@ -97,7 +97,7 @@ int pk_decode(void* stream, int model, int B, int n_layers, const void* input_id
               void* scratch, size_t scratch_bytes, int max_seq_len);
 
 /* Limits of pk_decode_noalloc: its fixed per-device array, and the largest max_seq_len per model. */
-#define PK_NOALLOC_SCRATCH_BYTES 4194304
+#define PK_NOALLOC_SCRATCH_BYTES 8388608
 #define PK_NOALLOC_MAX_SEQ_360M 1537
 #define PK_NOALLOC_MAX_SEQ_135M 2561
 

@@ -1613,8 +1613,6 @@ constexpr int TCB = 256;                  // max cached tokens per attention ite
 constexpr int IPW = 16;                   // max attention items per workgroup
 constexpr int MAX_ITEMS = NWG * IPW;
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 // Batched workspace regions, after the batch-1 layout (so one workspace serves both kernels).
 template <class G>

@@ -38,7 +38,14 @@ namespace sr {
 constexpr int AG = 32;                   // group A workgroups (wg % 8 == 0)
 constexpr int FG = NWG - AG;             // group F workgroups
 constexpr int VPU = 6;                   // bf16 values per 16-byte unit
-constexpr int REP = 1;                   // copies of each cross-XCD unit
+#ifndef PK_SR_REP
+#define PK_SR_REP 1
+#endif
+#ifndef PK_SR_UPL
+#define PK_SR_UPL 1
+#endif
+constexpr int REP = PK_SR_REP;           // copies of each cross-XCD unit
+constexpr int UPL = PK_SR_UPL;           // cross-XCD units per 64-byte line (fewer: fewer polls per line)
 constexpr int TCS = 256;                 // max cached tokens per attention chunk
 constexpr int DEPTH_SR = 8;              // DMA packets in flight per producer wave
 constexpr int LM_ROWS_SR = 16;           // LM-head rows per ring segment
@@ -64,7 +71,7 @@ enum SKind { K_H1, K_ACT, K_X, K_XQ, NK };
 template <class G>
 struct SWS {
   using S = SG<G>;
-  static constexpr int LINES = (S::IU + 3) / 4;
+  static constexpr int LINES = (S::IU + UPL - 1) / UPL;
   static constexpr int SLOTS = (G::L + 1) * NK;
   static constexpr size_t XCC_TAB = 0;                        // 32 units: the group-A XCC ids
   static constexpr size_t X0 = XCC_TAB + size_t(AG) * 16;     // cross-XCD vectors (bytes from the region base)
@@ -77,10 +84,11 @@ struct SWS {
   static constexpr size_t LOC_LAYER = (ATTN_U + S::HU) * 16;
   static constexpr size_t LOC_BYTES = LOC_LAYER * G::L;
   static constexpr size_t BYTES = LOC + LOC_BYTES;
-  // unit u of vector (kind, layer l, copy r): consecutive lines of a vector are SLOTS lines apart,
-  // so one vector's lines spread over the memory channels
+  // unit u of vector (kind, layer l, copy r): UPL units per line; consecutive lines of a vector are
+  // SLOTS lines apart, so one vector's lines spread over the memory channels
   __device__ static uint32_t xoff(int kind, int l, int r, int u) {
-    return uint32_t(X0 + ((size_t(r) * LINES + size_t(u >> 2)) * SLOTS + size_t(l) * NK + kind) * 64 + size_t(u & 3) * 16);
+    return uint32_t(X0 + ((size_t(r) * LINES + size_t(u / UPL)) * SLOTS + size_t(l) * NK + kind) * 64 +
+                    size_t(u % UPL) * 16);
   }
   __device__ static uint32_t loc(int l, size_t unit) { return uint32_t(size_t(l) * LOC_LAYER + unit * 16); }
 };
@@ -95,9 +103,19 @@ __device__ __forceinline__ u32x4 ld_unit(__amdgpu_buffer_rsrc_t r, uint32_t off)
   return __builtin_amdgcn_raw_buffer_load_b128(r, int(off), 0, 16);  // device scope (sc1)
 }
 
+// LlamaRMSNorm's scale rsqrt(mean(x^2) + eps) with the hardware reciprocal square root (HF on the GPU
+// uses an approximate rsqrt too) and the mean as sum * (1/n); within an ulp of the exact scale.
+template <int N>
+__device__ __forceinline__ float rms_rsq(float sumsq) {
+  return rsqrtf(sumsq * (1.0f / float(N)) + 1e-5f);
+}
+
 // ------------------------------------------------------------------------------------------------
 // Per-workgroup plan
 // ------------------------------------------------------------------------------------------------
+
+static_assert((SG<G360>::IU + FG - 1) / FG <= 2 && (SG<G135>::IU + FG - 1) / FG <= 2,
+              "the gate/up phase gives each wave one 6-row item: at most 2 act units per F workgroup");
 
 template <class G>
 struct PlanSR {
@@ -195,6 +213,7 @@ struct SmemSR {
     float qkvw[NCW][5 * 64];     // per-wave attention inputs (3 q heads, k_new, v_new; pre-RoPE)
     float sc[3][TCS + 4];        // per-head scores
     uint16_t pb[3][TCS + 4];     // per-head probabilities (bf16)
+    float ao[3][64];             // leader: the merged attention output of its 3 heads
   };
   uint8_t ring[RING];
   union {
@@ -203,7 +222,6 @@ struct SmemSR {
   };
   float keep[G::H];              // F: h1 (residual of down); A: x (residual of O, its own rows)
   float wo[NCW][3][64];          // per-wave P.V partials
-  float ao[3][64];               // leader: the merged attention output of its 3 heads
   float wml[NCW][2][3];          // per-wave softmax max / sum per head
   float cs[128];                 // cos [0, 32), sin [32, 64) of this position (fp32 values)
   float red[NCW];
@@ -213,6 +231,8 @@ struct SmemSR {
   float lm_val[NCW];
   int32_t lm_idx[NCW];
   alignas(16) uint32_t front[NPW];
+  alignas(16) uint32_t zero16[4];  // a 16-byte zero line: what lanes past the end of a row read
+  float part[NCW][8];              // per-wave partial results combined across the waves
   uint32_t consumed[NCW];
   uint32_t cbar;
   uint32_t go;                   // brackets the consumers have finished
@@ -362,7 +382,7 @@ struct CSR {
     ct = cw * 64 + lane;
     rx = rsrc(region_);
     rl = rx;
-    xr = P.wg % REP;
+    xr = (P.wg >> 3) % REP;
   }
   __device__ __forceinline__ void refresh() { asm volatile("" : "+v"(lane), "+v"(ct)); }
   __device__ __forceinline__ uint32_t next_seg(uint32_t bytes) {
@@ -403,6 +423,12 @@ struct CSR {
   }
   __device__ __forceinline__ uint4 ring16(uint32_t at) const {
     return *reinterpret_cast<const uint4*>(sm.ring + (at & (RB - 1)));
+  }
+  // ring16(at), or the zero line when !ok (one select on the address, no branch)
+  __device__ __forceinline__ uint4 ring16z(uint32_t at, bool ok) const {
+    const uint4* q = ok ? reinterpret_cast<const uint4*>(sm.ring + (at & (RB - 1)))
+                        : reinterpret_cast<const uint4*>(sm.zero16);
+    return *q;
   }
   // the consumers have finished bracket k: the producers may stream the next one
   __device__ __forceinline__ void bracket_done(uint32_t k) {
@@ -473,37 +499,21 @@ struct CSR {
 };
 
 // Rows r0 .. r0 + N - 1 of a ring segment of K-long bf16 rows, dotted with a lane's activation
-// chunks; the N sums are returned wave-uniform (the reductions interleaved).  Rows past the
-// segment read stale ring bytes whose sums the caller discards.
-template <int K, int N, class CT>
-__device__ __forceinline__ void dots_n(const CT& C, uint32_t seg, int r0, const XChunks<K, 8>& x, float (&out)[N]);
-
-// Long rows (down, K = I): the rows in two halves, so that a half's weights fit the registers.
-template <int K, int N, class CT>
-__device__ __forceinline__ void dots_split(const CT& C, uint32_t seg, int r0, const XChunks<K, 8>& x, float (&out)[N]) {
-  static_assert(N % 2 == 0, "two halves");
-  float a[N / 2], b[N / 2];
-  dots_n<K, N / 2>(C, seg, r0, x, a);
-  dots_n<K, N / 2>(C, seg, r0 + N / 2, x, b);
-#pragma unroll
-  for (int r = 0; r < N / 2; ++r) { out[r] = a[r]; out[N / 2 + r] = b[r]; }
-}
-
+// chunks (chunk lane + 64 c of each row); the N sums are returned wave-uniform.  Lanes past a row's
+// last chunk read the zero line (their activation chunk is zero too, but ring bytes past a row may
+// hold anything).  Rows past the segment read other ring bytes, whose sums the caller discards.
 template <int K, int N, class CT>
 __device__ __forceinline__ void dots_n(const CT& C, uint32_t seg, int r0, const XChunks<K, 8>& x, float (&out)[N]) {
   constexpr int CPL = Chunks<K>::CPL, CH = Chunks<K>::CH;
+  const bool tail_ok = CH % 64 == 0 || C.lane + 64 * (CPL - 1) < CH;
   uint4 w[N][CPL];
 #pragma unroll
   for (int r = 0; r < N; ++r)
 #pragma unroll
-    for (int c = 0; c < CPL; ++c)
-      w[r][c] = C.ring16(seg + uint32_t(r0 + r) * uint32_t(K * 2) + uint32_t(C.lane + 64 * c) * 16u);
-  if (CH % 64 != 0) {
-    const bool tail_ok = C.lane + 64 * (CPL - 1) < CH;
-#pragma unroll
-    for (int r = 0; r < N; ++r)
-      if (!tail_ok) w[r][CPL - 1] = make_uint4(0, 0, 0, 0);
-  }
+    for (int c = 0; c < CPL; ++c) {
+      const uint32_t at = seg + uint32_t(r0 + r) * uint32_t(K * 2) + uint32_t(C.lane + 64 * c) * 16u;
+      w[r][c] = c == CPL - 1 ? C.ring16z(at, tail_ok) : C.ring16(at);
+    }
 #pragma unroll
   for (int r = 0; r < N; ++r) {
     float acc = 0.f;
@@ -516,7 +526,42 @@ __device__ __forceinline__ void dots_n(const CT& C, uint32_t seg, int r0, const 
     }
     out[r] = acc;
   }
-  wave_sum_n<N>(out);
+  wave_rows<N>(out);
+}
+
+// Partial dots over one wave's quarter of K (chunks [w CH/4, (w+1) CH/4) of each row, chunk
+// w CH/4 + lane + 64 c for this lane; `x` holds the lane's activation chunks of that quarter).
+template <int K>
+struct Quarter {
+  static constexpr int CH = K / 8, CHW = CH / NCW, CPL = (CHW + 63) / 64;
+  static_assert(CH % NCW == 0, "K splits evenly over the waves");
+};
+template <int K, int N, class CT>
+__device__ __forceinline__ void dots_quarter(const CT& C, uint32_t seg, int r0, const uint4 (&x)[Quarter<K>::CPL],
+                                             float (&out)[N]) {
+  using Q = Quarter<K>;
+  const bool tail_ok = Q::CHW % 64 == 0 || C.lane + 64 * (Q::CPL - 1) < Q::CHW;
+  uint4 w[N][Q::CPL];
+#pragma unroll
+  for (int r = 0; r < N; ++r)
+#pragma unroll
+    for (int c = 0; c < Q::CPL; ++c) {
+      const uint32_t at = seg + uint32_t(r0 + r) * uint32_t(K * 2) + uint32_t(C.cw * Q::CHW + C.lane + 64 * c) * 16u;
+      w[r][c] = c == Q::CPL - 1 ? C.ring16z(at, tail_ok) : C.ring16(at);
+    }
+#pragma unroll
+  for (int r = 0; r < N; ++r) {
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < Q::CPL; ++c) {
+      acc = dot2(w[r][c].x, x[c].x, acc);
+      acc = dot2(w[r][c].y, x[c].y, acc);
+      acc = dot2(w[r][c].z, x[c].z, acc);
+      acc = dot2(w[r][c].w, x[c].w, acc);
+    }
+    out[r] = acc;
+  }
+  wave_rows<N>(out);
 }
 
 // Norm weights of a lane's chunks from the ring segment that carries them.
@@ -543,11 +588,11 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg) {
   const int g = P.g, lane = C.lane, w = C.cw;
   const int T_old = P.t1 - P.t0;
   const int T = T_old + (P.leader ? 1 : 0);
-  auto edge = [&](int k) { return k >= NCW ? T : ((T * k) / NCW) & ~1; };
+  // the waves take whole 16-token tiles of the chunk (the new token, at index T_old, included)
+  auto edge = [&](int k) { return k >= NCW ? T : ((T * k) / NCW) & ~15; };
   const int j0 = edge(w), j1 = edge(w + 1);
   const bool has_new = P.leader && j1 == T && T > j0;
   float* in = sm.at.qkvw[w];
-  const int part = lane & 7, grp = lane >> 3;
   // q of the 3 heads of KV head g (units 32g .. 32g + 31), and for the wave with the new token the
   // units holding its k and v rows
   {
@@ -582,72 +627,94 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg) {
   C.wait_filled(C.pos);  // the KV chunk is in the ring (streamed long before)
   wait_lgkm0();
   if (w == 0 && lane == 0) trace_at(p, l, 3, p.n_layers);
-  const float sgn = part < 4 ? -1.f : 1.f;
-  auto rope8 = [&](const float* head, uint32_t (&out)[4]) {
-    const float4 a0 = *reinterpret_cast<const float4*>(head + part * 8);
-    const float4 a1 = *reinterpret_cast<const float4*>(head + part * 8 + 4);
-    const float4 b0 = *reinterpret_cast<const float4*>(head + (part ^ 4) * 8);
-    const float4 b1 = *reinterpret_cast<const float4*>(head + (part ^ 4) * 8 + 4);
+  // RoPE of pieces pq (dims 8pq..8pq+7) and pq + 4 (dims 32+8pq..) of head hq < 3, and of k_new
+  // (HF: bf16(bf16(x cos) + bf16(rotate_half(x) sin)))
+  const int hq = lane & 15, pq = lane >> 4;
+  float cs8[8], sn8[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    cs8[e] = sm.cs[pq * 8 + e];
+    sn8[e] = sm.cs[32 + pq * 8 + e];
+  }
+  auto rope_pair = [&](const float* head, uint32_t (&lo)[4], uint32_t (&hi)[4]) {
+    const float4 a0 = *reinterpret_cast<const float4*>(head + pq * 8);
+    const float4 a1 = *reinterpret_cast<const float4*>(head + pq * 8 + 4);
+    const float4 b0 = *reinterpret_cast<const float4*>(head + 32 + pq * 8);
+    const float4 b1 = *reinterpret_cast<const float4*>(head + 32 + pq * 8 + 4);
     const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
     const float y[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-    const int f0 = (part & 3) * 8;
-    float r[8];
+    float rl[8], rh[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) r[e] = rnd(rnd(x[e] * sm.cs[f0 + e]) + rnd((sgn * y[e]) * sm.cs[32 + f0 + e]));
-#pragma unroll
-    for (int e = 0; e < 4; ++e) out[e] = pack2(r[2 * e], r[2 * e + 1]);
-  };
-  uint32_t q[3][4], kn[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-  for (int h = 0; h < 3; ++h) rope8(in + h * 64, q[h]);
-  if (w == 0 && lane == 0) trace_at(p, l, 35, p.n_layers);
-  auto score = [&](int j, const uint4& k, bool keep) {
-    float s3[3];
-#pragma unroll
-    for (int h = 0; h < 3; ++h) {
-      float a = dot2(q[h][0], k.x, 0.f);
-      a = dot2(q[h][1], k.y, a);
-      a = dot2(q[h][2], k.z, a);
-      a = dot2(q[h][3], k.w, a);
-      s3[h] = group8_sum(a);
+    for (int e = 0; e < 8; ++e) {
+      rl[e] = rnd(rnd(x[e] * cs8[e]) + rnd((-y[e]) * sn8[e]));
+      rh[e] = rnd(rnd(y[e] * cs8[e]) + rnd(x[e] * sn8[e]));
     }
-    if (part == 0 && keep)
 #pragma unroll
-      for (int h = 0; h < 3; ++h) sm.at.sc[h][j] = rnd(s3[h]) * 0.125f;
+    for (int e = 0; e < 4; ++e) {
+      lo[e] = pack2(rl[2 * e], rl[2 * e + 1]);
+      hi[e] = pack2(rh[2 * e], rh[2 * e + 1]);
+    }
   };
-  const int jc = min(j1, T_old);
-  for (int jb = j0; jb < jc; jb += 8) {
-    const int j = jb + grp;
-    score(j, j < jc ? C.ring16(seg + uint32_t(j) * 256u + uint32_t((part + j) & 7) * 16u) : make_uint4(0u, 0u, 0u, 0u),
-          j < jc);
-  }
-  if (has_new) {
-    rope8(in + 192, kn);
-    score(T_old, make_uint4(kn[0], kn[1], kn[2], kn[3]), grp == 0);
+  uint32_t qlo[4] = {0u, 0u, 0u, 0u}, qhi[4] = {0u, 0u, 0u, 0u};
+  if (hq < 3) rope_pair(in + hq * 64, qlo, qhi);
+  uint32_t klo[4] = {0u, 0u, 0u, 0u}, khi[4] = {0u, 0u, 0u, 0u};
+  if (has_new) rope_pair(in + 192, klo, khi);
+  if (w == 0 && lane == 0) trace_at(p, l, 35, p.n_layers);
+  // Scores on the matrix cores, D[token][head] = K[token][:] . q[head][:] per 16-token tile
+  // (v_mfma_f32_16x16x32_bf16, two k-steps over the 64 dimensions).  Lane l supplies row l%16 of A
+  // (token tile + l%16: pieces pq and pq + 4 of its K from the ring, or k_new) and column l%16 of B
+  // (q of head l%16 < 3, zero for the padding columns) and receives D[4 pq + jj][hq].  Tokens past
+  // the chunk read other ring bytes; only their own rows of D, which are not stored, see them.
+  {
+    const bf16x8 bq0 = __builtin_bit_cast(bf16x8, make_uint4(qlo[0], qlo[1], qlo[2], qlo[3]));
+    const bf16x8 bq1 = __builtin_bit_cast(bf16x8, make_uint4(qhi[0], qhi[1], qhi[2], qhi[3]));
+    for (int tb = j0; tb < j1; tb += 16) {
+      const int tok = tb + hq;
+      uint4 a0 = C.ring16(seg + uint32_t(tok) * 256u + uint32_t((pq + tok) & 7) * 16u);
+      uint4 a1 = C.ring16(seg + uint32_t(tok) * 256u + uint32_t((pq + 4 + tok) & 7) * 16u);
+      if (has_new && tok == T_old) {
+        a0 = make_uint4(klo[0], klo[1], klo[2], klo[3]);
+        a1 = make_uint4(khi[0], khi[1], khi[2], khi[3]);
+      }
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a0), bq0, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1), bq1, acc, 0, 0, 0);
+      if (hq < 3)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int t = tb + 4 * pq + jj;
+          if (t < j1) sm.at.sc[hq][t] = rnd(acc[jj]) * 0.125f;
+        }
+    }
   }
   wait_lgkm0();
   if (w == 0 && lane == 0) trace_at(p, l, 36, p.n_layers);
-  // chunk softmax statistics per head, over this wave's tokens, then over the chunk
-  float sv[3][2];
+  // chunk softmax statistics per head, over this wave's tokens, then over the chunk.  ev keeps
+  // exp(s - m_wave) of the lane's tokens; once the head's global max M and sum L are known the
+  // probabilities are bf16(ev * exp(m_wave - M) / L), HF's bf16(exp(s - M) / L) up to fp32 rounding.
+  float ev[3][2], m3[3];
 #pragma unroll
   for (int h = 0; h < 3; ++h)
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int j = j0 + lane + 64 * i;
-      sv[h][i] = j < j1 ? sm.at.sc[h][j] : -INFINITY;
+      ev[h][i] = j < j1 ? sm.at.sc[h][j] : -INFINITY;
     }
   {
-    float m3[3], l3[3];
+    float l3[3];
 #pragma unroll
-    for (int h = 0; h < 3; ++h) m3[h] = fmaxf(sv[h][0], sv[h][1]);
-    wave_max_n<3>(m3);
+    for (int h = 0; h < 3; ++h) m3[h] = fmaxf(ev[h][0], ev[h][1]);
+    wave_rows<3, true>(m3);
 #pragma unroll
     for (int h = 0; h < 3; ++h) {
       l3[h] = 0.f;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) l3[h] += sv[h][i] == -INFINITY ? 0.f : expf(sv[h][i] - m3[h]);
+      for (int i = 0; i < 2; ++i) {
+        ev[h][i] = ev[h][i] == -INFINITY ? 0.f : expf(ev[h][i] - m3[h]);
+        l3[h] += ev[h][i];
+      }
     }
-    wave_sum_n<3>(l3);
+    wave_rows<3>(l3);
     if (lane == 0)
 #pragma unroll
       for (int h = 0; h < 3; ++h) { sm.wml[w][0][h] = m3[h]; sm.wml[w][1][h] = l3[h]; }
@@ -707,11 +774,11 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg) {
   // probabilities with the global max and sum, rounded to bf16 before P.V as HF does
 #pragma unroll
   for (int h = 0; h < 3; ++h) {
-    const float inv = 1.0f / Lh[h];
+    const float scale = m3[h] == -INFINITY ? 0.f : expf(m3[h] - Mh[h]) * (1.0f / Lh[h]);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int j = j0 + lane + 64 * i;
-      if (j < j1) sm.at.pb[h][j] = uint16_t(f2bf(expf(sv[h][i] - Mh[h]) * inv));
+      if (j < j1) sm.at.pb[h][j] = uint16_t(f2bf(ev[h][i] * scale));
     }
   }
   wait_lgkm0();
@@ -762,28 +829,32 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg) {
     acc[h][1] += __shfl_xor(acc[h][1], 32);
   }
   C.release(C.pos_kv_end);
-  if (has_new && P.slot >= 0 && grp < 2) {
-    // KV append at slot_mapping[0] (block360_kernel.inc:124-135; slot < 0 skips): lanes 0-7 store
-    // the rotated new K, lanes 8-15 the new V, 8 dims (16 bytes) per lane
+  if (has_new && P.slot >= 0 && hq < 2) {
+    // KV append at slot_mapping[0] (block360_kernel.inc:124-135; slot < 0 skips): lane 16 q (k) and
+    // lane 16 q + 1 (v) store pieces q and q + 4 of the new token, 16 bytes each
     uint16_t* cache = reinterpret_cast<uint16_t*>(const_cast<void*>(sm.kvp[l]));
     const long long e = (P.slot / 16) * p.block_stride + (P.slot % 16) * p.token_stride +
-                        (long long)g * p.head_stride + (grp ? p.v_off : p.k_off) + part * 8;
-    uint32_t val[4];
-    if (grp == 0) {
+                        (long long)g * p.head_stride + (hq ? p.v_off : p.k_off);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) val[i] = kn[i];
-    } else {
+    for (int hv = 0; hv < 2; ++hv) {
+      const int piece = pq + 4 * hv;
+      uint32_t val[4];
+      if (hq == 0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) val[i] = pack2(in[256 + part * 8 + 2 * i], in[256 + part * 8 + 2 * i + 1]);
-    }
-    uint16_t* dst = cache + e;
-    if ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
-      st_global16(dst, val[0], val[1], val[2], val[3]);
-    } else {
+        for (int i = 0; i < 4; ++i) val[i] = hv ? khi[i] : klo[i];
+      } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        st_global2(dst + 2 * i, uint16_t(val[i] & 0xffffu));
-        st_global2(dst + 2 * i + 1, uint16_t(val[i] >> 16));
+        for (int i = 0; i < 4; ++i) val[i] = pack2(in[256 + piece * 8 + 2 * i], in[256 + piece * 8 + 2 * i + 1]);
+      }
+      uint16_t* dst = cache + e + piece * 8;
+      if ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+        st_global16(dst, val[0], val[1], val[2], val[3]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          st_global2(dst + 2 * i, uint16_t(val[i] & 0xffffu));
+          st_global2(dst + 2 * i + 1, uint16_t(val[i] >> 16));
+        }
       }
     }
   }
@@ -803,7 +874,7 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg) {
   }
   if (!P.leader) {
     if (w < 3) {
-      // 22 units of 3 floats; lane 3u + s holds float s of unit u: lane 3u writes the unit
+      // PU units of 3 floats per head; lane 3u writes unit u (floats 3u .. 3u+2)
       const float f1 = __shfl_down(O, 1), f2 = __shfl_down(O, 2);
       if (lane % 3 == 0)
         C.put_loc(l, W::PART_U + (size_t(P.rank) * 3 + w) * S::PU + lane / 3,
@@ -829,7 +900,7 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg) {
 #pragma unroll
     for (int k = 0; k < S::C - 1; ++k) tot += part_sum[k];
     tot += O;
-    sm.ao[w][lane] = rnd(tot);
+    sm.at.ao[w][lane] = rnd(tot);
   }
   C.cbar();
   if (w == 0 && lane < 32) {
@@ -838,7 +909,7 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg) {
 #pragma unroll
     for (int e = 0; e < VPU; ++e) {
       const int i = lane * VPU + e;
-      v[e] = sm.ao[i >> 6][i & 63];
+      v[e] = sm.at.ao[i >> 6][i & 63];
     }
     C.put_loc(l, W::ATTN_U + size_t(32 * g + lane), C.unit6(v));
   }
@@ -865,7 +936,7 @@ __device__ __forceinline__ void lm_head_sr(CSR<G>& C) {
   C.release(C.pos);
   C.refresh();
   const float ss = C.template poll_vec<1>(K_X, L, G::H, sm.xs, nullptr, 33);
-  const float rs = rms_scale(C.block_total(ss), G::H);
+  const float rs = rms_rsq<G::H>(C.block_total(ss));
   C.bracket_done(uint32_t(L + 1));
   XChunks<G::H, 8> x;
   load_x<G::H, 8, true>(x, sm.xs, nw, rs, C.lane);
@@ -883,39 +954,13 @@ __device__ __forceinline__ void lm_head_sr(CSR<G>& C) {
     const int r0 = P.v0 + j * LM_ROWS_SR;
     const int nrows = min(LM_ROWS_SR, P.v1 - r0);
     C.wait_filled(C.pos);
-    constexpr int RW = LM_ROWS_SR / NCW;  // rows cw, cw + 4, ... of the segment
+    constexpr int RW = LM_ROWS_SR / NCW;  // rows cw RW .. cw RW + RW - 1 of the segment
     float out[RW];
-#pragma unroll
-    for (int r = 0; r < RW; ++r) out[r] = 0.f;
-    {
-      constexpr int CPL = Chunks<G::H>::CPL, CH = Chunks<G::H>::CH;
-      uint4 wr[RW][CPL];
-#pragma unroll
-      for (int r = 0; r < RW; ++r)
-#pragma unroll
-        for (int c = 0; c < CPL; ++c)
-          wr[r][c] = C.ring16(seg + uint32_t(C.cw + NCW * r) * uint32_t(G::H * 2) + uint32_t(C.lane + 64 * c) * 16u);
-      if (CH % 64 != 0 && C.lane + 64 * (CPL - 1) >= CH)
-#pragma unroll
-        for (int r = 0; r < RW; ++r) wr[r][CPL - 1] = make_uint4(0, 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < RW; ++r) {
-        float acc = 0.f;
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-          acc = dot2(wr[r][c].x, x[c][0].x, acc);
-          acc = dot2(wr[r][c].y, x[c][0].y, acc);
-          acc = dot2(wr[r][c].z, x[c][0].z, acc);
-          acc = dot2(wr[r][c].w, x[c][0].w, acc);
-        }
-        out[r] = acc;
-      }
-      wave_sum_n<RW>(out);
-    }
+    dots_n<G::H, RW>(C, seg, C.cw * RW, x, out);
     C.release(C.pos);
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
-      const int row = C.cw + NCW * r;
+      const int row = C.cw * RW + r;
       if (row < nrows) {
         const float v = rnd(out[r]);
         const int idx = r0 + row;
@@ -966,29 +1011,37 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
       normw<G::H>(C, nw, segn);
       tr(l, 9);
       const float ss = C.template poll_vec<1>(K_H1, l, G::H, sm.xs, sm.keep, 40);
-      const float rs = rms_scale(C.block_total(ss), G::H);
+      const float rs = rms_rsq<G::H>(C.block_total(ss));
       tr(l, 10);
       {
         XChunks<G::H, 8> x;
         load_x<G::H, 8, true>(x, sm.xs, nw, rs, C.lane);
         tr(l, 21);
+        // gate rows of units 0 .. n-1, then up rows of the same units: one 6-row item per wave
         const int nunits = P.au1 - P.au0;
-        for (int j = C.cw; j < nunits; j += NCW) {
-          float og[VPU], ou[VPU];
-          dots_n<G::H, VPU>(C, segg, j * VPU, x, og);
-          tr(l, 22);
-          dots_n<G::H, VPU>(C, segu, j * VPU, x, ou);
-          tr(l, 23);
+        if (C.cw < 2 * nunits) {
+          const int j = C.cw % nunits;
+          float o[VPU];
+          dots_n<G::H, VPU>(C, C.cw < nunits ? segg : segu, j * VPU, x, o);
+          if (C.lane == 0)
+#pragma unroll
+            for (int e = 0; e < VPU; ++e) sm.part[C.cw][e] = o[e];
+        }
+        tr(l, 22);
+        C.cbar();
+        tr(l, 23);
+        if (C.cw < nunits) {
+          // lane e < 6 forms value e of unit cw, silu(bf16(gate)) * bf16(up); lane 0 stores the unit
+          const int e = min(C.lane, VPU - 1);
+          const float gv = rnd(sm.part[C.cw][e]), uv = rnd(sm.part[nunits + C.cw][e]);
+          const float act = rnd(gv / (1.0f + expf(-gv))) * uv;
           float a[VPU];
 #pragma unroll
-          for (int e = 0; e < VPU; ++e) {
-            const float gv = rnd(og[e]), uv = rnd(ou[e]);
-            const float silu = rnd(gv / (1.0f + expf(-gv)));
-            a[e] = silu * uv;
-          }
-          if (C.lane == 0) C.put_x(K_ACT, l, P.au0 + j, C.unit6(a));
-          tr(l, 24);
+          for (int k = 0; k < VPU; ++k)
+            a[k] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, act), k));
+          if (C.lane == 0) C.put_x(K_ACT, l, P.au0 + C.cw, C.unit6(a));
         }
+        tr(l, 24);
       }
       C.release(C.pos);
       tr(l, 11);
@@ -996,29 +1049,47 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
       C.refresh();
       const uint32_t segd = C.next_seg(sr_bytes(P, R_DOWN, 0));
       C.wait_filled(C.pos);
-      C.template poll_vec<2>(K_ACT, l, G::I, sm.xs, nullptr, 41);
+      const bool has_down = P.xu1 > P.xu0;  // workgroups without down rows do not need act
+      if (has_down) C.template poll_vec<2>(K_ACT, l, G::I, sm.xs, nullptr, 41);
       C.cbar();
       tr(l, 13);
-      if (P.xu1 > P.xu0 && C.cw == 0) {
-        XChunks<G::I, 8> x;
-        const XChunks<G::I, 8> none = {};
-        load_x<G::I, 8, false>(x, sm.xs, none, 1.f, C.lane);
+      if (has_down) {
+        // each wave: its quarter of K for the unit's 6 rows; the quarters are added in wave order
+        using Q = Quarter<G::I>;
+        uint4 xq[Q::CPL];
+#pragma unroll
+        for (int c = 0; c < Q::CPL; ++c) {
+          const int cq = C.lane + 64 * c;
+          const float* src = sm.xs + (C.cw * Q::CHW + min(cq, Q::CHW - 1)) * 8;
+          const float4 a = *reinterpret_cast<const float4*>(src);
+          const float4 b = *reinterpret_cast<const float4*>(src + 4);
+          const bool ok = cq < Q::CHW;
+          xq[c] = make_uint4(ok ? pack2(a.x, a.y) : 0u, ok ? pack2(a.z, a.w) : 0u, ok ? pack2(b.x, b.y) : 0u,
+                             ok ? pack2(b.z, b.w) : 0u);
+        }
         tr(l, 28);
         float od[VPU];
-        dots_split<G::I, VPU>(C, segd, 0, x, od);
+        dots_quarter<G::I, VPU>(C, segd, 0, xq, od);
+        if (C.lane == 0)
+#pragma unroll
+          for (int e = 0; e < VPU; ++e) sm.part[C.cw][e] = od[e];
+        C.cbar();
         tr(l, 29);
-        float y[VPU];
+        if (C.cw == 0) {
+          float y[VPU];
 #pragma unroll
-        for (int e = 0; e < VPU; ++e) {
-          const int r = min(P.d0 + e, G::H - 1);
-          y[e] = rnd(sm.keep[r] + rnd(od[e]));
-        }
-        if (C.lane == 0) C.put_x(K_X, l + 1, P.xu0, C.unit6(y));
-        if (p.layer_outputs && C.lane < VPU && P.d0 + C.lane < G::H) {
-          float yl = y[0];
+          for (int e = 0; e < VPU; ++e) {
+            const float d = ((sm.part[0][e] + sm.part[1][e]) + sm.part[2][e]) + sm.part[3][e];
+            const int r = min(P.d0 + e, G::H - 1);
+            y[e] = rnd(sm.keep[r] + rnd(d));
+          }
+          if (C.lane == 0) C.put_x(K_X, l + 1, P.xu0, C.unit6(y));
+          if (p.layer_outputs && C.lane < VPU && P.d0 + C.lane < G::H) {
+            float yl = y[0];
 #pragma unroll
-          for (int e = 1; e < VPU; ++e) yl = C.lane == e ? y[e] : yl;
-          p.layer_outputs[size_t(l) * G::H + P.d0 + C.lane] = uint16_t(f2bf(yl));
+            for (int e = 1; e < VPU; ++e) yl = C.lane == e ? y[e] : yl;
+            p.layer_outputs[size_t(l) * G::H + P.d0 + C.lane] = uint16_t(f2bf(yl));
+          }
         }
       }
       C.release(C.pos);
@@ -1050,7 +1121,7 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
     } else {
       ss = C.template poll_vec<1>(K_X, l, G::H, sm.xs, nullptr, 42);
     }
-    const float rs = rms_scale(C.block_total(ss), G::H);
+    const float rs = rms_rsq<G::H>(C.block_total(ss));
     tr(l, 1);
     {
       XChunks<G::H, 8> x;
@@ -1145,20 +1216,31 @@ __device__ __forceinline__ void consumer_a(CSR<G>& C) {
       const XChunks<G::H, 8> none = {};
       load_x<G::H, 8, false>(x, sm.xs, none, 1.f, C.lane);
       tr(l, 31);
-      const int nunits = P.ou1 - P.ou0;
-      for (int j = C.cw; j < nunits; j += NCW) {
-        float o[VPU];
-        dots_n<G::H, VPU>(C, sego, j * VPU, x, o);
-        tr(l, 32);
-        float h[VPU];
+      // the workgroup's O rows, RW consecutive rows per wave; then wave 0: h1 = bf16(x + bf16(o))
+      // per row and one unit per lane
+      constexpr int RW = (S::OU * VPU + NCW - 1) / NCW;
+      static_assert(RW <= 8, "sm.part holds 8 values per wave");
+      float o[RW];
+      dots_n<G::H, RW>(C, sego, C.cw * RW, x, o);
+      if (C.lane == 0)
 #pragma unroll
-        for (int e = 0; e < VPU; ++e) {
-          const int r = min((P.ou0 + j) * VPU + e, G::H - 1);
-          h[e] = rnd(sm.keep[r] + rnd(o[e]));
+        for (int r = 0; r < RW; ++r) sm.part[C.cw][r] = o[r];
+      tr(l, 32);
+      C.cbar();  // also: every wave has read xs
+      const int nrows = P.o1 - P.o0;
+      if (C.cw == 0 && nrows > 0) {
+        const int r = min(C.lane, nrows - 1);
+        const float h = rnd(sm.keep[P.o0 + r] + rnd(sm.part[r / RW][r % RW]));
+        if (C.lane < nrows) sm.xs[C.lane] = h;
+        wait_lgkm0();
+        if (C.lane < P.ou1 - P.ou0) {
+          float v[VPU];
+#pragma unroll
+          for (int e = 0; e < VPU; ++e) v[e] = sm.xs[C.lane * VPU + e];
+          C.put_x(K_H1, l, P.ou0 + C.lane, C.unit6(v));
         }
-        if (C.lane == 0) C.put_x(K_H1, l, P.ou0 + j, C.unit6(h));
-        tr(l, 33);
       }
+      tr(l, 33);
     }
     C.release(C.pos);
     tr(l, 8);
@@ -1237,6 +1319,7 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_sr(Params p, uint32_t* r
   if (threadIdx.x == 0) {
     for (int w = 0; w < NPW; ++w) sm.front[w] = 0;
     for (int w = 0; w < NCW; ++w) sm.consumed[w] = 0;
+    for (int i = 0; i < 4; ++i) sm.zero16[i] = 0u;
     sm.cbar = 0;
     sm.go = 0;
     sm.loc_l2 = 0;

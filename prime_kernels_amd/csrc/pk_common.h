@@ -159,6 +159,10 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   const bf16x2 v = {(__bf16)a, (__bf16)b};
   return __builtin_bit_cast(uint32_t, v);
 }
+// Operand and accumulator types of v_mfma_f32_16x16x32_bf16.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
 // acc + a.lo*b.lo + a.hi*b.hi over packed bf16 pairs (v_dot2_f32_bf16).
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), acc, false);
@@ -192,6 +196,67 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<0x143, 0xc>(v, v));
   return lane63(v);
 }
+// Lane swaps of gfx950: swap32 exchanges lanes 32-63 of `a` with lanes 0-31 of `b`; swap16 exchanges
+// the odd 16-lane rows of `a` with the even rows of `b` (v_permlane32_swap_b32 / v_permlane16_swap_b32).
+__device__ __forceinline__ void swap32(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                                  false, false);
+  // through plain integers: __builtin_bit_cast of r[1] itself reads element 0 with this compiler
+  const uint32_t r0 = r[0], r1 = r[1];
+  a = __uint_as_float(r0);
+  b = __uint_as_float(r1);
+}
+__device__ __forceinline__ void swap16(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                                  false, false);
+  // through plain integers: __builtin_bit_cast of r[1] itself reads element 0 with this compiler
+  const uint32_t r0 = r[0], r1 = r[1];
+  a = __uint_as_float(r0);
+  b = __uint_as_float(r1);
+}
+// Totals of N per-lane values over the wave (N <= 8), returned uniform, in about 2.5 N + 8 VALU
+// instructions: a transposed butterfly.  The cross-half swap leaves value 2i's partial sums in lanes
+// 0-31 and value 2i+1's in lanes 32-63 of one register; the cross-row swap then leaves one value per
+// 16-lane row (rows 0-3 holding values 4j, 4j+2, 4j+1, 4j+3); four full-row DPP steps finish each row.
+template <bool MAX>
+__device__ __forceinline__ float comb(float a, float b) { return MAX ? fmaxf(a, b) : a + b; }
+template <int N, bool MAX = false>
+__device__ __forceinline__ void wave_rows(float (&v)[N]) {
+  static_assert(N >= 1 && N <= 8, "up to 8 values");
+  constexpr int P = (N + 1) / 2, Q = (P + 1) / 2;
+  float a[P], b[Q];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    float x = v[2 * i], y = 2 * i + 1 < N ? v[2 * i + 1] : v[2 * i];
+    swap32(x, y);
+    a[i] = comb<MAX>(x, y);
+  }
+#pragma unroll
+  for (int j = 0; j < Q; ++j) {
+    float x = a[2 * j], y = 2 * j + 1 < P ? a[2 * j + 1] : a[2 * j];
+    swap16(x, y);
+    b[j] = comb<MAX>(x, y);
+  }
+#pragma unroll
+  for (int j = 0; j < Q; ++j) b[j] = comb<MAX>(b[j], dpp<0x128>(0.f, b[j]));  // row_ror:8
+#pragma unroll
+  for (int j = 0; j < Q; ++j) b[j] = comb<MAX>(b[j], dpp<0x124>(0.f, b[j]));  // row_ror:4
+#pragma unroll
+  for (int j = 0; j < Q; ++j) b[j] = comb<MAX>(b[j], dpp<0x4e>(0.f, b[j]));   // quad_perm [2,3,0,1]
+#pragma unroll
+  for (int j = 0; j < Q; ++j) b[j] = comb<MAX>(b[j], dpp<0xb1>(0.f, b[j]));   // quad_perm [1,0,3,2]
+  auto lane_of = [](float f, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), l));
+  };
+#pragma unroll
+  for (int j = 0; j < Q; ++j) {
+    v[4 * j] = lane_of(b[j], 0);
+    if (4 * j + 1 < N) v[4 * j + 1] = lane_of(b[j], 32);
+    if (4 * j + 2 < N) v[4 * j + 2] = lane_of(b[j], 16);
+    if (4 * j + 3 < N) v[4 * j + 3] = lane_of(b[j], 48);
+  }
+}
+
 // wave_max / wave_sum of N values at once: the same steps per value, the N chains interleaved so
 // that each DPP step's wait states are filled by the other chains instead of s_nop.
 template <int N>

@@ -130,12 +130,21 @@ def test_two_sequences_against_oracle_layer(contexts):
 
 
 def test_block_equals_one_layer_decode_path():
-    """block360_decode == the 1-layer decode step with the same vector in an embedding row."""
+    """block360_decode == the 1-layer decode step of the general kernel (the same arithmetic, so the
+    same bits) with the same vector in an embedding row.  The split-role kernel, which takes this
+    context by default, sums in another order; its parity is checked against the oracle."""
     _need_gpu()
+    from prime_kernels_amd import _native
+
     geom = O.with_layers(O.SMOLLM2_360M, 1)
     case = GC.random_kv_case(geom, 41, [300])
     x = case.w.embed[123].view(1, 960)
-    ref = case.kernel_step([123], [299], layer_outputs=True)
+    lib = _native.library()
+    old = lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, 0)
+    try:
+        ref = case.kernel_step([123], [299], layer_outputs=True)
+    finally:
+        lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, old)
     case.kv.caches[0].copy_(case.kvd[0].cpu())       # the decode step appended; undo is not needed: same values
     out, _, _ = _block(x, [299], [300], case.kv, case.w.layers[0], case.cos_sin)
     assert torch.equal(out[0].view(torch.int16), ref["layer_outputs"][0, 0].view(torch.int16))

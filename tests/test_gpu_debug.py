@@ -13,7 +13,9 @@ import torch
 from oracle import smollm2 as O
 from tests import gpu_cases as GC
 
-pytestmark = pytest.mark.gpu
+# batch-1 steps run on the general kernel, the only one with this path, so that the plain steps
+# compared with it bit for bit use the same arithmetic
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("general_kernel")]
 
 H, QKV, I, NH, SEQ, L = 960, 1600, 2560, 15, 8192, 32
 STAGE_SIZES = [("norm1", H), ("qkv", QKV), ("attn", H), ("o", H), ("h1", H), ("norm2", H), ("gate", I),

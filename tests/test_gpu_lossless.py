@@ -11,23 +11,11 @@ from oracle import lossless as LZ
 from oracle import smollm2 as O
 from tests import gpu_cases as GC
 
-pytestmark = pytest.mark.gpu
+# batch-1 steps run on the general kernel, the only one with this path, so that the plain steps
+# compared with it bit for bit use the same arithmetic
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("general_kernel")]
 
 ROWS, COLS = 5120, 960
-
-
-@pytest.fixture(autouse=True)
-def _general_kernel_for_dense_steps():
-    """The lossless gate/up stream is read by the general batch-1 kernel; the dense steps these tests
-    compare it with run on the same kernel (split-role steps sum in another order)."""
-    if not torch.cuda.is_available():
-        yield
-        return
-    from prime_kernels_amd import _native
-    lib = _native.library()
-    old = lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, 0)
-    yield
-    lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, old)
 
 
 def _need_gpu():
