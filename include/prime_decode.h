@@ -44,6 +44,10 @@ extern "C" {
 /* Options for pk_set_option. */
 #define PK_OPT_COOPERATIVE 1     /* 1: launch with hipLaunchCooperativeKernel (default 0, or PK_LAUNCH=cooperative) */
 #define PK_OPT_SPLIT_ROLE 2      /* 0: batch-1 steps stay on the general kernel (default 1, or PK_SPLIT_ROLE=0) */
+#define PK_OPT_L2_RECORDS 3      /* 0: batch-1 attention records stay in uncached memory even when a KV head's
+                                    chunks share an XCD (the path a placement mismatch takes; default 1) */
+#define PK_OPT_SKEW 4            /* != 0: arrival-skew test, the seed of pseudo-random delays every workgroup
+                                    takes before publishing exchange data (results must not change; default 0) */
 
 /* Models. */
 #define PK_MODEL_SMOLLM2_360M 360

@@ -223,8 +223,13 @@ def decode_step(model: Model, *, input_ids, positions, seq_lens, block_table, sl
         raise ValueError(f"block_table context capacity must be 1..{model.max_seq}")
     _check_tensor(embed, "embed", dtype=torch.bfloat16, device=device)
     _check_tensor(final_norm, "final_norm", dtype=torch.bfloat16, device=device, shape=(model.hidden,))
-    if embed.ndim != 2 or embed.shape != (VOCAB, model.hidden) or not embed.is_contiguous():
-        raise ValueError(f"embed must be contiguous BF16 [{VOCAB}, {model.hidden}]")
+    # the reference checks the hidden width only (decode_megakernel_360m/__init__.py:151-152); the
+    # tied LM head also needs the full vocabulary.  Input ids index embedding rows unchecked, as there.
+    lm_head = return_token_ids or logits_out is not None
+    if embed.ndim != 2 or embed.shape[1] != model.hidden or not embed.is_contiguous():
+        raise ValueError(f"embed must be contiguous BF16 [vocab, {model.hidden}]")
+    if lm_head and embed.shape[0] != VOCAB:
+        raise ValueError(f"the tied LM head needs embed of shape [{VOCAB}, {model.hidden}]")
     spec = model.layer_spec()
     for i, layer in enumerate(layers):
         if len(layer) != len(spec):
@@ -274,7 +279,7 @@ def decode_step(model: Model, *, input_ids, positions, seq_lens, block_table, sl
             raise ValueError("the lossless gate/up cache is for SmolLM2-360M bf16 weights")
         if encoded_gu.device != device:
             raise ValueError(f"encoded_gu must be on {device}")
-        if tuple(t.data_ptr() for t in encoded_gu._weights[:nl]) != tuple(layer[4].data_ptr() for layer in layers):
+        if tuple(t.data_ptr() for t in encoded_gu.weights[:nl]) != tuple(layer[4].data_ptr() for layer in layers):
             raise ValueError("encoded_gu was prepared for other gate_up tensors")
 
     rt = runtime(model, device)

@@ -20,6 +20,8 @@ PK_ERR_NOALLOC = 9115
 # pk_set_option options
 PK_OPT_COOPERATIVE = 1
 PK_OPT_SPLIT_ROLE = 2
+PK_OPT_L2_RECORDS = 3
+PK_OPT_SKEW = 4
 
 _lib = None
 

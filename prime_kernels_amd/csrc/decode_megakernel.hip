@@ -101,7 +101,10 @@ struct WS {
   static constexpr size_t STAT0 = REC0 + REC_LAYER * G::L;
   static constexpr size_t STAT_LAYER = size_t(NWG) * STAT_WORDS * 2;
   static constexpr size_t LM0 = STAT0 + STAT_LAYER * G::L;
-  static constexpr size_t TOTAL = LM0 + size_t(MAX_B) * NWG * 2;
+  // per-workgroup {XCC id, tag32} words: where the batch-1 attention workgroups really run
+  static constexpr size_t XCC0 = LM0 + size_t(MAX_B) * NWG * 2;
+  static constexpr size_t TOTAL = XCC0 + size_t(NWG) * 2;
+  __device__ static size_t xcc(int wg) { return XCC0 + size_t(wg) * 2; }
   // 32-bit word offset of the 64-bit word {bf16 value, tag32} of element i of vector (kind, layer l, sequence b)
   __device__ static size_t xw(int kind, int l, int b, int i) {
     return X0 + (((size_t(b) * XLINES + size_t(i >> 3)) * XSLOTS + size_t(l) * NKIND + kind) * 8 + size_t(i & 7)) * 2;
@@ -130,7 +133,7 @@ struct Plan {
   int n_lm;     // LM segments
   // attention (batch 1)
   int att;      // 1: this workgroup owns an attention chunk
-  int natt;     // workgroups with a chunk (0 .. natt-1)
+  int natt;     // workgroups with a chunk (which ones: `att`, never an index range)
   int g, c, C, t0, t1;   // kv head, chunk, chunks, cached token range [t0, t1)
   int S, pos;   // tokens attended (incl. new) and the new token's position
   long long slot;  // KV slot of the new token (slot_mapping[0]; < 0: no append)
@@ -151,8 +154,9 @@ struct Plan {
     natt = G::KVH * C;
     // Workgroups are dispatched to the 8 XCDs round-robin (workgroup i on XCC (i + s) mod 8, where
     // the start s carries over from earlier dispatches), so with chunk c of head g on workgroup
-    // g + 8c every chunk of a head shares an XCD and its L2.  Were that ever not so, the record
-    // polls would run into their bound and the launch would end with its abort word set.
+    // g + 8c every chunk of a head shares an XCD and its L2.  Each attention workgroup checks this
+    // at run time (its hardware XCC id against those of the head's other chunks, before the first
+    // record) and keeps the records in the uncached workspace when it does not hold.
     xcd = p.xws != nullptr && C <= NWG / 8 && G::KVH <= 8;
     att = xcd ? ((wg % 8) < G::KVH && (wg / 8) < C) : wg < natt;
     int below = 0;  // attention workgroups with a lower index
@@ -426,6 +430,7 @@ struct Consumer {
   uint32_t tag32;
   bool dead = false;
   int xr;                    // the copy of the batch-1 exchange vectors this workgroup polls
+  bool l2rec = false;        // the head's chunks share this XCC: records go through its L2
 
   __device__ __forceinline__ Consumer(const Params& p_, const PL& P_, SM& sm_, uint32_t ep)
       : p(p_), P(P_), sm(sm_) {
@@ -442,6 +447,7 @@ struct Consumer {
 
   // Batch-1 exchange word: element i of vector (kind, layer l), written to every copy.
   __device__ __forceinline__ void st_x(int kind, int l, int i, uint64_t v) const {
+    skew_delay(p.skew, P.wg, l, kind);
 #pragma unroll
     for (int r = 0; r < XREP; ++r) st_dev64(reinterpret_cast<uint64_t*>(p.ws + WS<G>::xw(kind, l, r, i)), v);
   }
@@ -1006,13 +1012,32 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   }
   const uint64_t tg = uint64_t(C.tag32) << 32;
   if (P.C > 1) {
+    if (l == 0 && P.xcd) {
+      // do the head's chunks (workgroups g + 8c) really share this XCC?  Every chunk reads the same
+      // C ids, so writers and readers of the records agree on where they are.
+      const uint32_t mine = __builtin_amdgcn_s_getreg((15 << 11) | (0 << 6) | 20) & 15u;
+      uint32_t differ = 0;
+      for (int c = lane; c < P.C; c += 64) {
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(p.ws + W::xcc(g + 8 * c));
+        Spin spin(p.ws, C.tag32, 13);
+        uint64_t v = ld_dev64(src);
+        while (uint32_t(v >> 32) != C.tag32) {
+          if (C.dead || !spin.again()) { C.dead = true; break; }
+          v = ld_dev64(src);
+        }
+        differ |= (uint32_t(v) & 15u) != mine ? 1u : 0u;
+      }
+      C.l2rec = p.l2_records && __builtin_amdgcn_ballot_w64(differ != 0u) == 0ull;
+    }
     // same-XCD records: plain stores reach the shared L2, the (sc1) polls read it there
-    uint64_t* stat_base = reinterpret_cast<uint64_t*>(P.xcd ? p.xws + (W::stat(l, size_t(g) * P.C) - W::REC0)
-                                                            : p.ws + W::stat(l, size_t(g) * P.C));
+    const bool l2 = P.xcd && C.l2rec;
+    uint64_t* stat_base = reinterpret_cast<uint64_t*>(l2 ? p.xws + (W::stat(l, size_t(g) * P.C) - W::REC0)
+                                                         : p.ws + W::stat(l, size_t(g) * P.C));
+    skew_delay(p.skew, P.wg, l, 11);
     if (w == 0 && lane < 6) {
       const int h = lane >> 1;
       const float v = (lane & 1) ? (h == 0 ? Lh[0] : h == 1 ? Lh[1] : Lh[2]) : (h == 0 ? Mh[0] : h == 1 ? Mh[1] : Mh[2]);
-      if (P.xcd) st_l2(stat_base + size_t(P.c) * STAT_WORDS + lane, tg | __float_as_uint(v));
+      if (l2) st_l2(stat_base + size_t(P.c) * STAT_WORDS + lane, tg | __float_as_uint(v));
       else st_dev64(stat_base + size_t(P.c) * STAT_WORDS + lane, tg | __float_as_uint(v));
     }
     // lane k polls chunk k (and k + 64): 3 x 16 bytes = (m, l) of the 3 heads
@@ -1164,10 +1189,12 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
 #pragma unroll
   for (int v = 0; v < NCW; ++v) O += sm.wo[v][hh][d];
   if (w == 0 && lane == 0) trace_at(p, l, 4, p.n_layers);
-  uint64_t* rec_base = reinterpret_cast<uint64_t*>(P.xcd ? p.xws + (W::rec(l, 0) - W::REC0) : p.ws + W::rec(l, 0));
+  const bool l2 = P.xcd && C.l2rec;
+  uint64_t* rec_base = reinterpret_cast<uint64_t*>(l2 ? p.xws + (W::rec(l, 0) - W::REC0) : p.ws + W::rec(l, 0));
   if (!P.leader) {
+    skew_delay(p.skew, P.wg, l, 12);
     uint64_t* dst = rec_base + size_t(g * P.C + P.c) * REC_WORDS + hh * 64 + d;
-    if (P.xcd) st_l2(dst, tg | __float_as_uint(O));
+    if (l2) st_l2(dst, tg | __float_as_uint(O));
     else st_dev64(dst, tg | __float_as_uint(O));
     return;
   }
@@ -1236,6 +1263,9 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
     }
   };
   if (C.ct == 0) trace_tail(p, 0);
+  if (P.att && P.xcd && P.C > 1 && C.ct == 0)  // where this chunk runs (HW_REG_XCC_ID)
+    st_dev64(reinterpret_cast<uint64_t*>(p.ws + W::xcc(P.wg)),
+             (uint64_t(C.tag32) << 32) | (__builtin_amdgcn_s_getreg((15 << 11) | (0 << 6) | 20) & 15u));
 
   for (int l = 0; l < p.n_layers; ++l) {
     // ---------------- P1: RMSNorm(x) + QKV ----------------
@@ -1478,6 +1508,7 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
       if (sm.lm_val[w] > bv || (sm.lm_val[w] == bv && sm.lm_idx[w] < bi)) { bv = sm.lm_val[w]; bi = sm.lm_idx[w]; }
     const uint32_t idx = C.dead ? LM_DEAD : p.lm_head ? uint32_t(bi) & 0xffffu : LM_NONE;
     const uint64_t rec = (uint64_t(C.tag32) << 32) | (uint64_t(idx) << 16) | f2bf(bv);
+    skew_delay(p.skew, P.wg, p.n_layers, 13);
     st_dev64(reinterpret_cast<uint64_t*>(p.ws + W::lm(b, P.wg)), rec);
   }
   if (P.wg != 0) {
@@ -1903,6 +1934,7 @@ template <class G>
 __device__ __forceinline__ void publish_flag(ConsumerB<G>& C, int kind, int l) {
   wait_vmcnt<0>();
   C.cbar();
+  skew_delay(C.p.skew, C.P.wg, l, kind);
   if (C.ct < WSB<G>::FREP) st_dev(C.p.ws + WSB<G>::flag(kind, l, C.P.wg, C.ct), C.tag32);
 }
 
@@ -2258,6 +2290,7 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
     ex += dpp<0xb1>(0.f, ex);
     ex += dpp<0x4e>(0.f, ex);
     if (lane < 12 && (lane & 3) == 0) { sm.at.cst[k][0][lane >> 2] = mx; sm.at.cst[k][1][lane >> 2] = ex; }
+    skew_delay(p.skew, P.wg, l, 14);
     if (it.C > 1 && lane < 12 && (lane & 3) == 0) {
       uint64_t* st = reinterpret_cast<uint64_t*>(p.ws + WSB<G>::stat(P.wg + k * NWG));
       st_dev64(st + 2 * (lane >> 2), tg | __float_as_uint(mx));
@@ -2398,6 +2431,7 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
       float O = 0.f;
 #pragma unroll
       for (int v = 0; v < NCW; ++v) O += wo[v][w][lane];
+      skew_delay(p.skew, P.wg, l, 15);
       if (leader) sm.at.own[k][w * 64 + lane] = O;
       else st_dev64(reinterpret_cast<uint64_t*>(p.ws + WSB<G>::rec(P.wg + k * NWG)) + w * 64 + lane, tg | __float_as_uint(O));
     }
@@ -2498,6 +2532,7 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
       if (DBG && p.debug) dbg_xs(dl(l) + Dbg<G>::NORM1);
       const floatx4 acc = mfma_tile<G, G::H>(C, segq, sm.tile);
       C.release(C.pos);
+      skew_delay(p.skew, P.wg, l, 16);
       if (C.cw == 0 && tok < B)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -2655,6 +2690,7 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
       }
     const uint32_t idx = C.dead ? LM_DEAD : p.lm_head ? uint32_t(bi) & 0xffffu : LM_NONE;
     const uint64_t rec = (uint64_t(C.tag32) << 32) | (uint64_t(idx) << 16) | f2bf(bv);
+    skew_delay(p.skew, P.wg, p.n_layers, 13);
     st_dev64(reinterpret_cast<uint64_t*>(p.ws + W::lm(C.ct, P.wg)), rec);
   }
   if (P.wg != 0) {
@@ -2855,6 +2891,8 @@ struct LaunchCache {
 struct Options {
   int cooperative = -1;
   int split_role = -1;
+  int l2_records = 1;
+  uint32_t skew = 0;
 };
 static Options g_opt;
 static int opt_cooperative() {
@@ -3106,6 +3144,8 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
   p.cs_fp32 = cs_fp32 ? 1 : 0;
   p.out_hidden = reinterpret_cast<uint16_t*>(out_hidden);
   p.h_dim = G::H;
+  p.l2_records = g_opt.l2_records;
+  p.skew = g_opt.skew;
   p.layer_outputs = reinterpret_cast<uint16_t*>(layer_outputs);
   p.out_logits = reinterpret_cast<uint16_t*>(out_logits);
   p.out_ids = reinterpret_cast<int64_t*>(out_ids);
@@ -3205,6 +3245,16 @@ extern "C" int pk_set_option(int option, int value) {
   if (option == PK_OPT_SPLIT_ROLE) {
     const int old = pk::opt_split_role();
     pk::g_opt.split_role = value ? 1 : 0;
+    return old;
+  }
+  if (option == PK_OPT_L2_RECORDS) {
+    const int old = pk::g_opt.l2_records;
+    pk::g_opt.l2_records = value ? 1 : 0;
+    return old;
+  }
+  if (option == PK_OPT_SKEW) {
+    const int old = int(pk::g_opt.skew);
+    pk::g_opt.skew = uint32_t(value);
     return old;
   }
   return -1;

@@ -439,11 +439,13 @@ struct CSR {
   }
   // one unit of cross-XCD vector (kind, l), to every copy
   __device__ __forceinline__ void put_x(int kind, int l, int u, u32x4 v) const {
+    skew_delay(p.skew, P.wg, l, kind);
 #pragma unroll
     for (int r = 0; r < REP; ++r) st_unit<16>(rx, W::xoff(kind, l, r, u), v);
   }
   // one unit of the group-A records (layer l, unit index)
   __device__ __forceinline__ void put_loc(int l, size_t unit, u32x4 v) const {
+    skew_delay(p.skew, P.wg, l, 8);
     if (sm.loc_l2) st_unit<0>(rl, W::loc(l, unit), v);
     else st_unit<16>(rl, W::loc(l, unit), v);
   }
@@ -980,6 +982,7 @@ __device__ __forceinline__ void lm_head_sr(CSR<G>& C) {
     int bi = sm.lm_idx[0];
     for (int w = 1; w < NCW; ++w)
       if (sm.lm_val[w] > bv || (sm.lm_val[w] == bv && sm.lm_idx[w] < bi)) { bv = sm.lm_val[w]; bi = sm.lm_idx[w]; }
+    skew_delay(p.skew, P.wg, p.n_layers, 9);
     st_unit<16>(C.rx, uint32_t(W::LMR + size_t(P.wg) * 16), u32x4{__float_as_uint(bv), uint32_t(bi), C.dead ? 1u : 0u, C.tag});
   }
   (void)S::HU;
@@ -1172,7 +1175,7 @@ __device__ __forceinline__ void consumer_a(CSR<G>& C) {
     C.template poll<1>(C.rx, AG, C.lane, 64, [&](int i) { return uint32_t(W::XCC_TAB + size_t(i) * 16); },
                        [&](int, const u32x4& v) { mismatch |= v.x != xcc ? 1u : 0u; }, 34);
     mismatch = __builtin_amdgcn_ballot_w64(mismatch != 0u) != 0ull ? 1u : 0u;
-    if (C.ct == 0) sm.loc_l2 = (mismatch == 0u && p.xws != nullptr) ? 1u : 0u;
+    if (C.ct == 0) sm.loc_l2 = (mismatch == 0u && p.xws != nullptr && p.l2_records) ? 1u : 0u;
     C.cbar();
     C.rl = sm.loc_l2 ? rsrc(p.xws) : rsrc(reinterpret_cast<uint8_t*>(C.region) + W::LOC);
   }

@@ -130,6 +130,8 @@ struct Params {
   const uint16_t* input_hidden;  // optional [B, H]: layer 0's input instead of the embedding rows
   uint32_t* host_status;       // host-visible [2]: epoch and wait site of the last step that gave up a wait
   int h_dim;                   // hidden size of the model (for the poisoned hidden state)
+  int l2_records;              // 0: batch-1 attention records stay in the uncached workspace
+  uint32_t skew;               // != 0: seed of the arrival-skew test's delays before each publish
   int sr_max_s;                // > 0: the split-role kernel was launched for this step and does contexts
                                // up to sr_max_s tokens (the general batch-1 kernel then leaves them)
 };
@@ -434,6 +436,18 @@ struct Spin {
     return true;
   }
 };
+
+// Arrival-skew test (Params::skew != 0): before publishing exchange data, a workgroup sleeps a
+// pseudo-random 0..23 x 512 cycles drawn from (seed, workgroup, layer, site), so values arrive in
+// orders the hardware rarely produces on its own.  Results must not change.  Uniform per wave.
+__device__ __forceinline__ void skew_delay(uint32_t seed, int wg, int l, int site) {
+  if (seed == 0u) return;
+  uint32_t h = seed * 0x9e3779b1u ^ uint32_t(wg) * 0x85ebca77u ^ uint32_t(l * 64 + site) * 0xc2b2ae3du;
+  h ^= h >> 15;
+  h *= 0x2c1b3c6du;
+  h ^= h >> 12;
+  for (uint32_t k = h % 24u; k > 0u; --k) __builtin_amdgcn_s_sleep(8);
+}
 
 // Index field values of a workgroup's end record: one of its waits gave up / no LM head.
 constexpr uint32_t LM_DEAD = 0xffffu, LM_NONE = 0xfffeu;

@@ -28,51 +28,66 @@ HEAD_DIM = MODEL.head_dim
 BLOCK_SIZE = 16
 EPS = 1e-5
 
-_encoded_caches: dict = {}
+class _PerDevice:
+    """One encoded gate/up cache per device, built from one set of gate_up tensors."""
+
+    def __init__(self):
+        self._by_device: dict = {}
+
+    def get(self, device):
+        return self._by_device.get(torch.device(device))
+
+    def build(self, weights):
+        device = weights[0].device
+        have = self._by_device.get(device)
+        if have is not None:
+            if [t.data_ptr() for t in have.weights] != [t.data_ptr() for t in weights]:
+                raise RuntimeError("the lossless cache of this device was prepared for other gate_up tensors; "
+                                   "re-encode new values in place with refresh_weights")
+            return have
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("prepare_weights must be called before graph capture")
+        from prime_kernels_amd.lossless_bf16 import EncodedGUCache
+
+        built = EncodedGUCache(weights)
+        self._by_device[device] = built
+        return built
 
 
-def _gate_up_weights(layers):
+_caches = _PerDevice()
+
+
+def _gate_up_of(layers) -> tuple:
+    """The gate_up tensor (index 4) of each of the 32 six-tensor layer tuples."""
+    layers = list(layers)
     if len(layers) != LAYERS or any(len(layer) != 6 for layer in layers):
-        raise ValueError(f"layers must contain {LAYERS} six-tensor layer tuples")
+        raise ValueError(f"expected {LAYERS} layer tuples of six tensors")
     return tuple(layer[4] for layer in layers)
 
 
 def prepare_weights(layers):
-    """Prepare the stable encoded gate/up cache eagerly, before graph capture."""
-    weights = _gate_up_weights(layers)
-    device = weights[0].device
-    cache = _encoded_caches.get(device)
-    if cache is not None:
-        if tuple(t.data_ptr() for t in cache._weights) != tuple(t.data_ptr() for t in weights):
-            raise RuntimeError("lossless cache cannot change native GU allocations after preparation")
-        return cache
-    if torch.cuda.is_current_stream_capturing():
-        raise RuntimeError("prepare_weights must run before graph capture")
-    from prime_kernels_amd.lossless_bf16 import EncodedGUCache
-
-    cache = EncodedGUCache(weights)
-    _encoded_caches[device] = cache
-    return cache
+    """Build (or return) this device's encoded gate/up cache; call it before any graph capture."""
+    return _caches.build(_gate_up_of(layers))
 
 
 def refresh_weights(layers):
-    """Synchronously re-encode the stable cache after a layerwise weight reload."""
-    weights = _gate_up_weights(layers)
-    cache = _encoded_caches.get(weights[0].device)
+    """Re-encode the device's cache after its gate_up tensors were reloaded in place (synchronous).
+    Without a prepared cache this does nothing."""
+    weights = _gate_up_of(layers)
+    cache = _caches.get(weights[0].device)
     if cache is not None:
         cache.refresh(weights)
 
 
 def cache_statistics(device=None):
-    key = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-    cache = _encoded_caches.get(key)
-    return cache.statistics() if cache is not None else None
+    """statistics() of the device's cache (default: the current CUDA device), or None."""
+    cache = _caches.get(device if device is not None else torch.device("cuda", torch.cuda.current_device()))
+    return None if cache is None else cache.statistics()
 
 
 def decode_step(**kw):
-    """decode_megakernel_360m.decode_step with this device's prepared cache (if any)."""
-    cache = _encoded_caches.get(kw["input_ids"].device)
-    return _decode_step(MODEL, encoded_gu=cache, **kw)
+    """decode_megakernel_360m.decode_step, reading the device's prepared cache when there is one."""
+    return _decode_step(MODEL, encoded_gu=_caches.get(kw["input_ids"].device), **kw)
 
 
 def workspace(device):

@@ -1,7 +1,7 @@
-"""CPU checks of the serving integration (prime_kernels_amd.decode_backend), the routing rules of the
-reference's vLLM backend patch (b2-reproducibility-r1/decode_backend.after.py): geometry routing,
-model and metadata eligibility, step selection, the patched forward's routing and statistics, and
-the mixed-batch repair's row selection.  The decode step here is a recording stand-in; the GPU
+"""CPU checks of the serving integration (prime_kernels_amd.decode_backend), whose routing rules follow
+the reference's vLLM backend module (b2-reproducibility-r1/decode_backend.after.py): geometry routing,
+model and metadata eligibility, the route and its statistics key, the patched forward's routing and
+statistics, and the mixed-batch repair's row selection.  The decode step here is a recording stand-in; the GPU
 checks (tests/test_gpu_backend.py) run the real step."""
 
 from dataclasses import dataclass, field
@@ -65,67 +65,72 @@ def _meta(batch, width=4, qlen=1, **over):
 
 
 def test_geometry_routing():
-    assert D._kernel_name_for_config(_config("360m")) == D.KERNEL_NAME_360M
-    assert D._kernel_name_for_config(_config("135m")) == D.KERNEL_NAME_135M
+    assert D.kernel_for_config(_config("360m")) == D.KERNEL_NAME_360M
+    assert D.kernel_for_config(_config("135m")) == D.KERNEL_NAME_135M
     for bad in (dict(num_hidden_layers=31), dict(rms_norm_eps=1e-6), dict(num_key_value_heads=3),
                 dict(head_dim=128), dict(intermediate_size=2048)):
-        assert D._kernel_name_for_config(_config("360m", **bad)) is None, bad
+        assert D.kernel_for_config(_config("360m", **bad)) is None, bad
 
 
 def test_geometry_routing_hf_config():
     transformers = pytest.importorskip("transformers")
     c = transformers.LlamaConfig(hidden_size=960, intermediate_size=2560, num_hidden_layers=32,
                                  num_attention_heads=15, num_key_value_heads=5, rms_norm_eps=1e-5)
-    assert D._kernel_name_for_config(c) == D.KERNEL_NAME_360M
+    assert D.kernel_for_config(c) == D.KERNEL_NAME_360M
 
 
 def test_model_eligibility():
-    assert D._model_kernel_name(_model("360m")) == D.KERNEL_NAME_360M
-    assert D._model_kernel_name(_model("135m")) == D.KERNEL_NAME_135M
-    assert D._model_eligible(_model("135m")) and not D._model_eligible(_model("360m"))
-    assert D._model_kernel_name(_model("360m", embed_dtype=torch.float16)) is None
+    assert D.kernel_for_model(_model("360m")) == D.KERNEL_NAME_360M
+    assert D.kernel_for_model(_model("135m")) == D.KERNEL_NAME_135M
+    assert D.kernel_for_model(_model("360m", embed_dtype=torch.float16)) is None
     m = _model("360m")
     m.aux_hidden_state_layers = (2,)
-    assert D._model_kernel_name(m) is None
+    assert D.kernel_for_model(m) is None
     m = _model("360m")
     m.tp_size = 2
-    assert D._model_kernel_name(m) is None
+    assert D.kernel_for_model(m) is None
 
 
 def test_metadata_eligibility_rules():
     model = _model("360m")
     K = D.KERNEL_NAME_360M
-    assert D._metadata_eligible(_meta(3), model, K, 3)
-    assert not D._metadata_eligible(OtherMetadata(**vars(_meta(3))), model, K, 3)
-    assert not D._metadata_eligible(_meta(3, qlen=2), model, K, 3)
-    assert not D._metadata_eligible(_meta(3), model, K, 2)          # num_actual_tokens != batch
-    assert not D._metadata_eligible(_meta(17), model, K, 17)        # over the batch limit
-    assert D._metadata_eligible(_meta(16), model, K, 16)
-    assert not D._metadata_eligible(_meta(3, block_table=_meta(3).block_table.long()), model, K, 3)
-    assert not D._metadata_eligible(_meta(3, width=12288 // 16 + 1), model, K, 3)
-    assert D._metadata_eligible(_meta(3, width=12288 // 16), model, K, 3)
-    assert not D._metadata_eligible(_meta(3, block_table=_meta(3).block_table.t().contiguous().t()), model, K, 3)
+    assert D.metadata_fits(_meta(3), model, K, 3)
+    assert not D.metadata_fits(OtherMetadata(**vars(_meta(3))), model, K, 3)
+    assert not D.metadata_fits(_meta(3, qlen=2), model, K, 3)
+    assert not D.metadata_fits(_meta(3), model, K, 2)          # num_actual_tokens != batch
+    assert not D.metadata_fits(_meta(17), model, K, 17)        # over the batch limit
+    assert D.metadata_fits(_meta(16), model, K, 16)
+    assert not D.metadata_fits(_meta(3, block_table=_meta(3).block_table.long()), model, K, 3)
+    assert not D.metadata_fits(_meta(3, width=12288 // 16 + 1), model, K, 3)
+    assert D.metadata_fits(_meta(3, width=12288 // 16), model, K, 3)
+    assert not D.metadata_fits(_meta(3, block_table=_meta(3).block_table.t().contiguous().t()), model, K, 3)
     bad = _model("360m")
     bad.layers[5].self_attn.attn.kv_cache = torch.zeros(9, 5, 16, 128, dtype=BF16)   # shapes differ
-    assert not D._metadata_eligible(_meta(3), bad, K, 3)
+    assert not D.metadata_fits(_meta(3), bad, K, 3)
     bad = _model("360m")
     for layer in bad.layers:
         layer.self_attn.attn.kv_cache = torch.zeros(8, 16, 5, 128, dtype=BF16)         # heads/tokens swapped
-    assert not D._metadata_eligible(_meta(3), bad, K, 3)
+    assert not D.metadata_fits(_meta(3), bad, K, 3)
     # the 135M geometry checks its own KV head count
-    assert D._metadata_eligible(_meta(2), _model("135m"), D.KERNEL_NAME_135M, 2)
-    assert not D._metadata_eligible(_meta(2), _model("135m"), K, 2)
+    assert D.metadata_fits(_meta(2), _model("135m"), D.KERNEL_NAME_135M, 2)
+    assert not D.metadata_fits(_meta(2), _model("135m"), K, 2)
 
 
-def test_select_decode_step():
+def test_route_and_its_reasons():
     model = _model("360m")
     step = object()
     steps = {D.KERNEL_NAME_360M: step}
-    assert D._select_decode_step(steps, model, D.KERNEL_NAME_360M, _meta(2), 2) is step
-    assert D._select_decode_step(steps, model, None, _meta(2), 2) is None
-    assert D._select_decode_step(steps, model, D.KERNEL_NAME_135M, _meta(2), 2) is None
-    assert D._select_decode_step(steps, model, D.KERNEL_NAME_360M, None, 2) is None
-    assert D._select_decode_step(steps, model, D.KERNEL_NAME_360M, _meta(0), 0) is None
+    assert D.route(steps, model, D.KERNEL_NAME_360M, _meta(2), 2) == (step, None)
+    assert D.route(steps, model, None, _meta(2), 2) == (None, "stock_ineligible")
+    assert D.route(steps, model, D.KERNEL_NAME_135M, _meta(2), 2) == (None, "stock_kernel_unavailable")
+    assert D.route(steps, model, D.KERNEL_NAME_360M, None, 2) == (None, "stock_not_pure_decode")
+    assert D.route(steps, model, D.KERNEL_NAME_360M, _meta(2, qlen=2), 2) == (None, "stock_not_pure_decode")
+    assert D.route(steps, model, D.KERNEL_NAME_360M, _meta(3), 2) == (None, "stock_decode_over_max_batch")
+    assert D.route(steps, model, D.KERNEL_NAME_360M, _meta(17), 17) == (None, "stock_decode_over_max_batch")
+    assert D.route(steps, model, D.KERNEL_NAME_360M, _meta(0), 0) == (None, "stock_unsupported_metadata")
+    bt64 = _meta(2).block_table.long()
+    assert D.route(steps, model, D.KERNEL_NAME_360M, _meta(2, block_table=bt64), 2) == \
+        (None, "stock_unsupported_metadata")
 
 
 class Recorder:
@@ -147,7 +152,7 @@ def _patched(model, steps, meta_by_call):
         stock.append(input_ids.shape[0])
         return torch.zeros(input_ids.shape[0], 960)
 
-    fwd = D.make_forward(original, steps, attn_metadata_fn=lambda m: meta_by_call[0])
+    fwd = D.patched_forward(original, steps, attn_metadata_fn=lambda m: meta_by_call[0])
     return fwd, stock
 
 
@@ -193,7 +198,7 @@ def test_repair_mixed_decode_rows():
                  slot_mapping=torch.arange(5, dtype=torch.int64) + 200)
     ids = torch.tensor([11, 12, 13, 14, 15]); pos = torch.tensor([8, 0, 1, 2, 6])
     hidden = torch.arange(5 * 960, dtype=torch.float32).view(5, 960)
-    out = D._repair_mixed_decode(model, {D.KERNEL_NAME_360M: rec}, ids, pos, hidden, {"l0": meta})
+    out = D.repair_mixed_batch(model, {D.KERNEL_NAME_360M: rec}, ids, pos, hidden, {"l0": meta})
     kw = rec.calls[0]
     assert torch.equal(kw["input_ids"], torch.tensor([11, 15])) and torch.equal(kw["positions"], torch.tensor([8, 6]))
     assert torch.equal(kw["seq_lens"], meta.seq_lens[[0, 2]])
@@ -204,10 +209,10 @@ def test_repair_mixed_decode_rows():
     assert D.stats["backend_mixed_decode"] == 2
     # pure decode or pure prefill: nothing to repair
     h2 = hidden[:2].clone()
-    assert D._repair_mixed_decode(model, {D.KERNEL_NAME_360M: rec}, ids[:2], pos[:2], h2, {"l0": _meta(2)}) is h2
+    assert D.repair_mixed_batch(model, {D.KERNEL_NAME_360M: rec}, ids[:2], pos[:2], h2, {"l0": _meta(2)}) is h2
     pre = _meta(1, qlen=5, num_actual_tokens=5, query_start_loc=torch.tensor([0, 5], dtype=torch.int32))
     h = torch.zeros(5, 960)
-    assert D._repair_mixed_decode(model, {D.KERNEL_NAME_360M: rec}, ids, pos, h, {"l0": pre}) is h
+    assert D.repair_mixed_batch(model, {D.KERNEL_NAME_360M: rec}, ids, pos, h, {"l0": pre}) is h
 
 
 def test_monkey_patch_installs_once(tmp_path, monkeypatch):

@@ -78,7 +78,7 @@ def test_patched_forward_pure_decode_equals_decode_step():
         return torch.zeros(input_ids.shape[0], 960, device=dev)
 
     D.stats.clear()
-    fwd = D.make_forward(stock, {D.KERNEL_NAME_360M: mod.decode_step},
+    fwd = D.patched_forward(stock, {D.KERNEL_NAME_360M: mod.decode_step},
                          attn_metadata_fn=lambda m: {"model.layers.0.self_attn.attn": meta})
     routed = fwd(served, ids, positions, None).clone()
     torch.cuda.synchronize()
@@ -116,7 +116,7 @@ def test_mixed_batch_repair_replaces_decode_rows():
     stock = torch.randn(5, 960, device=dev).to(torch.bfloat16)
     caches0 = [c.clone() for c in kv.caches]
     D.stats.clear()
-    out = D._repair_mixed_decode(served, {D.KERNEL_NAME_360M: mod.decode_step}, ids, positions, stock,
+    out = D.repair_mixed_batch(served, {D.KERNEL_NAME_360M: mod.decode_step}, ids, positions, stock,
                                  {"model.layers.0.self_attn.attn": meta})
     torch.cuda.synchronize()
     out = out.clone()

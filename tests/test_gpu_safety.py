@@ -148,3 +148,105 @@ def test_epoch_wrap_and_16_bit_jumps_with_alternating_batches():
             assert torch.equal(h0.view(torch.int16), h1.view(torch.int16)), (mode, k)
             assert torch.equal(i0, i1) and torch.equal(l0.view(torch.int16), l1.view(torch.int16)), (mode, k)
         assert all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(kv_ref, kv_got)), mode
+
+
+def test_embed_check_follows_the_reference_without_lm_head():
+    """Without an LM head the embedding needs only the hidden width, as in the reference
+    (decode_megakernel_360m/__init__.py:151-152): a 1000-row embedding gives the full one's step for
+    ids below 1000.  With token ids or logits requested the full vocabulary is required."""
+    _need_gpu()
+    mod, model, embed, final_norm, lw, kv, cos_sin = _setup(1, [200])
+    dev = embed.device
+    small = embed[:1000].contiguous()
+    kv0 = [c.clone() for c in kv.caches]
+
+    def step(e, **extra):
+        for c, c0 in zip(kv.caches, kv0):
+            c.copy_(c0)
+        out = mod.decode_step(
+            input_ids=torch.tensor([999], device=dev), positions=torch.tensor([200], device=dev),
+            seq_lens=torch.tensor([201], dtype=torch.int32, device=dev), block_table=kv.block_table[:1].contiguous(),
+            slot_mapping=torch.tensor([kv.slot(0, 200)], device=dev), embed=e, layers=lw, final_norm=final_norm,
+            kv_caches=kv.caches, cos_sin_cache=cos_sin, eps=1e-5, num_layers=len(lw), **extra)
+        torch.cuda.synchronize()
+        return out.clone()
+
+    assert torch.equal(step(small).view(torch.int16), step(embed).view(torch.int16))
+    with pytest.raises(ValueError, match="LM head"):
+        step(small, return_token_ids=True)
+    with pytest.raises(ValueError, match="embed"):
+        step(embed[:, :900].contiguous())
+
+
+@pytest.mark.parametrize("split_role", [1, 0], ids=["split_role", "general"])
+def test_attention_records_through_uncached_memory_give_the_same_bits(split_role):
+    """A KV head's chunks exchange their softmax statistics and partials through their XCD's L2 when
+    the run-time check finds them on one XCC, else through the uncached workspace.
+    PK_OPT_L2_RECORDS=0 forces the second path, the one a placement mismatch takes: same bits."""
+    _need_gpu()
+    from prime_kernels_amd import _native
+
+    lib = _native.library()
+    mod, model, embed, final_norm, lw, kv, cos_sin = _setup(1, [900])
+    kv0 = [c.clone() for c in kv.caches]
+    old_sr = lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, split_role)
+    try:
+        outs = []
+        for l2 in (1, 0):
+            old_l2 = lib.pk_set_option(_native.PK_OPT_L2_RECORDS, l2)
+            try:
+                for c, c0 in zip(kv.caches, kv0):
+                    c.copy_(c0)
+                h, i, lg = _step(mod, embed, final_norm, lw, kv, cos_sin, [321], [900])
+                torch.cuda.synchronize()
+                outs.append((h, i, lg.clone(), [c.clone() for c in kv.caches]))
+            finally:
+                lib.pk_set_option(_native.PK_OPT_L2_RECORDS, old_l2)
+        (h0, i0, l0, k0), (h1, i1, l1, k1) = outs
+        assert not torch.isnan(h0.float()).any()
+        assert torch.equal(h0.view(torch.int16), h1.view(torch.int16)) and torch.equal(i0, i1)
+        assert torch.equal(l0.view(torch.int16), l1.view(torch.int16))
+        assert all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(k0, k1))
+        assert mod.workspace(embed.device).pending_failure() == (0, 0)
+    finally:
+        lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, old_sr)
+
+
+@pytest.mark.parametrize("case", ["b1_split_role", "b1_general", "b16_ragged"])
+def test_arrival_skew_leaves_every_bit_unchanged(case):
+    """Arrival-skew test of the tagged exchange protocol: with PK_OPT_SKEW every workgroup sleeps a
+    pseudo-random 0..23 x 512 cycles (from the seed, the workgroup, the layer and the site) before each
+    publish, so exchanged values arrive in orders the hardware rarely produces on its own.  Hidden
+    state, greedy ids, logits and the whole KV caches stay bit-identical to the undelayed step, for
+    two seeds."""
+    _need_gpu()
+    from prime_kernels_amd import _native
+
+    lib = _native.library()
+    batch = 16 if case == "b16_ragged" else 1
+    contexts = [40 + 53 * b for b in range(batch)] if batch > 1 else [900]
+    mod, model, embed, final_norm, lw, kv, cos_sin = _setup(batch, contexts)
+    kv0 = [c.clone() for c in kv.caches]
+    ids = [(11 + 97 * b) % 49152 for b in range(batch)]
+    old_sr = lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, 0 if case == "b1_general" else 1)
+    try:
+        outs = []
+        for seed in (0, 1, 7):
+            old = lib.pk_set_option(_native.PK_OPT_SKEW, seed)
+            try:
+                for c, c0 in zip(kv.caches, kv0):
+                    c.copy_(c0)
+                h, i, lg = _step(mod, embed, final_norm, lw, kv, cos_sin, ids, contexts)
+                torch.cuda.synchronize()
+                outs.append((h, i, lg.clone(), [c.clone() for c in kv.caches]))
+            finally:
+                lib.pk_set_option(_native.PK_OPT_SKEW, old)
+            assert mod.workspace(embed.device).pending_failure() == (0, 0), seed
+        h0, i0, l0, k0 = outs[0]
+        assert not torch.isnan(h0.float()).any()
+        for seed, (h, i, lg, kc) in zip((1, 7), outs[1:]):
+            assert torch.equal(h.view(torch.int16), h0.view(torch.int16)), seed
+            assert torch.equal(i, i0) and torch.equal(lg.view(torch.int16), l0.view(torch.int16)), seed
+            assert all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(kc, k0)), seed
+    finally:
+        lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, old_sr)
