@@ -1,14 +1,19 @@
-"""Decode throughput of SmolLM2-360M (bf16, batch 1, 1024-token context) on one MI355X.
-(--batch 16: BASELINE config 4, 16 sequences with ragged contexts; --weights mxfp8: config 5.)
+"""Decode throughput of SmolLM2 on one MI355X: the hot path's one step, timed.
 
-One step = one greedy decode step of the full model (32 layers + tied LM head + argmax), i.e. one
-launch of the persistent megakernel.  The KV cache holds a synthetic 1024-token context
-(N(0,1) bf16), weights are seeded random-init (N(0,0.02) bf16): BASELINE config 3.  W untimed
-warmup steps, then exactly K timed steps starting at position 1024 (context 1025 .. 1024+K),
-bracketed by synchronisation and HIP events on the launch stream.
+Default: SmolLM2-360M, bf16, batch 1, 1024-token context (the headline).
+--model 135m: SmolLM2-135M, 512-token context (config 2); --batch 16: 360M with 16 ragged contexts
+(config 4); --weights mxfp8: 360M MXFP8 projections at an 8192-token context (config 5); --lossless:
+the 360M gate/up weights streamed through the lossless codec.
 
-Prints one JSON line with the metric, the HBM roofline of the kernel (algorithmic bytes per step
-from the reference's own accounting) and a CPU baseline (the oracle's eager step on host cores).
+One step = one greedy decode step of the full model (all layers + tied LM head + argmax), one
+kernel launch.  The KV cache holds a synthetic context (N(0,1) bf16), weights are seeded
+random-init (N(0,0.02) bf16).  W untimed warmup steps, then exactly K timed steps starting at the
+context length (context S+1 .. S+K), bracketed by synchronisation and HIP events on the launch
+stream; greedy ids are fed back on the device.
+
+Prints one JSON line with the metric, the HBM roofline of the kernel (algorithmic bytes per step,
+the accounting of SURVEY.md's roofline row; traffic from the committed rocprofv3 FETCH/WRITE
+summary of the same workload) and a CPU baseline (the oracle's eager step on the host's cores).
 """
 
 from __future__ import annotations
@@ -24,50 +29,91 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
-CONTEXT = 1024
-W_LAYER_360M = 19_664_640        # bf16 projections + norms of one layer
-W_LAYER_360M_MXFP8 = 10_141_440  # e4m3 projections + one e8m0 byte per 32 weights + bf16 norms
-E_LMHEAD_360M = 94_371_840
-KV_TOKEN_360M = 40_960
-HIDDEN_BYTES = 1_920
+VOCAB = 49152
 
 
-def step_bytes(S, layers: int = 32, weights: str = "bf16") -> int:
-    """Algorithmic bytes of one step whose sequences attend S tokens each (S counts the new one;
-    an int for one sequence or a list for a batch): the weights and the LM head once per step,
-    per sequence its cached K/V, the appended K/V and the hidden state in and out."""
-    w = W_LAYER_360M if weights == "bf16" else W_LAYER_360M_MXFP8
-    seqs = [S] if isinstance(S, int) else list(S)
-    return layers * w + E_LMHEAD_360M + sum(KV_TOKEN_360M * s + KV_TOKEN_360M + 2 * HIDDEN_BYTES for s in seqs)
+class Bytes:
+    """Algorithmic HBM bytes of one decode step of a SmolLM2 geometry."""
+
+    def __init__(self, hidden, inter, heads, kv_heads, layers, head_dim=64):
+        qkv = (heads + 2 * kv_heads) * head_dim
+        mats = qkv * hidden + hidden * hidden + 2 * inter * hidden + hidden * inter
+        self.layers = layers
+        self.layer_bf16 = 2 * mats + 2 * 2 * hidden                  # projections + the two norms
+        self.layer_mxfp8 = mats + mats // 32 + 2 * 2 * hidden        # e4m3 + one e8m0 per 32 + norms
+        self.lm_head = VOCAB * hidden * 2
+        self.kv_token = layers * kv_heads * 2 * head_dim * 2         # K and V of every layer, bf16
+        self.hidden_bytes = hidden * 2
+
+    def step(self, S, weights: str = "bf16") -> int:
+        """Bytes of one step whose sequences attend S tokens each (S counts the new one; an int for one
+        sequence or a list for a batch): weights and LM head once, per sequence its cached K/V, the
+        appended K/V and the hidden state in and out."""
+        w = self.layer_bf16 if weights == "bf16" else self.layer_mxfp8
+        seqs = [S] if isinstance(S, int) else list(S)
+        return self.layers * w + self.lm_head + sum(self.kv_token * (s + 1) + 2 * self.hidden_bytes for s in seqs)
 
 
-def cpu_baseline(seconds: float = 15.0) -> dict:
-    """The oracle's eager bf16 step (oracle/smollm2.py) on this host's cores, full 360M model,
-    1024-token synthetic context; a bounded sample of steps (about `seconds` of CPU work)."""
+BYTES = {"360m": Bytes(960, 2560, 15, 5, 32), "135m": Bytes(576, 1536, 9, 3, 30)}
+assert BYTES["360m"].layer_bf16 == 19_664_640 and BYTES["360m"].layer_mxfp8 == 10_141_440
+
+
+def step_bytes(S, layers: int = 32, weights: str = "bf16", model: str = "360m") -> int:
+    """Algorithmic bytes of one step (see Bytes.step); `layers` other than the model's scales the weights."""
+    b = BYTES[model]
+    full = b.step(S, weights)
+    return full - (b.layers - layers) * (b.layer_bf16 if weights == "bf16" else b.layer_mxfp8)
+
+
+def physical_cores() -> tuple:
+    """(physical cores among the CPUs this process may run on, those CPUs, os.cpu_count())."""
+    cpus = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in cpus:
+        try:
+            base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+            cores.add((int(open(base + "physical_package_id").read()), int(open(base + "core_id").read())))
+        except (OSError, ValueError):
+            cores.add((0, c))
+    return len(cores), len(cpus), os.cpu_count()
+
+
+def cpu_baseline(model: str, context: int, steps: int = 256, seconds: float = 60.0,
+                 one_thread_steps: int = 16, one_thread_seconds: float = 25.0) -> dict:
+    """The oracle's eager bf16 step (oracle/smollm2.py, pinned to HF eager) on this host: the median
+    wall time per greedy step over `steps` steps (or as many as `seconds` allow) with one thread per
+    physical core, and a 1-thread median over a shorter sample.  Untimed first step (the prefill is
+    the synthetic KV context)."""
     import torch
     from oracle import smollm2 as O
 
-    threads = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
-    geom = O.SMOLLM2_360M
+    geom = O.SMOLLM2_360M if model == "360m" else O.SMOLLM2_135M
     w = O.make_weights(geom, 7)
-    kv = O.make_paged_kv(geom, 1, CONTEXT + 64, seed=11)
-    cos_sin = O.rope_cos_sin(CONTEXT + 64)
-    O.decode_step(w, [5], [CONTEXT], kv, cos_sin)  # untimed warmup
-    times = []
-    t_end = time.perf_counter() + seconds
-    k = 1
-    while time.perf_counter() < t_end and k < 60:
-        t0 = time.perf_counter()
-        O.decode_step(w, [5 + k], [CONTEXT + k], kv, cos_sin)
-        times.append(time.perf_counter() - t0)
-        k += 1
-    times.sort()
-    med = times[len(times) // 2]
-    return {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{len(times)} greedy steps of the full 360M model at context {CONTEXT + 1}..{CONTEXT + len(times)} "
-                      f"(median step {med * 1e3:.1f} ms, torch {torch.__version__} CPU eager bf16, "
-                      f"os.cpu_count()={os.cpu_count()})"}
+    kv = O.make_paged_kv(geom, 1, context + steps + 64, seed=11)
+    cos_sin = O.rope_cos_sin(context + steps + 64)
+    n, affinity, logical = physical_cores()
+
+    def run(threads, max_steps, budget, first_pos):
+        torch.set_num_threads(threads)
+        tok = O.decode_step(w, [5], [first_pos], kv, cos_sin)["ids"][0]   # untimed
+        times, t_end, k = [], time.perf_counter() + budget, 1
+        while k <= max_steps and time.perf_counter() < t_end:
+            t0 = time.perf_counter()
+            tok = O.decode_step(w, [int(tok)], [first_pos + k], kv, cos_sin)["ids"][0]
+            times.append(time.perf_counter() - t0)
+            k += 1
+        times.sort()
+        return times[len(times) // 2], len(times)
+
+    med, done = run(n, steps, seconds, context)
+    med1, done1 = run(1, one_thread_steps, one_thread_seconds, context + steps + 2)
+    return {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": n, "kind": "port",
+            "one_thread": {"value": round(1.0 / med1, 3), "unit": "tok/s", "steps": done1},
+            "physical_cores": n, "affinity_cpus": affinity, "os_cpu_count": logical,
+            "sample": f"median of {done} greedy steps of the full {model.upper()} model at context "
+                      f"{context + 1}..{context + done}, {n} threads (one per physical core of this process's "
+                      f"CPU set of {affinity}; os.cpu_count()={logical}); 1 thread: median of {done1} steps "
+                      f"(torch {torch.__version__} CPU eager bf16)"}
 
 
 def main() -> None:
@@ -75,8 +121,11 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--model", choices=("360m", "135m"), default="360m",
+                    help="SmolLM2-360M (default; configs 3-5) or SmolLM2-135M (config 2, 512-token context)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=60.0,
+                    help="time bound of the CPU baseline's multi-thread sample (256 steps at most)")
     ap.add_argument("--weights", choices=("bf16", "mxfp8"), default="bf16",
                     help="projection weights: bf16 (BASELINE config 3, the default) or MXFP8 (config 5)")
     ap.add_argument("--context", type=int, default=None,
@@ -88,7 +137,11 @@ def main() -> None:
     ap.add_argument("--lossless", action="store_true",
                     help="stream the gate/up weights through the lossless codec (batch 1, bf16)")
     args = ap.parse_args()
-    context = args.context if args.context is not None else (CONTEXT if args.weights == "bf16" else 8192)
+    if args.model == "135m" and (args.weights != "bf16" or args.lossless):
+        print("--model 135m runs bf16 weights", file=sys.stderr)
+        sys.exit(2)
+    default_ctx = 512 if args.model == "135m" else (1024 if args.weights == "bf16" else 8192)
+    context = args.context if args.context is not None else default_ctx
     B = args.batch
     if not 1 <= B <= 16 or (B > 1 and args.weights != "bf16"):
         print("--batch takes 1..16 sequences, with bf16 weights above 1", file=sys.stderr)
@@ -107,7 +160,8 @@ def main() -> None:
     from prime_kernels_amd import workload as WL
     from prime_kernels_amd._decode import StepLauncher
 
-    mod = pk.load("decode_megakernel_360m" if args.weights == "bf16" else "decode_megakernel_360m_mxfp8")
+    name = {"135m": "decode_megakernel"}.get(args.model, "decode_megakernel_360m")
+    mod = pk.load(name if args.weights == "bf16" else "decode_megakernel_360m_mxfp8")
     model = mod.MODEL
     dev = torch.device("cuda:0")
     K, W = args.steps, args.warmup
@@ -118,7 +172,7 @@ def main() -> None:
         rng = np.random.default_rng(args.seed)
         contexts = [int(x) for x in rng.integers(128, 4097, B)]
         first_ids = [int(x) for x in rng.integers(0, 49152, B)]
-    embed, final_norm, layers = WL.random_weights(pk.load("decode_megakernel_360m").MODEL, 1234, dev)
+    embed, final_norm, layers = WL.random_weights(pk.load(name).MODEL, 1234, dev)
     if args.weights == "mxfp8":
         layers = mod.quantize_layers(layers)
     cache = None
@@ -160,27 +214,32 @@ def main() -> None:
     if not bool(((ids >= 0) & (ids < 49152)).all()):
         raise RuntimeError("greedy ids out of range")
 
-    total_bytes = sum(step_bytes([c + 1 + k for c in contexts], weights=args.weights) - gu_bytes_saved
+    total_bytes = sum(BYTES[args.model].step([c + 1 + k for c in contexts], args.weights) - gu_bytes_saved
                       for k in range(K))
     ms_per_step = ms / K
     achieved = total_bytes / (ms * 1e-3) / 1e9
     traffic = None
-    tname = (f"decode360_b{B}_ragged" if B > 1 else
-             f"decode360_{'' if args.weights == 'bf16' else 'mxfp8_'}{'lossless_' if args.lossless else ''}"
-             f"ctx{context}")
+    mtag = "decode135" if args.model == "135m" else "decode360"
+    tname = (f"{mtag}_b{B}_ragged" if B > 1 else
+             f"{mtag}_{'' if args.weights == 'bf16' else 'mxfp8_'}{'lossless_' if args.lossless else ''}ctx{context}")
     tfile = ROOT / "profiles" / f"{tname}_traffic.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+    mname = "SmolLM2-135M" if args.model == "135m" else "SmolLM2-360M"
     wname = ("bf16 lossless-GU" if args.lossless else "bf16") if args.weights == "bf16" else "MXFP8-weight"
     ctx_name = f"ctx={context}" if B == 1 else "ragged ctx 128..4096"
-    workload = (f"smollm2-360m greedy decode, batch 1, {context}-token context, K steps at context "
+    layers_n = len(layers)
+    workload = (f"{mname.lower()} greedy decode, batch 1, {context}-token context, K steps at context "
                 f"{context + 1}..{context}+K" + (", MXFP8 projection weights" if args.weights == "mxfp8" else "")
                 + (", gate/up streamed through the lossless codec" if args.lossless else "")
                 if B == 1 else
-                f"smollm2-360m greedy decode, batch {B}, contexts drawn uniformly from 128..4096 "
+                f"{mname.lower()} greedy decode, batch {B}, contexts drawn uniformly from 128..4096 "
                 f"(seed {args.seed}, mean {sum(contexts) / B:.0f}), K steps per sequence")
+    kernel = ("split-role batch-1 kernel (contexts up to its limit; the general kernel beyond)"
+              if B == 1 and args.weights == "bf16" and not args.lossless else
+              "batched MFMA kernel" if B > 1 else "general batch-1 kernel")
     line = {
-        "metric": f"decode tok/s, SmolLM2-360M {wname} bs={B} {ctx_name}; % of HBM roofline",
+        "metric": f"decode tok/s, {mname} {wname} bs={B} {ctx_name}; % of HBM roofline",
         "value": round(B * K / (ms * 1e-3), 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -195,16 +254,18 @@ def main() -> None:
                 (", projections quantised to MXFP8 on the GPU" if args.weights == "mxfp8" else "") +
                 ", KV context N(0,1) bf16, greedy ids fed back on device)",
         "config": {"workload": workload,
-                   "batch": B, "context": context if B == 1 else contexts, "layers": 32, "weights": args.weights,
+                   "batch": B, "context": context if B == 1 else contexts, "layers": layers_n, "weights": args.weights,
                    "gate_up": "lossless codec" if args.lossless else "dense",
-                   "lm_head": "tied, fused argmax", "launch": "one cooperative kernel per step, 256 workgroups"},
+                   "lm_head": "tied, fused argmax",
+                   "launch": f"one persistent launch per step, 256 workgroups (one per CU): {kernel}"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": f"profiles/{tname}_traffic.json" if traffic is not None else None,
                      "bytes_per_step": round(total_bytes / K)},
         "host_wall_ms_per_step": round(wall * 1e3 / K, 5),
     }
-    if not args.no_cpu_baseline and args.weights == "bf16" and B == 1:
-        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    if not args.no_cpu_baseline and args.weights == "bf16" and B == 1 and not args.lossless:
+        line["cpu_baseline"] = cpu_baseline(args.model, context, seconds=args.cpu_seconds)
     print(json.dumps(line), flush=True)
 
 
