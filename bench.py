@@ -236,7 +236,7 @@ def main() -> None:
                 f"{mname.lower()} greedy decode, batch {B}, contexts drawn uniformly from 128..4096 "
                 f"(seed {args.seed}, mean {sum(contexts) / B:.0f}), K steps per sequence")
     kernel = ("split-role batch-1 kernel (contexts up to its limit; the general kernel beyond)"
-              if B == 1 and args.weights == "bf16" and not args.lossless else
+              if B == 1 and args.weights == "bf16" else
               "batched MFMA kernel" if B > 1 else "general batch-1 kernel")
     line = {
         "metric": f"decode tok/s, {mname} {wname} bs={B} {ctx_name}; % of HBM roofline",

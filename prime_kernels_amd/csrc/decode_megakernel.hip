@@ -61,17 +61,6 @@ struct Dbg {
   __device__ static size_t head_pos(int b, int head, int pos) { return (size_t(b) * G::NH + head) * SEQ + pos; }
 };
 
-// A layer's lossless gate/up encoding as this workgroup streams it (on = 0: dense gate/up): the
-// plane / header / escape arrays, and for gate (0) and up (1) the first escape ordinal of the
-// workgroup's rows and their number of escapes.
-struct GUE {
-  const uint8_t* plane;
-  const uint32_t* hdr;
-  const uint16_t* raw;
-  uint32_t on;
-  uint32_t first[2];
-  uint32_t cnt[2];
-};
 
 // Exchange-buffer layout (32-bit words).  The per-layer vectors (qkv, attn, h1, act, x) of tagged
 // bf16 words are stored line-interleaved: 64-byte line k of vector (kind, layer, b) is line slot
@@ -692,27 +681,6 @@ __device__ __forceinline__ void dots_ring_q(const Consumer<G>& C, uint32_t segq,
   }
 #pragma unroll
   for (int r = 0; r < MAXR; ++r) out[r] = wave_sum(out[r]);
-}
-
-// The 8 bf16 words (4 packed pairs) of a lossless chunk: plane bytes p (sign | mantissa) and the
-// header's base exponent and 3-bit deltas give word_i = (p_i & 0x80) << 8 | (base + d_i) << 7 |
-// (p_i & 0x7f) (prime_kernels/lossless_bf16/csrc/lossless_bf16.cu:94-101).  Per pair of words,
-// in one register: v_perm copies plane bytes 2j, 2j+1 into both bytes of the low / high half, so
-// one mask keeps each sign at bit 15 / 31 and each mantissa at bits 0-6 / 16-22; the pair's 6 delta
-// bits d times 0x100080 is d << 7 | d << 20, whose bits 7-9 and 23-25 are the two deltas in
-// exponent position; the base exponent is added to both halves at once.  No field overflows into
-// the next: every exponent of a plain chunk is at most 254 + 7 < 256.
-__device__ __forceinline__ uint4 lossless_chunk(uint2 p, uint32_t h) {
-  const uint32_t base7 = (h >> 24) * 0x00800080u;
-  uint32_t out[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t t = __builtin_amdgcn_perm(0u, j < 2 ? p.x : p.y, (j & 1) ? 0x03030202u : 0x01010000u);
-    const uint32_t d = __builtin_amdgcn_ubfe(h, 6 * j, 6);
-    const uint32_t e7 = (__umul24(d, 0x100080u) & 0x03800380u) + base7;
-    out[j] = (t & 0x807F807Fu) | e7;
-  }
-  return make_uint4(out[0], out[1], out[2], out[3]);
 }
 
 // The lossless-encoded gate and up rows of P4 as the 16-byte chunks dots_ring would read from a
@@ -3201,7 +3169,7 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
   // so the host never has to read it (no synchronisation, and the pair can be captured in a graph).
   if constexpr (G::WF == 0) {
     const int model = G::H == 960 ? PK_MODEL_SMOLLM2_360M : PK_MODEL_SMOLLM2_135M;
-    if (opt_split_role() && !encoded_gu && !input_hidden) {
+    if (opt_split_role() && !input_hidden) {
       p.sr_max_s = sr_max_seq(model);
       const int e = sr_launch(model, p, reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(state->ws) + ws_general_bytes()),
                               reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(state->rec) + rec_general_bytes()), s,

@@ -181,16 +181,21 @@ struct PlanSR {
 // rows, up rows, down rows; k >= 1) then norm1 and the QKV rows of layer k (k < L); bracket L ends
 // with the final-norm weights and the LM-head segments.  Group A, bracket k < L: the KV chunk and
 // the O rows of layer k; bracket L: the final-norm weights and the LM-head segments.
-enum SRSeg { R_NORM2, R_GATE, R_UP, R_DOWN, R_NORM1, R_QKV, R_KV, R_O, R_FNORM, R_LM };
+enum SRSeg { R_NORM2, R_GATE, R_GATE_H, R_GATE_R, R_UP, R_UP_H, R_UP_R, R_DOWN, R_NORM1, R_QKV, R_KV, R_O, R_FNORM, R_LM };
 
 template <class G>
-__device__ __forceinline__ uint32_t sr_bytes(const PlanSR<G>& P, int kind, int lm_index) {
+__device__ __forceinline__ uint32_t sr_bytes(const PlanSR<G>& P, int kind, int lm_index, const GUE* e = nullptr) {
+  const bool enc = e != nullptr && e->on != 0u;  // this layer's gate/up through the lossless codec
   switch (kind) {
     case R_NORM2:
     case R_NORM1:
     case R_FNORM: return G::H * 2;
     case R_GATE:
-    case R_UP: return uint32_t(P.a1 - P.a0) * G::H * 2;
+    case R_UP: return uint32_t(P.a1 - P.a0) * G::H * (enc ? 1u : 2u);  // plane rows: 1 byte per weight
+    case R_GATE_H:
+    case R_UP_H: return enc ? uint32_t(P.a1 - P.a0) * (G::H / 8) * 4u : 0u;  // one header per 8 weights
+    case R_GATE_R: return enc ? e->cnt[0] * 16u : 0u;                      // the rows' escaped chunks
+    case R_UP_R: return enc ? e->cnt[1] * 16u : 0u;
     case R_DOWN: return uint32_t(P.d1 - P.d0) * G::I * 2;
     case R_QKV: return uint32_t(P.q1 - P.q0) * G::H * 2;
     case R_KV: return uint32_t(P.t1 - P.t0) * 256u;
@@ -226,6 +231,7 @@ struct SmemSR {
   float cs[128];                 // cos [0, 32), sin [32, 64) of this position (fp32 values)
   float red[NCW];
   LayerW lw[G::L];
+  GUE gue[G::L];                 // group F: each layer's lossless gate/up stream of this workgroup
   const void* kvp[G::L];
   int32_t blk[TCS / 16 + 2];
   float lm_val[NCW];
@@ -262,7 +268,8 @@ __device__ __forceinline__ void producer_sr(const Params& p, const PlanSR<G>& P,
     if (lane == 0) st_lds(&sm.front[pw], first_pending_packet * PKT);
   };
   auto issue = [&](int kind, int layer, int lm_index) {
-    const uint32_t bytes = sr_bytes(P, kind, lm_index);
+    const GUE* ge = kind >= R_GATE && kind <= R_UP_R ? &sm.gue[layer] : nullptr;
+    const uint32_t bytes = sr_bytes(P, kind, lm_index, ge);
     const uint32_t npk = pad_pkt(bytes) / PKT;
     if (npk == 0 || dead) return;
     const uint8_t* base = nullptr;
@@ -271,8 +278,14 @@ __device__ __forceinline__ void producer_sr(const Params& p, const PlanSR<G>& P,
     const LayerW& Lw = sm.lw[layer];
     switch (kind) {
       case R_NORM2: base = u8(Lw.norm2); break;
-      case R_GATE: base = u8(Lw.gate_up) + size_t(P.a0) * G::H * 2; break;
-      case R_UP: base = u8(Lw.gate_up) + size_t(G::I + P.a0) * G::H * 2; break;
+      case R_GATE: base = ge->on ? ge->plane + size_t(P.a0) * G::H : u8(Lw.gate_up) + size_t(P.a0) * G::H * 2; break;
+      case R_GATE_H: base = u8(ge->hdr + size_t(P.a0) * (G::H / 8)); break;
+      case R_GATE_R: base = u8(ge->raw + size_t(ge->first[0]) * 8); break;
+      case R_UP:
+        base = ge->on ? ge->plane + size_t(G::I + P.a0) * G::H : u8(Lw.gate_up) + size_t(G::I + P.a0) * G::H * 2;
+        break;
+      case R_UP_H: base = u8(ge->hdr + size_t(G::I + P.a0) * (G::H / 8)); break;
+      case R_UP_R: base = u8(ge->raw + size_t(ge->first[1]) * 8); break;
       case R_DOWN: base = u8(Lw.down) + size_t(P.d0) * G::I * 2; break;
       case R_NORM1: base = u8(Lw.norm1); break;
       case R_QKV: base = u8(Lw.qkv) + size_t(P.q0) * G::H * 2; break;
@@ -334,7 +347,11 @@ __device__ __forceinline__ void producer_sr(const Params& p, const PlanSR<G>& P,
       if (k > 0) {
         issue(R_NORM2, k - 1, 0);
         issue(R_GATE, k - 1, 0);
+        issue(R_GATE_H, k - 1, 0);
+        issue(R_GATE_R, k - 1, 0);
         issue(R_UP, k - 1, 0);
+        issue(R_UP_H, k - 1, 0);
+        issue(R_UP_R, k - 1, 0);
         issue(R_DOWN, k - 1, 0);
       }
       if (k < L) {
@@ -424,6 +441,12 @@ struct CSR {
   __device__ __forceinline__ uint4 ring16(uint32_t at) const {
     return *reinterpret_cast<const uint4*>(sm.ring + (at & (RB - 1)));
   }
+  __device__ __forceinline__ uint2 ring8(uint32_t at) const {
+    return *reinterpret_cast<const uint2*>(sm.ring + (at & (RB - 1)));
+  }
+  __device__ __forceinline__ uint32_t ring4(uint32_t at) const {
+    return *reinterpret_cast<const uint32_t*>(sm.ring + (at & (RB - 1)));
+  }
   // ring16(at), or the zero line when !ok (one select on the address, no branch)
   __device__ __forceinline__ uint4 ring16z(uint32_t at, bool ok) const {
     const uint4* q = ok ? reinterpret_cast<const uint4*>(sm.ring + (at & (RB - 1)))
@@ -505,10 +528,9 @@ struct CSR {
 // last chunk read the zero line (their activation chunk is zero too, but ring bytes past a row may
 // hold anything).  Rows past the segment read other ring bytes, whose sums the caller discards.
 template <int K, int N, class CT>
-__device__ __forceinline__ void dots_n(const CT& C, uint32_t seg, int r0, const XChunks<K, 8>& x, float (&out)[N]) {
+__device__ __forceinline__ void ring_rows(const CT& C, uint32_t seg, int r0, uint4 (&w)[N][Chunks<K>::CPL]) {
   constexpr int CPL = Chunks<K>::CPL, CH = Chunks<K>::CH;
   const bool tail_ok = CH % 64 == 0 || C.lane + 64 * (CPL - 1) < CH;
-  uint4 w[N][CPL];
 #pragma unroll
   for (int r = 0; r < N; ++r)
 #pragma unroll
@@ -516,6 +538,53 @@ __device__ __forceinline__ void dots_n(const CT& C, uint32_t seg, int r0, const 
       const uint32_t at = seg + uint32_t(r0 + r) * uint32_t(K * 2) + uint32_t(C.lane + 64 * c) * 16u;
       w[r][c] = c == CPL - 1 ? C.ring16z(at, tail_ok) : C.ring16(at);
     }
+}
+
+// The same chunks rebuilt from a lossless segment set: plane rows (K bytes each) at segp, header rows
+// (K/8 words) at segh, the escaped chunks of the segment's rows (ordinals first, first + 1, ...) at
+// segr.  Every chunk is rebuilt (an escaped one's result is then replaced by its raw chunk), so the
+// words are the dense ones bit for bit; lanes past a row's last chunk get zeros, as from the zero line.
+template <int K, int N, class CT>
+__device__ __forceinline__ void lossless_rows(const CT& C, uint32_t segp, uint32_t segh, uint32_t segr, uint32_t first,
+                                              int r0, uint4 (&w)[N][Chunks<K>::CPL]) {
+  constexpr int CPL = Chunks<K>::CPL, CH = Chunks<K>::CH;
+  const bool tail_ok = CH % 64 == 0 || C.lane + 64 * (CPL - 1) < CH;
+  uint2 pl[N][CPL];
+  uint32_t hd[N][CPL];
+#pragma unroll
+  for (int r = 0; r < N; ++r)
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const uint32_t row = uint32_t(r0 + r), ch = uint32_t(C.lane + 64 * c);
+      hd[r][c] = C.ring4(segh + (row * uint32_t(CH) + ch) * 4u);
+      pl[r][c] = C.ring8(segp + row * uint32_t(K) + ch * 8u);
+    }
+#pragma unroll
+  for (int r = 0; r < N; ++r)
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      w[r][c] = lossless_chunk(pl[r][c], hd[r][c]);
+      asm volatile("" : "+v"(w[r][c].x), "+v"(w[r][c].y), "+v"(w[r][c].z), "+v"(w[r][c].w));
+    }
+#pragma unroll
+  for (int r = 0; r < N; ++r)
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const uint32_t h = hd[r][c];
+      const bool esc = (h >> 24) == 255u;
+      const uint4 e = C.ring16(segr + (esc ? (h & 0xFFFFFFu) - first : 0u) * 16u);
+      const bool ok = c < CPL - 1 || tail_ok;
+      w[r][c].x = !ok ? 0u : esc ? e.x : w[r][c].x;
+      w[r][c].y = !ok ? 0u : esc ? e.y : w[r][c].y;
+      w[r][c].z = !ok ? 0u : esc ? e.z : w[r][c].z;
+      w[r][c].w = !ok ? 0u : esc ? e.w : w[r][c].w;
+    }
+}
+
+// out[r] = w[r] . x over a lane's chunks, totals over the wave, returned wave-uniform.
+template <int K, int N>
+__device__ __forceinline__ void dots_w(const uint4 (&w)[N][Chunks<K>::CPL], const XChunks<K, 8>& x, float (&out)[N]) {
+  constexpr int CPL = Chunks<K>::CPL;
 #pragma unroll
   for (int r = 0; r < N; ++r) {
     float acc = 0.f;
@@ -529,6 +598,13 @@ __device__ __forceinline__ void dots_n(const CT& C, uint32_t seg, int r0, const 
     out[r] = acc;
   }
   wave_rows<N>(out);
+}
+
+template <int K, int N, class CT>
+__device__ __forceinline__ void dots_n(const CT& C, uint32_t seg, int r0, const XChunks<K, 8>& x, float (&out)[N]) {
+  uint4 w[N][Chunks<K>::CPL];
+  ring_rows<K, N>(C, seg, r0, w);
+  dots_w<K, N>(w, x, out);
 }
 
 // Partial dots over one wave's quarter of K (chunks [w CH/4, (w+1) CH/4) of each row, chunk
@@ -1006,9 +1082,14 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
       const int l = k - 1;
       // ---- RMSNorm(h1) + gate/up + SwiGLU of layer l ----
       C.refresh();
+      const GUE& ge = sm.gue[l];
       const uint32_t segn = C.next_seg(sr_bytes(P, R_NORM2, 0));
-      const uint32_t segg = C.next_seg(sr_bytes(P, R_GATE, 0));
-      const uint32_t segu = C.next_seg(sr_bytes(P, R_UP, 0));
+      const uint32_t segg = C.next_seg(sr_bytes(P, R_GATE, 0, &ge));
+      const uint32_t segg_h = C.next_seg(sr_bytes(P, R_GATE_H, 0, &ge));
+      const uint32_t segg_r = C.next_seg(sr_bytes(P, R_GATE_R, 0, &ge));
+      const uint32_t segu = C.next_seg(sr_bytes(P, R_UP, 0, &ge));
+      const uint32_t segu_h = C.next_seg(sr_bytes(P, R_UP_H, 0, &ge));
+      const uint32_t segu_r = C.next_seg(sr_bytes(P, R_UP_R, 0, &ge));
       C.wait_filled(C.pos);
       XChunks<G::H, 8> nw;
       normw<G::H>(C, nw, segn);
@@ -1023,9 +1104,15 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
         // gate rows of units 0 .. n-1, then up rows of the same units: one 6-row item per wave
         const int nunits = P.au1 - P.au0;
         if (C.cw < 2 * nunits) {
-          const int j = C.cw % nunits;
+          const int j = C.cw % nunits, m = C.cw < nunits ? 0 : 1;
           float o[VPU];
-          dots_n<G::H, VPU>(C, C.cw < nunits ? segg : segu, j * VPU, x, o);
+          uint4 w[VPU][Chunks<G::H>::CPL];
+          if (ge.on)  // the dense words rebuilt from the lossless stream (bit-identical)
+            lossless_rows<G::H, VPU>(C, m ? segu : segg, m ? segu_h : segg_h, m ? segu_r : segg_r, ge.first[m],
+                                     j * VPU, w);
+          else
+            ring_rows<G::H, VPU>(C, m ? segu : segg, j * VPU, w);
+          dots_w<G::H, VPU>(w, x, o);
           if (C.lane == 0)
 #pragma unroll
             for (int e = 0; e < VPU; ++e) sm.part[C.cw][e] = o[e];
@@ -1327,15 +1414,32 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_sr(Params p, uint32_t* r
     sm.go = 0;
     sm.loc_l2 = 0;
   }
+  PlanSR<G> P;
+  P.init(p, blockIdx.x);
   for (int i = threadIdx.x; i < p.n_layers; i += WG_THREADS) {
     const void* const* t = p.layers + size_t(i) * 6;
     LayerW w{};
     w.norm1 = t[0]; w.qkv = t[1]; w.o = t[2]; w.norm2 = t[3]; w.gate_up = t[4]; w.down = t[5];
     sm.lw[i] = w;
     sm.kvp[i] = p.kv[i];
+    // lossless gate/up (SmolLM2-360M): this workgroup's act rows [a0, a1) of each matrix and their escapes
+    GUE e{};
+    if (p.encoded_gu != nullptr && !P.a && P.a1 > P.a0) {
+      const EncodedGULayer d = p.encoded_gu[i];
+      if (*d.enabled != 0u) {
+        e.plane = d.plane;
+        e.hdr = d.headers;
+        e.raw = d.raw;
+        e.on = 1u;
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          e.first[m] = d.row_offsets[m * G::I + P.a0];
+          e.cnt[m] = d.row_offsets[m * G::I + P.a1] - e.first[m];
+        }
+      }
+    }
+    sm.gue[i] = e;
   }
-  PlanSR<G> P;
-  P.init(p, blockIdx.x);
   if (P.att) {
     const int nb = (P.t1 > P.t0) ? ((P.t1 - 1) / 16 - P.t0 / 16 + 1) : 0;
     for (int i = threadIdx.x; i < nb; i += WG_THREADS) sm.blk[i] = p.block_table[P.t0 / 16 + i];

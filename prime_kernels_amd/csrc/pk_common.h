@@ -449,6 +449,39 @@ __device__ __forceinline__ void skew_delay(uint32_t seed, int wg, int l, int sit
   for (uint32_t k = h % 24u; k > 0u; --k) __builtin_amdgcn_s_sleep(8);
 }
 
+// A layer's lossless gate/up encoding as this workgroup streams it (on = 0: dense gate/up): the
+// plane / header / escape arrays, and for gate (0) and up (1) the first escape ordinal of the
+// workgroup's rows and their number of escapes.
+struct GUE {
+  const uint8_t* plane;
+  const uint32_t* hdr;
+  const uint16_t* raw;
+  uint32_t on;
+  uint32_t first[2];
+  uint32_t cnt[2];
+};
+
+// The 8 bf16 words (4 packed pairs) of a lossless chunk: plane bytes p (sign | mantissa) and the
+// header's base exponent and 3-bit deltas give word_i = (p_i & 0x80) << 8 | (base + d_i) << 7 |
+// (p_i & 0x7f) (prime_kernels/lossless_bf16/csrc/lossless_bf16.cu:94-101).  Per pair of words,
+// in one register: v_perm copies plane bytes 2j, 2j+1 into both bytes of the low / high half, so
+// one mask keeps each sign at bit 15 / 31 and each mantissa at bits 0-6 / 16-22; the pair's 6 delta
+// bits d times 0x100080 is d << 7 | d << 20, whose bits 7-9 and 23-25 are the two deltas in
+// exponent position; the base exponent is added to both halves at once.  No field overflows into
+// the next: every exponent of a plain chunk is at most 254 + 7 < 256.
+__device__ __forceinline__ uint4 lossless_chunk(uint2 p, uint32_t h) {
+  const uint32_t base7 = (h >> 24) * 0x00800080u;
+  uint32_t out[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t t = __builtin_amdgcn_perm(0u, j < 2 ? p.x : p.y, (j & 1) ? 0x03030202u : 0x01010000u);
+    const uint32_t d = __builtin_amdgcn_ubfe(h, 6 * j, 6);
+    const uint32_t e7 = (__umul24(d, 0x100080u) & 0x03800380u) + base7;
+    out[j] = (t & 0x807F807Fu) | e7;
+  }
+  return make_uint4(out[0], out[1], out[2], out[3]);
+}
+
 // Index field values of a workgroup's end record: one of its waits gave up / no LM head.
 constexpr uint32_t LM_DEAD = 0xffffu, LM_NONE = 0xfffeu;
 constexpr int G_HMAX = 960;

@@ -22,8 +22,7 @@ def golden_dir() -> Path:
 def general_kernel():
     """Batch-1 steps on the general kernel for the test (the split-role kernel, the default for
     contexts up to its limit, sums in another order): for tests that compare a batch-1 step bit for
-    bit with a path only the general kernel has (per-stage debug capture, lossless gate/up, the
-    single-block ABI)."""
+    bit with a path only the general kernel has (per-stage debug capture, the single-block ABI)."""
     import torch
 
     if not torch.cuda.is_available():

@@ -11,9 +11,21 @@ from oracle import lossless as LZ
 from oracle import smollm2 as O
 from tests import gpu_cases as GC
 
-# batch-1 steps run on the general kernel, the only one with this path, so that the plain steps
-# compared with it bit for bit use the same arithmetic
-pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("general_kernel")]
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(params=["split_role", "general"])
+def batch1_kernel(request):
+    """Both batch-1 kernels stream the encoding; each must match its own dense step bit for bit."""
+    if not torch.cuda.is_available():
+        yield request.param
+        return
+    from prime_kernels_amd import _native
+
+    lib = _native.library()
+    old = lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, 1 if request.param == "split_role" else 0)
+    yield request.param
+    lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, old)
 
 ROWS, COLS = 5120, 960
 
@@ -192,7 +204,7 @@ def _step(mod, model, embed, final_norm, layers, kv, cos_sin, ids, ctx, lossless
 
 
 @pytest.mark.parametrize("n_layers,ctx", [(2, 300), (32, 1024)])
-def test_lossless_step_bit_identical_to_dense(n_layers, ctx):
+def test_lossless_step_bit_identical_to_dense(n_layers, ctx, batch1_kernel):
     _need_gpu()
     import prime_kernels_amd as pk
     from prime_kernels_amd import workload as WL
@@ -221,7 +233,7 @@ def test_lossless_step_bit_identical_to_dense(n_layers, ctx):
         assert all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(kv_d, kv.caches)), step
 
 
-def test_lossless_step_with_a_disabled_layer_and_module_api():
+def test_lossless_step_with_a_disabled_layer_and_module_api(batch1_kernel):
     """A layer whose escapes overflowed reads its dense matrix; the module's prepare / refresh /
     statistics / decode_step surface; still bit-identical to the dense step."""
     _need_gpu()
@@ -231,6 +243,7 @@ def test_lossless_step_with_a_disabled_layer_and_module_api():
     mod = pk.load("decode_megakernel_360m_lossless")
     dense = pk.load("decode_megakernel_360m")
     model, embed, final_norm, layers = _model_360m(51)
+    mod._caches._by_device.clear()  # a device's cache is bound to one set of tensors; these are new
     cache = mod.prepare_weights(layers)
     assert mod.prepare_weights(layers) is cache
     gu1 = layers[1][4]
@@ -257,7 +270,7 @@ def test_lossless_step_with_a_disabled_layer_and_module_api():
     assert torch.equal(hd.view(torch.int16), hl.view(torch.int16))
 
 
-def test_lossless_two_layers_against_oracle():
+def test_lossless_two_layers_against_oracle(batch1_kernel):
     """The lossless step against the CPU oracle on the same (CPU-drawn) weights and cache."""
     _need_gpu()
     import prime_kernels_amd as pk
