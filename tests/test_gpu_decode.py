@@ -178,7 +178,12 @@ def test_block360_config1_stages(golden):
     out = res["layer_outputs"][0, 0].float()
     want = from_bits(g["out"]).float()
     cos = torch.nn.functional.cosine_similarity(out, want, dim=0).item()
-    assert cos >= GC.COS_MIN and (out - want).abs().max().item() <= 0.1, cos
+    # the bar of the per-stage block test: within 2^-6 relative plus 2e-3 of the vector's scale
+    tol = 2 ** -6 * want.abs() + 2e-3 * want.abs().max()
+    err = (out - want).abs()
+    print("config-1 block via decode_step: max abs", err.max().item(), "identical",
+          GC.identical_fraction(out, want), "cos", cos)
+    assert cos >= GC.COS_MIN and bool((err <= tol).all()), (cos, err.max().item())
     slot = kv.slot(0, ctx)
     got = case.kvd[0][slot // 16, :, slot % 16].cpu().float()
     assert torch.allclose(got[:, :64], from_bits(g["k_rot"]).float(), rtol=2 ** -6, atol=2e-2)

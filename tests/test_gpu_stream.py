@@ -1,0 +1,186 @@
+"""Full-depth 256-step token streams against the oracle: BASELINE configs 2, 3 and 5.
+
+Each config is "a prompt, then 256 generated tokens" at batch 1 on the whole model
+(research/smollm2_360m_decode/validation-summary.json:22-28 reports the reference's own stream
+validation).  Three implementations run the same stream side by side, each keeping its own paged KV
+cache from the same initial fill: the HIP kernel (through the package's decode_step), the CPU oracle
+(oracle/smollm2.py) and the oracle's algorithm on GPU tensors in PyTorch eager ("eager-GPU": the same
+rounding points, another accumulation order).  The token stream is teacher-forced: step t+1 feeds
+the oracle's greedy id of step t to all three, so they see identical inputs while their caches
+evolve independently.  The prompt's keys and values are a seeded N(0, 1) fill of the cache (the
+workload of the benchmark), not a prefill pass.
+
+Per step the test records the logits error and cosine of the kernel and of eager-GPU against the
+oracle, whether each one's greedy id equals the oracle's, and the oracle's top-1 minus top-2 margin
+wherever one of them differs.  The bar:
+  * logits: every step within max(LOGIT_ATOL, FLOOR_FACTOR x the largest eager-GPU error of the
+    stream); mean error within max(LOGIT_ATOL / 2, MEAN_FACTOR x eager-GPU's mean error); cosine at
+    every step at least min(COS_MIN, 1 - FLOOR_FACTOR x (1 - eager-GPU's lowest cosine));
+  * greedy ids: equal to the oracle's at every step whose oracle margin exceeds that logits bound
+    (no near-tie escape above it), and flips at near-ties at most MISS_FACTOR x eager-GPU's count
+    plus MISS_SLACK (random-init logits are flat: most steps' top-2 margin is a few bf16 ulps);
+  * the whole cache, every layer: slots the stream never wrote bit-identical to the initial fill
+    (no stray writes), the written slots within max(bf16 KV tolerance, FLOOR_FACTOR x eager-GPU's
+    error on the same layer).
+With PK_STREAM_REPORT set to a directory, every step's figures are written there as JSON.
+"""
+
+from __future__ import annotations
+
+import json
+import os
+import time
+
+import pytest
+import torch
+
+from oracle import smollm2 as O
+from tests import gpu_cases as GC
+
+pytestmark = pytest.mark.gpu
+
+STEPS = 256
+FLOOR_FACTOR = GC.FLOOR_FACTOR
+MEAN_FACTOR = 1.5
+MISS_FACTOR, MISS_SLACK = 2, 8       # greedy flips at near-ties: at most 2x eager-GPU's count + 8
+KV_RTOL, KV_ATOL = 2 ** -6, 2e-2     # one appended K/V row (bf16), as the per-step append checks
+
+
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+def _margin(logits: torch.Tensor, best: int) -> float:
+    """Top-1 minus the best other logit (0 at a tie; the greedy id is the first maximal index)."""
+    v = logits.float().clone()
+    top = v[best].item()
+    v[best] = -float("inf")
+    return top - v.max().item()
+
+
+def _compare(got: torch.Tensor, want: torch.Tensor) -> tuple[float, float]:
+    g, w = got.float(), want.float()
+    return (g - w).abs().max().item(), torch.nn.functional.cosine_similarity(g, w, dim=0).item()
+
+
+def _stream(case: GC.Case, context: int, first_token: int, label: str) -> dict:
+    """Run STEPS teacher-forced steps from position `context`; return the per-step report and the
+    three caches' final state."""
+    geom = case.geom
+    eager_kv = O.PagedKV([c.to(case.dev) for c in case.kv.caches], case.btd, case.kv.block_size)
+    eager_w = O.Weights(geom, case.wd.embed, case.wd.final_norm, case.wd.layers)
+    initial = [c.clone() for c in case.kv.caches]
+    tok, rows = first_token, []
+    t0 = time.time()
+    for s in range(STEPS):
+        pos = context + s
+        k = case.kernel_step([tok], [pos])
+        e = O.decode_step(eager_w, [tok], [pos], eager_kv, case.csd)
+        r = case.oracle_step([tok], [pos])
+        ref = r["logits"][0]
+        best = int(r["ids"][0])
+        margin = _margin(ref, best)
+        k_err, k_cos = _compare(k["logits"][0], ref)
+        e_err, e_cos = _compare(e["logits"][0].cpu(), ref)
+        k_id, e_id = int(k["ids"][0]), int(e["ids"][0])
+        rows.append({"step": s, "token": tok, "oracle_id": best, "oracle_margin": round(margin, 5),
+                     "kernel_err": round(k_err, 5), "kernel_cos": round(k_cos, 7), "kernel_id": k_id,
+                     "eager_err": round(e_err, 5), "eager_cos": round(e_cos, 7), "eager_id": e_id})
+        tok = best
+    print(f"{label}: {STEPS} steps in {time.time() - t0:.1f} s", flush=True)
+    return {"rows": rows, "initial": initial, "eager_kv": [c.cpu() for c in eager_kv.caches]}
+
+
+def _written_mask(case: GC.Case, context: int, shape) -> torch.Tensor:
+    """[blocks, block_size] True where the stream appended (positions context .. context+STEPS-1)."""
+    mask = torch.zeros((shape[0], shape[1]), dtype=torch.bool)
+    for pos in range(context, context + STEPS):
+        slot = case.kv.slot(0, pos)
+        mask[slot // case.kv.block_size, slot % case.kv.block_size] = True
+    return mask
+
+
+def _check(case: GC.Case, context: int, out: dict, label: str) -> dict:
+    rows = out["rows"]
+    k_err = torch.tensor([r["kernel_err"] for r in rows])
+    e_err = torch.tensor([r["eager_err"] for r in rows])
+    bound = max(GC.LOGIT_ATOL, FLOOR_FACTOR * e_err.max().item())
+    mean_bound = max(GC.LOGIT_ATOL / 2, MEAN_FACTOR * e_err.mean().item())
+    cos_min = min(GC.COS_MIN, 1.0 - FLOOR_FACTOR * (1.0 - min(r["eager_cos"] for r in rows)))
+    k_miss = [r for r in rows if r["kernel_id"] != r["oracle_id"]]
+    e_miss = [r for r in rows if r["eager_id"] != r["oracle_id"]]
+    summary = {
+        "label": label, "steps": STEPS, "context": context,
+        "kernel": {"max_err": k_err.max().item(), "mean_err": k_err.mean().item(),
+                   "min_cos": min(r["kernel_cos"] for r in rows), "argmax_agree": STEPS - len(k_miss),
+                   "mismatch_margins": [r["oracle_margin"] for r in k_miss]},
+        "eager_gpu": {"max_err": e_err.max().item(), "mean_err": e_err.mean().item(),
+                      "min_cos": min(r["eager_cos"] for r in rows), "argmax_agree": STEPS - len(e_miss),
+                      "mismatch_margins": [r["oracle_margin"] for r in e_miss]},
+        "bounds": {"logits_max": bound, "logits_mean": mean_bound, "cos_min": cos_min},
+    }
+    # whole cache, every layer (checked after the report is written)
+    layers = []
+    for li, (kc, oc, ec, init) in enumerate(zip(case.kvd, case.kv.caches, out["eager_kv"], out["initial"])):
+        # [blocks, block_size, kv_heads, 2D]: one row per slot
+        kc, oc, ec, init = (t.permute(0, 2, 1, 3) for t in (kc.cpu(), oc, ec, init))
+        mask = _written_mask(case, context, kc.shape)
+        kw, ow, ew = kc[mask].float(), oc[mask].float(), ec[mask].float()
+        e_kv = (ew - ow).abs().max().item()
+        tol = torch.maximum(KV_RTOL * ow.abs() + KV_ATOL, torch.full_like(ow, FLOOR_FACTOR * e_kv))
+        layers.append({"layer": li, "kernel_err": round((kw - ow).abs().max().item(), 5), "eager_err": round(e_kv, 5),
+                       "within": bool(((kw - ow).abs() <= tol).all()),
+                       "untouched_equal": torch.equal(kc[~mask].view(torch.int16), init[~mask].view(torch.int16)),
+                       "oracle_untouched_equal": torch.equal(oc[~mask].view(torch.int16), init[~mask].view(torch.int16))})
+    summary["cache_layers"] = layers
+    report_dir = os.environ.get("PK_STREAM_REPORT")
+    if report_dir:
+        os.makedirs(report_dir, exist_ok=True)
+        with open(os.path.join(report_dir, f"{label}.json"), "w") as f:
+            json.dump({"summary": summary, "steps": rows}, f)
+    print(json.dumps({k: v for k, v in summary.items() if k != "cache_layers"}), flush=True)
+    # the bar
+    for c in layers:
+        assert c["untouched_equal"], f"{label}: layer {c['layer']}: a slot outside the stream's appends changed"
+        assert c["oracle_untouched_equal"]
+        assert c["within"], f"{label}: layer {c['layer']}: appended K/V off the oracle: {c}"
+    assert k_err.max().item() <= bound, f"{label}: logits error {k_err.max().item()} > {bound}"
+    assert k_err.mean().item() <= mean_bound, f"{label}: mean logits error {k_err.mean().item()} > {mean_bound}"
+    assert summary["kernel"]["min_cos"] >= cos_min, f"{label}: logits cosine below {cos_min}"
+    hard = [r for r in k_miss if r["oracle_margin"] > bound]
+    assert not hard, f"{label}: greedy ids differ at steps with a resolvable oracle margin: {hard[:4]}"
+    # near-tie flips are as frequent as a second accumulation order makes them, not systematically more
+    assert len(k_miss) <= MISS_FACTOR * len(e_miss) + MISS_SLACK, \
+        f"{label}: {len(k_miss)} greedy flips against eager-GPU's {len(e_miss)}"
+    return summary
+
+
+def _run(case: GC.Case, context: int, first_token: int, label: str) -> dict:
+    out = _stream(case, context, first_token, label)
+    return _check(case, context, out, label)
+
+
+def test_stream_config2_135m_ctx512():
+    """SmolLM2-135M (30 layers), 512-token prompt, 256 generated tokens."""
+    _need_gpu()
+    ctx = 512
+    case = GC.random_kv_case(O.SMOLLM2_135M, 2002, [ctx], capacity=ctx + STEPS + 16, norm_jitter=0.0)
+    _run(case, ctx, 4321, "stream_135m_ctx512")
+
+
+def test_stream_config3_360m_ctx1024():
+    """SmolLM2-360M (32 layers), 1024-token prompt, 256 generated tokens."""
+    _need_gpu()
+    ctx = 1024
+    case = GC.random_kv_case(O.SMOLLM2_360M, 3003, [ctx], capacity=ctx + STEPS + 16, norm_jitter=0.0)
+    _run(case, ctx, 1234, "stream_360m_ctx1024")
+
+
+def test_stream_config5_360m_mxfp8_ctx8192():
+    """SmolLM2-360M with MXFP8 linear weights, 8192-token prompt, 256 generated
+    tokens.  The oracle and eager-GPU run the exact bf16 dequantisation of the kernel's codes."""
+    _need_gpu()
+    ctx = 8192
+    case = GC.mxfp8_case(O.SMOLLM2_360M, 5005, [ctx + STEPS], norm_jitter=0.0)
+    _run(case, ctx, 777, "stream_360m_mxfp8_ctx8192")
