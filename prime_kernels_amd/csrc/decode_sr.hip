@@ -47,7 +47,10 @@ constexpr int VPU = 6;                   // bf16 values per 16-byte unit
 constexpr int REP = PK_SR_REP;           // copies of each cross-XCD unit
 constexpr int UPL = PK_SR_UPL;           // cross-XCD units per 64-byte line (fewer: fewer polls per line)
 constexpr int TCS = 256;                 // max cached tokens per attention chunk
-constexpr int DEPTH_SR = 8;              // DMA packets in flight per producer wave
+#ifndef PK_SR_DEPTH
+#define PK_SR_DEPTH 8
+#endif
+constexpr int DEPTH_SR = PK_SR_DEPTH;    // DMA packets in flight per producer wave
 constexpr int LM_ROWS_SR = 16;           // LM-head rows per ring segment
 
 __device__ __forceinline__ bool in_a(int wg) { return (wg & 7) == 0; }
@@ -116,6 +119,8 @@ __device__ __forceinline__ float rms_rsq(float sumsq) {
 
 static_assert((SG<G360>::IU + FG - 1) / FG <= 2 && (SG<G135>::IU + FG - 1) / FG <= 2,
               "the gate/up phase gives each wave one 6-row item: at most 2 act units per F workgroup");
+static_assert((SG<G360>::QU + FG - 1) / FG <= NCW && (SG<G135>::QU + FG - 1) / FG <= NCW,
+              "the QKV phase gives each wave at most one unit");
 
 template <class G>
 struct PlanSR {
@@ -216,8 +221,6 @@ struct SmemSR {
   static constexpr int XS = G::I > G::H ? G::I : G::H;
   struct Attn {
     float qkvw[NCW][5 * 64];     // per-wave attention inputs (3 q heads, k_new, v_new; pre-RoPE)
-    float sc[3][TCS + 4];        // per-head scores
-    uint16_t pb[3][TCS + 4];     // per-head probabilities (bf16)
     float ao[3][64];             // leader: the merged attention output of its 3 heads
   };
   uint8_t ring[RING];
@@ -256,6 +259,7 @@ __device__ __forceinline__ void producer_sr(const Params& p, const PlanSR<G>& P,
   const int lane = threadIdx.x & 63;
   const uint32_t ring_base = uint32_t(reinterpret_cast<uintptr_t>(sm.ring));
   uint32_t n = 0;  // global packet index at the start of the current segment
+  uint32_t room = RING;  // ring bytes the consumers have released, plus the ring size
   Spin spin(p.ws, epoch, 21);
   bool dead = false;
   auto cmin = [&]() -> uint32_t {
@@ -296,12 +300,17 @@ __device__ __forceinline__ void producer_sr(const Params& p, const PlanSR<G>& P,
     }
     for (uint32_t i = (uint32_t(pw) + NPW - n % NPW) % NPW; i < npk && !dead; i += NPW) {
       const uint32_t gn = n + i;
-      if ((gn + 1) * PKT > cmin() + RING) {
-        wait_vmcnt<0>();
-        publish(gn);
-        while ((gn + 1) * PKT > cmin() + RING)
-          if (!spin.again()) { dead = true; break; }
-        if (dead) break;
+      // ring space: `room` is the end of the free ring as last read; the consumers' counters are read
+      // again only when a packet would pass it
+      if ((gn + 1) * PKT > room) {
+        room = cmin() + RING;
+        if ((gn + 1) * PKT > room) {
+          wait_vmcnt<0>();
+          publish(gn);
+          while ((gn + 1) * PKT > (room = cmin() + RING))
+            if (!spin.again()) { dead = true; break; }
+          if (dead) break;
+        }
       }
       const uint32_t off = i * PKT + uint32_t(lane) * 16u;
       const uint8_t* src;
@@ -615,11 +624,9 @@ struct Quarter {
   static_assert(CH % NCW == 0, "K splits evenly over the waves");
 };
 template <int K, int N, class CT>
-__device__ __forceinline__ void dots_quarter(const CT& C, uint32_t seg, int r0, const uint4 (&x)[Quarter<K>::CPL],
-                                             float (&out)[N]) {
+__device__ __forceinline__ void quarter_rows(const CT& C, uint32_t seg, int r0, uint4 (&w)[N][Quarter<K>::CPL]) {
   using Q = Quarter<K>;
   const bool tail_ok = Q::CHW % 64 == 0 || C.lane + 64 * (Q::CPL - 1) < Q::CHW;
-  uint4 w[N][Q::CPL];
 #pragma unroll
   for (int r = 0; r < N; ++r)
 #pragma unroll
@@ -627,6 +634,11 @@ __device__ __forceinline__ void dots_quarter(const CT& C, uint32_t seg, int r0, 
       const uint32_t at = seg + uint32_t(r0 + r) * uint32_t(K * 2) + uint32_t(C.cw * Q::CHW + C.lane + 64 * c) * 16u;
       w[r][c] = c == Q::CPL - 1 ? C.ring16z(at, tail_ok) : C.ring16(at);
     }
+}
+template <int K, int N>
+__device__ __forceinline__ void dots_quarter_w(const uint4 (&w)[N][Quarter<K>::CPL], const uint4 (&x)[Quarter<K>::CPL],
+                                               float (&out)[N]) {
+  using Q = Quarter<K>;
 #pragma unroll
   for (int r = 0; r < N; ++r) {
     float acc = 0.f;
@@ -656,8 +668,111 @@ __device__ __forceinline__ void normw(const CT& C, XChunks<K, 8>& nw, uint32_t s
 // Group A: attention for one chunk (KV head g, chunk c), then the merge, O and h1
 // ------------------------------------------------------------------------------------------------
 
+// Total (sum, or max for MAX) of a value over the four 16-lane rows of a wave, for each of the 16
+// columns; every lane gets its column's total (one cross-half and one cross-row swap).
+template <bool MAX>
+__device__ __forceinline__ float column_total(float v) {
+  float a = v, b = v;
+  swap32(a, b);
+  v = comb<MAX>(a, b);
+  a = v;
+  b = v;
+  swap16(a, b);
+  return comb<MAX>(a, b);
+}
+
+// DPP row shifts by 3i lanes (i < 5, a compile-time constant after unrolling): row_shr moves lane
+// c - 3i to lane c, row_shl lane c + 3i to lane c, within each 16-lane row (lanes with no source get
+// -inf for the max variant, 0 otherwise).
+template <bool NEG_INF>
+__device__ __forceinline__ float dpp_shr3(int i, float v) {
+  const float o = NEG_INF ? -INFINITY : 0.f;
+  switch (i) {
+    case 1: return dpp<0x113>(o, v);
+    case 2: return dpp<0x116>(o, v);
+    case 3: return dpp<0x119>(o, v);
+    case 4: return dpp<0x11c>(o, v);
+    default: return v;
+  }
+}
+__device__ __forceinline__ uint32_t dpp_shl3u(int i, uint32_t v) {
+  const float f = __uint_as_float(v);
+  switch (i) {
+    case 1: return __float_as_uint(dpp<0x103>(0.f, f));
+    case 2: return __float_as_uint(dpp<0x106>(0.f, f));
+    case 3: return __float_as_uint(dpp<0x109>(0.f, f));
+    case 4: return __float_as_uint(dpp<0x10c>(0.f, f));
+    default: return v;
+  }
+}
+// Per-head totals (sum, or max for MAX) of the compacted layout: lane c of each row holds a value of
+// head c % 3 (c < 15; lane 15 must hold the identity).  Lanes c, c-3, c-6, c-9, c-12 are combined
+// within the row (lanes 12-14 then hold the row's totals of heads 0-2), the four rows are combined,
+// and the three totals come back wave-uniform.
+template <bool MAX>
+__device__ __forceinline__ void head_totals(float v, float (&out)[3]) {
+  v = comb<MAX>(v, dpp_shr3<MAX>(1, v));
+  v = comb<MAX>(v, dpp_shr3<MAX>(2, v));
+  v = comb<MAX>(v, dpp_shr3<MAX>(4, v));
+  v = column_total<MAX>(v);
+#pragma unroll
+  for (int h = 0; h < 3; ++h)
+    out[h] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 12 + h));
+}
+
+// 16-token tiles of a chunk, tile t to wave t % NCW: at most MT per wave
+constexpr int MT = (TCS + 1 + 16 * NCW - 1) / (16 * NCW);
+struct ChunkRegs {
+  uint32_t va[MT][4][2];    // V of the wave's tiles: A operands of the P.V tiles (bf16 pairs)
+};
+
+// The wave's V from the ring into registers, long before q arrives (the chunk was streamed in during
+// the previous layer; V needs one 2-byte read per element, K is loaded with 16-byte reads just
+// before q).  P.V uses v_mfma_f32_16x16x16_bf16 with V as the A operand, once per 16 dims: lane l
+// supplies V[tile*16 + 4(l/16) + e][16 mf + l%16], e < 4.  Cached tokens only (the new token is
+// handled apart): later elements are zero.  Reads past the chunk stay inside the ring.
 template <class G>
-__device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg) {
+__device__ __forceinline__ void chunk_load(CSR<G>& C, uint32_t seg, ChunkRegs& R) {
+  const PlanSR<G>& P = C.P;
+  SmemSR<G>& sm = C.sm;
+  const int w = C.cw, lane = C.lane;
+  const int T_old = P.t1 - P.t0;
+  const int NT = (T_old + 15) >> 4;
+  const int nt = NT > w ? (NT - w + NCW - 1) / NCW : 0;
+  const int hq = lane & 15, pq = lane >> 4;
+  // V element (mf, e) of this lane sits at byte tile*4096 + vo[mf][e] of the segment: token
+  // 4 pq + e of the tile, piece (dim / 8 + token) % 8 of the token's V half, dim 16 mf + hq
+  uint32_t vo[4][4];
+#pragma unroll
+  for (int mf = 0; mf < 4; ++mf)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      vo[mf][e] = uint32_t(4 * pq + e) * 256u + 128u + uint32_t((2 * mf + (hq >> 3) + 4 * pq + e) & 7) * 16u +
+                  uint32_t(hq & 7) * 2u;
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    if (i >= nt) continue;
+    const int tile = w + NCW * i;
+    const uint32_t base = seg + uint32_t(tile) * 4096u;
+    uint32_t h[4][4];
+#pragma unroll
+    for (int mf = 0; mf < 4; ++mf)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        h[mf][e] = *reinterpret_cast<const uint16_t*>(sm.ring + ((base + vo[mf][e]) & (RING - 1)));
+#pragma unroll
+    for (int mf = 0; mf < 4; ++mf) {
+      const int j = tile * 16 + 4 * pq;
+      const uint32_t v0 = j < T_old ? h[mf][0] : 0u, v1 = j + 1 < T_old ? h[mf][1] : 0u;
+      const uint32_t v2 = j + 2 < T_old ? h[mf][2] : 0u, v3 = j + 3 < T_old ? h[mf][3] : 0u;
+      R.va[i][mf][0] = v0 | (v1 << 16);
+      R.va[i][mf][1] = v2 | (v3 << 16);
+    }
+  }
+}
+
+template <class G>
+__device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, ChunkRegs& R) {
   using S = SG<G>;
   using W = SWS<G>;
   const Params& p = C.p;
@@ -665,12 +780,25 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg) {
   SmemSR<G>& sm = C.sm;
   const int g = P.g, lane = C.lane, w = C.cw;
   const int T_old = P.t1 - P.t0;
-  const int T = T_old + (P.leader ? 1 : 0);
-  // the waves take whole 16-token tiles of the chunk (the new token, at index T_old, included)
-  auto edge = [&](int k) { return k >= NCW ? T : ((T * k) / NCW) & ~15; };
-  const int j0 = edge(w), j1 = edge(w + 1);
-  const bool has_new = P.leader && j1 == T && T > j0;
+  // 16-token tiles of the chunk's cached tokens, tile t to wave t % NCW; the new token (the leader's)
+  // is taken apart by the last wave, which has the fewest tiles
+  const int NT = (T_old + 15) >> 4;
+  const int nt = NT > w ? (NT - w + NCW - 1) / NCW : 0;
+  const bool has_new = P.leader && w == NCW - 1;
+  const int hq = lane & 15, pq = lane >> 4;
   float* in = sm.at.qkvw[w];
+  uint32_t (&va)[MT][4][2] = R.va;
+  // K of the wave's tiles, the A operands of the score tiles (v_mfma_f32_16x16x32_bf16): lane l
+  // supplies row l%16 (token tile*16 + l%16), dims 8(l/16) .. +7 and 32 + 8(l/16) .. +7
+  uint4 ka[MT][2];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    if (i >= nt) continue;
+    const int tok = (w + NCW * i) * 16 + hq;
+    const uint32_t row = seg + uint32_t(tok) * 256u;
+    ka[i][0] = C.ring16(row + uint32_t((pq + tok) & 7) * 16u);
+    ka[i][1] = C.ring16(row + uint32_t((pq + 4 + tok) & 7) * 16u);
+  }
   // q of the 3 heads of KV head g (units 32g .. 32g + 31), and for the wave with the new token the
   // units holding its k and v rows
   {
@@ -702,12 +830,12 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg) {
                        30);
   }
   if (w == 0 && lane == 0) trace_at(p, l, 34, p.n_layers);
-  C.wait_filled(C.pos);  // the KV chunk is in the ring (streamed long before)
+  if (has_new && lane == 0) trace_at(p, l, 38, p.n_layers);
   wait_lgkm0();
   if (w == 0 && lane == 0) trace_at(p, l, 3, p.n_layers);
+  if (has_new && lane == 0) trace_at(p, l, 4, p.n_layers);
   // RoPE of pieces pq (dims 8pq..8pq+7) and pq + 4 (dims 32+8pq..) of head hq < 3, and of k_new
   // (HF: bf16(bf16(x cos) + bf16(rotate_half(x) sin)))
-  const int hq = lane & 15, pq = lane >> 4;
   float cs8[8], sn8[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -736,68 +864,93 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg) {
   uint32_t qlo[4] = {0u, 0u, 0u, 0u}, qhi[4] = {0u, 0u, 0u, 0u};
   if (hq < 3) rope_pair(in + hq * 64, qlo, qhi);
   uint32_t klo[4] = {0u, 0u, 0u, 0u}, khi[4] = {0u, 0u, 0u, 0u};
-  if (has_new) rope_pair(in + 192, klo, khi);
+  // the new token's scores q_h . k_new: lane (h, pq) dots pieces pq and pq + 4, the four rows add up
+  float s_new[3] = {-INFINITY, -INFINITY, -INFINITY};
+  if (has_new) {
+    rope_pair(in + 192, klo, khi);
+    float d = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      d = dot2(qlo[i], klo[i], d);
+      d = dot2(qhi[i], khi[i], d);
+    }
+    d = column_total<false>(d);
+#pragma unroll
+    for (int h = 0; h < 3; ++h)
+      s_new[h] = rnd(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, d), h))) * 0.125f;
+  }
   if (w == 0 && lane == 0) trace_at(p, l, 35, p.n_layers);
-  // Scores on the matrix cores, D[token][head] = K[token][:] . q[head][:] per 16-token tile
-  // (v_mfma_f32_16x16x32_bf16, two k-steps over the 64 dimensions).  Lane l supplies row l%16 of A
-  // (token tile + l%16: pieces pq and pq + 4 of its K from the ring, or k_new) and column l%16 of B
-  // (q of head l%16 < 3, zero for the padding columns) and receives D[4 pq + jj][hq].  Tokens past
-  // the chunk read other ring bytes; only their own rows of D, which are not stored, see them.
+  if (has_new && lane == 0) trace_at(p, l, 5, p.n_layers);
+  // Scores on the matrix cores, D[token][head] = K[token][:] . q[head][:] per tile (two k-steps over
+  // the 64 dims); lane l supplies column l%16 of B (q of head l%16 < 3, zero padding columns) and
+  // receives D[4(l/16) + jj][l%16], the score of head l%16 for token tile*16 + 4(l/16) + jj.  Rows
+  // of tokens past the chunk hold other ring bytes' products and are masked below.
+  floatx4 sacc[MT];
   {
     const bf16x8 bq0 = __builtin_bit_cast(bf16x8, make_uint4(qlo[0], qlo[1], qlo[2], qlo[3]));
     const bf16x8 bq1 = __builtin_bit_cast(bf16x8, make_uint4(qhi[0], qhi[1], qhi[2], qhi[3]));
-    for (int tb = j0; tb < j1; tb += 16) {
-      const int tok = tb + hq;
-      uint4 a0 = C.ring16(seg + uint32_t(tok) * 256u + uint32_t((pq + tok) & 7) * 16u);
-      uint4 a1 = C.ring16(seg + uint32_t(tok) * 256u + uint32_t((pq + 4 + tok) & 7) * 16u);
-      if (has_new && tok == T_old) {
-        a0 = make_uint4(klo[0], klo[1], klo[2], klo[3]);
-        a1 = make_uint4(khi[0], khi[1], khi[2], khi[3]);
-      }
-      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a0), bq0, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1), bq1, acc, 0, 0, 0);
-      if (hq < 3)
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int t = tb + 4 * pq + jj;
-          if (t < j1) sm.at.sc[hq][t] = rnd(acc[jj]) * 0.125f;
-        }
+    for (int i = 0; i < MT; ++i) {
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+      if (i < nt) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[i][0]), bq0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[i][1]), bq1, acc, 0, 0, 0);
+      }
+      sacc[i] = acc;
     }
   }
-  wait_lgkm0();
   if (w == 0 && lane == 0) trace_at(p, l, 36, p.n_layers);
-  // chunk softmax statistics per head, over this wave's tokens, then over the chunk.  ev keeps
-  // exp(s - m_wave) of the lane's tokens; once the head's global max M and sum L are known the
-  // probabilities are bf16(ev * exp(m_wave - M) / L), HF's bf16(exp(s - M) / L) up to fp32 rounding.
-  float ev[3][2], m3[3];
-#pragma unroll
-  for (int h = 0; h < 3; ++h)
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int j = j0 + lane + 64 * i;
-      ev[h][i] = j < j1 ? sm.at.sc[h][j] : -INFINITY;
-    }
+  if (has_new && lane == 0) trace_at(p, l, 9, p.n_layers);
+  // The wave's softmax statistics.  Only columns 0-2 of a score tile hold heads, so tile i's columns
+  // move to lanes 3i .. 3i+2 of each 16-lane row (DPP row_shr:3i): lane c of a row then holds the
+  // scores of head c % 3 in tile c / 3 (c < 3 MT), four tokens, and the exps below run on 4 values
+  // per lane instead of 4 MT.  Scores bf16(q.k) / 8 as HF; ev keeps exp(s - m_wave).  Once the
+  // head's global max M and sum L are known the probabilities are bf16(ev * exp(m_wave - M) / L),
+  // HF's bf16(exp(s - M) / L) up to fp32 rounding.
+  static_assert(3 * MT <= 16, "three columns per tile fit a 16-lane row");
+  const int ct = hq / 3, ch = hq - 3 * ct;
+  float ev[4];
   {
-    float l3[3];
 #pragma unroll
-    for (int h = 0; h < 3; ++h) m3[h] = fmaxf(ev[h][0], ev[h][1]);
-    wave_rows<3, true>(m3);
+    for (int jj = 0; jj < 4; ++jj) {
+      float v = sacc[0][jj];
+#pragma unroll
+      for (int i = 1; i < MT; ++i) {
+        const float t = dpp_shr3<true>(i, sacc[i][jj]);
+        v = ct == i ? t : v;
+      }
+      const int t = (w + NCW * ct) * 16 + 4 * pq + jj;
+      const bool ok = ct < nt && t < T_old;
+      ev[jj] = ok ? rnd(v) * 0.125f : -INFINITY;
+    }
+  }
+  float m = fmaxf(fmaxf(ev[0], ev[1]), fmaxf(ev[2], ev[3]));
+  float mw[3], lw[3];
+  head_totals<true>(m, mw);
+#pragma unroll
+  for (int h = 0; h < 3; ++h) mw[h] = fmaxf(mw[h], s_new[h]);
+  m = ch == 0 ? mw[0] : ch == 1 ? mw[1] : mw[2];
+  float lsum = 0.f;
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    ev[jj] = ev[jj] == -INFINITY ? 0.f : expf(ev[jj] - m);
+    lsum += ev[jj];
+  }
+  head_totals<false>(lsum, lw);
+  float ev_new[3];
+#pragma unroll
+  for (int h = 0; h < 3; ++h) {
+    ev_new[h] = s_new[h] == -INFINITY ? 0.f : expf(s_new[h] - mw[h]);
+    lw[h] += ev_new[h];
+  }
+  if (lane == 0)
 #pragma unroll
     for (int h = 0; h < 3; ++h) {
-      l3[h] = 0.f;
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        ev[h][i] = ev[h][i] == -INFINITY ? 0.f : expf(ev[h][i] - m3[h]);
-        l3[h] += ev[h][i];
-      }
+      sm.wml[w][0][h] = mw[h];
+      sm.wml[w][1][h] = lw[h];
     }
-    wave_rows<3>(l3);
-    if (lane == 0)
-#pragma unroll
-      for (int h = 0; h < 3; ++h) { sm.wml[w][0][h] = m3[h]; sm.wml[w][1][h] = l3[h]; }
-  }
   if (w == 0 && lane == 0) trace_at(p, l, 37, p.n_layers);
+  if (has_new && lane == 0) trace_at(p, l, 39, p.n_layers);
   C.cbar();
   float mq = -INFINITY, lq = 0.f;
   if (lane < 4 * 3) {
@@ -849,62 +1002,46 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg) {
     for (int h = 0; h < 3; ++h) { Mh[h] = M[h]; Lh[h] = s[h]; }
   }
   if (w == 0 && lane == 0) trace_at(p, l, 18, p.n_layers);
-  // probabilities with the global max and sum, rounded to bf16 before P.V as HF does
+  // P.V on the matrix cores with the probabilities rounded to bf16 as HF does.  The scores'
+  // accumulator layout is the B layout of v_mfma_f32_16x16x16_bf16 (lane l: head l%16, tokens
+  // tile*16 + 4(l/16) + e), so tile i's B operand is the compacted probabilities moved back from
+  // lanes 3i .. 3i+2 (DPP row_shl:3i); columns 3-15 of B and D are unused.  D[4(l/16) + j][l%16]
+  // accumulates dim 16 mf + 4(l/16) + j of head l%16 over the wave's tiles.
+  typedef short bf16x4_t __attribute__((ext_vector_type(4)));
+  floatx4 oacc[4];
 #pragma unroll
-  for (int h = 0; h < 3; ++h) {
-    const float scale = m3[h] == -INFINITY ? 0.f : expf(m3[h] - Mh[h]) * (1.0f / Lh[h]);
+  for (int mf = 0; mf < 4; ++mf) oacc[mf] = floatx4{0.f, 0.f, 0.f, 0.f};
+  {
+    const float Mq = ch == 0 ? Mh[0] : ch == 1 ? Mh[1] : Mh[2];
+    const float Lq = ch == 0 ? Lh[0] : ch == 1 ? Lh[1] : Lh[2];
+    const float scale = m != -INFINITY ? expf(m - Mq) * (1.0f / Lq) : 0.f;
+    const uint32_t p01 = pack2(ev[0] * scale, ev[1] * scale), p23 = pack2(ev[2] * scale, ev[3] * scale);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int j = j0 + lane + 64 * i;
-      if (j < j1) sm.at.pb[h][j] = uint16_t(f2bf(ev[h][i] * scale));
+    for (int i = 0; i < MT; ++i) {
+      if (i >= nt) continue;
+      const uint2 pb = make_uint2(dpp_shl3u(i, p01), dpp_shl3u(i, p23));
+#pragma unroll
+      for (int mf = 0; mf < 4; ++mf)
+        oacc[mf] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+            __builtin_bit_cast(bf16x4_t, make_uint2(va[i][mf][0], va[i][mf][1])), __builtin_bit_cast(bf16x4_t, pb),
+            oacc[mf], 0, 0, 0);
     }
-  }
-  wait_lgkm0();
-  // P.V: lane = (half, d2) owns dims 2*d2, 2*d2+1; token pairs alternate between the halves
-  const int half = lane >> 5, d2 = lane & 31;
-  const int jo1 = min(j1, T_old);
-  const int npairs = jo1 > j0 ? (jo1 - j0) / 2 : 0;
-  const uint32_t voff = uint32_t(d2 & 3) * 4u;
-  float acc[3][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
-  auto vslot = [&](int j) { return seg + uint32_t(j) * 256u + 128u + uint32_t(((d2 >> 2) + j) & 7) * 16u + voff; };
-#pragma unroll 4
-  for (int k = half; k < npairs; k += 2) {
-    const int j = j0 + 2 * k;
-    const uint32_t va = *reinterpret_cast<const uint32_t*>(sm.ring + (vslot(j) & (RING - 1)));
-    const uint32_t vb = *reinterpret_cast<const uint32_t*>(sm.ring + (vslot(j + 1) & (RING - 1)));
-    const uint32_t lo = __builtin_amdgcn_perm(vb, va, 0x05040100u);
-    const uint32_t hi = __builtin_amdgcn_perm(vb, va, 0x07060302u);
+    if (has_new && hq < 3) {
+      // the new token: p = bf16(exp(s_new - m_wave) exp(m_wave - M) / L) of head hq times its v
+      const float mh = hq == 0 ? mw[0] : hq == 1 ? mw[1] : mw[2];
+      const float en = hq == 0 ? ev_new[0] : hq == 1 ? ev_new[1] : ev_new[2];
+      const float Mn = hq == 0 ? Mh[0] : hq == 1 ? Mh[1] : Mh[2];
+      const float Ln = hq == 0 ? Lh[0] : hq == 1 ? Lh[1] : Lh[2];
+      const float pn = rnd(en * (expf(mh - Mn) * (1.0f / Ln)));
 #pragma unroll
-    for (int h = 0; h < 3; ++h) {
-      const uint32_t pp = *reinterpret_cast<const uint32_t*>(&sm.at.pb[h][j]);
-      acc[h][0] = dot2(pp, lo, acc[h][0]);
-      acc[h][1] = dot2(pp, hi, acc[h][1]);
-    }
-  }
-  if (half == 0) {
-    if (jo1 > j0 && ((jo1 - j0) & 1)) {
-      const int j = jo1 - 1;
-      const uint32_t v = *reinterpret_cast<const uint32_t*>(sm.ring + (vslot(j) & (RING - 1)));
-#pragma unroll
-      for (int h = 0; h < 3; ++h) {
-        const float pj = bf2f(sm.at.pb[h][j]);
-        acc[h][0] = fmaf(pj, bf_lo(v), acc[h][0]);
-        acc[h][1] = fmaf(pj, bf_hi(v), acc[h][1]);
+      for (int mf = 0; mf < 4; ++mf) {
+        const float4 v = *reinterpret_cast<const float4*>(in + 256 + 16 * mf + 4 * pq);
+        oacc[mf][0] = fmaf(pn, v.x, oacc[mf][0]);
+        oacc[mf][1] = fmaf(pn, v.y, oacc[mf][1]);
+        oacc[mf][2] = fmaf(pn, v.z, oacc[mf][2]);
+        oacc[mf][3] = fmaf(pn, v.w, oacc[mf][3]);
       }
     }
-    if (has_new) {
-#pragma unroll
-      for (int h = 0; h < 3; ++h) {
-        const float pj = bf2f(sm.at.pb[h][T_old]);
-        acc[h][0] = fmaf(pj, in[256 + 2 * d2], acc[h][0]);
-        acc[h][1] = fmaf(pj, in[256 + 2 * d2 + 1], acc[h][1]);
-      }
-    }
-  }
-#pragma unroll
-  for (int h = 0; h < 3; ++h) {
-    acc[h][0] += __shfl_xor(acc[h][0], 32);
-    acc[h][1] += __shfl_xor(acc[h][1], 32);
   }
   C.release(C.pos_kv_end);
   if (has_new && P.slot >= 0 && hq < 2) {
@@ -936,12 +1073,10 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg) {
       }
     }
   }
-  if (lane < 32)
+  if (hq < 3)
 #pragma unroll
-    for (int h = 0; h < 3; ++h) {
-      sm.wo[w][h][2 * d2] = acc[h][0];
-      sm.wo[w][h][2 * d2 + 1] = acc[h][1];
-    }
+    for (int mf = 0; mf < 4; ++mf)
+      *reinterpret_cast<float4*>(&sm.wo[w][hq][16 * mf + 4 * pq]) = make_float4(oacc[mf][0], oacc[mf][1], oacc[mf][2], oacc[mf][3]);
   C.cbar();
   if (w == 0 && lane == 0) trace_at(p, l, 19, p.n_layers);
   // wave h < 3: head 3g + h.  The chunk's partial sum of p.v in fixed wave order, fp32.
@@ -1093,6 +1228,19 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
       C.wait_filled(C.pos);
       XChunks<G::H, 8> nw;
       normw<G::H>(C, nw, segn);
+      // gate rows of units 0 .. n-1, then up rows of the same units: one 6-row item per wave.  The
+      // item's weights go from the ring into registers before h1 arrives.
+      const int nunits = P.au1 - P.au0;
+      const bool item = C.cw < 2 * nunits;
+      uint4 w[VPU][Chunks<G::H>::CPL];
+      if (item) {
+        const int j = C.cw % nunits, m = C.cw < nunits ? 0 : 1;
+        if (ge.on)  // the dense words rebuilt from the lossless stream (bit-identical)
+          lossless_rows<G::H, VPU>(C, m ? segu : segg, m ? segu_h : segg_h, m ? segu_r : segg_r, ge.first[m],
+                                   j * VPU, w);
+        else
+          ring_rows<G::H, VPU>(C, m ? segu : segg, j * VPU, w);
+      }
       tr(l, 9);
       const float ss = C.template poll_vec<1>(K_H1, l, G::H, sm.xs, sm.keep, 40);
       const float rs = rms_rsq<G::H>(C.block_total(ss));
@@ -1101,17 +1249,8 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
         XChunks<G::H, 8> x;
         load_x<G::H, 8, true>(x, sm.xs, nw, rs, C.lane);
         tr(l, 21);
-        // gate rows of units 0 .. n-1, then up rows of the same units: one 6-row item per wave
-        const int nunits = P.au1 - P.au0;
-        if (C.cw < 2 * nunits) {
-          const int j = C.cw % nunits, m = C.cw < nunits ? 0 : 1;
+        if (item) {
           float o[VPU];
-          uint4 w[VPU][Chunks<G::H>::CPL];
-          if (ge.on)  // the dense words rebuilt from the lossless stream (bit-identical)
-            lossless_rows<G::H, VPU>(C, m ? segu : segg, m ? segu_h : segg_h, m ? segu_r : segg_r, ge.first[m],
-                                     j * VPU, w);
-          else
-            ring_rows<G::H, VPU>(C, m ? segu : segg, j * VPU, w);
           dots_w<G::H, VPU>(w, x, o);
           if (C.lane == 0)
 #pragma unroll
@@ -1140,12 +1279,15 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
       const uint32_t segd = C.next_seg(sr_bytes(P, R_DOWN, 0));
       C.wait_filled(C.pos);
       const bool has_down = P.xu1 > P.xu0;  // workgroups without down rows do not need act
+      // each wave: its quarter of K for the unit's 6 rows, weights into registers before act arrives;
+      // the quarters are added in wave order
+      using Q = Quarter<G::I>;
+      uint4 wd[VPU][Q::CPL];
+      if (has_down) quarter_rows<G::I, VPU>(C, segd, 0, wd);
       if (has_down) C.template poll_vec<2>(K_ACT, l, G::I, sm.xs, nullptr, 41);
       C.cbar();
       tr(l, 13);
       if (has_down) {
-        // each wave: its quarter of K for the unit's 6 rows; the quarters are added in wave order
-        using Q = Quarter<G::I>;
         uint4 xq[Q::CPL];
 #pragma unroll
         for (int c = 0; c < Q::CPL; ++c) {
@@ -1159,7 +1301,7 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
         }
         tr(l, 28);
         float od[VPU];
-        dots_quarter<G::I, VPU>(C, segd, 0, xq, od);
+        dots_quarter_w<G::I, VPU>(wd, xq, od);
         if (C.lane == 0)
 #pragma unroll
           for (int e = 0; e < VPU; ++e) sm.part[C.cw][e] = od[e];
@@ -1194,6 +1336,10 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
     C.wait_filled(C.pos);
     XChunks<G::H, 8> nw;
     normw<G::H>(C, nw, segn);
+    // the weights of the wave's first unit (a workgroup has at most NCW units), before x arrives
+    const int nq = P.qu1 - P.qu0;
+    uint4 wq[VPU][Chunks<G::H>::CPL];
+    if (C.cw < nq) ring_rows<G::H, VPU>(C, segq, C.cw * VPU, wq);
     tr(l, 0);
     float ss;
     if (l == 0) {
@@ -1217,12 +1363,11 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
       XChunks<G::H, 8> x;
       load_x<G::H, 8, true>(x, sm.xs, nw, rs, C.lane);
       tr(l, 25);
-      const int nunits = P.qu1 - P.qu0;
-      for (int j = C.cw; j < nunits; j += NCW) {
+      if (C.cw < nq) {
         float o[VPU];
-        dots_n<G::H, VPU>(C, segq, j * VPU, x, o);
+        dots_w<G::H, VPU>(wq, x, o);
         tr(l, 26);
-        if (C.lane == 0) C.put_x(K_XQ, l, P.qu0 + j, C.unit6(o));
+        if (C.lane == 0) C.put_x(K_XQ, l, P.qu0 + C.cw, C.unit6(o));
         tr(l, 27);
       }
     }
@@ -1271,6 +1416,14 @@ __device__ __forceinline__ void consumer_a(CSR<G>& C) {
     const uint32_t segkv = C.next_seg(sr_bytes(P, R_KV, 0));
     C.pos_kv_end = C.pos;
     const uint32_t sego = C.next_seg(sr_bytes(P, R_O, 0));
+    ChunkRegs R;
+    tr(l, 0);
+    if (P.att) {
+      C.wait_filled(C.pos);
+      tr(l, 21);
+      chunk_load<G>(C, segkv, R);
+      tr(l, 22);
+    }
     // x_l rows of this workgroup's O rows (the residual): layer 0 read the embedding above
     if (l > 0) {
       const int nu = P.ou1 - P.ou0;
@@ -1286,11 +1439,16 @@ __device__ __forceinline__ void consumer_a(CSR<G>& C) {
                          35);
     }
     tr(l, 6);
-    if (P.att) attention_sr<G>(C, l, segkv);
+    if (P.att) attention_sr<G>(C, l, segkv, R);
     else C.release(C.pos_kv_end);
     // every group-A workgroup: the merged attention vector, then its O rows + residual -> h1
     C.cbar();  // the attention scratch shares storage with xs
     C.wait_filled(C.pos);
+    // the workgroup's O rows, RW consecutive rows per wave, into registers before attn arrives
+    constexpr int RW = (S::OU * VPU + NCW - 1) / NCW;
+    static_assert(RW <= 8, "sm.part holds 8 values per wave");
+    uint4 wo[RW][Chunks<G::H>::CPL];
+    ring_rows<G::H, RW>(C, sego, C.cw * RW, wo);
     C.template poll<1>(C.rl, S::HU, C.ct, NCT, [&](int u) { return W::loc(l, W::ATTN_U + size_t(u)); },
                        [&](int u, const u32x4& v) {
                          const float f[VPU] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y), bf_lo(v.z), bf_hi(v.z)};
@@ -1306,12 +1464,9 @@ __device__ __forceinline__ void consumer_a(CSR<G>& C) {
       const XChunks<G::H, 8> none = {};
       load_x<G::H, 8, false>(x, sm.xs, none, 1.f, C.lane);
       tr(l, 31);
-      // the workgroup's O rows, RW consecutive rows per wave; then wave 0: h1 = bf16(x + bf16(o))
-      // per row and one unit per lane
-      constexpr int RW = (S::OU * VPU + NCW - 1) / NCW;
-      static_assert(RW <= 8, "sm.part holds 8 values per wave");
+      // the O rows' dots; then wave 0: h1 = bf16(x + bf16(o)) per row and one unit per lane
       float o[RW];
-      dots_n<G::H, RW>(C, sego, C.cw * RW, x, o);
+      dots_w<G::H, RW>(wo, x, o);
       if (C.lane == 0)
 #pragma unroll
         for (int r = 0; r < RW; ++r) sm.part[C.cw][r] = o[r];
