@@ -307,6 +307,7 @@ __device__ __forceinline__ void producer(const Params& p, const Plan<G>& P, Smem
   __builtin_amdgcn_s_barrier();  // consumers may read blk[] after this
 
   uint32_t n = 0;  // global packet index at the start of the current segment
+  uint32_t room = RING;  // ring bytes the consumers have released, plus the ring size
   Spin spin(p.ws, epoch, 1);
   bool dead = false;
   auto cmin = [&]() -> uint32_t {
@@ -364,10 +365,12 @@ __device__ __forceinline__ void producer(const Params& p, const Plan<G>& P, Smem
     }
     for (uint32_t i = (uint32_t(pw) + NPW - n % NPW) % NPW; i < npk && !dead; i += NPW) {
       const uint32_t gn = n + i;
-      if ((gn + 1) * PKT > cmin() + RING) {
+      // `room`: the end of the free ring as last read; the consumers' counters only grow, so they are
+      // read again only when a packet would pass it
+      if ((gn + 1) * PKT > room && (gn + 1) * PKT > (room = cmin() + RING)) {
         wait_vmcnt<0>();
         publish(gn);
-        while ((gn + 1) * PKT > cmin() + RING)
+        while ((gn + 1) * PKT > (room = cmin() + RING))
           if (!spin.again()) { dead = true; break; }
         if (dead) break;
       }

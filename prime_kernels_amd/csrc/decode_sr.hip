@@ -64,9 +64,24 @@ struct SG {
   static constexpr int NATT = C * G::KVH;
   static constexpr int PU = 22;                         // units of one head's 64 fp32 partial sums
   static constexpr int OU = (HU + AG - 1) / AG;         // most O units per group-A workgroup
+  // O rows loaded before the attention partials are polled (10 chunk records per thread leave no
+  // room for them in the SmolLM2-135M build without spills)
+  static constexpr bool O_EARLY = C <= 6;
   static_assert(G::GQA == 3 && (3 * 64) % VPU == 0 && G::H % VPU == 0, "head groups are whole units");
   static_assert(C >= 1 && C <= 16, "chunks per KV head");
 };
+
+// The qkv vector in slot order.  Its q and k parts are laid out by RoPE pair: slots 2p and 2p + 1
+// hold dims d and d + 32 (d = p % 32) of head p / 32 (the q heads, then the k heads), so that the
+// workgroup producing a 6-value unit holds both halves of its three pairs and applies RoPE itself;
+// the v part is in row order.  qkv_row(s) is the projection row of slot s.
+template <class G>
+__device__ __forceinline__ int qkv_row(int s) {
+  constexpr int ROPE = (G::NH + G::KVH) * 64;
+  if (s >= ROPE) return s;
+  const int pr = s >> 1;
+  return (pr >> 5) * 64 + (pr & 31) + 32 * (s & 1);
+}
 
 // Workspace (uncached, 32-bit words), placed after the general kernels' layout (base word SR0) so
 // that no word is ever read in a format it was not written in; the header (epoch, abort) is shared.
@@ -81,10 +96,9 @@ struct SWS {
   static constexpr size_t XBYTES = size_t(REP) * LINES * SLOTS * 64;
   static constexpr size_t LMR = X0 + XBYTES;                  // per-workgroup end records: NWG units
   static constexpr size_t LOC = LMR + size_t(NWG) * 16;      // group-A records when they cannot stay in L2
-  // group-A records per layer, in units: statistics (2 per chunk), partials (3 heads x PU per chunk),
-  // the merged attention vector (HU)
-  static constexpr size_t STAT_U = 0, PART_U = size_t(AG) * 2, ATTN_U = PART_U + size_t(AG) * 3 * S::PU;
-  static constexpr size_t LOC_LAYER = (ATTN_U + S::HU) * 16;
+  // group-A records per layer, in units: statistics (2 per chunk), partials (3 heads x PU per chunk)
+  static constexpr size_t STAT_U = 0, PART_U = size_t(AG) * 2;
+  static constexpr size_t LOC_LAYER = (PART_U + size_t(AG) * 3 * S::PU) * 16;
   static constexpr size_t LOC_BYTES = LOC_LAYER * G::L;
   static constexpr size_t BYTES = LOC + LOC_BYTES;
   // unit u of vector (kind, layer l, copy r): UPL units per line; consecutive lines of a vector are
@@ -221,7 +235,6 @@ struct SmemSR {
   static constexpr int XS = G::I > G::H ? G::I : G::H;
   struct Attn {
     float qkvw[NCW][5 * 64];     // per-wave attention inputs (3 q heads, k_new, v_new; pre-RoPE)
-    float ao[3][64];             // leader: the merged attention output of its 3 heads
   };
   uint8_t ring[RING];
   union {
@@ -231,7 +244,6 @@ struct SmemSR {
   float keep[G::H];              // F: h1 (residual of down); A: x (residual of O, its own rows)
   float wo[NCW][3][64];          // per-wave P.V partials
   float wml[NCW][2][3];          // per-wave softmax max / sum per head
-  float cs[128];                 // cos [0, 32), sin [32, 64) of this position (fp32 values)
   float red[NCW];
   LayerW lw[G::L];
   GUE gue[G::L];                 // group F: each layer's lossless gate/up stream of this workgroup
@@ -292,7 +304,7 @@ __device__ __forceinline__ void producer_sr(const Params& p, const PlanSR<G>& P,
       case R_UP_R: base = u8(ge->raw + size_t(ge->first[1]) * 8); break;
       case R_DOWN: base = u8(Lw.down) + size_t(P.d0) * G::I * 2; break;
       case R_NORM1: base = u8(Lw.norm1); break;
-      case R_QKV: base = u8(Lw.qkv) + size_t(P.q0) * G::H * 2; break;
+      case R_QKV: break;  // rows gathered in slot order below
       case R_KV: cache = u8(sm.kvp[layer]); break;
       case R_O: base = u8(Lw.o) + size_t(P.o0) * G::H * 2; break;
       case R_FNORM: base = u8(p.final_norm); break;
@@ -325,6 +337,10 @@ __device__ __forceinline__ void producer_sr(const Params& p, const PlanSR<G>& P,
         const long long e = (long long)blk * p.block_stride + (long long)(t & 15) * p.token_stride +
                             (long long)P.g * p.head_stride + (piece ? p.v_off : p.k_off) + part * 8;
         src = cache + e * 2;
+      } else if (kind == R_QKV) {
+        // rows in slot order (qkv_row): byte `off` of the segment is in row q0 + off / (2 H)
+        const uint32_t ri = off / uint32_t(G::H * 2), cb = off - ri * uint32_t(G::H * 2);
+        src = u8(Lw.qkv) + size_t(qkv_row<G>(P.q0 + int(ri))) * G::H * 2 + cb;
       } else {
         src = base + off;
       }
@@ -403,14 +419,16 @@ struct CSR {
   __device__ __forceinline__ CSR(const Params& p_, const PlanSR<G>& P_, SmemSR<G>& sm_, uint32_t ep,
                                  uint32_t* region_)
       : p(p_), P(P_), sm(sm_), tag(ep), region(region_) {
-    cw = (threadIdx.x >> 6) - NPW;
+    cw = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6) - NPW);  // wave-uniform, in an SGPR
     lane = threadIdx.x & 63;
     ct = cw * 64 + lane;
     rx = rsrc(region_);
     rl = rx;
     xr = (P.wg >> 3) % REP;
   }
-  __device__ __forceinline__ void refresh() { asm volatile("" : "+v"(lane), "+v"(ct)); }
+  // lane, thread and wave indices made opaque once per bracket, so that nothing derived from them is
+  // hoisted out of the layer loop (and spilled there)
+  __device__ __forceinline__ void refresh() { asm volatile("" : "+v"(lane), "+v"(ct), "+s"(cw)); }
   __device__ __forceinline__ uint32_t next_seg(uint32_t bytes) {
     const uint32_t s = pos;
     pos += pad_pkt(bytes);
@@ -751,7 +769,11 @@ __device__ __forceinline__ void chunk_load(CSR<G>& C, uint32_t seg, ChunkRegs& R
                   uint32_t(hq & 7) * 2u;
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
-    if (i >= nt) continue;
+    if (i >= nt) {  // defined all the same: registers left undefined stay live across the layer loop
+#pragma unroll
+      for (int mf = 0; mf < 4; ++mf) R.va[i][mf][0] = R.va[i][mf][1] = 0u;
+      continue;
+    }
     const int tile = w + NCW * i;
     const uint32_t base = seg + uint32_t(tile) * 4096u;
     uint32_t h[4][4];
@@ -793,6 +815,7 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
   uint4 ka[MT][2];
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
+    ka[i][0] = ka[i][1] = make_uint4(0u, 0u, 0u, 0u);
     if (i >= nt) continue;
     const int tok = (w + NCW * i) * 16 + hq;
     const uint32_t row = seg + uint32_t(tok) * 256u;
@@ -813,9 +836,14 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
                        },
                        [&](int i, const u32x4& v) {
                          const float f[VPU] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y), bf_lo(v.z), bf_hi(v.z)};
+                         // q and k slots come in RoPE-pair order (qkv_row): local slot r of a
+                         // head is dim r / 2 + 32 (r % 2); v slots are in row order
                          if (i < nq) {
 #pragma unroll
-                           for (int e = 0; e < VPU; ++e) in[i * VPU + e] = f[e];
+                           for (int e = 0; e < VPU; ++e) {
+                             const int ls = i * VPU + e;
+                             in[(ls & ~63) + ((ls & 63) >> 1) + 32 * (ls & 1)] = f[e];
+                           }
                          } else {
                            const int kv = i < nq + kn ? 0 : 1;
                            const int u = kv ? vu0 + i - nq - kn : ku0 + i - nq;
@@ -823,7 +851,8 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
 #pragma unroll
                            for (int e = 0; e < VPU; ++e) {
                              const int row = u * VPU + e - base;
-                             if (row >= 0 && row < 64) in[192 + 64 * kv + row] = f[e];
+                             const int dim = kv ? row : (row >> 1) + 32 * (row & 1);
+                             if (row >= 0 && row < 64) in[192 + 64 * kv + dim] = f[e];
                            }
                          }
                        },
@@ -834,40 +863,23 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
   wait_lgkm0();
   if (w == 0 && lane == 0) trace_at(p, l, 3, p.n_layers);
   if (has_new && lane == 0) trace_at(p, l, 4, p.n_layers);
-  // RoPE of pieces pq (dims 8pq..8pq+7) and pq + 4 (dims 32+8pq..) of head hq < 3, and of k_new
-  // (HF: bf16(bf16(x cos) + bf16(rotate_half(x) sin)))
-  float cs8[8], sn8[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    cs8[e] = sm.cs[pq * 8 + e];
-    sn8[e] = sm.cs[32 + pq * 8 + e];
-  }
-  auto rope_pair = [&](const float* head, uint32_t (&lo)[4], uint32_t (&hi)[4]) {
+  // q of head hq < 3 and the new token's k (both roped by their producers) as bf16 pieces pq (dims
+  // 8pq .. 8pq+7) and pq + 4 (dims 32 + 8pq ..), the operands below
+  auto pieces = [&](const float* head, uint32_t (&lo)[4], uint32_t (&hi)[4]) {
     const float4 a0 = *reinterpret_cast<const float4*>(head + pq * 8);
     const float4 a1 = *reinterpret_cast<const float4*>(head + pq * 8 + 4);
     const float4 b0 = *reinterpret_cast<const float4*>(head + 32 + pq * 8);
     const float4 b1 = *reinterpret_cast<const float4*>(head + 32 + pq * 8 + 4);
-    const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-    const float y[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-    float rl[8], rh[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      rl[e] = rnd(rnd(x[e] * cs8[e]) + rnd((-y[e]) * sn8[e]));
-      rh[e] = rnd(rnd(y[e] * cs8[e]) + rnd(x[e] * sn8[e]));
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      lo[e] = pack2(rl[2 * e], rl[2 * e + 1]);
-      hi[e] = pack2(rh[2 * e], rh[2 * e + 1]);
-    }
+    lo[0] = pack2(a0.x, a0.y); lo[1] = pack2(a0.z, a0.w); lo[2] = pack2(a1.x, a1.y); lo[3] = pack2(a1.z, a1.w);
+    hi[0] = pack2(b0.x, b0.y); hi[1] = pack2(b0.z, b0.w); hi[2] = pack2(b1.x, b1.y); hi[3] = pack2(b1.z, b1.w);
   };
   uint32_t qlo[4] = {0u, 0u, 0u, 0u}, qhi[4] = {0u, 0u, 0u, 0u};
-  if (hq < 3) rope_pair(in + hq * 64, qlo, qhi);
+  if (hq < 3) pieces(in + hq * 64, qlo, qhi);
   uint32_t klo[4] = {0u, 0u, 0u, 0u}, khi[4] = {0u, 0u, 0u, 0u};
   // the new token's scores q_h . k_new: lane (h, pq) dots pieces pq and pq + 4, the four rows add up
   float s_new[3] = {-INFINITY, -INFINITY, -INFINITY};
   if (has_new) {
-    rope_pair(in + 192, klo, khi);
+    pieces(in + 192, klo, khi);
     float d = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -901,6 +913,8 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
   }
   if (w == 0 && lane == 0) trace_at(p, l, 36, p.n_layers);
   if (has_new && lane == 0) trace_at(p, l, 9, p.n_layers);
+  // The softmax exponentials inside attention use the hardware exp2 (__expf): within a few fp32 ulp
+  // of expf, far below the bf16 rounding of p.
   // The wave's softmax statistics.  Only columns 0-2 of a score tile hold heads, so tile i's columns
   // move to lanes 3i .. 3i+2 of each 16-lane row (DPP row_shr:3i): lane c of a row then holds the
   // scores of head c % 3 in tile c / 3 (c < 3 MT), four tokens, and the exps below run on 4 values
@@ -933,14 +947,14 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
   float lsum = 0.f;
 #pragma unroll
   for (int jj = 0; jj < 4; ++jj) {
-    ev[jj] = ev[jj] == -INFINITY ? 0.f : expf(ev[jj] - m);
+    ev[jj] = ev[jj] == -INFINITY ? 0.f : __expf(ev[jj] - m);
     lsum += ev[jj];
   }
   head_totals<false>(lsum, lw);
   float ev_new[3];
 #pragma unroll
   for (int h = 0; h < 3; ++h) {
-    ev_new[h] = s_new[h] == -INFINITY ? 0.f : expf(s_new[h] - mw[h]);
+    ev_new[h] = s_new[h] == -INFINITY ? 0.f : __expf(s_new[h] - mw[h]);
     lw[h] += ev_new[h];
   }
   if (lane == 0)
@@ -959,7 +973,7 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
   }
   float mx = fmaxf(mq, dpp<0xb1>(mq, mq));
   mx = fmaxf(mx, dpp<0x4e>(mx, mx));
-  float ex = mq == -INFINITY ? 0.f : lq * expf(mq - mx);
+  float ex = mq == -INFINITY ? 0.f : lq * __expf(mq - mx);
   ex += dpp<0xb1>(0.f, ex);
   ex += dpp<0x4e>(0.f, ex);
   float Mh[3], Lh[3];
@@ -996,7 +1010,7 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
     float M[3] = {m[0], m[1], m[2]};
     wave_max_n<3>(M);
 #pragma unroll
-    for (int h = 0; h < 3; ++h) s[h] = ((lane & 1) && lane < 2 * S::C && m[h] != -INFINITY) ? st[h] * expf(m[h] - M[h]) : 0.f;
+    for (int h = 0; h < 3; ++h) s[h] = ((lane & 1) && lane < 2 * S::C && m[h] != -INFINITY) ? st[h] * __expf(m[h] - M[h]) : 0.f;
     wave_sum_n<3>(s);
 #pragma unroll
     for (int h = 0; h < 3; ++h) { Mh[h] = M[h]; Lh[h] = s[h]; }
@@ -1014,7 +1028,7 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
   {
     const float Mq = ch == 0 ? Mh[0] : ch == 1 ? Mh[1] : Mh[2];
     const float Lq = ch == 0 ? Lh[0] : ch == 1 ? Lh[1] : Lh[2];
-    const float scale = m != -INFINITY ? expf(m - Mq) * (1.0f / Lq) : 0.f;
+    const float scale = m != -INFINITY ? __expf(m - Mq) * (1.0f / Lq) : 0.f;
     const uint32_t p01 = pack2(ev[0] * scale, ev[1] * scale), p23 = pack2(ev[2] * scale, ev[3] * scale);
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
@@ -1032,7 +1046,7 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
       const float en = hq == 0 ? ev_new[0] : hq == 1 ? ev_new[1] : ev_new[2];
       const float Mn = hq == 0 ? Mh[0] : hq == 1 ? Mh[1] : Mh[2];
       const float Ln = hq == 0 ? Lh[0] : hq == 1 ? Lh[1] : Lh[2];
-      const float pn = rnd(en * (expf(mh - Mn) * (1.0f / Ln)));
+      const float pn = rnd(en * (__expf(mh - Mn) * (1.0f / Ln)));
 #pragma unroll
       for (int mf = 0; mf < 4; ++mf) {
         const float4 v = *reinterpret_cast<const float4*>(in + 256 + 16 * mf + 4 * pq);
@@ -1085,48 +1099,70 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
 #pragma unroll
     for (int v = 0; v < NCW; ++v) O += sm.wo[v][w][lane];
   }
-  if (!P.leader) {
-    if (w < 3) {
-      // PU units of 3 floats per head; lane 3u writes unit u (floats 3u .. 3u+2)
-      const float f1 = __shfl_down(O, 1), f2 = __shfl_down(O, 2);
-      if (lane % 3 == 0)
-        C.put_loc(l, W::PART_U + (size_t(P.rank) * 3 + w) * S::PU + lane / 3,
-                  u32x4{__float_as_uint(O), __float_as_uint(lane + 1 < 64 ? f1 : 0.f),
-                        __float_as_uint(lane + 2 < 64 ? f2 : 0.f), C.tag});
-    }
-    return;
-  }
-  // leader: add the partials of chunks 0 .. C-2 in chunk order (this chunk is C-1), round once
   if (w < 3) {
-    float part_sum[S::C];
-#pragma unroll
-    for (int k = 0; k < S::C; ++k) part_sum[k] = 0.f;
-    C.template poll<S::C - 1 < 1 ? 1 : S::C - 1>(
-        C.rl, S::C - 1, 0, 1,
-        [&](int k) { return W::loc(l, W::PART_U + (size_t(g + G::KVH * k) * 3 + w) * S::PU + lane / 3); },
-        [&](int k, const u32x4& v) {
-          const uint32_t s = lane % 3;
-          part_sum[k] = __uint_as_float(s == 0 ? v.x : s == 1 ? v.y : v.z);
-        },
-        32);
-    float tot = 0.f;
-#pragma unroll
-    for (int k = 0; k < S::C - 1; ++k) tot += part_sum[k];
-    tot += O;
-    sm.at.ao[w][lane] = rnd(tot);
-  }
-  C.cbar();
-  if (w == 0 && lane < 32) {
-    // the head group's 192 values are units 32g .. 32g+31 of the attention vector
-    float v[VPU];
-#pragma unroll
-    for (int e = 0; e < VPU; ++e) {
-      const int i = lane * VPU + e;
-      v[e] = sm.at.ao[i >> 6][i & 63];
-    }
-    C.put_loc(l, W::ATTN_U + size_t(32 * g + lane), C.unit6(v));
+    // PU units of 3 floats per head; lane 3u writes unit u (floats 3u .. 3u+2).  The workgroups doing
+    // the O projection add the chunks' partials of each head in chunk order.
+    const float f1 = __shfl_down(O, 1), f2 = __shfl_down(O, 2);
+    if (lane % 3 == 0)
+      C.put_loc(l, W::PART_U + (size_t(P.rank) * 3 + w) * S::PU + lane / 3,
+                u32x4{__float_as_uint(O), __float_as_uint(lane + 1 < 64 ? f1 : 0.f),
+                      __float_as_uint(lane + 2 < 64 ? f2 : 0.f), C.tag});
   }
   if (w == 0 && lane == 0) trace_at(p, l, 20, p.n_layers);
+}
+
+// The attention vector of layer l into xs: per head unit (three dims of one head) the partial sums
+// of the head's C chunks, added in chunk order in fp32 and rounded to bf16 once (HF's bf16(p.v)).
+// Thread t takes head units t, t + NCT, ...; each is polled in all C chunk records.
+template <class G>
+__device__ __forceinline__ void attention_vector(CSR<G>& C, int l) {
+  using S = SG<G>;
+  using W = SWS<G>;
+  constexpr int NHU = G::NH * S::PU;                 // head units of the attention vector
+  constexpr int R = (NHU + NCT - 1) / NCT;
+  static_assert(R * S::C <= 24, "partials polled per thread");
+  static_assert(R <= 2, "two head units per thread at most");
+  // chunk c of head h = 3g + w is group-A rank g + KVH c: its records are KVH * 3 * PU units apart,
+  // and head unit hu = h PU + u of chunk 0 is record PART_U + (3 g + w) PU + u = PART_U + hu
+  constexpr uint32_t CSTRIDE = uint32_t(G::KVH) * 3u * uint32_t(S::PU) * 16u;
+  const int hu0 = C.ct, hu1 = C.ct + NCT;
+  const uint32_t b0 = W::loc(l, W::PART_U + size_t(hu0 < NHU ? hu0 : 0));
+  const uint32_t b1 = W::loc(l, W::PART_U + size_t(hu1 < NHU ? hu1 : 0));
+  u32x4 v0[S::C], v1[S::C];
+  // every load issued at once; then each head unit's set is polled to completion and summed
+#pragma unroll
+  for (int c = 0; c < S::C; ++c) v0[c] = ld_unit(C.rl, b0 + uint32_t(c) * CSTRIDE);
+  if (R > 1 && hu1 < NHU)
+#pragma unroll
+    for (int c = 0; c < S::C; ++c) v1[c] = ld_unit(C.rl, b1 + uint32_t(c) * CSTRIDE);
+  auto settle = [&](u32x4 (&v)[S::C], uint32_t b, int hu) {
+    if (hu >= NHU) return;
+    Spin spin(C.p.ws, C.tag, 36);
+    while (true) {
+      uint32_t pend = 0;
+#pragma unroll
+      for (int c = 0; c < S::C; ++c) pend |= v[c].w != C.tag ? 1u << c : 0u;
+      if (!pend) break;
+      if (C.dead || !spin.again()) { C.dead = true; break; }
+#pragma unroll
+      for (int c = 0; c < S::C; ++c)
+        if ((pend >> c) & 1u) v[c] = ld_unit(C.rl, b + uint32_t(c) * CSTRIDE);
+    }
+    float t0 = 0.f, t1 = 0.f, t2 = 0.f;
+#pragma unroll
+    for (int c = 0; c < S::C; ++c) {
+      t0 += __uint_as_float(v[c].x);
+      t1 += __uint_as_float(v[c].y);
+      t2 += __uint_as_float(v[c].z);
+    }
+    const int h = hu / S::PU, d = 3 * (hu - h * S::PU);
+    float* dst = C.sm.xs + h * 64 + d;
+    dst[0] = rnd(t0);
+    if (d + 1 < 64) dst[1] = rnd(t1);
+    if (d + 2 < 64) dst[2] = rnd(t2);
+  };
+  settle(v0, b0, hu0);
+  if (R > 1) settle(v1, b1, hu1);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1212,6 +1248,21 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
   SmemSR<G>& sm = C.sm;
   const int L = p.n_layers;
   auto tr = [&](int l, int ev) { if (C.ct == 0) trace_at(p, l, ev, p.n_layers); };
+  // cos and sin (fp32 values) of this position for the three RoPE pairs of the wave's qkv unit,
+  // which is the same in every layer
+  float rc[VPU / 2], rsn[VPU / 2];
+  {
+    const int s0 = (P.qu0 + C.cw) * VPU;
+#pragma unroll
+    for (int k = 0; k < VPU / 2; ++k) {
+      const int d = ((s0 + 2 * k) >> 1) & 31;
+      const size_t at = size_t(P.pos) * 64;
+      rc[k] = p.cs_fp32 ? reinterpret_cast<const float*>(p.cos_sin)[at + d]
+                        : bf2f(reinterpret_cast<const uint16_t*>(p.cos_sin)[at + d]);
+      rsn[k] = p.cs_fp32 ? reinterpret_cast<const float*>(p.cos_sin)[at + 32 + d]
+                         : bf2f(reinterpret_cast<const uint16_t*>(p.cos_sin)[at + 32 + d]);
+    }
+  }
   for (int k = 0; k <= L; ++k) {
     if (k > 0) {
       const int l = k - 1;
@@ -1367,6 +1418,20 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
         float o[VPU];
         dots_w<G::H, VPU>(wq, x, o);
         tr(l, 26);
+        // q = bf16(W x); the pairs of the q and k slots get HF's RoPE,
+        // bf16(bf16(x cos) + bf16(rotate_half(x) sin)), here
+        const int s0 = (P.qu0 + C.cw) * VPU;
+#pragma unroll
+        for (int e = 0; e < VPU; e += 2) {
+          const float x0 = rnd(o[e]), x1 = rnd(o[e + 1]);
+          o[e] = x0;
+          o[e + 1] = x1;
+          if (s0 + e < (G::NH + G::KVH) * 64) {
+            const float cs = rc[e / 2], sn = rsn[e / 2];
+            o[e] = rnd(rnd(x0 * cs) + rnd((-x1) * sn));
+            o[e + 1] = rnd(rnd(x1 * cs) + rnd(x0 * sn));
+          }
+        }
         if (C.lane == 0) C.put_x(K_XQ, l, P.qu0 + C.cw, C.unit6(o));
         tr(l, 27);
       }
@@ -1389,10 +1454,7 @@ __device__ __forceinline__ void consumer_a(CSR<G>& C) {
   SmemSR<G>& sm = C.sm;
   const int L = p.n_layers;
   auto tr = [&](int l, int ev) { if (C.ct == 0) trace_at(p, l, ev, p.n_layers); };
-  // this position's cos/sin row (fp32 values) and layer 0's input rows
-  for (int i = C.ct; i < 64; i += NCT)
-    sm.cs[i] = p.cs_fp32 ? reinterpret_cast<const float*>(p.cos_sin)[size_t(P.pos) * 64 + i]
-                         : bf2f(reinterpret_cast<const uint16_t*>(p.cos_sin)[size_t(P.pos) * 64 + i]);
+  // layer 0's input rows (the residual of this workgroup's O rows)
   {
     long long id = p.ids_i64 ? reinterpret_cast<const int64_t*>(p.input_ids)[0]
                              : reinterpret_cast<const int32_t*>(p.input_ids)[0];
@@ -1444,18 +1506,15 @@ __device__ __forceinline__ void consumer_a(CSR<G>& C) {
     // every group-A workgroup: the merged attention vector, then its O rows + residual -> h1
     C.cbar();  // the attention scratch shares storage with xs
     C.wait_filled(C.pos);
-    // the workgroup's O rows, RW consecutive rows per wave, into registers before attn arrives
+    // the workgroup's O rows, RW consecutive rows per wave, into registers: while the partials
+    // arrive where the register budget allows it (SmolLM2-360M), else after them
     constexpr int RW = (S::OU * VPU + NCW - 1) / NCW;
     static_assert(RW <= 8, "sm.part holds 8 values per wave");
     uint4 wo[RW][Chunks<G::H>::CPL];
-    ring_rows<G::H, RW>(C, sego, C.cw * RW, wo);
-    C.template poll<1>(C.rl, S::HU, C.ct, NCT, [&](int u) { return W::loc(l, W::ATTN_U + size_t(u)); },
-                       [&](int u, const u32x4& v) {
-                         const float f[VPU] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y), bf_lo(v.z), bf_hi(v.z)};
-#pragma unroll
-                         for (int e = 0; e < VPU; ++e) sm.xs[u * VPU + e] = f[e];
-                       },
-                       36);
+    if (S::O_EARLY) ring_rows<G::H, RW>(C, sego, C.cw * RW, wo);
+    C.refresh();  // the record loads below may not move up into the attention code
+    attention_vector<G>(C, l);
+    if (!S::O_EARLY) ring_rows<G::H, RW>(C, sego, C.cw * RW, wo);
     tr(l, 30);
     C.cbar();
     tr(l, 7);
