@@ -1724,21 +1724,42 @@ struct PlanB {
     for (int b = 0; b < B; ++b) nitems += G::KVH * chunks(sS[b]);
     ni = nitems > wg ? (nitems - wg + NWG - 1) / NWG : 0;
   }
-  // item index -> sequence b, KV head g, chunk c of C, index of chunk 0 of (b, g), cached tokens [t0, t1)
+  // chunks of exactly tc cached tokens of a sequence (its last chunk may be shorter, or hold no cached
+  // token when S = 1)
+  __device__ __forceinline__ int full(int S) const { return (max(S, 1) - 1) / tc; }
+  // Item `it` of the assignment order (workgroup wg takes items wg, wg + NWG, ...): every full chunk,
+  // in (sequence, KV head, chunk) order, then every short last chunk, so that the workgroups holding
+  // one item more than the rest hold a short one.  Returns sequence b, KV head g, chunk c of C, the
+  // (sequence, head, chunk) index `base` of chunk 0 of (b, g) (base + c keys the chunk's records),
+  // and the cached tokens [t0, t1).
   __device__ __forceinline__ void item(const int32_t* sS, int it, int& b, int& g, int& c, int& C, int& base,
                                        int& t0, int& t1) const {
-    int acc = 0;
-    b = 0;
-    C = chunks(sS[0]);
-    for (; b < B; ++b) {
-      C = chunks(sS[b]);
-      if (it < acc + G::KVH * C) break;
-      acc += G::KVH * C;
+    int nfull = 0;
+    for (int s = 0; s < B; ++s) nfull += G::KVH * full(sS[s]);
+    int acc = 0, first = 0;  // items of the part passed, (sequence, head, chunk) index of sequence b
+    if (it < nfull) {
+      for (b = 0; b < B - 1; ++b) {
+        const int n = G::KVH * full(sS[b]);
+        if (it < acc + n) break;
+        acc += n;
+        first += G::KVH * chunks(sS[b]);
+      }
+      const int nf = max(full(sS[b]), 1);
+      g = (it - acc) / nf;
+      c = (it - acc) - g * nf;
+    } else {
+      const int r = it - nfull;
+      for (b = 0; b < B - 1; ++b) {
+        const int n = G::KVH * (chunks(sS[b]) - full(sS[b]));
+        if (r < acc + n) break;
+        acc += n;
+        first += G::KVH * chunks(sS[b]);
+      }
+      g = r - acc;
+      c = full(sS[b]);
     }
-    const int r = it - acc;
-    g = r / C;
-    c = r % C;
-    base = acc + g * C;
+    C = chunks(sS[b]);
+    base = first + g * C;
     const int old = max(sS[b], 1) - 1;
     t0 = min(c * tc, old);
     t1 = min((c + 1) * tc, old);
@@ -2263,7 +2284,7 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
     if (lane < 12 && (lane & 3) == 0) { sm.at.cst[k][0][lane >> 2] = mx; sm.at.cst[k][1][lane >> 2] = ex; }
     skew_delay(p.skew, P.wg, l, 14);
     if (it.C > 1 && lane < 12 && (lane & 3) == 0) {
-      uint64_t* st = reinterpret_cast<uint64_t*>(p.ws + WSB<G>::stat(P.wg + k * NWG));
+      uint64_t* st = reinterpret_cast<uint64_t*>(p.ws + WSB<G>::stat(it.base + it.c));
       st_dev64(st + 2 * (lane >> 2), tg | __float_as_uint(mx));
       st_dev64(st + 2 * (lane >> 2) + 1, tg | __float_as_uint(ex));
     }
@@ -2404,7 +2425,7 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
       for (int v = 0; v < NCW; ++v) O += wo[v][w][lane];
       skew_delay(p.skew, P.wg, l, 15);
       if (leader) sm.at.own[k][w * 64 + lane] = O;
-      else st_dev64(reinterpret_cast<uint64_t*>(p.ws + WSB<G>::rec(P.wg + k * NWG)) + w * 64 + lane, tg | __float_as_uint(O));
+      else st_dev64(reinterpret_cast<uint64_t*>(p.ws + WSB<G>::rec(it.base + it.c)) + w * 64 + lane, tg | __float_as_uint(O));
     }
     trk(k, 31 + 2 * k);
   }

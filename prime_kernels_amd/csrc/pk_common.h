@@ -259,6 +259,58 @@ __device__ __forceinline__ void wave_rows(float (&v)[N]) {
   }
 }
 
+// Total (sum, or max for MAX) of a value over the four 16-lane rows of a wave, for each of the 16
+// columns; every lane gets its column's total (one cross-half and one cross-row swap).
+template <bool MAX>
+__device__ __forceinline__ float column_total(float v) {
+  float a = v, b = v;
+  swap32(a, b);
+  v = comb<MAX>(a, b);
+  a = v;
+  b = v;
+  swap16(a, b);
+  return comb<MAX>(a, b);
+}
+
+// DPP row shifts by 3i lanes (i < 5, a compile-time constant after unrolling): row_shr moves lane
+// c - 3i to lane c, row_shl lane c + 3i to lane c, within each 16-lane row (lanes with no source get
+// -inf for the max variant, 0 otherwise).
+template <bool NEG_INF>
+__device__ __forceinline__ float dpp_shr3(int i, float v) {
+  const float o = NEG_INF ? -INFINITY : 0.f;
+  switch (i) {
+    case 1: return dpp<0x113>(o, v);
+    case 2: return dpp<0x116>(o, v);
+    case 3: return dpp<0x119>(o, v);
+    case 4: return dpp<0x11c>(o, v);
+    default: return v;
+  }
+}
+__device__ __forceinline__ uint32_t dpp_shl3u(int i, uint32_t v) {
+  const float f = __uint_as_float(v);
+  switch (i) {
+    case 1: return __float_as_uint(dpp<0x103>(0.f, f));
+    case 2: return __float_as_uint(dpp<0x106>(0.f, f));
+    case 3: return __float_as_uint(dpp<0x109>(0.f, f));
+    case 4: return __float_as_uint(dpp<0x10c>(0.f, f));
+    default: return v;
+  }
+}
+// Per-head totals (sum, or max for MAX) of the compacted layout: lane c of each row holds a value of
+// head c % 3 (c < 15; lane 15 must hold the identity).  Lanes c, c-3, c-6, c-9, c-12 are combined
+// within the row (lanes 12-14 then hold the row's totals of heads 0-2), the four rows are combined,
+// and the three totals come back wave-uniform.
+template <bool MAX>
+__device__ __forceinline__ void head_totals(float v, float (&out)[3]) {
+  v = comb<MAX>(v, dpp_shr3<MAX>(1, v));
+  v = comb<MAX>(v, dpp_shr3<MAX>(2, v));
+  v = comb<MAX>(v, dpp_shr3<MAX>(4, v));
+  v = column_total<MAX>(v);
+#pragma unroll
+  for (int h = 0; h < 3; ++h)
+    out[h] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 12 + h));
+}
+
 // wave_max / wave_sum of N values at once: the same steps per value, the N chains interleaved so
 // that each DPP step's wait states are filled by the other chains instead of s_nop.
 template <int N>
