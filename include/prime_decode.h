@@ -83,10 +83,11 @@ int pk_test_set_epoch(void* stream, unsigned epoch);
 int pk_test_abort_next(void* stream);
 
 /* One greedy decode step for B = 1..16 sequences (vLLM FLASH_ATTN metadata, paged KV
- * [blocks, KVH, 16, 128]; contexts may differ per sequence).  B = 1 runs the GEMV kernel; B >= 2
- * runs the batched kernel, whose projections and LM head are MFMA tiles over all B tokens, so the
- * weights are read once per step for the whole batch.  The reference caps SmolLM2-360M at B <= 2
- * (decode_megakernel_360m/__init__.py:46).
+ * [blocks, KVH, 16, 128]; contexts may differ per sequence).  B = 1 runs the split-role kernel
+ * while max_seq_len is at most PK_NOALLOC_MAX_SEQ_360M / _135M (PK_OPT_SPLIT_ROLE 1, the default),
+ * else the general GEMV kernel; B >= 2 runs the batched kernel, whose projections and LM head are
+ * MFMA tiles over all B tokens, so the weights are read once per step for the whole batch.  The
+ * reference caps SmolLM2-360M at B <= 2 (decode_megakernel_360m/__init__.py:46).
  *   layers: device table [n_layers][6] of pointers (norm1, qkv, o, norm2, gate_up, down), bf16.
  *   kv: device table [n_layers] of cache base pointers; K at k_off, V at v_off (elements).
  *   out_hidden [B, H] bf16 receives the final-normed hidden state.

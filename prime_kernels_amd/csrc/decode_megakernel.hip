@@ -3212,7 +3212,7 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
 // ------------------------------------------------------------------------------------------------
 
 // Diagnostics: per-phase wall-clock timestamps for the next launches (NULL disables).
-// Layout: [256 workgroups][n_layers * 16 + 4] uint64.
+// Layout: [256 workgroups][n_layers * 40 + 4] uint64.
 extern "C" void pk_set_trace(void* buf) { pk::g_trace = reinterpret_cast<unsigned long long*>(buf); }
 
 // Allocate and zero the current device's state now (outside any stream capture); later calls on

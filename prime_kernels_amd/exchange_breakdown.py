@@ -14,8 +14,8 @@ Trace events used (index within a layer's 40 slots):
     17 local stats, 18 global stats, 19 PV done, 5 attention written (merge leaders); 7 attention
     polled, 8 O done; 10 h1 ready, 11 gate/up done; 13 act ready, 14 down done.
   split-role kernel: group F (workgroups with wg % 8 != 0) 1, 2, 10, 11, 13, 14 as above; group A
-    (wg % 8 == 0) 3 attention start, 17, 18, 19 as above, 20 merge done (leaders), 7 attention
-    polled, 8 O done.
+    (wg % 8 == 0) 3 attention start, 17, 18, 19 as above, 20 chunk partials published, 7 attention
+    vector summed from the partials, 8 O done.
 """
 
 from __future__ import annotations
@@ -26,9 +26,13 @@ import json
 import numpy as np
 import torch
 
-COLUMNS = ["QKV", "qkv hop", "rope+scores+local stats", "stats exchange", "PV", "partials+merge",
+# "(rope) scores + local stats": RoPE of q is part of it on the general kernel, done by the QKV
+# producers on the split-role kernel.  "partials": from P.V to the chunk partials published (the
+# leader's merge included on the general kernel); "attn hop": from there to the O workgroups
+# starting (which add the partials themselves on the split-role kernel).
+COLUMNS = ["QKV", "qkv hop", "(rope) scores + local stats", "stats exchange", "PV", "partials",
            "attn hop", "O", "h1 hop", "gate/up", "act hop", "down", "x hop"]
-EXCHANGES = {"qkv hop", "stats exchange", "partials+merge", "attn hop", "h1 hop", "act hop", "x hop"}
+EXCHANGES = {"qkv hop", "stats exchange", "partials", "attn hop", "h1 hop", "act hop", "x hop"}
 WGS = 256
 SLOTS = 40
 
@@ -91,7 +95,7 @@ def _rows(ev: np.ndarray, split_role: bool) -> np.ndarray:
     for l in range(ev.shape[1] - 1):
         e, nxt = ev[:, l, :], ev[:, l + 1, :]
         att = np.array([w for w in A if not np.isnan(e[w, start])])
-        if split_role:
+        if split_role:  # every chunk publishes its partials
             lead = np.array([w for w in att if not np.isnan(e[w, 20])])
             merged = mx(e[lead, 20])
         else:
