@@ -1839,6 +1839,7 @@ __device__ __forceinline__ void producer_b(const Params& p, const PlanB<G>& P, S
     const uint8_t* cache = nullptr;
     const LayerW& Lw = sm.lw[layer];
     auto u8 = [](const void* q) { return reinterpret_cast<const uint8_t*>(q); };
+    int blkv = 0;  // K/V segments: lane i holds the block id of the item's i-th 16-token block
     switch (kind) {
       case B_NORM1: base = u8(Lw.norm1); break;
       case B_QKV: base = u8(Lw.qkv) + size_t(P.q0) * G::H * 2; break;
@@ -1847,6 +1848,7 @@ __device__ __forceinline__ void producer_b(const Params& p, const PlanB<G>& P, S
         ig = sm.it[idx].g;
         it0 = sm.it[idx].t0;
         cache = u8(sm.kvp[layer]);
+        blkv = lane < TCB / 16 + 2 ? sm.blk[idx][lane] : 0;
         break;
       case B_O: base = u8(Lw.o) + size_t(P.o0) * G::H * 2; break;
       case B_NORM2: base = u8(Lw.norm2); break;
@@ -1871,10 +1873,12 @@ __device__ __forceinline__ void producer_b(const Params& p, const PlanB<G>& P, S
       const uint8_t* src = nullptr;
       if (off < bytes) {
         if (kind == B_K || kind == B_V) {
+          // 8 tokens per packet, all in one 16-token block (items start on a block boundary), so
+          // the block id is the same for every lane: read it from the register, no LDS wait
           const int jt = int(off >> 7);
           const int part = int(((off >> 4) - uint32_t(jt)) & 7u);
           const int t = it0 + jt;
-          const int blk = sm.blk[idx][t / 16 - it0 / 16];
+          const int blk = __builtin_amdgcn_readlane(blkv, int(i >> 1));
           const long long e = (long long)blk * p.block_stride + (long long)(t & 15) * p.token_stride +
                               (long long)ig * p.head_stride + (kind == B_V ? p.v_off : p.k_off) + part * 8;
           src = cache + e * 2;
@@ -2188,6 +2192,7 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
     }
     uint32_t klo[4] = {0u, 0u, 0u, 0u}, khi[4] = {0u, 0u, 0u, 0u};
     if (has_new) rope_pair(in + 192, klo, khi);
+    if (k == 0) trk(0, 38);  // diagnostics: item 0 roped
     if (has_new && sm.sSlot[b] >= 0 && hq < 2) {  // KV append (block360_kernel.inc:124-135)
       // lane 16q (k) / 16q + 1 (v) writes pieces q and q + 4 of the new token
       const long long slot = sm.sSlot[b];
@@ -2220,9 +2225,15 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
     const bf16x8 bq0 = __builtin_bit_cast(bf16x8, make_uint4(qlo[0], qlo[1], qlo[2], qlo[3]));
     const bf16x8 bq1 = __builtin_bit_cast(bf16x8, make_uint4(qhi[0], qhi[1], qhi[2], qhi[3]));
     const int ntiles = (j1 - j0 + 15) / 16;
+    static_assert((TCB + 1 + NCW - 1) / NCW + 15 <= 5 * 16, "a wave's tokens of an item fit 5 tiles");
+    // per tile: K rows from the ring (or k_new), two MFMAs, the scores bf16(q.k) / 8 (HF) stored
+    // for pass B and kept in registers (sv, -inf past the wave's tokens) for the statistics
+    float sv[5][4];
 #pragma unroll
     for (int ti = 0; ti < 5; ++ti) {
-      if (ti >= ntiles) break;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) sv[ti][jj] = -INFINITY;
+      if (ti >= ntiles) continue;
       const int tok = j0 + ti * 16 + hq;       // A row of this lane
       uint4 a0 = make_uint4(0u, 0u, 0u, 0u), a1 = make_uint4(0u, 0u, 0u, 0u);
       if (tok < T_old) {
@@ -2240,7 +2251,9 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
         for (int jj = 0; jj < 4; ++jj) {
           const int t = j0 + ti * 16 + 4 * pq + jj;
           if (t < j1) {
-            sm.at.sc[k][hq][t] = uint16_t(f2bf(rnd(acc[jj]) * 0.125f));
+            const float sc = rnd(acc[jj]) * 0.125f;
+            sv[ti][jj] = sc;
+            sm.at.sc[k][hq][t] = uint16_t(f2bf(sc));
             const int pos = it.t0 + t;
             if (dbg_attn && pos < int(Dbg<G>::SEQ)) {
               p.debug[Dbg<G>::AQK + Dbg<G>::head_pos(b, g * 3 + hq, pos)] = uint16_t(f2bf(acc[jj]));
@@ -2250,22 +2263,33 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
         }
     }
     wait_lgkm0();
+    if (k == 0) trk(0, 39);  // diagnostics: item 0's score tiles stored
     C.release(C.pos);  // this item's K is no longer read
-    // per-wave (max, sum) of each head over the wave's tokens, two tokens per lane from LDS
+    // per-wave (max, sum) of each head: tile ti's head columns 0-2 move to lanes 3ti .. 3ti+2 of
+    // each 16-lane row (DPP row_shr:3ti), so lane c holds head c % 3's scores of tile c / 3
+    {
+      const int ct = hq / 3, ch = hq - 3 * ct;
+      float ev[4];
 #pragma unroll
-    for (int h = 0; h < 3; ++h) {
-      float sv[2];
+      for (int jj = 0; jj < 4; ++jj) {
+        float v = sv[0][jj];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int j = j0 + lane + 64 * i;
-        sv[i] = j < j1 ? bf2f(sm.at.sc[k][h][j]) : -INFINITY;
+        for (int i = 1; i < 5; ++i) {
+          const float t = dpp_shr3<true>(i, sv[i][jj]);
+          v = ct == i ? t : v;
+        }
+        ev[jj] = ct < 5 ? v : -INFINITY;
       }
-      const float m = wave_max(fmaxf(sv[0], sv[1]));
+      float mw[3], lw[3];
+      head_totals<true>(fmaxf(fmaxf(ev[0], ev[1]), fmaxf(ev[2], ev[3])), mw);
+      const float m = ch == 0 ? mw[0] : ch == 1 ? mw[1] : mw[2];
       float ls = 0.f;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) ls += sv[i] == -INFINITY ? 0.f : expf(sv[i] - m);
-      ls = wave_sum(ls);
-      if (lane == 0) { sm.at.wml[k][w][0][h] = m; sm.at.wml[k][w][1][h] = ls; }
+      for (int jj = 0; jj < 4; ++jj) ls += ev[jj] == -INFINITY ? 0.f : expf(ev[jj] - m);
+      head_totals<false>(ls, lw);
+      if (lane == 0)
+#pragma unroll
+        for (int h = 0; h < 3; ++h) { sm.at.wml[k][w][0][h] = mw[h]; sm.at.wml[k][w][1][h] = lw[h]; }
     }
     trk(k, 20 + 3 * k);
   }
