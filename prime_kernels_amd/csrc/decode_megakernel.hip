@@ -1649,6 +1649,7 @@ struct SmemB {
   static constexpr int XS = G::I > G::H ? G::I : G::H;
   struct Attn {
     float qb[IPW][5 * 64];            // per item: 3 q heads, then (leader items) the new k and v
+    uint16_t qr[IPW][4][64];          // per item: the roped q heads and (leaders) new k, bf16
     uint16_t sc[IPW][3][TCB + 2];     // bf16 scores of every item of this workgroup
     uint16_t pb[3][TCB + 4];          // bf16 probabilities (each wave its own token range)
     float own[IPW][3 * 64];           // leader items: this chunk's partial sums of p.v
@@ -2135,6 +2136,19 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
     }
   }
   C.cbar();
+  // RoPE of every item's q heads (and the leaders' new k) once, all waves at once: pair (d, d + 32)
+  // of a head gives bf16(bf16(x cos) + bf16(-y sin)) and bf16(bf16(y cos) + bf16(x sin)), HF's
+  // rounding (modeling_llama.py:138-160); the items' score tiles read the bf16 pieces from qr
+  for (int i = C.ct; i < P.ni * 4 * 32; i += NCT) {
+    const int k = i >> 7, hv = (i >> 5) & 3, d = i & 31;
+    if (hv == 3 && sm.it[k].c != sm.it[k].C - 1) continue;
+    const float* head = sm.at.qb[k] + hv * 64;
+    const float* cs = sm.at.csr[sm.it[k].b];
+    const float x = head[d], y = head[d + 32], c = cs[d], s = cs[32 + d];
+    sm.at.qr[k][hv][d] = uint16_t(f2bf(rnd(rnd(x * c) + rnd((-y) * s))));
+    sm.at.qr[k][hv][d + 32] = uint16_t(f2bf(rnd(rnd(y * c) + rnd(x * s))));
+  }
+  C.cbar();
   tri(4);
   // ---- A: scores and per-wave statistics of every item ----
   // Scores on the matrix cores: D[token][head] = K[token][:] . q[head][:] as 16-token tiles,
@@ -2157,41 +2171,22 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
     trk(k, 18 + 3 * k);
     C.wait_filled(C.pos);
     trk(k, 19 + 3 * k);
-    // RoPE of pieces pq (first half) and pq + 4 (second half) of a head: dims 8pq..8pq+7 and +32
-    float cs8[8], sn8[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      cs8[e] = sm.at.csr[b][pq * 8 + e];
-      sn8[e] = sm.at.csr[b][32 + pq * 8 + e];
-    }
-    auto rope_pair = [&](const float* head, uint32_t (&lo)[4], uint32_t (&hi)[4]) {
-      const float4 a0 = *reinterpret_cast<const float4*>(head + pq * 8);
-      const float4 a1 = *reinterpret_cast<const float4*>(head + pq * 8 + 4);
-      const float4 b0 = *reinterpret_cast<const float4*>(head + 32 + pq * 8);
-      const float4 b1 = *reinterpret_cast<const float4*>(head + 32 + pq * 8 + 4);
-      const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-      const float y[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-      float rl[8], rh[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        rl[e] = rnd(rnd(x[e] * cs8[e]) + rnd((-y[e]) * sn8[e]));
-        rh[e] = rnd(rnd(y[e] * cs8[e]) + rnd(x[e] * sn8[e]));
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        lo[e] = pack2(rl[2 * e], rl[2 * e + 1]);
-        hi[e] = pack2(rh[2 * e], rh[2 * e + 1]);
-      }
+    // the roped pieces pq (dims 8pq .. 8pq+7) and pq + 4 (dims 32 + 8pq ..) of a head, bf16
+    auto rope_pair = [&](int hv, uint32_t (&lo)[4], uint32_t (&hi)[4]) {
+      const uint4 a = *reinterpret_cast<const uint4*>(&sm.at.qr[k][hv][pq * 8]);
+      const uint4 c = *reinterpret_cast<const uint4*>(&sm.at.qr[k][hv][32 + pq * 8]);
+      lo[0] = a.x; lo[1] = a.y; lo[2] = a.z; lo[3] = a.w;
+      hi[0] = c.x; hi[1] = c.y; hi[2] = c.z; hi[3] = c.w;
     };
     uint32_t qlo[4] = {0u, 0u, 0u, 0u}, qhi[4] = {0u, 0u, 0u, 0u};
-    if (hq < 3) rope_pair(in + hq * 64, qlo, qhi);
+    if (hq < 3) rope_pair(hq, qlo, qhi);
     if (dbg_attn && it.c == 0 && w == 0 && hq < 3) {
       uint16_t* dq = p.debug + Dbg<G>::AQ + size_t(b) * G::H + (g * 3 + hq) * 64 + pq * 8;
       *reinterpret_cast<uint4*>(dq) = make_uint4(qlo[0], qlo[1], qlo[2], qlo[3]);
       *reinterpret_cast<uint4*>(dq + 32) = make_uint4(qhi[0], qhi[1], qhi[2], qhi[3]);
     }
     uint32_t klo[4] = {0u, 0u, 0u, 0u}, khi[4] = {0u, 0u, 0u, 0u};
-    if (has_new) rope_pair(in + 192, klo, khi);
+    if (has_new) rope_pair(3, klo, khi);
     if (k == 0) trk(0, 38);  // diagnostics: item 0 roped
     if (has_new && sm.sSlot[b] >= 0 && hq < 2) {  // KV append (block360_kernel.inc:124-135)
       // lane 16q (k) / 16q + 1 (v) writes pieces q and q + 4 of the new token
@@ -2228,24 +2223,30 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
     static_assert((TCB + 1 + NCW - 1) / NCW + 15 <= 5 * 16, "a wave's tokens of an item fit 5 tiles");
     // per tile: K rows from the ring (or k_new), two MFMAs, the scores bf16(q.k) / 8 (HF) stored
     // for pass B and kept in registers (sv, -inf past the wave's tokens) for the statistics
+    // every tile's K rows are read before the first MFMA, so the LDS reads overlap
+    uint4 ka[5][2];
+#pragma unroll
+    for (int ti = 0; ti < 5; ++ti) {
+      ka[ti][0] = ka[ti][1] = make_uint4(0u, 0u, 0u, 0u);
+      if (ti >= ntiles) continue;
+      const int tok = j0 + ti * 16 + hq;       // A row of this lane
+      if (tok < T_old) {
+        ka[ti][0] = C.ring16(segk + kvb_slot(tok, pq));
+        ka[ti][1] = C.ring16(segk + kvb_slot(tok, pq + 4));
+      } else if (tok == T_old && leader) {
+        ka[ti][0] = make_uint4(klo[0], klo[1], klo[2], klo[3]);
+        ka[ti][1] = make_uint4(khi[0], khi[1], khi[2], khi[3]);
+      }
+    }
     float sv[5][4];
 #pragma unroll
     for (int ti = 0; ti < 5; ++ti) {
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) sv[ti][jj] = -INFINITY;
       if (ti >= ntiles) continue;
-      const int tok = j0 + ti * 16 + hq;       // A row of this lane
-      uint4 a0 = make_uint4(0u, 0u, 0u, 0u), a1 = make_uint4(0u, 0u, 0u, 0u);
-      if (tok < T_old) {
-        a0 = C.ring16(segk + kvb_slot(tok, pq));
-        a1 = C.ring16(segk + kvb_slot(tok, pq + 4));
-      } else if (tok == T_old && leader) {
-        a0 = make_uint4(klo[0], klo[1], klo[2], klo[3]);
-        a1 = make_uint4(khi[0], khi[1], khi[2], khi[3]);
-      }
       floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a0), bq0, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1), bq1, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[ti][0]), bq0, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[ti][1]), bq1, acc, 0, 0, 0);
       if (hq < 3)
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
@@ -2382,13 +2383,25 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
     const bool has_new = leader && j1 == T && T > j0;
     const uint32_t segv = C.next_seg(uint32_t(T_old) * 128u);
     const float* in = sm.at.qb[k];
+    {
+      // the three heads' statistics and scores are read before any probability is stored
+      float M[3], inv[3];
 #pragma unroll
-    for (int h = 0; h < 3; ++h) {
-      const float M = sm.at.gml[k][0][h], inv = 1.0f / sm.at.gml[k][1][h];
+      for (int h = 0; h < 3; ++h) {
+        M[h] = sm.at.gml[k][0][h];
+        inv[h] = 1.0f / sm.at.gml[k][1][h];
+      }
       for (int j = j0 + lane; j < j1; j += 64) {
-        sm.at.pb[h][j] = uint16_t(f2bf(expf(bf2f(sm.at.sc[k][h][j]) - M) * inv));
-        if (dbg_attn && it.t0 + j < int(Dbg<G>::SEQ))
-          p.debug[Dbg<G>::APR + Dbg<G>::head_pos(it.b, it.g * 3 + h, it.t0 + j)] = sm.at.pb[h][j];
+        float s[3];
+#pragma unroll
+        for (int h = 0; h < 3; ++h) s[h] = bf2f(sm.at.sc[k][h][j]);
+#pragma unroll
+        for (int h = 0; h < 3; ++h) {
+          const uint16_t pv = uint16_t(f2bf(expf(s[h] - M[h]) * inv[h]));
+          sm.at.pb[h][j] = pv;
+          if (dbg_attn && it.t0 + j < int(Dbg<G>::SEQ))
+            p.debug[Dbg<G>::APR + Dbg<G>::head_pos(it.b, it.g * 3 + h, it.t0 + j)] = pv;
+        }
       }
     }
     wait_lgkm0();
@@ -2397,6 +2410,7 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
     const int jo1 = min(j1, T_old);
     const int npairs = jo1 > j0 ? (jo1 - j0) / 2 : 0;
     float acc[3][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
+#pragma unroll 4
     for (int kp = half; kp < npairs; kp += 2) {
       const int j = j0 + 2 * kp;
       const uint32_t va = C.ring4(segv + kvb_slot(j, d2 >> 2) + voff);
