@@ -1972,35 +1972,71 @@ template <class G>
 __device__ __forceinline__ void norm_staged(ConsumerB<G>& C, uint32_t segw) {
   SmemB<G>& sm = C.sm;
   constexpr int CH = G::H / 8;
-  for (int b = C.cw; b < C.P.B; b += NCW) {
-    float s = 0.f;
-    for (int c = C.lane; c < CH; c += 64) {
-      const uint4 v = *reinterpret_cast<const uint4*>(sm.xs + b * G::H + c * 8);
-      const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+  constexpr int SPW = (BMAX + NCW - 1) / NCW;  // sequences per wave
+  static_assert(CH <= 128, "two 8-value chunks per lane cover a row");
+  {
+    // the wave's sequences together: every load first, then the sums and their reductions, then
+    // lane i forms the scale of the wave's i-th sequence (one divide / square root chain per wave)
+    uint4 v[SPW][2];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float lo = bf_lo(u[e]), hi = bf_hi(u[e]);
-        s += lo * lo + hi * hi;
+    for (int i = 0; i < SPW; ++i) {
+      const int b = C.cw + NCW * i;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int c = C.lane + 64 * h;
+        v[i][h] = b < C.P.B && c < CH ? *reinterpret_cast<const uint4*>(sm.xs + b * G::H + c * 8)
+                                      : make_uint4(0u, 0u, 0u, 0u);
       }
     }
-    s = wave_sum(s);
-    if (C.lane == 0) sm.rsb[b] = rms_scale(s, G::H);
+    float s[SPW];
+#pragma unroll
+    for (int i = 0; i < SPW; ++i) {
+      s[i] = 0.f;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t u[4] = {v[i][h].x, v[i][h].y, v[i][h].z, v[i][h].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = bf_lo(u[e]), hi = bf_hi(u[e]);
+          s[i] += lo * lo + hi * hi;
+        }
+      }
+    }
+    wave_sum_n<SPW>(s);
+    float mine = s[0];
+#pragma unroll
+    for (int i = 1; i < SPW; ++i) mine = C.lane == i ? s[i] : mine;
+    const int b = C.cw + NCW * C.lane;
+    if (C.lane < SPW && b < C.P.B) sm.rsb[b] = rms_scale(mine, G::H);
   }
   C.cbar();
-  for (int i = C.ct; i < C.P.B * CH; i += NCT) {
-    const int b = i / CH, c = i - b * CH;
-    uint4* px = reinterpret_cast<uint4*>(sm.xs + b * G::H + c * 8);
-    const uint4 v = *px;
-    const uint4 wv = C.ring16(segw + uint32_t(c) * 16u);
-    const float rs = sm.rsb[b];
-    const uint32_t u[4] = {v.x, v.y, v.z, v.w}, wu[4] = {wv.x, wv.y, wv.z, wv.w};
-    uint32_t o[4];
+  // 8-value chunks of all rows, four per thread in flight: loads first, then the stores
+  constexpr int U = 4;
+  for (int i0 = C.ct; i0 < C.P.B * CH; i0 += U * NCT) {
+    uint4 v[U], wv[U];
+    float rs[U];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t t = pack2(bf_lo(u[e]) * rs, bf_hi(u[e]) * rs);
-      o[e] = pack2(bf_lo(wu[e]) * bf_lo(t), bf_hi(wu[e]) * bf_hi(t));
+    for (int u = 0; u < U; ++u) {
+      const int i = min(i0 + u * NCT, C.P.B * CH - 1);
+      const int b = i / CH, c = i - b * CH;
+      v[u] = *reinterpret_cast<const uint4*>(sm.xs + b * G::H + c * 8);
+      wv[u] = C.ring16(segw + uint32_t(c) * 16u);
+      rs[u] = sm.rsb[b];
     }
-    *px = make_uint4(o[0], o[1], o[2], o[3]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * NCT;
+      if (i >= C.P.B * CH) continue;
+      const int b = i / CH, c = i - b * CH;
+      const uint32_t x[4] = {v[u].x, v[u].y, v[u].z, v[u].w}, wu[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t t = pack2(bf_lo(x[e]) * rs[u], bf_hi(x[e]) * rs[u]);
+        o[e] = pack2(bf_lo(wu[e]) * bf_lo(t), bf_hi(wu[e]) * bf_hi(t));
+      }
+      *reinterpret_cast<uint4*>(sm.xs + b * G::H + c * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
   }
   C.cbar();
 }
@@ -2014,6 +2050,7 @@ __device__ __forceinline__ floatx4 mfma_part(const ConsumerB<G>& C, uint32_t seg
   const int s0 = KS * w / nw, s1 = KS * (w + 1) / nw;
   const int row = C.lane & 15, kq = (C.lane >> 4) * 8;
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
   for (int s = s0; s < s1; ++s) {
     const int k = s * 32 + kq;
     const uint4 a = C.ring16(seg + uint32_t(row * K + k) * 2u);
