@@ -1650,7 +1650,7 @@ struct SmemB {
   struct Attn {
     float qb[IPW][5 * 64];            // per item: 3 q heads, then (leader items) the new k and v
     uint16_t qr[IPW][4][64];          // per item: the roped q heads and (leaders) new k, bf16
-    uint16_t sc[IPW][3][TCB + 2];     // bf16 scores of every item of this workgroup
+    uint16_t sc[IPW][3][TCB + 4];     // bf16 scores of every item of this workgroup (rows 8-byte aligned)
     uint16_t pb[3][TCB + 4];          // bf16 probabilities (each wave its own token range)
     float own[IPW][3 * 64];           // leader items: this chunk's partial sums of p.v
     float wml[IPW][NCW][2][3];        // per item and wave: softmax max / sum per head
@@ -2284,22 +2284,28 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
       floatx4 acc = {0.f, 0.f, 0.f, 0.f};
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[ti][0]), bq0, acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[ti][1]), bq1, acc, 0, 0, 0);
-      if (hq < 3)
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int t = j0 + ti * 16 + 4 * pq + jj;
-          if (t < j1) {
-            const float sc = rnd(acc[jj]) * 0.125f;
-            sv[ti][jj] = sc;
-            sm.at.sc[k][hq][t] = uint16_t(f2bf(sc));
-            const int pos = it.t0 + t;
-            if (dbg_attn && pos < int(Dbg<G>::SEQ)) {
-              p.debug[Dbg<G>::AQK + Dbg<G>::head_pos(b, g * 3 + hq, pos)] = uint16_t(f2bf(acc[jj]));
-              p.debug[Dbg<G>::ASC + Dbg<G>::head_pos(b, g * 3 + hq, pos)] = sm.at.sc[k][hq][t];
-            }
-          }
+      for (int jj = 0; jj < 4; ++jj) {
+        const int t = j0 + ti * 16 + 4 * pq + jj;
+        sv[ti][jj] = t < j1 ? rnd(acc[jj]) * 0.125f : -INFINITY;
+        const int pos = it.t0 + t;
+        if (dbg_attn && hq < 3 && t < j1 && pos < int(Dbg<G>::SEQ)) {
+          p.debug[Dbg<G>::AQK + Dbg<G>::head_pos(b, g * 3 + hq, pos)] = uint16_t(f2bf(acc[jj]));
+          p.debug[Dbg<G>::ASC + Dbg<G>::head_pos(b, g * 3 + hq, pos)] = uint16_t(f2bf(sv[ti][jj]));
         }
+      }
     }
+    // the scores of a lane's four consecutive tokens as one 8-byte store per tile, after the MFMAs.
+    // Every wave's range but the last ends on a 16-token boundary, so only the last wave's final
+    // group can pass its end T, writing -inf into slots T .. T + 2 of the row's padding (T <= TCB + 1).
+    if (hq < 3)
+#pragma unroll
+      for (int ti = 0; ti < 5; ++ti) {
+        const int t = j0 + ti * 16 + 4 * pq;
+        if (ti < ntiles && t < j1)
+          *reinterpret_cast<uint2*>(&sm.at.sc[k][hq][t]) =
+              make_uint2(pack2(sv[ti][0], sv[ti][1]), pack2(sv[ti][2], sv[ti][3]));
+      }
     wait_lgkm0();
     if (k == 0) trk(0, 39);  // diagnostics: item 0's score tiles stored
     C.release(C.pos);  // this item's K is no longer read
