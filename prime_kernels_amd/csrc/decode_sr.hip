@@ -691,6 +691,13 @@ constexpr int MT = (TCS + 1 + 16 * NCW - 1) / (16 * NCW);
 struct ChunkRegs {
   uint32_t va[MT][4][2];    // V of the wave's tiles: A operands of the P.V tiles (bf16 pairs)
 };
+// Waves that take the chunk's 16-token tiles (tile t to wave t % NW, its (t / NW)-th): all NCW,
+// except in the leader chunk when the first NCW - 1 can hold every tile; its last wave then has
+// only the new token, whose k and v come from other producers than q and tend to arrive later.
+template <class G>
+__device__ __forceinline__ int tile_waves(const PlanSR<G>& P, int NT) {
+  return P.leader && NT <= (NCW - 1) * MT ? NCW - 1 : NCW;
+}
 
 // The wave's V from the ring into registers, long before q arrives (the chunk was streamed in during
 // the previous layer; V needs one 2-byte read per element, K is loaded with 16-byte reads just
@@ -704,7 +711,8 @@ __device__ __forceinline__ void chunk_load(CSR<G>& C, uint32_t seg, ChunkRegs& R
   const int w = C.cw, lane = C.lane;
   const int T_old = P.t1 - P.t0;
   const int NT = (T_old + 15) >> 4;
-  const int nt = NT > w ? (NT - w + NCW - 1) / NCW : 0;
+  const int NW = tile_waves<G>(P, NT);
+  const int nt = w < NW && NT > w ? (NT - w + NW - 1) / NW : 0;
   const int hq = lane & 15, pq = lane >> 4;
   // V element (mf, e) of this lane sits at byte tile*4096 + vo[mf][e] of the segment: token
   // 4 pq + e of the tile, piece (dim / 8 + token) % 8 of the token's V half, dim 16 mf + hq
@@ -722,7 +730,7 @@ __device__ __forceinline__ void chunk_load(CSR<G>& C, uint32_t seg, ChunkRegs& R
       for (int mf = 0; mf < 4; ++mf) R.va[i][mf][0] = R.va[i][mf][1] = 0u;
       continue;
     }
-    const int tile = w + NCW * i;
+    const int tile = w + NW * i;
     const uint32_t base = seg + uint32_t(tile) * 4096u;
     uint32_t h[4][4];
 #pragma unroll
@@ -750,10 +758,11 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
   SmemSR<G>& sm = C.sm;
   const int g = P.g, lane = C.lane, w = C.cw;
   const int T_old = P.t1 - P.t0;
-  // 16-token tiles of the chunk's cached tokens, tile t to wave t % NCW; the new token (the leader's)
-  // is taken apart by the last wave, which has the fewest tiles
+  // 16-token tiles of the chunk's cached tokens, tile t to wave t % NW (tile_waves); the new token
+  // (the leader's) is taken apart by the last wave, which has the fewest tiles or none
   const int NT = (T_old + 15) >> 4;
-  const int nt = NT > w ? (NT - w + NCW - 1) / NCW : 0;
+  const int NW = tile_waves<G>(P, NT);
+  const int nt = w < NW && NT > w ? (NT - w + NW - 1) / NW : 0;
   const bool has_new = P.leader && w == NCW - 1;
   const int hq = lane & 15, pq = lane >> 4;
   float* in = sm.at.qkvw[w];
@@ -765,7 +774,7 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
   for (int i = 0; i < MT; ++i) {
     ka[i][0] = ka[i][1] = make_uint4(0u, 0u, 0u, 0u);
     if (i >= nt) continue;
-    const int tok = (w + NCW * i) * 16 + hq;
+    const int tok = (w + NW * i) * 16 + hq;
     const uint32_t row = seg + uint32_t(tok) * 256u;
     ka[i][0] = C.ring16(row + uint32_t((pq + tok) & 7) * 16u);
     ka[i][1] = C.ring16(row + uint32_t((pq + 4 + tok) & 7) * 16u);
@@ -871,39 +880,50 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
   // HF's bf16(exp(s - M) / L) up to fp32 rounding.
   static_assert(3 * MT <= 16, "three columns per tile fit a 16-lane row");
   const int ct = hq / 3, ch = hq - 3 * ct;
-  float ev[4];
-  {
+  float ev[4] = {0.f, 0.f, 0.f, 0.f}, m = -INFINITY;
+  float mw[3], lw[3], ev_new[3];
+  if (nt > 0) {
+    {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        float v = sacc[0][jj];
+#pragma unroll
+        for (int i = 1; i < MT; ++i) {
+          const float t = dpp_shr3<true>(i, sacc[i][jj]);
+          v = ct == i ? t : v;
+        }
+        const int t = (w + NW * ct) * 16 + 4 * pq + jj;
+        const bool ok = ct < nt && t < T_old;
+        ev[jj] = ok ? rnd(v) * 0.125f : -INFINITY;
+      }
+    }
+    m = fmaxf(fmaxf(ev[0], ev[1]), fmaxf(ev[2], ev[3]));
+    head_totals<true>(m, mw);
+#pragma unroll
+    for (int h = 0; h < 3; ++h) mw[h] = fmaxf(mw[h], s_new[h]);
+    m = ch == 0 ? mw[0] : ch == 1 ? mw[1] : mw[2];
+    float lsum = 0.f;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
-      float v = sacc[0][jj];
-#pragma unroll
-      for (int i = 1; i < MT; ++i) {
-        const float t = dpp_shr3<true>(i, sacc[i][jj]);
-        v = ct == i ? t : v;
-      }
-      const int t = (w + NCW * ct) * 16 + 4 * pq + jj;
-      const bool ok = ct < nt && t < T_old;
-      ev[jj] = ok ? rnd(v) * 0.125f : -INFINITY;
+      ev[jj] = ev[jj] == -INFINITY ? 0.f : __expf(ev[jj] - m);
+      lsum += ev[jj];
     }
-  }
-  float m = fmaxf(fmaxf(ev[0], ev[1]), fmaxf(ev[2], ev[3]));
-  float mw[3], lw[3];
-  head_totals<true>(m, mw);
+    head_totals<false>(lsum, lw);
 #pragma unroll
-  for (int h = 0; h < 3; ++h) mw[h] = fmaxf(mw[h], s_new[h]);
-  m = ch == 0 ? mw[0] : ch == 1 ? mw[1] : mw[2];
-  float lsum = 0.f;
+    for (int h = 0; h < 3; ++h) {
+      ev_new[h] = s_new[h] == -INFINITY ? 0.f : __expf(s_new[h] - mw[h]);
+      lw[h] += ev_new[h];
+    }
+  } else {
+    // no cached tile (the leader's new-token wave when the other waves hold every tile): the new
+    // token's scores alone, max s_new and sum exp(0) = 1, the values the general path gives
 #pragma unroll
-  for (int jj = 0; jj < 4; ++jj) {
-    ev[jj] = ev[jj] == -INFINITY ? 0.f : __expf(ev[jj] - m);
-    lsum += ev[jj];
-  }
-  head_totals<false>(lsum, lw);
-  float ev_new[3];
-#pragma unroll
-  for (int h = 0; h < 3; ++h) {
-    ev_new[h] = s_new[h] == -INFINITY ? 0.f : __expf(s_new[h] - mw[h]);
-    lw[h] += ev_new[h];
+    for (int h = 0; h < 3; ++h) {
+      mw[h] = s_new[h];
+      ev_new[h] = s_new[h] == -INFINITY ? 0.f : 1.f;
+      lw[h] = ev_new[h];
+    }
+    m = ch == 0 ? mw[0] : ch == 1 ? mw[1] : mw[2];
   }
   if (lane == 0)
 #pragma unroll
