@@ -138,6 +138,13 @@ struct Plan {
     const int old = S - 1;
     int C0 = old <= 0 ? 1 : max((old + TC_LONG - 1) / TC_LONG, min((old + TC_SHORT - 1) / TC_SHORT, C_SHORT));
     C0 = min(C0, NWG / G::KVH);
+    // at most NCT - 192 chunks: a chunk's merge slice (192 / C values, rounded up) times C records
+    // is then at most NCT (one read per consumer thread); 12288 / 64 tokens fit a chunk
+    static_assert(kMaxSeq / (NCT - REC_WORDS) <= TC_MAX, "the chunk cap leaves chunks of at most TC_MAX");
+    C0 = min(C0, NCT - REC_WORDS);
+    // no more chunks than one XCD holds (NWG / 8, the same-XCD records below) while chunks of at
+    // most TC_MAX tokens allow it: at 8192 cached tokens 32 chunks of 256-288 instead of 47 of 176
+    C0 = min(C0, max(NWG / 8, (old + TC_MAX - 1) / TC_MAX));
     const int tc = old <= 0 ? 16 : ((old + C0 - 1) / C0 + 15) / 16 * 16;
     C = old <= 0 ? 1 : (old + tc - 1) / tc;
     natt = G::KVH * C;
@@ -273,6 +280,7 @@ struct Smem {
   float red[NCW];
   float wml[NCW][2][3];          // per-wave softmax max / sum per head
   float wo[NCW][3][64];          // per-wave P.V partial per head
+  float mg[NCT];                 // attention merge: the head's chunk records of this chunk's slice
   LayerW lw[G::L];               // layer pointer table (read by the producers from LDS)
   const void* kvp[G::L];         // per-layer KV cache base
   GUE gue[G::L];                 // per-layer lossless gate/up streams of this workgroup
@@ -1153,58 +1161,50 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
     }
   C.cbar();
   if (w == 0 && lane == 0) trace_at(p, l, 19, p.n_layers);
-  if (w >= 3) return;
-  // wave w: head h = 3g + w.  The chunk's partial sum of p.v (fixed wave order), fp32.
-  const int hh = w, d = lane;
-  float O = 0.f;
-#pragma unroll
-  for (int v = 0; v < NCW; ++v) O += sm.wo[v][hh][d];
-  if (w == 0 && lane == 0) trace_at(p, l, 4, p.n_layers);
   const bool l2 = P.xcd && C.l2rec;
   uint64_t* rec_base = reinterpret_cast<uint64_t*>(l2 ? p.xws + (W::rec(l, 0) - W::REC0) : p.ws + W::rec(l, 0));
-  if (!P.leader) {
+  // every chunk (the leader too) publishes its partial sum of p.v, fp32, wave w < 3 head 3g + w
+  // (the 4 waves' parts added in fixed wave order)
+  if (w < 3) {
+    float O = 0.f;
+#pragma unroll
+    for (int v = 0; v < NCW; ++v) O += sm.wo[v][w][lane];
+    if (w == 0 && lane == 0) trace_at(p, l, 4, p.n_layers);
     skew_delay(p.skew, P.wg, l, 12);
-    uint64_t* dst = rec_base + size_t(g * P.C + P.c) * REC_WORDS + hh * 64 + d;
+    uint64_t* dst = rec_base + size_t(g * P.C + P.c) * REC_WORDS + w * 64 + lane;
     if (l2) st_l2(dst, tg | __float_as_uint(O));
     else st_dev64(dst, tg | __float_as_uint(O));
-    return;
   }
-  // leader: sum the chunk partials 0..C-1 in chunk order (this chunk is C-1), round once
-  const float o_own = O;
-  O = 0.f;
-  constexpr int MB = 16;  // chunk records polled at once
-  for (int c0 = 0; c0 < P.C - 1; c0 += MB) {
-    const int nc = min(MB, P.C - 1 - c0);
-    uint64_t ro[MB];
-    uint32_t pend = 0;
-#pragma unroll
-    for (int k = 0; k < MB; ++k)
-      if (k < nc) {
-        ro[k] = ld_dev64(rec_base + size_t(g * P.C + c0 + k) * REC_WORDS + hh * 64 + d);
-        pend |= 1u << k;
-      }
+  // The head's 192 attention values are summed by its C chunks: chunk c adds the slice
+  // [192 c / C, 192 (c + 1) / C) over all C records, in chunk order, and rounds once (HF's
+  // bf16(p.v) of the whole head).  Read i (i < slice x C <= 192 + C <= NCT: C is capped at
+  // NCT - 192) is record i % C of value lo + i / C, one per consumer thread, all in flight
+  // together; one thread per value then adds its C records from LDS.
+  const int lo = (REC_WORDS * P.c) / P.C, nval = (REC_WORDS * (P.c + 1)) / P.C - lo;
+  const int t = C.ct;
+  for (int i = t; i < nval * P.C; i += NCT) {
+    const int vi = i / P.C, k = i - vi * P.C;
+    const uint64_t* src = rec_base + size_t(g * P.C + k) * REC_WORDS + lo + vi;
+    uint64_t v = ld_dev64(src);
     Spin spin(p.ws, C.tag32, 5);
-    while (true) {
-#pragma unroll
-      for (int k = 0; k < MB; ++k)
-        if (((pend >> k) & 1u) && uint32_t(ro[k] >> 32) == C.tag32) pend &= ~(1u << k);
-      if (!pend) break;
+    while (uint32_t(v >> 32) != C.tag32) {
       if (C.dead || !spin.again()) { C.dead = true; break; }
-#pragma unroll
-      for (int k = 0; k < MB; ++k)
-        if ((pend >> k) & 1u) ro[k] = ld_dev64(rec_base + size_t(g * P.C + c0 + k) * REC_WORDS + hh * 64 + d);
+      v = ld_dev64(src);
     }
-#pragma unroll
-    for (int k = 0; k < MB; ++k)
-      if (k < nc) O += __uint_as_float(uint32_t(ro[k]));
+    sm.mg[i] = __uint_as_float(uint32_t(v));
   }
+  C.cbar();
   if (w == 0 && lane == 0) trace_at(p, l, 20, p.n_layers);
-  O += o_own;
-  C.st_x(X_ATTN, l, (g * 3 + hh) * 64 + d, C.w64(O));
-  if (DBG && p.debug) {
-    const uint16_t ob = uint16_t(f2bf(O));
-    p.debug[size_t(l) * Dbg<G>::LAYER + Dbg<G>::ATTN + (g * 3 + hh) * 64 + d] = ob;
-    if (l == p.debug_layer) p.debug[Dbg<G>::APV + (g * 3 + hh) * 64 + d] = ob;
+  if (t < nval) {
+    float O = 0.f;
+    for (int k = 0; k < P.C; ++k) O += sm.mg[t * P.C + k];
+    const int e = g * REC_WORDS + lo + t;  // head 3g + (lo + t) / 64, dim (lo + t) % 64
+    C.st_x(X_ATTN, l, e, C.w64(O));
+    if (DBG && p.debug) {
+      const uint16_t ob = uint16_t(f2bf(O));
+      p.debug[size_t(l) * Dbg<G>::LAYER + Dbg<G>::ATTN + e] = ob;
+      if (l == p.debug_layer) p.debug[Dbg<G>::APV + e] = ob;
+    }
   }
   if (w == 0 && lane == 0) trace_at(p, l, 5, p.n_layers);
 }

@@ -58,7 +58,7 @@ constexpr int DEPTH = PK_DMA_DEPTH;      // packets in flight per producer wave 
 // exchanges wait in (16 -> 24: +11%, 32: +19%; 8 is 0.3-0.4% faster than 16 at contexts 1024 to
 // 8192, also with a depth of 32 for the LM-head segments alone, which is slower).
 constexpr int DEPTH_B = 32;
-constexpr int TC_MAX = 256;              // max cached tokens per attention chunk (64 KB of K/V)
+constexpr int TC_MAX = 288;              // max cached tokens per attention chunk (72 KB of K/V)
 // Batch-1 chunking of a KV head's cached tokens: chunks of up to TC_LONG tokens, but at least
 // C_SHORT chunks of at least TC_SHORT tokens while the context allows (measured at 360M batch 1:
 // more chunks shorten each chunk's work, and the exchanges between a head's chunks, through its
