@@ -188,7 +188,7 @@ struct Plan {
     } else {
       v0 = v1 = 0;
     }
-    n_lm = (v1 - v0 + LM_ROWS - 1) / LM_ROWS;
+    n_lm = (v1 - v0 + LM_ROWS_G - 1) / LM_ROWS_G;
   }
 };
 
@@ -200,7 +200,7 @@ struct Rows {
   static constexpr int O = per_wave((G::H + NWG / 2 - 1) / (NWG / 2));
   static constexpr int ACT = per_wave((G::I + NWG - 1) / NWG);
   static constexpr int DOWN = per_wave((G::H + NWG - 1) / NWG);
-  static constexpr int LM = LM_ROWS / NCW;
+  static constexpr int LM = LM_ROWS_G / NCW;
 };
 
 // Segments a workgroup streams, in stream order.  Per layer: norm1 weights, QKV rows, the
@@ -242,8 +242,8 @@ __device__ __forceinline__ uint32_t seg_bytes(const Plan<G>& P, int kind, int lm
     case S_DOWN: return uint32_t(P.d1 - P.d0) * G::I * WB;
     case S_DOWN_S: return G::WF ? uint32_t(P.d1 - P.d0) * scale_stride(G::I) : 0u;
     default: {
-      const int r0 = P.v0 + lm_index * LM_ROWS;
-      const int r1 = min(r0 + LM_ROWS, P.v1);
+      const int r0 = P.v0 + lm_index * LM_ROWS_G;
+      const int r1 = min(r0 + LM_ROWS_G, P.v1);
       return uint32_t(r1 - r0) * G::H * 2;
     }
   }
@@ -339,7 +339,7 @@ __device__ __forceinline__ void producer(const Params& p, const Plan<G>& P, Smem
     } else if (kind == S_FNORM) {
       base = reinterpret_cast<const uint8_t*>(p.final_norm);
     } else if (kind == S_LM) {
-      base = reinterpret_cast<const uint8_t*>(p.embed) + size_t(P.v0 + lm_index * LM_ROWS) * G::H * 2;
+      base = reinterpret_cast<const uint8_t*>(p.embed) + size_t(P.v0 + lm_index * LM_ROWS_G) * G::H * 2;
     } else if (kind == S_CS) {
       base = reinterpret_cast<const uint8_t*>(p.cos_sin) + size_t(P.pos) * 64 * (p.cs_fp32 ? 4 : 2);
     } else {
@@ -1446,8 +1446,8 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
   int best_i = 0x7fffffff;
   for (int j = 0; j < P.n_lm; ++j) {  // no segments without the LM head
     const uint32_t seg = C.next_seg(seg_bytes(P, S_LM, j, p.cs_fp32));
-    const int r0 = P.v0 + j * LM_ROWS;
-    const int nrows = min(LM_ROWS, P.v1 - r0);
+    const int r0 = P.v0 + j * LM_ROWS_G;
+    const int nrows = min(LM_ROWS_G, P.v1 - r0);
     C.wait_filled(C.pos);
     float out[R::LM];
     dots_ring<G, G::H, R::LM>(C, seg, nrows, x, out);

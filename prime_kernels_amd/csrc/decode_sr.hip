@@ -51,7 +51,7 @@ constexpr int TCS = 256;                 // max cached tokens per attention chun
 #define PK_SR_DEPTH 8
 #endif
 constexpr int DEPTH_SR = PK_SR_DEPTH;    // DMA packets in flight per producer wave
-constexpr int LM_ROWS_SR = 16;           // LM-head rows per ring segment
+constexpr int LM_ROWS_SR = 24;           // LM-head rows per ring segment, 6 per consumer wave (16: -1.5%)
 
 __device__ __forceinline__ bool in_a(int wg) { return (wg & 7) == 0; }
 

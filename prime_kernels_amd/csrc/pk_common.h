@@ -67,7 +67,8 @@ constexpr int TC_MAX = 288;              // max cached tokens per attention chun
 constexpr int TC_LONG = 128;
 constexpr int TC_SHORT = 64;
 constexpr int C_SHORT = 16;
-constexpr int LM_ROWS = 16;              // LM-head rows per ring segment
+constexpr int LM_ROWS = 16;              // LM-head rows per ring segment (batched kernel: one MFMA tile)
+constexpr int LM_ROWS_G = 24;            // LM-head rows per ring segment (general batch-1 kernel), 6 per wave
 constexpr int MAX_B = 16;                // exchange-buffer slots per layer
 constexpr int REC_WORDS = 3 * 64;        // attention partial: 3 heads x sum(p.v)[64], 64-bit words
 constexpr int STAT_WORDS = 6;            // chunk softmax statistics: 3 heads x (max, sum), 64-bit words
