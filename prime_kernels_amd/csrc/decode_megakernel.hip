@@ -1583,8 +1583,14 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel(Params p) {
   Plan<G> P;
   P.init(p, blockIdx.x);
   const uint32_t epoch = step_epoch(p.ws);
-  if (threadIdx.x < 64 * NPW) producer<G>(p, P, sm, epoch);
-  else consumer<G, DBG>(p, P, sm, epoch);
+  if (threadIdx.x < 64 * NPW) {
+    producer<G>(p, P, sm, epoch);
+  } else {
+    // the consumer waves are the step's critical path: their instructions win the SIMD's issue
+    // over the producer waves' DMA issue and ring polling when both are ready (+4.4% at config 5)
+    __builtin_amdgcn_s_setprio(1);
+    consumer<G, DBG>(p, P, sm, epoch);
+  }
   __syncthreads();
   if (blockIdx.x == 0 && threadIdx.x == 0) st_dev(p.ws + HDR_EPOCH, epoch);
   trace_end(p);
@@ -2847,8 +2853,14 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_kernel_b(Params p) {
   PlanB<G> P;
   P.init(p, sm.sS, blockIdx.x);
   const uint32_t epoch = step_epoch(p.ws);
-  if (threadIdx.x < 64 * NPW) producer_b<G>(p, P, sm, epoch);
-  else consumer_b<G, DBG>(p, P, sm, epoch);
+  if (threadIdx.x < 64 * NPW) {
+    producer_b<G>(p, P, sm, epoch);
+  } else {
+    // the consumer waves are the step's critical path: their instructions win the SIMD's issue
+    // over the producer waves' DMA issue and ring polling when both are ready (+4.7% at config 4)
+    __builtin_amdgcn_s_setprio(1);
+    consumer_b<G, DBG>(p, P, sm, epoch);
+  }
   __syncthreads();
   if (blockIdx.x == 0 && threadIdx.x == 0) st_dev(p.ws + HDR_EPOCH, epoch);
   trace_end(p);

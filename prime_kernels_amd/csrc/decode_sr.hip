@@ -1632,6 +1632,9 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_sr(Params p, uint32_t* r
   if (threadIdx.x < 64 * NPW) {
     producer_sr<G>(p, P, sm, epoch);
   } else {
+    // the consumer waves are the step's critical path: their instructions win the SIMD's issue
+    // over the producer waves' DMA issue and ring polling when both are ready (+3.4% at ctx 1024)
+    __builtin_amdgcn_s_setprio(1);
     CSR<G> C(p, P, sm, epoch, region);
     if (P.a) consumer_a<G>(C);
     else consumer_f<G>(C);
