@@ -2281,6 +2281,10 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
         ka[ti][1] = make_uint4(khi[0], khi[1], khi[2], khi[3]);
       }
     }
+    // every K row this wave uses is in registers: the segment goes back to the producers before
+    // the MFMAs, so the next item's K streams meanwhile
+    wait_lgkm0();
+    C.release(C.pos);
     float sv[5][4];
 #pragma unroll
     for (int ti = 0; ti < 5; ++ti) {
@@ -2314,7 +2318,6 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
       }
     wait_lgkm0();
     if (k == 0) trk(0, 39);  // diagnostics: item 0's score tiles stored
-    C.release(C.pos);  // this item's K is no longer read
     // per-wave (max, sum) of each head: tile ti's head columns 0-2 move to lanes 3ti .. 3ti+2 of
     // each 16-lane row (DPP row_shr:3ti), so lane c holds head c % 3's scores of tile c / 3
     {
