@@ -895,7 +895,7 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
       *reinterpret_cast<uint4*>(p.debug + Dbg<G>::AQ + (g * 3 + h) * 64 + part * 8) =
           make_uint4(q[h][0], q[h][1], q[h][2], q[h][3]);
   if (w == 0 && lane == 0) trace_at(p, l, 16, p.n_layers);
-  // scores: 8 lanes per token (8 dims each), 8 tokens per pass; s = bf16(q.k) * 1/8 (exact scale)
+  // the new token's score: 8 lanes per token (8 dims each); s = bf16(q.k) * 1/8 (exact scale)
   auto score = [&](int j, const uint4& k, bool keep) {
     float s3[3];
 #pragma unroll
@@ -917,9 +917,57 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
       }
   };
   const int jc = min(j1, T_old);  // this wave's cached tokens end here
-  for (int jb = j0; jb < jc; jb += 8) {
-    const int j = jb + grp;
-    score(j, j < jc ? C.ring16(seg + kv_slot(j, 0, part)) : make_uint4(0u, 0u, 0u, 0u), j < jc);
+  // The cached tokens' scores on the matrix cores, 16-token tiles from j0: D[token][head] =
+  // K[token][:] . q[head][:] (v_mfma_f32_16x16x32_bf16, two k-steps over the 64 dims).  Lane l
+  // supplies row l%16 of A (token tile*16 + l%16, pieces l/16 and l/16 + 4 of its K) and column l%16
+  // of B (q of head l%16 < 3, zero columns past it), and receives the scores of head l%16 for tokens
+  // tile*16 + 4(l/16) .. +3.  The rotated q pieces go through LDS, over the pre-RoPE q every lane of
+  // this wave has read.
+  {
+    constexpr int MTG = ((TC_MAX + 1 + NCW - 1) / NCW + 2 + 15) / 16;  // tiles of a wave's tokens
+    static_assert(MTG <= 5, "a wave's cached tokens fit 5 tiles");
+    const int hq = lane & 15, pq = lane >> 4;
+    uint4* qr = reinterpret_cast<uint4*>(in);  // [3 heads][8 pieces]
+    if (grp == 0)
+#pragma unroll
+      for (int h = 0; h < 3; ++h) qr[h * 8 + part] = make_uint4(q[h][0], q[h][1], q[h][2], q[h][3]);
+    const int ntl = jc > j0 ? (jc - j0 + 15) >> 4 : 0;
+    uint4 ka[MTG][2];
+#pragma unroll
+    for (int i = 0; i < MTG; ++i) {
+      ka[i][0] = ka[i][1] = make_uint4(0u, 0u, 0u, 0u);
+      if (i < ntl) {
+        const int tok = j0 + 16 * i + hq;  // past jc: other ring bytes, whose scores are not kept
+        ka[i][0] = C.ring16(seg + kv_slot(tok, 0, pq));
+        ka[i][1] = C.ring16(seg + kv_slot(tok, 0, pq + 4));
+      }
+    }
+    uint4 b0 = make_uint4(0u, 0u, 0u, 0u), b1 = make_uint4(0u, 0u, 0u, 0u);
+    if (hq < 3) {
+      b0 = qr[hq * 8 + pq];
+      b1 = qr[hq * 8 + pq + 4];
+    }
+    const bf16x8 bq0 = __builtin_bit_cast(bf16x8, b0), bq1 = __builtin_bit_cast(bf16x8, b1);
+#pragma unroll
+    for (int i = 0; i < MTG; ++i) {
+      if (i >= ntl) continue;
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[i][0]), bq0, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[i][1]), bq1, acc, 0, 0, 0);
+      if (hq < 3)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int j = j0 + 16 * i + 4 * pq + jj;
+          if (j < jc) {
+            sm.at.sc[hq][j] = rnd(acc[jj]) * 0.125f;
+            if (dbg_attn && P.t0 + j < int(Dbg<G>::SEQ)) {
+              p.debug[Dbg<G>::AQK + Dbg<G>::head_pos(b, g * 3 + hq, P.t0 + j)] = uint16_t(f2bf(acc[jj]));
+              p.debug[Dbg<G>::ASC + Dbg<G>::head_pos(b, g * 3 + hq, P.t0 + j)] =
+                  uint16_t(f2bf(rnd(acc[jj]) * 0.125f));
+            }
+          }
+        }
+    }
   }
   if (has_new) {
     // the new key and value, RoPE on the key, and its score (every 8-lane group computes it; the
