@@ -992,6 +992,8 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   if (w == 0 && lane == 0) trace_at(p, l, 17, p.n_layers);
   // chunk softmax statistics per head: max and sum of exp over this wave's tokens, then over the
   // chunk (all waves), then over all chunks of KV head g (one exchange of 3 x (max, sum) records).
+  // The exponentials here and in the probabilities use the hardware exp2 (__expf): within a few
+  // fp32 ulp of expf, far below the bf16 rounding of p.
   // A wave holds at most 128 tokens (chunks are at most TC_MAX + 1), so 2 scores per lane and head.
   static_assert(TC_MAX + 1 - ((3 * (TC_MAX + 1) / NCW) & ~1) <= 128 && (TC_MAX + 1) / NCW + 2 <= 128,
                 "per-wave token ranges fit two per lane");
@@ -1012,7 +1014,7 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
     for (int h = 0; h < 3; ++h) {
       l3[h] = 0.f;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) l3[h] += sv[h][i] == -INFINITY ? 0.f : expf(sv[h][i] - m3[h]);
+      for (int i = 0; i < 2; ++i) l3[h] += sv[h][i] == -INFINITY ? 0.f : __expf(sv[h][i] - m3[h]);
     }
     wave_sum_n<3>(l3);
     if (lane == 0)
@@ -1028,7 +1030,7 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
   }
   float mx = fmaxf(mq, dpp<0xb1>(mq, mq));  // quad_perm [1,0,3,2]
   mx = fmaxf(mx, dpp<0x4e>(mx, mx));         // quad_perm [2,3,0,1]
-  float ex = mq == -INFINITY ? 0.f : lq * expf(mq - mx);
+  float ex = mq == -INFINITY ? 0.f : lq * __expf(mq - mx);
   ex += dpp<0xb1>(0.f, ex);
   ex += dpp<0x4e>(0.f, ex);
   float Mh[3], Lh[3];
@@ -1107,7 +1109,7 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
       Lh[h] = 0.f;
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        if (lane + 64 * i < P.C) Lh[h] += __uint_as_float(s[i][h].z) * expf(__uint_as_float(s[i][h].x) - Mh[h]);
+        if (lane + 64 * i < P.C) Lh[h] += __uint_as_float(s[i][h].z) * __expf(__uint_as_float(s[i][h].x) - Mh[h]);
     }
     wave_sum_n<3>(Lh);
   }
@@ -1121,7 +1123,7 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
     for (int i = 0; i < 2; ++i) {
       const int j = j0 + lane + 64 * i;
       if (j < j1) {
-        sm.at.pb[h][j] = uint16_t(f2bf(expf(sv[h][i] - Mh[h]) * inv));
+        sm.at.pb[h][j] = uint16_t(f2bf(__expf(sv[h][i] - Mh[h]) * inv));
         if (dbg_attn && P.t0 + j < int(Dbg<G>::SEQ))
           p.debug[Dbg<G>::APR + Dbg<G>::head_pos(b, g * 3 + h, P.t0 + j)] = sm.at.pb[h][j];
       }
