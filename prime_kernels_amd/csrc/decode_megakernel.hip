@@ -2388,7 +2388,7 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
       const float m = ch == 0 ? mw[0] : ch == 1 ? mw[1] : mw[2];
       float ls = 0.f;
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) ls += ev[jj] == -INFINITY ? 0.f : expf(ev[jj] - m);
+      for (int jj = 0; jj < 4; ++jj) ls += ev[jj] == -INFINITY ? 0.f : __expf(ev[jj] - m);
       head_totals<false>(ls, lw);
       if (lane == 0)
 #pragma unroll
@@ -2405,7 +2405,7 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
     if (lane < 12) { mq = sm.at.wml[k][lane & 3][0][lane >> 2]; lq = sm.at.wml[k][lane & 3][1][lane >> 2]; }
     float mx = fmaxf(mq, dpp<0xb1>(mq, mq));
     mx = fmaxf(mx, dpp<0x4e>(mx, mx));
-    float ex = mq == -INFINITY ? 0.f : lq * expf(mq - mx);
+    float ex = mq == -INFINITY ? 0.f : lq * __expf(mq - mx);
     ex += dpp<0xb1>(0.f, ex);
     ex += dpp<0x4e>(0.f, ex);
     if (lane < 12 && (lane & 3) == 0) { sm.at.cst[k][0][lane >> 2] = mx; sm.at.cst[k][1][lane >> 2] = ex; }
@@ -2466,14 +2466,16 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
         const float mk = mine ? __uint_as_float(v[i][h].x) : -INFINITY;
         const float lk = mine ? __uint_as_float(v[i][h].z) : 0.f;
         const float m = wave_max(mk);
-        const float ls = wave_sum(mk == -INFINITY ? 0.f : lk * expf(mk - m));
+        const float ls = wave_sum(mk == -INFINITY ? 0.f : lk * __expf(mk - m));
         if (lane == 0) { sm.at.gml[k][0][h] = m; sm.at.gml[k][1][h] = ls; }
       }
     }
   }
   C.cbar();
   tri(6);
-  // ---- B: probabilities and P.V of every item ----
+  // ---- B: probabilities and P.V of every item (the softmax exponentials, here and in the
+  // statistics above, on the hardware exp2, __expf: within a few fp32 ulp of expf, far below the
+  // bf16 rounding of p) ----
   const int half = lane >> 5, d2 = lane & 31;
   const uint32_t voff = uint32_t(d2 & 3) * 4u;
   for (int k = 0; k < P.ni; ++k) {
@@ -2499,7 +2501,7 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
         for (int h = 0; h < 3; ++h) s[h] = bf2f(sm.at.sc[k][h][j]);
 #pragma unroll
         for (int h = 0; h < 3; ++h) {
-          const uint16_t pv = uint16_t(f2bf(expf(s[h] - M[h]) * inv[h]));
+          const uint16_t pv = uint16_t(f2bf(__expf(s[h] - M[h]) * inv[h]));
           sm.at.pb[h][j] = pv;
           if (dbg_attn && it.t0 + j < int(Dbg<G>::SEQ))
             p.debug[Dbg<G>::APR + Dbg<G>::head_pos(it.b, it.g * 3 + h, it.t0 + j)] = pv;
