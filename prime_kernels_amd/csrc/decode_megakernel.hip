@@ -1130,51 +1130,55 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
     }
   }
   wait_lgkm0();
-  // P.V: lane = (half, d2) owns dims 2*d2, 2*d2+1; token pairs alternate between the halves
-  const int half = lane >> 5, d2 = lane & 31;
+  // P.V: lane = (quarter qv, d4) owns dims 4 d4 .. 4 d4 + 3 (8 bytes of a token's V); token pairs
+  // go round-robin to the four 16-lane quarters, whose sums are added at the end
+  const int qv = lane >> 4, d4 = lane & 15;
   const int jo1 = min(j1, T_old);
   const int npairs = jo1 > j0 ? (jo1 - j0) / 2 : 0;
-  const uint32_t voff = uint32_t(d2 & 3) * 4u;
-  float acc[3][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
+  const uint32_t voff = uint32_t(d4 & 1) * 8u;
+  float acc[3][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll 4
-  for (int k = half; k < npairs; k += 2) {
+  for (int k = qv; k < npairs; k += 4) {
     const int j = j0 + 2 * k;
-    const uint32_t va = C.ring4(seg + kv_slot(j, 1, d2 >> 2) + voff);
-    const uint32_t vb = C.ring4(seg + kv_slot(j + 1, 1, d2 >> 2) + voff);
-    const uint32_t lo = __builtin_amdgcn_perm(vb, va, 0x05040100u);  // {v_j[2d2], v_j+1[2d2]}
-    const uint32_t hi = __builtin_amdgcn_perm(vb, va, 0x07060302u);  // {v_j[2d2+1], v_j+1[2d2+1]}
+    const uint2 va = C.ring8(seg + kv_slot(j, 1, d4 >> 1) + voff);
+    const uint2 vb = C.ring8(seg + kv_slot(j + 1, 1, d4 >> 1) + voff);
+    // {v_j[d], v_j+1[d]} for the lane's four dims d
+    const uint32_t v0 = __builtin_amdgcn_perm(vb.x, va.x, 0x05040100u), v1 = __builtin_amdgcn_perm(vb.x, va.x, 0x07060302u);
+    const uint32_t v2 = __builtin_amdgcn_perm(vb.y, va.y, 0x05040100u), v3 = __builtin_amdgcn_perm(vb.y, va.y, 0x07060302u);
 #pragma unroll
     for (int h = 0; h < 3; ++h) {
       const uint32_t pp = *reinterpret_cast<const uint32_t*>(&sm.at.pb[h][j]);
-      acc[h][0] = dot2(pp, lo, acc[h][0]);
-      acc[h][1] = dot2(pp, hi, acc[h][1]);
+      acc[h][0] = dot2(pp, v0, acc[h][0]);
+      acc[h][1] = dot2(pp, v1, acc[h][1]);
+      acc[h][2] = dot2(pp, v2, acc[h][2]);
+      acc[h][3] = dot2(pp, v3, acc[h][3]);
     }
   }
-  if (half == 0) {
+  if (qv == 0) {
     if (jo1 > j0 && ((jo1 - j0) & 1)) {  // odd cached token at the end of the range
       const int j = jo1 - 1;
-      const uint32_t v = C.ring4(seg + kv_slot(j, 1, d2 >> 2) + voff);
+      const uint2 v = C.ring8(seg + kv_slot(j, 1, d4 >> 1) + voff);
+      const float vf[4] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y)};
 #pragma unroll
       for (int h = 0; h < 3; ++h) {
         const float pj = bf2f(sm.at.pb[h][j]);
-        acc[h][0] = fmaf(pj, bf_lo(v), acc[h][0]);
-        acc[h][1] = fmaf(pj, bf_hi(v), acc[h][1]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[h][i] = fmaf(pj, vf[i], acc[h][i]);
       }
     }
     if (has_new) {
 #pragma unroll
       for (int h = 0; h < 3; ++h) {
         const float pj = bf2f(sm.at.pb[h][T_old]);
-        acc[h][0] = fmaf(pj, in[256 + 2 * d2], acc[h][0]);
-        acc[h][1] = fmaf(pj, in[256 + 2 * d2 + 1], acc[h][1]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[h][i] = fmaf(pj, in[256 + 4 * d4 + i], acc[h][i]);
       }
     }
   }
 #pragma unroll
-  for (int h = 0; h < 3; ++h) {
-    acc[h][0] += __shfl_xor(acc[h][0], 32);
-    acc[h][1] += __shfl_xor(acc[h][1], 32);
-  }
+  for (int h = 0; h < 3; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[h][i] = column_total<false>(acc[h][i]);
   C.release(C.pos);  // this wave no longer reads the K/V chunk
   if (has_new && P.slot >= 0 && grp < 2) {
     // KV append at slot_mapping[b] (block360_kernel.inc:124-135; slot < 0 skips): lanes 0-7 store
@@ -1203,12 +1207,11 @@ __device__ __forceinline__ void attention(Consumer<G>& C, int l, uint32_t segc, 
       }
     }
   }
-  if (lane < 32)
+  if (lane < 16)
 #pragma unroll
-    for (int h = 0; h < 3; ++h) {
-      sm.wo[w][h][2 * d2] = acc[h][0];
-      sm.wo[w][h][2 * d2 + 1] = acc[h][1];
-    }
+    for (int h = 0; h < 3; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sm.wo[w][h][4 * d4 + i] = acc[h][i];
   C.cbar();
   if (w == 0 && lane == 0) trace_at(p, l, 19, p.n_layers);
   const bool l2 = P.xcd && C.l2rec;
