@@ -2479,8 +2479,10 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
   // ---- B: probabilities and P.V of every item (the softmax exponentials, here and in the
   // statistics above, on the hardware exp2, __expf: within a few fp32 ulp of expf, far below the
   // bf16 rounding of p) ----
-  const int half = lane >> 5, d2 = lane & 31;
-  const uint32_t voff = uint32_t(d2 & 3) * 4u;
+  // P.V: lane = (quarter qv, d4) owns dims 4 d4 .. 4 d4 + 3 (8 bytes of a token's V); token pairs
+  // go round-robin to the four 16-lane quarters, whose sums are added at the end
+  const int qv = lane >> 4, d4 = lane & 15;
+  const uint32_t voff = uint32_t(d4 & 1) * 8u;
   for (int k = 0; k < P.ni; ++k) {
     const ItemB it = sm.it[k];
     const bool leader = it.c == it.C - 1;
@@ -2516,51 +2518,56 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
     C.wait_filled(C.pos);  // this item's V
     const int jo1 = min(j1, T_old);
     const int npairs = jo1 > j0 ? (jo1 - j0) / 2 : 0;
-    float acc[3][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
+    float acc[3][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll 4
-    for (int kp = half; kp < npairs; kp += 2) {
+    for (int kp = qv; kp < npairs; kp += 4) {
       const int j = j0 + 2 * kp;
-      const uint32_t va = C.ring4(segv + kvb_slot(j, d2 >> 2) + voff);
-      const uint32_t vb = C.ring4(segv + kvb_slot(j + 1, d2 >> 2) + voff);
-      const uint32_t lo = __builtin_amdgcn_perm(vb, va, 0x05040100u);
-      const uint32_t hi = __builtin_amdgcn_perm(vb, va, 0x07060302u);
+      const uint2 va = C.ring8(segv + kvb_slot(j, d4 >> 1) + voff);
+      const uint2 vb = C.ring8(segv + kvb_slot(j + 1, d4 >> 1) + voff);
+      // {v_j[d], v_j+1[d]} for the lane's four dims d
+      const uint32_t v0 = __builtin_amdgcn_perm(vb.x, va.x, 0x05040100u), v1 = __builtin_amdgcn_perm(vb.x, va.x, 0x07060302u);
+      const uint32_t v2 = __builtin_amdgcn_perm(vb.y, va.y, 0x05040100u), v3 = __builtin_amdgcn_perm(vb.y, va.y, 0x07060302u);
 #pragma unroll
       for (int h = 0; h < 3; ++h) {
         const uint32_t pp = *reinterpret_cast<const uint32_t*>(&sm.at.pb[h][j]);
-        acc[h][0] = dot2(pp, lo, acc[h][0]);
-        acc[h][1] = dot2(pp, hi, acc[h][1]);
+        acc[h][0] = dot2(pp, v0, acc[h][0]);
+        acc[h][1] = dot2(pp, v1, acc[h][1]);
+        acc[h][2] = dot2(pp, v2, acc[h][2]);
+        acc[h][3] = dot2(pp, v3, acc[h][3]);
       }
     }
-    if (half == 0) {
+    if (qv == 0) {
       if (jo1 > j0 && ((jo1 - j0) & 1)) {
         const int j = jo1 - 1;
-        const uint32_t v = C.ring4(segv + kvb_slot(j, d2 >> 2) + voff);
+        const uint2 v = C.ring8(segv + kvb_slot(j, d4 >> 1) + voff);
+        const float vf[4] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y)};
 #pragma unroll
         for (int h = 0; h < 3; ++h) {
           const float pj = bf2f(sm.at.pb[h][j]);
-          acc[h][0] = fmaf(pj, bf_lo(v), acc[h][0]);
-          acc[h][1] = fmaf(pj, bf_hi(v), acc[h][1]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[h][i] = fmaf(pj, vf[i], acc[h][i]);
         }
       }
       if (has_new) {
 #pragma unroll
         for (int h = 0; h < 3; ++h) {
           const float pj = bf2f(sm.at.pb[h][T_old]);
-          acc[h][0] = fmaf(pj, in[256 + 2 * d2], acc[h][0]);
-          acc[h][1] = fmaf(pj, in[256 + 2 * d2 + 1], acc[h][1]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[h][i] = fmaf(pj, in[256 + 4 * d4 + i], acc[h][i]);
         }
       }
     }
-#pragma unroll
-    for (int h = 0; h < 3; ++h) {
-      acc[h][0] += __shfl_xor(acc[h][0], 32);
-      acc[h][1] += __shfl_xor(acc[h][1], 32);
-    }
     C.release(C.pos);  // this item's V is no longer read
-    float (*wo)[3][64] = sm.at.wo[k & 1];
-    if (lane < 32)
 #pragma unroll
-      for (int h = 0; h < 3; ++h) { wo[w][h][2 * d2] = acc[h][0]; wo[w][h][2 * d2 + 1] = acc[h][1]; }
+    for (int h = 0; h < 3; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[h][i] = column_total<false>(acc[h][i]);
+    float (*wo)[3][64] = sm.at.wo[k & 1];
+    if (lane < 16)
+#pragma unroll
+      for (int h = 0; h < 3; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wo[w][h][4 * d4 + i] = acc[h][i];
     // one barrier per item: wo[k & 1] is next written by item k + 2, after the barrier of item k + 1,
     // and pb is only read by the wave that wrote it, before this barrier
     C.cbar();
