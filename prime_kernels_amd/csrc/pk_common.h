@@ -53,11 +53,14 @@ constexpr int WG_THREADS = 64 * (NPW + NCW);
 constexpr uint32_t RING = 128u * 1024u;  // LDS ring bytes (power of two)
 constexpr uint32_t PKT = 1024;           // one LDS-DMA instruction: 64 lanes x 16 B
 constexpr int DEPTH = PK_DMA_DEPTH;      // packets in flight per producer wave (batch 1)
-// The batched kernel streams 1.4-2.5 GB of paged K/V per step and gains from more packets in
-// flight (32: -0.8% at config 4); at batch 1 more in flight lengthens the memory queues the
-// exchanges wait in (16 -> 24: +11%, 32: +19%; 8 is 0.3-0.4% faster than 16 at contexts 1024 to
-// 8192, also with a depth of 32 for the LM-head segments alone, which is slower).
-constexpr int DEPTH_B = 32;
+// The batched kernel: a producer wave marks a packet as landed only once DEPTH_B - 1 newer ones
+// are issued (or its queue drains), so a deep queue hides the end of each K or V segment from the
+// consumers until the next segment has streamed; at config 4 depth 32 / 16 / 8 / 4 / 3 / 2 gave
+// 7,695 / 7,709 / 7,892 / 8,362 / 8,409 / 8,401 tok/s.
+#ifndef PK_DMA_DEPTH_B
+#define PK_DMA_DEPTH_B 3
+#endif
+constexpr int DEPTH_B = PK_DMA_DEPTH_B;
 constexpr int TC_MAX = 288;              // max cached tokens per attention chunk (72 KB of K/V)
 // Batch-1 chunking of a KV head's cached tokens: chunks of up to TC_LONG tokens, but at least
 // C_SHORT chunks of at least TC_SHORT tokens while the context allows (measured at 360M batch 1:
