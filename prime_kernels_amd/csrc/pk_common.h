@@ -41,7 +41,7 @@ constexpr int NWG = 256;                 // persistent workgroups (one per CU)
 #define PK_PRODUCER_WAVES 4
 #endif
 #ifndef PK_DMA_DEPTH
-#define PK_DMA_DEPTH 8
+#define PK_DMA_DEPTH 4                   // general batch-1 kernel (MXFP8 ctx 8192: 4 / 3 / 8 = 1,279 / 1,278 / 1,275 tok/s)
 #endif
 #ifndef PK_POLL_SLEEP
 #define PK_POLL_SLEEP 0                  // s_sleep units (64 clocks) between polls (0: -0.2% at batch 1, -0.9% at 16, against 1)
