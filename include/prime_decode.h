@@ -77,10 +77,22 @@ int pk_set_option(int option, int value);
  * without clearing it; the next decode call on the device returns PK_ERR_ABORTED and clears it. */
 int pk_state_read(void* stream, size_t word, unsigned* out, int n);
 int pk_state_status(void* stream, unsigned* out);
+/* pk_state_status that also clears the report, so the next decode call does not report that step
+ * again (no reference counterpart). */
+int pk_state_take(void* stream, unsigned* out);
 /* Test hooks (synchronous; no reference counterpart): set the step epoch of the current device's
  * state, or mark the next step as failed so that each of its bounded waits gives up at once. */
 int pk_test_set_epoch(void* stream, unsigned epoch);
 int pk_test_abort_next(void* stream);
+/* Test hook (synchronous; no reference counterpart): the exchange-unit integrity check.  Workgroups
+ * publish 16-byte units {3 payload words, tag} with the decode kernels' stores, the payload a function
+ * of (tag, unit), and read every unit back with the kernels' polling loads, comparing the payload of
+ * each unit they accept.  mode 0: all 256 workgroups, uncached memory (pk_decode's cross-XCD units);
+ * 1: ordinary memory (pk_decode_noalloc's array); 2: the 32 workgroups of one XCD, plain stores
+ * (attention records through the XCD's L2).  slot: 16 (four units per 64-byte line, from different
+ * workgroups) or 64 (one per line).  out[4] = {torn units, polls given up, units checked, mask of
+ * the XCC ids the participating workgroups ran on}. */
+int pk_test_exchange_units(int mode, int rounds, int slot, unsigned* out);
 
 /* One greedy decode step for B = 1..16 sequences (vLLM FLASH_ATTN metadata, paged KV
  * [blocks, KVH, 16, 128]; contexts may differ per sequence).  B = 1 runs the split-role kernel

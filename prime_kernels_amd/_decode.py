@@ -108,6 +108,16 @@ class _Runtime:
             raise RuntimeError(f"state read failed: {_native.status_string(rc)}")
         return list(buf)
 
+    def take_failure(self, stream=None) -> tuple:
+        """pending_failure, clearing the report: the next decode call on the device then does not
+        report that step again.  Does not synchronise."""
+        buf = (ctypes.c_uint * 2)()
+        with torch.cuda.device(self.device):
+            rc = self.lib.pk_state_take(self._stream(stream), buf)
+        if rc != 0:
+            raise RuntimeError(f"state read failed: {_native.status_string(rc)}")
+        return buf[0], buf[1]
+
     def pending_failure(self, stream=None) -> tuple:
         """(epoch, wait site) of a step on the device that gave up a bounded wait and has not been
         reported by a decode call yet; (0, 0) when there is none.  Does not synchronise."""
@@ -127,6 +137,16 @@ def runtime(model: Model, device: torch.device) -> _Runtime:
     if key not in _runtimes:
         _runtimes[key] = _Runtime(model, device)
     return _runtimes[key]
+
+
+def check_embed_shape(embed, model: Model) -> None:
+    """The embedding table must be [VOCAB, hidden] and contiguous.  The kernels read row `id` of it
+    for each input id with the id clamped to 0..VOCAB-1 on the device, and the tied LM head reads every
+    row, so a table of another row count would be read past its end or have rows that no id reaches.
+    (The reference checks the hidden width only, decode_megakernel_360m/__init__.py:151-152, and its
+    kernel indexes the table unchecked.)"""
+    if embed.ndim != 2 or tuple(embed.shape) != (VOCAB, model.hidden) or not embed.is_contiguous():
+        raise ValueError(f"embed must be contiguous BF16 [{VOCAB}, {model.hidden}], got {tuple(embed.shape)}")
 
 
 def _check_tensor(tensor, name, *, dtype=None, device=None, shape=None):
@@ -166,11 +186,12 @@ def _failure_message(model: Model, rc: int) -> str:
 
 def check_failures(model: Model, device: torch.device, stream=None) -> None:
     """Synchronise `device` and raise RuntimeError if a decode step on it gave up a bounded wait
-    since the last report (decode calls report such a step at the next call; this reports it now)."""
+    since the last report (decode calls report such a step at the next call; this reports it now,
+    and clears the report, so the next call does not raise for the same step)."""
     rt = runtime(model, device)
     s = rt._stream(stream)
     torch.cuda.synchronize(device)
-    epoch, site = rt.pending_failure(s)
+    epoch, site = rt.take_failure(s)
     if epoch:
         raise RuntimeError(f"{model.name}: the step with epoch {epoch} gave up a bounded wait (site {site}); "
                            f"its outputs were poisoned")
@@ -223,13 +244,8 @@ def decode_step(model: Model, *, input_ids, positions, seq_lens, block_table, sl
         raise ValueError(f"block_table context capacity must be 1..{model.max_seq}")
     _check_tensor(embed, "embed", dtype=torch.bfloat16, device=device)
     _check_tensor(final_norm, "final_norm", dtype=torch.bfloat16, device=device, shape=(model.hidden,))
-    # the reference checks the hidden width only (decode_megakernel_360m/__init__.py:151-152); the
-    # tied LM head also needs the full vocabulary.  Input ids index embedding rows unchecked, as there.
+    check_embed_shape(embed, model)
     lm_head = return_token_ids or logits_out is not None
-    if embed.ndim != 2 or embed.shape[1] != model.hidden or not embed.is_contiguous():
-        raise ValueError(f"embed must be contiguous BF16 [vocab, {model.hidden}]")
-    if lm_head and embed.shape[0] != VOCAB:
-        raise ValueError(f"the tied LM head needs embed of shape [{VOCAB}, {model.hidden}]")
     spec = model.layer_spec()
     for i, layer in enumerate(layers):
         if len(layer) != len(spec):

@@ -34,6 +34,8 @@ SIGNATURES = {
     "pk_set_option": (ci, [ci, ci]),
     "pk_state_read": (ci, [vp, sz, ctypes.POINTER(ctypes.c_uint), ci]),
     "pk_state_status": (ci, [vp, ctypes.POINTER(ctypes.c_uint)]),
+    "pk_state_take": (ci, [vp, ctypes.POINTER(ctypes.c_uint)]),
+    "pk_test_exchange_units": (ci, [ci, ci, ci, ctypes.POINTER(ctypes.c_uint)]),
     "pk_test_set_epoch": (ci, [vp, ctypes.c_uint]),
     "pk_test_abort_next": (ci, [vp]),
     "pk_decode": (ci, [vp, ci, ci, ci, vp, ci, vp, vp, vp, vp, vp, ci, vp, vp, vp,

@@ -1577,8 +1577,8 @@ __device__ __forceinline__ void consumer(const Params& p, const Plan<G>& P, Smem
   }
   if (fail) {
     step_failed(p, C.tag32, C.ct, b);
-    if (p.out_logits)  // workgroup 0's own logits rows
-      for (int i = P.v0 + C.ct; i < P.v1; i += NCT) p.out_logits[size_t(b) * G::V + i] = 0x7fc0;
+    if (p.out_logits)  // every logits row of the sequence (best effort: see step_failed)
+      for (int i = C.ct; i < G::V; i += NCT) p.out_logits[size_t(b) * G::V + i] = 0x7fc0;
   }
 }
 
@@ -2883,8 +2883,8 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
   if (fail)
     for (int b = 0; b < B; ++b) {
       step_failed(p, C.tag32, C.ct, b);
-      if (p.out_logits)  // workgroup 0's own logits rows
-        for (int i = P.v0 + C.ct; i < P.v1; i += NCT) p.out_logits[size_t(b) * G::V + i] = 0x7fc0;
+      if (p.out_logits)  // every logits row of the sequence (best effort: see step_failed)
+        for (int i = C.ct; i < G::V; i += NCT) p.out_logits[size_t(b) * G::V + i] = 0x7fc0;
     }
 }
 
@@ -3430,6 +3430,17 @@ extern "C" int pk_state_status(void* stream, unsigned* out) {
   if (rc != PK_OK) return rc;
   out[0] = __atomic_load_n(&st->host[0], __ATOMIC_ACQUIRE);
   out[1] = __atomic_load_n(&st->host[1], __ATOMIC_ACQUIRE);
+  return PK_OK;
+}
+
+// The pending failure report of the current device, cleared: the next decode call then does not
+// report that step again.  out[0] the epoch (0: none), out[1] the wait site.
+extern "C" int pk_state_take(void* stream, unsigned* out) {
+  pk::DevState* st = nullptr;
+  const int rc = pk::get_state(stream, &st);
+  if (rc != PK_OK) return rc;
+  out[1] = __atomic_load_n(&st->host[1], __ATOMIC_ACQUIRE);
+  out[0] = __atomic_exchange_n(&st->host[0], 0u, __ATOMIC_ACQ_REL);
   return PK_OK;
 }
 

@@ -14,9 +14,13 @@
 //
 // Exchange format: 16-byte units {three 32-bit payload words, 32-bit step tag}, written with one
 // 16-byte store and read with one 16-byte load (a payload of 6 bf16 or 3 fp32).  A reader polls a
-// unit until its tag equals the step epoch.  Cross-XCD units live in uncached device memory
-// (device-scope stores and loads); group A's records live in ordinary device memory written with
-// plain stores into the XCD's L2 and read with device-scope loads.  At the start of a launch the
+// unit until its tag equals the step epoch and then uses the payload read by that same load: the
+// scheme relies on a 16-byte store being seen whole by a 16-byte load (never the new tag with an
+// old payload), which the GPU test test_gpu_safety.py::test_exchange_units_are_never_torn checks.
+// Cross-XCD units live in uncached device memory (device-scope stores and loads) for pk_decode; for
+// pk_decode_noalloc they live in an ordinary (cached) device array, where the device-scope (sc1)
+// stores and loads alone keep them coherent across XCDs.  Group A's records live in ordinary device
+// memory written with plain stores into the XCD's L2 and read with device-scope loads.  At the start of a launch the
 // group-A workgroups check that they really share one XCC (hardware register XCC_ID); if not, the
 // records go through the uncached workspace instead.
 //
@@ -1563,6 +1567,8 @@ __device__ __forceinline__ void final_gather(CSR<G>& C) {
   if (fail) {
     if (C.ct == 0 && !aborted(p.ws, epoch)) raise_abort(p.ws, epoch, 25);
     for (int i = C.ct; i < G::H; i += NCT) p.out_hidden[i] = 0x7fc0;
+    if (p.out_logits)  // every logits row (best effort: a straggler may still store its own rows)
+      for (int i = C.ct; i < G::V; i += NCT) p.out_logits[i] = 0x7fc0;
   }
   if (C.ct == 0) {
     bv = sm.lm_val[0];
@@ -1644,12 +1650,120 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_sr(Params p, uint32_t* r
   trace_end(p);
 }
 
+// ------------------------------------------------------------------------------------------------
+// Exchange-unit integrity check (test hook).  `rounds` rounds; in round r each participating
+// workgroup stores `upw` units (one per lane of its first wave) with tag = base + r and three payload
+// words derived from (tag, unit), exactly as the decode kernels publish (one 16-byte store with the
+// given cache bits), into a region of its own for the round; then every participant polls all units
+// of the round with the decode kernels' 16-byte device-scope loads and compares the payload of every
+// unit it accepts (tag current) with the expected words.  out[0] counts mismatches (a torn unit:
+// current tag, stale or mixed payload), out[1] polls given up, out[2] units checked, out[3] is the
+// mask of XCC ids the participants ran on.  Every wait is bounded; a mismatch is counted, never
+// waited on.
+// ------------------------------------------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t unit_word(uint32_t tag, uint32_t unit, uint32_t k) {
+  uint32_t h = tag * 0x9e3779b1u ^ (unit + 1u) * 0x85ebca77u ^ (k + 1u) * 0xc2b2ae3du;
+  h ^= h >> 15;
+  h *= 0x2c1b3c6du;
+  h ^= h >> 12;
+  return h;
+}
+
+template <int AUX_ST>
+__global__ void __launch_bounds__(NCT, 1) unit_check(uint8_t* buf, uint32_t buf_bytes, uint32_t base, int rounds,
+                                                     int upw, int slot, int one_xcd, uint32_t* out) {
+  const int wg = blockIdx.x, t = threadIdx.x;
+  if (one_xcd && !in_a(wg)) return;
+  const int np = one_xcd ? AG : NWG;                     // participating workgroups
+  const int rank = one_xcd ? wg >> 3 : wg;
+  const int nu = np * upw;                               // units per round
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(buf, (short)0, int(buf_bytes), 0x00020000);
+  uint32_t bad = 0, gave_up = 0, checked = 0;
+  for (int k = 0; k < rounds; ++k) {
+    const uint32_t tag = base + uint32_t(k);
+    const uint32_t round_off = uint32_t(k) * uint32_t(nu) * uint32_t(slot);
+    if (t < upw) {
+      const uint32_t u = uint32_t(rank * upw + t);
+      st_unit<AUX_ST>(r, round_off + u * uint32_t(slot),
+                      u32x4{unit_word(tag, u, 0), unit_word(tag, u, 1), unit_word(tag, u, 2), tag});
+    }
+    for (int u = t; u < nu; u += NCT) {
+      const uint32_t off = round_off + uint32_t(u) * uint32_t(slot);
+      u32x4 v = ld_unit(r, off);
+      uint32_t n = 0;
+      while (v.w != tag && ++n < (1u << 20)) {
+        asm volatile("" ::: "memory");  // the load is issued again on every pass (not hoisted)
+        v = ld_unit(r, off);
+      }
+      if (v.w != tag) { ++gave_up; continue; }
+      ++checked;
+      bad += (v.x != unit_word(tag, u, 0) || v.y != unit_word(tag, u, 1) || v.z != unit_word(tag, u, 2)) ? 1u : 0u;
+    }
+  }
+  if (bad) atomicAdd(out + 0, bad);
+  if (gave_up) atomicAdd(out + 1, gave_up);
+  atomicAdd(out + 2, checked);
+  if (t == 0) atomicOr(out + 3, 1u << (__builtin_amdgcn_s_getreg((15 << 11) | (0 << 6) | 20) & 15u));  // XCC_ID
+}
+
 }  // namespace sr
 }  // namespace pk
 
 // ------------------------------------------------------------------------------------------------
 // Host side
 // ------------------------------------------------------------------------------------------------
+
+// Test hook: the exchange-unit integrity check on the current device (synchronous).  mode 0: 256
+// workgroups, uncached memory, device-scope stores and loads (pk_decode's cross-XCD units); mode 1:
+// the same in ordinary device memory (pk_decode_noalloc's array); mode 2: the 32 workgroups of one
+// XCD under round-robin dispatch, ordinary memory, plain stores and device-scope loads (group A's
+// records through the XCD's L2).  `slot` is the bytes between units (16: four units, stored by
+// different workgroups, share each 64-byte line; 64: one unit per line as the decode kernels place
+// them).  out receives {mismatches, polls given up, units checked, mask of the XCC ids the
+// participating workgroups ran on}.  The buffers are allocated on the
+// first call on a device and kept until the process ends.  No reference counterpart.
+extern "C" int pk_test_exchange_units(int mode, int rounds, int slot, unsigned* out) {
+  using namespace pk;
+  static uint8_t* ubuf[64] = {};
+  static uint8_t* cbuf[64] = {};
+  static uint32_t* cnt[64] = {};
+  static uint32_t next_base[64] = {};
+  constexpr int UPW = 4;                      // units per workgroup and round
+  constexpr size_t BYTES = size_t(64) << 20;
+  if (mode < 0 || mode > 2 || (slot != 16 && slot != 64) || rounds < 1 ||
+      size_t(rounds) * NWG * UPW * size_t(slot) > BYTES || out == nullptr)
+    return PK_ERR_BLOCK;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return PK_ERR_RESIDENCY;
+  if (!ubuf[dev]) {
+    if ((e = hipExtMallocWithFlags(reinterpret_cast<void**>(&ubuf[dev]), BYTES, hipDeviceMallocUncached)) != hipSuccess) return e;
+    if ((e = hipMalloc(reinterpret_cast<void**>(&cbuf[dev]), BYTES)) != hipSuccess) return e;
+    if ((e = hipMalloc(reinterpret_cast<void**>(&cnt[dev]), 16)) != hipSuccess) return e;
+    if ((e = hipMemset(ubuf[dev], 0, BYTES)) != hipSuccess) return e;
+    if ((e = hipMemset(cbuf[dev], 0, BYTES)) != hipSuccess) return e;
+    next_base[dev] = 1u;
+  }
+  if ((e = hipMemset(cnt[dev], 0, 16)) != hipSuccess) return e;  // 4 counters
+  const uint32_t base = next_base[dev];
+  next_base[dev] += uint32_t(rounds);
+  uint8_t* buf = mode == 0 ? ubuf[dev] : cbuf[dev];
+  const uint32_t bytes = uint32_t(BYTES);
+  int one_xcd = mode == 2 ? 1 : 0;
+  void* args[] = {&buf, const_cast<uint32_t*>(&bytes), const_cast<uint32_t*>(&base), &rounds,
+                  const_cast<int*>(&UPW), &slot, &one_xcd, &cnt[dev]};
+  const void* fn = mode == 2 ? reinterpret_cast<const void*>(sr::unit_check<0>)
+                             : reinterpret_cast<const void*>(sr::unit_check<16>);
+  // one workgroup per CU: the LDS this launch asks for keeps a second one off every CU
+  if ((e = hipLaunchKernel(fn, dim3(NWG), dim3(NCT), args, 96 * 1024, nullptr)) != hipSuccess) return e;
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+  uint32_t h[4] = {0, 0, 0, 0};
+  if ((e = hipMemcpy(h, cnt[dev], 16, hipMemcpyDeviceToHost)) != hipSuccess) return e;
+  for (int i = 0; i < 4; ++i) out[i] = h[i];
+  return PK_OK;
+}
 
 namespace pk {
 namespace sr {

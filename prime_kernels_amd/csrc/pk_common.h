@@ -544,7 +544,9 @@ constexpr int G_HMAX = 960;
 
 // Workgroup 0, when a step gave up a wait: the abort word (if no wait raised it), the host-visible
 // report {epoch, wait site}, and sequence b's hidden state set to NaN.  Called by every consumer
-// thread `ct` of workgroup 0.
+// thread `ct` of workgroup 0.  The callers then also set every logits row of the step to NaN; a
+// workgroup still in its last phases when workgroup 0 gave up waiting for it can store its own rows
+// after that, so only the token ids (-1) and the hidden state are guaranteed to be poisoned.
 __device__ __forceinline__ void step_failed(const Params& p, uint32_t epoch, int ct, int b) {
   if (ct == 0) {
     if (ld_dev(p.ws + HDR_ABORT) != epoch) raise_abort(p.ws, epoch, 25);

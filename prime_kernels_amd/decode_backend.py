@@ -9,8 +9,8 @@ and the `_prime_rl_decode_backend` marker on the patched forward.
 Design.  A forward call is routed in three steps:
 
 1. the model's kernel (`kernel_for_model`): a SmolLM2-135M or -360M geometry (`_Geometry`, compared
-   with the HF config) with a bf16 embedding, a fused QKV projection, no auxiliary hidden-state
-   layers and a single tensor/pipeline rank;
+   with the HF config, vocabulary size included) with a bf16 embedding, a fused QKV projection, no
+   auxiliary hidden-state layers and a single tensor/pipeline rank;
 2. the batch (`route`): FLASH_ATTN metadata of a pure decode batch (one query token per request)
    within the kernel's batch and context limits, over KV caches in the layout the kernel reads
    (`metadata_fits`).  Every decision, taken or not, is counted in `stats`;
@@ -62,16 +62,17 @@ class _Geometry:
     kv_heads: int
     head_dim: int
     eps: float
+    vocab: int
 
     @classmethod
     def of_config(cls, c) -> "_Geometry":
         head_dim = getattr(c, "head_dim", None) or c.hidden_size // c.num_attention_heads
         return cls(c.hidden_size, c.intermediate_size, c.num_hidden_layers, c.num_attention_heads,
-                   c.num_key_value_heads, head_dim, c.rms_norm_eps)
+                   c.num_key_value_heads, head_dim, c.rms_norm_eps, c.vocab_size)
 
     @classmethod
     def of_kernel(cls, m) -> "_Geometry":
-        return cls(m.hidden, m.inter, m.layers, m.heads, m.kv_heads, m.head_dim, _decode.EPS)
+        return cls(m.hidden, m.inter, m.layers, m.heads, m.kv_heads, m.head_dim, _decode.EPS, _decode.VOCAB)
 
 
 _KERNEL_OF_GEOMETRY = {_Geometry.of_kernel(m): name for name, m in MODELS.items()}

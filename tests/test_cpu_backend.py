@@ -31,9 +31,9 @@ class OtherMetadata(FlashAttentionMetadata):
 
 def _config(name="360m", **over):
     base = dict(hidden_size=960, intermediate_size=2560, num_hidden_layers=32, num_attention_heads=15,
-                num_key_value_heads=5, rms_norm_eps=1e-5) if name == "360m" else dict(
+                num_key_value_heads=5, rms_norm_eps=1e-5, vocab_size=49152) if name == "360m" else dict(
         hidden_size=576, intermediate_size=1536, num_hidden_layers=30, num_attention_heads=9,
-        num_key_value_heads=3, rms_norm_eps=1e-5)
+        num_key_value_heads=3, rms_norm_eps=1e-5, vocab_size=49152)
     base.update(over)
     return NS(**base)
 
@@ -68,14 +68,15 @@ def test_geometry_routing():
     assert D.kernel_for_config(_config("360m")) == D.KERNEL_NAME_360M
     assert D.kernel_for_config(_config("135m")) == D.KERNEL_NAME_135M
     for bad in (dict(num_hidden_layers=31), dict(rms_norm_eps=1e-6), dict(num_key_value_heads=3),
-                dict(head_dim=128), dict(intermediate_size=2048)):
+                dict(head_dim=128), dict(intermediate_size=2048), dict(vocab_size=49153), dict(vocab_size=32000)):
         assert D.kernel_for_config(_config("360m", **bad)) is None, bad
 
 
 def test_geometry_routing_hf_config():
     transformers = pytest.importorskip("transformers")
     c = transformers.LlamaConfig(hidden_size=960, intermediate_size=2560, num_hidden_layers=32,
-                                 num_attention_heads=15, num_key_value_heads=5, rms_norm_eps=1e-5)
+                                 num_attention_heads=15, num_key_value_heads=5, rms_norm_eps=1e-5,
+                                 vocab_size=49152)
     assert D.kernel_for_config(c) == D.KERNEL_NAME_360M
 
 

@@ -144,6 +144,20 @@ def test_wrapper_contract_errors_on_cpu_tensors():
         m.decode_step(**dict(kw, layers=[()] * 3))
 
 
+def test_embedding_table_must_have_the_full_vocabulary():
+    """The kernels clamp input ids to 0..49151 and the tied LM head reads every row, so the wrapper
+    takes only a contiguous [49152, hidden] table: fewer rows would be read past their end, more
+    would hold rows no id reaches."""
+    from prime_kernels_amd import _decode
+    for model in (_decode.SMOLLM2_360M, _decode.SMOLLM2_135M):
+        _decode.check_embed_shape(torch.zeros(49152, model.hidden, dtype=torch.bfloat16), model)
+        for rows in (1, 49151, 49153, 65536):
+            with pytest.raises(ValueError, match="embed"):
+                _decode.check_embed_shape(torch.zeros(rows, model.hidden, dtype=torch.bfloat16), model)
+        with pytest.raises(ValueError, match="embed"):
+            _decode.check_embed_shape(torch.zeros(model.hidden, 49152, dtype=torch.bfloat16).t(), model)
+
+
 def test_manifest_lists_built_sources():
     for name in pk.KERNELS:
         s = pk.spec(name)

@@ -47,7 +47,7 @@ def _served(batch, cap, seed=5):
                                       attn=NS(kv_cache=kv.caches[i], layer_name="model.layers.0.self_attn.attn")),
                          mlp=NS(gate_up_proj=NS(weight=gu), down_proj=NS(weight=down))))
     cfg = NS(hidden_size=960, intermediate_size=2560, num_hidden_layers=32, num_attention_heads=15,
-             num_key_value_heads=5, rms_norm_eps=1e-5)
+             num_key_value_heads=5, rms_norm_eps=1e-5, vocab_size=49152)
     served = NS(config=cfg, layers=layers, embed_tokens=NS(weight=embed),
                 norm=NS(weight=final_norm, variance_epsilon=1e-5))
     return mod, served, kv, cs

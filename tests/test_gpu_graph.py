@@ -45,9 +45,23 @@ def _fill(kv, st, ids, positions):
     st["slot_mapping"].copy_(torch.tensor([kv.slot(b, p) for b, p in enumerate(positions)], device=dev))
 
 
+@pytest.mark.parametrize("launch", ["ordinary", "cooperative"])
 @pytest.mark.parametrize("batch", [1, 3])
-def test_decode_step_replays_from_a_graph(batch):
+def test_decode_step_replays_from_a_graph(batch, launch):
+    """Also with the kernels launched cooperatively (PK_OPT_COOPERATIVE), the captured launch
+    replaying the eager step bit for bit."""
     _need_gpu()
+    from prime_kernels_amd import _native
+
+    lib = _native.library()
+    old = lib.pk_set_option(_native.PK_OPT_COOPERATIVE, 1 if launch == "cooperative" else 0)
+    try:
+        _replay_check(batch)
+    finally:
+        lib.pk_set_option(_native.PK_OPT_COOPERATIVE, old)
+
+
+def _replay_check(batch):
     ctxs = [300 + 97 * b for b in range(batch)]
     mod, kv, st, logits, kw = _setup(batch, ctxs)
     kv0 = [c.clone() for c in kv.caches]

@@ -2,8 +2,11 @@
 
 * A step whose bounded waits give up (forced from the host with pk_test_abort_next, so every wait
   gives up at its first check and every kernel still ends normally) returns NaN hidden state and
-  logits and token ids -1, is reported by pk_state_status, makes the next call raise RuntimeError
-  (PK_ERR_ABORTED), and leaves the following steps correct.
+  logits and token ids -1, is reported by pk_state_status, makes the next call (or check_failures)
+  raise RuntimeError once, and leaves the following steps correct.
+* Exchange units are never seen torn: a unit whose tag is current carries its own payload
+  (pk_test_exchange_units, in every memory kind the kernels use).
+* The cooperative launch (PK_OPT_COOPERATIVE) gives the ordinary launch's bits on every kernel.
 * Exchange words carry the full 32-bit step epoch: steps that alternate batch sizes (so some words
   are not rewritten every step) give the same bits across the epoch's 32-bit wrap and across jumps
   of 65,536 and 65,535 epochs, where a 16-bit tag (with or without a skipped zero) would accept a
@@ -51,8 +54,11 @@ def _step(mod, embed, final_norm, lw, kv, cos_sin, ids, positions):
     return hid.clone(), out_ids.clone(), logits
 
 
+@pytest.mark.parametrize("report", ["next_call", "check_failures"])
 @pytest.mark.parametrize("path", ["split_role", "general", "batched"])
-def test_abandoned_wait_poisons_outputs_and_is_reported(path):
+def test_abandoned_wait_poisons_outputs_and_is_reported(path, report):
+    """The failed step is reported once: by the next decode call (which launches nothing), or by
+    check_failures, after which the next call runs normally."""
     _need_gpu()
     from prime_kernels_amd import _native
 
@@ -86,9 +92,14 @@ def test_abandoned_wait_poisons_outputs_and_is_reported(path):
         assert torch.isnan(lg_bad.float()).all(), "logits not poisoned"
         epoch, site = rt.pending_failure()
         assert epoch != 0, "no failure report"
-        # the next call reports it (and launches nothing)
-        with pytest.raises(RuntimeError, match="gave_up_a_bounded_wait"):
-            _step(mod, embed, final_norm, lw, kv, cos_sin, ids, contexts)
+        if report == "next_call":
+            # the next call reports it (and launches nothing)
+            with pytest.raises(RuntimeError, match="gave_up_a_bounded_wait"):
+                _step(mod, embed, final_norm, lw, kv, cos_sin, ids, contexts)
+        else:
+            from prime_kernels_amd import _decode
+            with pytest.raises(RuntimeError, match="gave up a bounded wait"):
+                _decode.check_failures(model, embed.device)
         assert rt.pending_failure() == (0, 0)
         # and the step after that is correct again
         restore()
@@ -150,32 +161,29 @@ def test_epoch_wrap_and_16_bit_jumps_with_alternating_batches():
         assert all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(kv_ref, kv_got)), mode
 
 
-def test_embed_check_follows_the_reference_without_lm_head():
-    """Without an LM head the embedding needs only the hidden width, as in the reference
-    (decode_megakernel_360m/__init__.py:151-152): a 1000-row embedding gives the full one's step for
-    ids below 1000.  With token ids or logits requested the full vocabulary is required."""
+def test_embed_table_must_have_the_full_vocabulary():
+    """The kernels clamp input ids to 0..49151 and the tied LM head reads every row, so decode_step
+    refuses an embedding of any other row count (fewer rows would be read past their end), with or
+    without the LM head, and one of another width."""
     _need_gpu()
     mod, model, embed, final_norm, lw, kv, cos_sin = _setup(1, [200])
     dev = embed.device
-    small = embed[:1000].contiguous()
-    kv0 = [c.clone() for c in kv.caches]
 
     def step(e, **extra):
-        for c, c0 in zip(kv.caches, kv0):
-            c.copy_(c0)
-        out = mod.decode_step(
+        return mod.decode_step(
             input_ids=torch.tensor([999], device=dev), positions=torch.tensor([200], device=dev),
             seq_lens=torch.tensor([201], dtype=torch.int32, device=dev), block_table=kv.block_table[:1].contiguous(),
             slot_mapping=torch.tensor([kv.slot(0, 200)], device=dev), embed=e, layers=lw, final_norm=final_norm,
             kv_caches=kv.caches, cos_sin_cache=cos_sin, eps=1e-5, num_layers=len(lw), **extra)
-        torch.cuda.synchronize()
-        return out.clone()
 
-    assert torch.equal(step(small).view(torch.int16), step(embed).view(torch.int16))
-    with pytest.raises(ValueError, match="LM head"):
-        step(small, return_token_ids=True)
-    with pytest.raises(ValueError, match="embed"):
-        step(embed[:, :900].contiguous())
+    bigger = torch.cat([embed, embed[:64]]).contiguous()
+    for e in (embed[:1000].contiguous(), bigger, embed[:, :900].contiguous()):
+        with pytest.raises(ValueError, match="embed"):
+            step(e)
+        with pytest.raises(ValueError, match="embed"):
+            step(e, return_token_ids=True)
+    torch.cuda.synchronize()
+    assert mod.workspace(dev).pending_failure() == (0, 0)
 
 
 @pytest.mark.parametrize("split_role", [1, 0], ids=["split_role", "general"])
@@ -248,5 +256,76 @@ def test_arrival_skew_leaves_every_bit_unchanged(case):
             assert torch.equal(h.view(torch.int16), h0.view(torch.int16)), seed
             assert torch.equal(i, i0) and torch.equal(lg.view(torch.int16), l0.view(torch.int16)), seed
             assert all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(kc, k0)), seed
+    finally:
+        lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, old_sr)
+
+
+@pytest.mark.parametrize("slot", [64, 16])
+@pytest.mark.parametrize("mode", [0, 1, 2], ids=["uncached", "cached_sc1", "xcd_l2"])
+def test_exchange_units_are_never_torn(mode, slot):
+    """The exchanges accept a 16-byte unit {3 payload words, tag} once its tag is current and use the
+    payload of that same load, which relies on 16-byte stores never being seen torn.  Workgroups
+    publish units whose payload is a function of (tag, unit) with the kernels' stores and read every
+    unit back with their polling loads for 400 rounds: no accepted unit may carry another payload, in
+    uncached memory (pk_decode's cross-XCD units), ordinary memory with device-scope accesses
+    (pk_decode_noalloc's array) and one XCD's L2 (attention records), with one unit per 64-byte
+    line (the kernels' placement) and four units from different workgroups per line."""
+    _need_gpu()
+    import ctypes
+
+    from prime_kernels_amd import _native
+
+    lib = _native.library()
+    out = (ctypes.c_uint * 4)()
+    rounds = 400
+    print(f"mode {mode} slot {slot}", flush=True)
+    assert lib.pk_test_exchange_units(mode, rounds, slot, out) == 0
+    torn, gave_up, checked, xcc_mask = list(out)
+    participants = 32 if mode == 2 else 256
+    if mode == 2 and bin(xcc_mask).count("1") != 1:
+        pytest.skip(f"the 32 workgroups did not share one XCC (mask {xcc_mask:#x}); the kernels then use uncached records")
+    assert torn == 0, (torn, gave_up, checked)
+    assert gave_up == 0, (torn, gave_up, checked)
+    assert checked == rounds * participants * participants * 4, checked
+
+
+@pytest.mark.parametrize("path", ["split_role", "general", "batched", "mxfp8"])
+def test_cooperative_launch_gives_the_same_bits(path):
+    """The decode kernels run with the ordinary launch by default; PK_OPT_COOPERATIVE (or
+    PK_LAUNCH=cooperative) launches them with hipLaunchCooperativeKernel as the reference does
+    (block360_kernel.inc:914-920).  Both launches give the same hidden state, ids, logits and caches."""
+    _need_gpu()
+    from prime_kernels_amd import _native
+
+    lib = _native.library()
+    batch = 3 if path == "batched" else 1
+    contexts = [300 + 41 * b for b in range(batch)] if path != "mxfp8" else [2100]
+    mod, model, embed, final_norm, lw, kv, cos_sin = _setup(batch, contexts)
+    if path == "mxfp8":
+        import prime_kernels_amd as pk
+        from prime_kernels_amd import mxfp8
+        mod = pk.load("decode_megakernel_360m_mxfp8")
+        lw = mxfp8.quantize_layers(lw)
+    kv0 = [c.clone() for c in kv.caches]
+    ids = [(57 + 13 * b) % 49152 for b in range(batch)]
+    old_sr = lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, 0 if path == "general" else 1)
+    try:
+        outs = []
+        for coop in (0, 1):
+            old = lib.pk_set_option(_native.PK_OPT_COOPERATIVE, coop)
+            try:
+                for c, c0 in zip(kv.caches, kv0):
+                    c.copy_(c0)
+                h, i, lg = _step(mod, embed, final_norm, lw, kv, cos_sin, ids, contexts)
+                torch.cuda.synchronize()
+                outs.append((h, i, lg.clone(), [c.clone() for c in kv.caches]))
+            finally:
+                lib.pk_set_option(_native.PK_OPT_COOPERATIVE, old)
+            assert mod.workspace(embed.device).pending_failure() == (0, 0), coop
+        (h0, i0, l0, k0), (h1, i1, l1, k1) = outs
+        assert not torch.isnan(h0.float()).any()
+        assert torch.equal(h0.view(torch.int16), h1.view(torch.int16)) and torch.equal(i0, i1)
+        assert torch.equal(l0.view(torch.int16), l1.view(torch.int16))
+        assert all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(k0, k1))
     finally:
         lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, old_sr)
