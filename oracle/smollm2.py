@@ -355,7 +355,7 @@ def decode_step(w: Weights, ids, positions, kv: PagedKV, cos_sin: torch.Tensor, 
 def prefill(w: Weights, prompt: torch.Tensor, kv: PagedKV, cos_sin: torch.Tensor, b: int = 0,
             start: int = 0) -> None:
     """Fill sequence b's cache for prompt tokens by running the decode step one token at a time
-    (slow; for small prompts in tests).  Larger caches come from `random` fills or GPU prefill."""
+    (slow; for small prompts in tests).  prefill_batched is HF's own prompt pass."""
     for i, tok in enumerate(prompt.tolist()):
         p = start + i
         one = Weights(w.geom, w.embed, w.final_norm, w.layers)
@@ -365,6 +365,52 @@ def prefill(w: Weights, prompt: torch.Tensor, kv: PagedKV, cos_sin: torch.Tensor
             past_k, past_v = kv.gather(li, b, p, w.geom.head_dim)
             x, k_new, v_new = decoder_layer(w.geom, w.layers[li], x, p, cos_sin, past_k, past_v)
             kv.write(li, slot, k_new, v_new)
+
+
+@torch.no_grad()
+def prefill_batched(w: Weights, prompt: torch.Tensor, kv: PagedKV, cos_sin: torch.Tensor, b: int = 0) -> dict:
+    """HF's prompt pass (LlamaModel.forward over all prompt tokens at once, modeling_llama.py:367-414,
+    with the eager attention of :191-214 under the 4-D float causal mask that
+    transformers/masking_utils.py:538-604 builds for eager attention: 0 where a position is visible,
+    the dtype's minimum elsewhere, added to the scaled scores), writing sequence b's K/V for positions
+    0..P-1 into `kv`.  The same batched ops as HF, so on the CPU the cache and the last position's
+    logits are HF's bit for bit (pinned by tests/golden fixtures).  Returns the final-normed hidden
+    state [H] and the logits [V] of the last prompt position and their argmax (LlamaForCausalLM
+    computes the LM head over every position, :479-480, and the greedy pick reads the last row)."""
+    geom = w.geom
+    H, D, NH, KVH, I = geom.hidden, geom.head_dim, geom.heads, geom.kv_heads, geom.inter
+    P = int(prompt.numel())
+    x = w.embed[prompt.view(-1).long()].view(1, P, H)
+    cos, sin = full_cos_sin(cos_sin[:P])
+    cos, sin = cos.view(1, 1, P, D), sin.view(1, 1, P, D)
+    visible = torch.ones(P, P, dtype=torch.bool).tril()
+    mask = torch.where(visible, torch.tensor(0.0, dtype=BF16), torch.finfo(BF16).min).view(1, 1, P, P)
+    slots = [kv.slot(b, p) for p in range(P)]
+    blocks = torch.tensor([s // kv.block_size for s in slots])
+    offs = torch.tensor([s % kv.block_size for s in slots])
+    for li, (norm1, qkv, o_w, norm2, gate_up, down) in enumerate(w.layers):
+        residual = x
+        h = rms_norm(x, norm1, geom.eps)
+        q = F.linear(h, qkv[:H]).view(1, P, NH, D).transpose(1, 2)
+        k = F.linear(h, qkv[H:H + KVH * D]).view(1, P, KVH, D).transpose(1, 2)
+        v = F.linear(h, qkv[H + KVH * D:]).view(1, P, KVH, D).transpose(1, 2)
+        q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+        key_states, value_states = repeat_kv(k, NH // KVH), repeat_kv(v, NH // KVH)
+        scores = torch.matmul(q, key_states.transpose(2, 3)) * D ** -0.5
+        scores = scores + mask
+        probs = F.softmax(scores, dim=-1, dtype=torch.float32).to(q.dtype)
+        attn = torch.matmul(probs, value_states).transpose(1, 2).contiguous().reshape(1, P, H).contiguous()
+        x = residual + F.linear(attn, o_w)
+        residual = x
+        h2 = rms_norm(x, norm2, geom.eps)
+        x = residual + F.linear(F.silu(F.linear(h2, gate_up[:I])) * F.linear(h2, gate_up[I:]), down)
+        # K/V of every prompt position into the paged cache ([KVH, P, D] -> slot rows)
+        cache = kv.caches[li]
+        cache[blocks, :, offs, :D] = k[0].transpose(0, 1)
+        cache[blocks, :, offs, D:] = v[0].transpose(0, 1)
+    hf = rms_norm(x, w.final_norm, geom.eps)
+    logits = F.linear(hf, w.embed)[0, -1]
+    return {"hidden": hf[0, -1], "logits": logits, "id": int(torch.argmax(logits, dim=-1))}
 
 
 def ordered_bf16(t: torch.Tensor) -> torch.Tensor:

@@ -13,6 +13,13 @@ copy (transformers 5.15.0, torch CPU) -- never the reference -- and records:
   * `block360_stages.npz`: BASELINE config 1, one SmolLM2-360M decoder layer on a hidden-state
     input N(0,1) with a KV cache pre-filled with 512 positions of N(0,1), every stage output
     captured with forward hooks (the reference debug stages, block360_kernel.inc:1-13).
+  * `<config>_full.npz`: BASELINE configs 2 and 3 at full depth (SmolLM2-135M, 30 layers, a
+    512-token prompt; SmolLM2-360M, 32 layers, a 1024-token prompt), seeded weights and a seeded
+    uniform random prompt, HF's eager prompt pass, then 256 greedy eager decode steps: the prompt,
+    the 257 greedy ids (ids[0] from the prompt pass, ids[s+1] from decode step s), the final-normed
+    hidden state at steps 0..7 and 255, top-32 logits of the prompt pass and of every step, full
+    bf16 logits at steps 0 and 255.  The prompt pass's K/V cache (tens of MB) is not stored: the
+    json holds the SHA-256 of every layer's K and V [KVH, P, D] bf16 bits instead.
 
 bf16 arrays are stored as their uint16 bit patterns.  Run from the repo root:
     python tests/golden/make_golden.py
@@ -123,6 +130,50 @@ def greedy_fixture(base: O.Geometry, tag: str, seed: int) -> dict:
             "weights_sha256": w.fingerprint()}
 
 
+FULL_STEPS = 256
+HIDDEN_STEPS = list(range(8)) + [FULL_STEPS - 1]
+
+
+def full_fixture(geom: O.Geometry, tag: str, seed: int, prompt_len: int) -> dict:
+    """BASELINE config 2 / 3 at full depth: prompt pass, then FULL_STEPS greedy steps."""
+    w = O.make_weights(geom, seed)
+    model = hf_model(geom, w)
+    g = torch.Generator().manual_seed(seed + 1)
+    prompt = torch.randint(0, geom.vocab, (1, prompt_len), generator=g)
+    normed = {}
+    model.model.norm.register_forward_hook(lambda _m, _i, out: normed.update(h=out.detach()))
+    with torch.no_grad():
+        out = model(input_ids=prompt, use_cache=True)
+        cache = out.past_key_values
+        kv_sha = {}
+        for li in range(geom.layers):
+            k, v = cache_kv(cache, li)
+            kv_sha[f"layers.{li}.k"] = O.sha256_tensor(k.contiguous())
+            kv_sha[f"layers.{li}.v"] = O.sha256_tensor(v.contiguous())
+        pv, pi = torch.topk(out.logits[0, -1].float(), 32)
+        tok = out.logits[0, -1].argmax().view(1, 1)
+        ids, hidden, top_v, top_i, full = [int(tok)], [], [], [], []
+        for step in range(FULL_STEPS):
+            o = model(input_ids=tok, past_key_values=cache, use_cache=True,
+                      position_ids=torch.tensor([[prompt_len + step]]))
+            lg = o.logits[0, -1]
+            if step in HIDDEN_STEPS:
+                hidden.append(bits(normed["h"][0, -1]))
+            tv, ti = torch.topk(lg.float(), 32)
+            top_v.append(bits(tv)), top_i.append(ti.numpy().astype(np.int32))
+            if step in (0, FULL_STEPS - 1):
+                full.append(bits(lg))
+            tok = lg.argmax().view(1, 1)
+            ids.append(int(tok))
+    np.savez_compressed(OUT / f"{tag}_full.npz", prompt=prompt[0].numpy().astype(np.int32),
+                        ids=np.array(ids, dtype=np.int32), hidden=np.stack(hidden), top_v=np.stack(top_v),
+                        top_i=np.stack(top_i), full_logits=np.stack(full), prefill_top_v=bits(pv),
+                        prefill_top_i=pi.numpy().astype(np.int32))
+    return {"geometry": geom.__dict__, "seed": seed, "norm_jitter": 0.0, "prompt_len": prompt_len,
+            "steps": FULL_STEPS, "hidden_steps": HIDDEN_STEPS, "full_logit_steps": [0, FULL_STEPS - 1],
+            "prefill_kv_sha256": kv_sha, "weights_sha256": w.fingerprint()}
+
+
 def block_fixture(seed: int) -> dict:
     """one 360M block, hidden input N(0,1), 512 cached positions N(0,1)."""
     from transformers import DynamicCache
@@ -178,10 +229,12 @@ def main() -> None:
     import transformers
 
     torch.set_num_threads(8)
-    meta = {"transformers": transformers.__version__, "torch": torch.__version__,
+    meta = {"transformers": transformers.__version__, "torch": torch.__version__, "torch_threads": 8,
             "fixtures": {"smollm2_360m": greedy_fixture(O.SMOLLM2_360M, "smollm2_360m", WEIGHT_SEED),
                          "smollm2_135m": greedy_fixture(O.SMOLLM2_135M, "smollm2_135m", WEIGHT_SEED + 100),
-                         "block360": block_fixture(WEIGHT_SEED + 200)}}
+                         "block360": block_fixture(WEIGHT_SEED + 200),
+                         "config2_135m": full_fixture(O.SMOLLM2_135M, "config2_135m", 2002, 512),
+                         "config3_360m": full_fixture(O.SMOLLM2_360M, "config3_360m", 3003, 1024)}}
     (OUT / "golden.json").write_text(json.dumps(meta, indent=1, sort_keys=True) + "\n")
     print("wrote", sorted(p.name for p in OUT.glob("*.npz")))
 

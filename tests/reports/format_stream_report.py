@@ -61,6 +61,25 @@ def main(src: str, dst: str) -> None:
         out += ["```", "", "Whole cache after the stream, per layer (max abs err of the appended K/V; kernel / eager):", "",
                 "```", " ".join(f"{c['layer']}:{c['kernel_err']:.3f}/{c['eager_err']:.3f}"
                                 for c in data[name]["summary"]["cache_layers"]), "```"]
+    hf = [("hf_config2_135m", "config 2: SmolLM2-135M, HF's 512-token prompt pass and 256 greedy ids"),
+          ("hf_config3_360m", "config 3: SmolLM2-360M, HF's 1024-token prompt pass and 256 greedy ids")]
+    hf_data = {n: json.loads((Path(src) / f"{n}.json").read_text()) for n, _ in hf if (Path(src) / f"{n}.json").exists()}
+    if hf_data:
+        out += ["", "## Against HF transformers itself (tests/golden/config*_full.npz)", "",
+                "Teacher-forced over HF's own greedy stream from its prompt pass (the oracle's batched prompt pass "
+                "rebuilds the cache; `HF cache bits` says whether the box's CPU reproduced HF's cache bit for bit). "
+                "Errors are max abs over HF's top-32 logits of each step.", "",
+                "| stream | HF cache bits | kernel max / mean err | eager-GPU max / mean err | argmax agree kernel | "
+                "argmax agree eager | HF margins at kernel flips | top-32 bound |", "|---|---|---|---|---|---|---|---|"]
+        for n, title in hf:
+            if n not in hf_data:
+                continue
+            s_ = hf_data[n]["summary"]
+            k, e = s_["kernel"], s_["eager_gpu"]
+            steps = len(hf_data[n]["steps"])
+            out.append(f"| {title} | {s_['prompt_cache_is_hf_bits']} | {k['top32_max_err']:.4f} / {k['top32_mean_err']:.4f} | "
+                       f"{e['top32_max_err']:.4f} / {e['top32_mean_err']:.4f} | {k['argmax_agree']}/{steps} | "
+                       f"{e['argmax_agree']}/{steps} | {k['mismatch_margins']} | {s_['bounds']['top32_max']:.4f} |")
     Path(dst).write_text("\n".join(out) + "\n")
 
 

@@ -40,7 +40,7 @@ def golden(golden_dir):
 @pytest.mark.parametrize("key", ["smollm2_360m", "smollm2_135m"])
 def test_golden_greedy_teacher_forced(golden, key):
     """2-layer models from the HF goldens: every step's logits within tolerance of HF's, greedy
-    ids equal, KV appends within tolerance (the cache is teacher-forced from the golden K/V)."""
+    ids equal to HF's, KV appends within tolerance (the cache is teacher-forced from the golden K/V)."""
     _need_gpu()
     meta, gdir = golden
     fx = meta["fixtures"][key]
@@ -67,9 +67,8 @@ def test_golden_greedy_teacher_forced(golden, key):
             c = GC.compare_logits(res["logits"][0], from_bits(g["full_logits"][full_i]))
             full_i += 1
             assert c["max_abs"] <= GC.LOGIT_ATOL and c["cos"] >= GC.COS_MIN, c
-        ref = case.oracle_step([int(ids[step])], [pos])  # bit-identical to HF (test_oracle.py)
-        assert int(ref["ids"][0]) == int(ids[step + 1])
-        assert GC.greedy_ok(int(res["ids"][0]), ref["logits"][0]), f"step {step} greedy id"
+        # HF's top-2 margin is at least 0.1 at every step of these fixtures: the id must be HF's
+        assert int(res["ids"][0]) == int(ids[step + 1]), f"step {step} greedy id {int(res['ids'][0])}"
         slot = kv.slot(0, pos)
         for li in range(geom.layers):
             got = case.kvd[li][slot // 16, :, slot % 16].cpu().float()

@@ -68,6 +68,58 @@ def test_greedy_135m_matches_hf(meta, golden_dir):
     _run_greedy(meta, golden_dir, "smollm2_135m")
 
 
+def full_depth_prefill(meta, golden_dir, key):
+    """Weights and the oracle's batched prompt pass of a full-depth HF fixture (BASELINE config 2 or
+    3): (fixture meta, geometry, weights, paged cache, rope table, prompt-pass result, fixture
+    arrays)."""
+    fx = meta["fixtures"][key]
+    geom = _geom(fx["geometry"])
+    w = O.make_weights(geom, fx["seed"], norm_jitter=fx["norm_jitter"])
+    assert w.fingerprint() == fx["weights_sha256"], "seeded weight generator drifted"
+    g = np.load(golden_dir / f"{key}_full.npz")
+    P, steps = fx["prompt_len"], fx["steps"]
+    kv = O.make_paged_kv(geom, 1, P + steps + 16, seed=None)
+    cos_sin = O.rope_cos_sin(P + steps + 16, geom.head_dim, geom.theta)
+    pre = O.prefill_batched(w, torch.from_numpy(g["prompt"].astype(np.int64)), kv, cos_sin)
+    return fx, geom, w, kv, cos_sin, pre, g
+
+
+@pytest.mark.parametrize("key", ["config2_135m", "config3_360m"])
+def test_full_depth_stream_matches_hf(meta, golden_dir, key):
+    """BASELINE configs 2 and 3 at full depth against HF transformers 5.15.0 (tests/golden
+    config*_full.npz): the oracle's prompt pass gives HF's cache (SHA-256 of every layer's K and V)
+    and prompt logits, then 256 free-running greedy steps give HF's ids, its top-32 logits at every
+    step, its hidden state at steps 0..7 and 255 and its full logits at steps 0 and 255, bit for bit.
+    Run with the thread count the fixtures were written with (CPU GEMM blocking may depend on it)."""
+    threads = torch.get_num_threads()
+    torch.set_num_threads(meta.get("torch_threads", threads))
+    try:
+        fx, geom, w, kv, cos_sin, pre, g = full_depth_prefill(meta, golden_dir, key)
+        P, steps = fx["prompt_len"], fx["steps"]
+        for li in range(geom.layers):
+            k, v = kv.gather(li, 0, P, geom.head_dim)
+            assert O.sha256_tensor(k[0]) == fx["prefill_kv_sha256"][f"layers.{li}.k"], f"prompt K layer {li}"
+            assert O.sha256_tensor(v[0]) == fx["prefill_kv_sha256"][f"layers.{li}.v"], f"prompt V layer {li}"
+        pi = torch.from_numpy(g["prefill_top_i"].astype(np.int64))
+        assert torch.equal(pre["logits"][pi], from_bits(g["prefill_top_v"]))
+        ids = g["ids"]
+        assert pre["id"] == int(ids[0])
+        hidden_i, full_i = 0, 0
+        for step in range(steps):
+            res = O.decode_step(w, [int(ids[step])], [P + step], kv, cos_sin)
+            top_i = torch.from_numpy(g["top_i"][step].astype(np.int64))
+            assert torch.equal(res["logits"][0][top_i], from_bits(g["top_v"][step])), f"top-32 logits step {step}"
+            if step in fx["hidden_steps"]:
+                assert torch.equal(res["hidden"][0], from_bits(g["hidden"][hidden_i])), f"hidden step {step}"
+                hidden_i += 1
+            if step in fx["full_logit_steps"]:
+                assert torch.equal(res["logits"][0], from_bits(g["full_logits"][full_i])), f"logits step {step}"
+                full_i += 1
+            assert int(res["ids"][0]) == int(ids[step + 1]), f"greedy id step {step}"
+    finally:
+        torch.set_num_threads(threads)
+
+
 def test_block360_stages_match_hf(meta, golden_dir):
     fx = meta["fixtures"]["block360"]
     geom = _geom(fx["geometry"])
