@@ -2,6 +2,7 @@
 into one markdown report:
 
     PK_STREAM_REPORT=out python -m pytest tests/test_gpu_stream.py -m gpu -s
+(the batch-16 and HF streams add their sections when their JSON files are present)
     python tests/reports/format_stream_report.py out tests/reports/stream_full_depth.md
 """
 
@@ -61,6 +62,20 @@ def main(src: str, dst: str) -> None:
         out += ["```", "", "Whole cache after the stream, per layer (max abs err of the appended K/V; kernel / eager):", "",
                 "```", " ".join(f"{c['layer']}:{c['kernel_err']:.3f}/{c['eager_err']:.3f}"
                                 for c in data[name]["summary"]["cache_layers"]), "```"]
+    b16 = Path(src) / "stream_360m_b16_ragged.json"
+    if b16.exists():
+        s_ = json.loads(b16.read_text())["summary"]
+        k, e, b = s_["kernel"], s_["eager_gpu"], s_["bounds"]
+        n = s_["steps"] * s_["sequences"]
+        out += ["", "## Config 4: SmolLM2-360M, 16 ragged sequences (batched kernel)", "",
+                f"Contexts {s_['contexts']}, {s_['steps']} teacher-forced steps per sequence ({n} sequence-steps).", "",
+                "| kernel max / mean err | eager-GPU max / mean err | kernel min cos | eager min cos | argmax agree kernel | "
+                "argmax agree eager | largest oracle margin at a kernel flip | logits bound | cache: kernel / eager max err, "
+                "untouched slots equal |", "|---|---|---|---|---|---|---|---|---|",
+                f"| {k['max_err']:.4f} / {k['mean_err']:.4f} | {e['max_err']:.4f} / {e['mean_err']:.4f} | {k['min_cos']:.5f} | "
+                f"{e['min_cos']:.5f} | {k['argmax_agree']}/{n} | {e['argmax_agree']}/{n} | "
+                f"{max(k['mismatch_margins'], default=0):.4f} | {b['logits_max']:.4f} | "
+                f"{s_['cache']['kernel_max_err']:.4f} / {s_['cache']['eager_max_err']:.4f}, {s_['cache']['untouched_equal']} |"]
     hf = [("hf_config2_135m", "config 2: SmolLM2-135M, HF's 512-token prompt pass and 256 greedy ids"),
           ("hf_config3_360m", "config 3: SmolLM2-360M, HF's 1024-token prompt pass and 256 greedy ids")]
     hf_data = {n: json.loads((Path(src) / f"{n}.json").read_text()) for n, _ in hf if (Path(src) / f"{n}.json").exists()}

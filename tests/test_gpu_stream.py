@@ -298,3 +298,93 @@ def test_hf_stream_config3_360m():
     """BASELINE config 3 against HF itself: SmolLM2-360M, HF's 1024-token prompt pass, 256 steps."""
     _need_gpu()
     _check_hf(_hf_stream("config3_360m"))
+
+
+STEPS_B16 = 64
+
+
+@pytest.mark.timeout(900)
+def test_stream_config4_b16_ragged():
+    """SmolLM2-360M (32 layers), 16 sequences with contexts drawn uniformly from
+    128..4096 (the bench's draw), 64 teacher-forced steps on the batched kernel.  Per sequence the
+    same bars as the batch-1 streams (logits against the oracle within the eager-GPU floor, greedy
+    flips only at near-ties and at most MISS_SLACK more than eager-GPU's), then the whole cache of
+    every layer: slots no sequence appended bit-identical to the initial fill, appended K/V within
+    the bf16 tolerance or the eager floor."""
+    _need_gpu()
+    import numpy as np
+
+    rng = np.random.default_rng(4)
+    contexts = [int(x) for x in rng.integers(128, 4097, 16)]
+    B = len(contexts)
+    geom = O.SMOLLM2_360M
+    case = GC.random_kv_case(geom, 4004, contexts, norm_jitter=0.0,
+                             capacity=max(contexts) + STEPS_B16 + 16)
+    eager_kv = O.PagedKV([c.to(case.dev) for c in case.kv.caches], case.btd, case.kv.block_size)
+    eager_w = O.Weights(geom, case.wd.embed, case.wd.final_norm, case.wd.layers)
+    initial = [c.clone() for c in case.kv.caches]
+    toks = [int(x) for x in rng.integers(0, geom.vocab, B)]
+    rows = [[] for _ in range(B)]
+    t0 = time.time()
+    for s in range(STEPS_B16):
+        pos = [c + s for c in contexts]
+        k = case.kernel_step(toks, pos)
+        e = O.decode_step(eager_w, toks, pos, eager_kv, case.csd)
+        r = case.oracle_step(toks, pos)
+        for b in range(B):
+            ref, best = r["logits"][b], int(r["ids"][b])
+            k_err, k_cos = _compare(k["logits"][b], ref)
+            e_err, e_cos = _compare(e["logits"][b].cpu(), ref)
+            rows[b].append({"step": s, "oracle_id": best, "oracle_margin": round(_margin(ref, best), 5),
+                            "kernel_err": k_err, "kernel_cos": k_cos, "kernel_id": int(k["ids"][b]),
+                            "eager_err": e_err, "eager_cos": e_cos, "eager_id": int(e["ids"][b])})
+        toks = [int(x) for x in r["ids"]]
+        if s % 16 == 15:
+            print(f"config4 stream: {s + 1} steps in {time.time() - t0:.1f} s", flush=True)
+    flat = [x for rb in rows for x in rb]
+    k_err = torch.tensor([x["kernel_err"] for x in flat])
+    e_err = torch.tensor([x["eager_err"] for x in flat])
+    bound = max(GC.LOGIT_ATOL, FLOOR_FACTOR * e_err.max().item())
+    mean_bound = max(GC.LOGIT_ATOL / 2, MEAN_FACTOR * e_err.mean().item())
+    cos_min = min(GC.COS_MIN, 1.0 - FLOOR_FACTOR * (1.0 - min(x["eager_cos"] for x in flat)))
+    k_miss = [x for x in flat if x["kernel_id"] != x["oracle_id"]]
+    e_miss = [x for x in flat if x["eager_id"] != x["oracle_id"]]
+    # the whole cache: [blocks, block_size] mask of every slot the stream appended to
+    mask = torch.zeros(case.kv.caches[0].shape[0], case.kv.block_size, dtype=torch.bool)
+    for b, c in enumerate(contexts):
+        for p in range(c, c + STEPS_B16):
+            slot = case.kv.slot(b, p)
+            mask[slot // case.kv.block_size, slot % case.kv.block_size] = True
+    cache = []
+    for li, (kc, oc, ec, init) in enumerate(zip(case.kvd, case.kv.caches, eager_kv.caches, initial)):
+        kc, oc, ec, init = (t.cpu().permute(0, 2, 1, 3) for t in (kc, oc, ec, init))
+        kw, ow, ew = kc[mask].float(), oc[mask].float(), ec[mask].float()
+        e_kv = (ew - ow).abs().max().item()
+        tol = torch.maximum(KV_RTOL * ow.abs() + KV_ATOL, torch.full_like(ow, FLOOR_FACTOR * e_kv))
+        cache.append({"layer": li, "kernel_err": (kw - ow).abs().max().item(), "eager_err": e_kv,
+                      "within": bool(((kw - ow).abs() <= tol).all()),
+                      "untouched_equal": torch.equal(kc[~mask].view(torch.int16), init[~mask].view(torch.int16))})
+    summary = {"label": "stream_360m_b16_ragged", "steps": STEPS_B16, "sequences": B, "contexts": contexts,
+               "kernel": {"max_err": k_err.max().item(), "mean_err": k_err.mean().item(),
+                          "min_cos": min(x["kernel_cos"] for x in flat), "argmax_agree": len(flat) - len(k_miss),
+                          "mismatch_margins": [x["oracle_margin"] for x in k_miss]},
+               "eager_gpu": {"max_err": e_err.max().item(), "mean_err": e_err.mean().item(),
+                             "min_cos": min(x["eager_cos"] for x in flat), "argmax_agree": len(flat) - len(e_miss),
+                             "mismatch_margins": [x["oracle_margin"] for x in e_miss]},
+               "bounds": {"logits_max": bound, "logits_mean": mean_bound, "cos_min": cos_min},
+               "cache": {"kernel_max_err": max(c["kernel_err"] for c in cache),
+                         "eager_max_err": max(c["eager_err"] for c in cache),
+                         "untouched_equal": all(c["untouched_equal"] for c in cache)}}
+    report_dir = os.environ.get("PK_STREAM_REPORT")
+    if report_dir:
+        os.makedirs(report_dir, exist_ok=True)
+        with open(os.path.join(report_dir, "stream_360m_b16_ragged.json"), "w") as f:
+            json.dump({"summary": summary, "steps": rows, "cache_layers": cache}, f)
+    print(json.dumps(summary), flush=True)
+    for c in cache:
+        assert c["untouched_equal"], f"config4: layer {c['layer']}: a slot outside the appends changed"
+        assert c["within"], f"config4: layer {c['layer']}: appended K/V off the oracle: {c}"
+    assert k_err.max().item() <= bound, f"config4: logits error {k_err.max().item()} > {bound}"
+    assert k_err.mean().item() <= mean_bound, f"config4: mean logits error {k_err.mean().item()} > {mean_bound}"
+    assert summary["kernel"]["min_cos"] >= cos_min
+    _assert_flips(k_miss, e_miss, "config4")
