@@ -1453,7 +1453,10 @@ __device__ __forceinline__ void consumer_a(CSR<G>& C) {
     ChunkRegs R;
     tr(l, 0);
     if (P.att) {
-      C.wait_filled(C.pos);
+      // the KV chunk only: the O rows (needed after the attention) may still be streaming, as they
+      // are in the first layer, whose chunk streams into an empty ring at the start of the launch
+      // (tile reads past the chunk's last token read other ring bytes, which the masks discard)
+      C.wait_filled(C.pos_kv_end);
       tr(l, 21);
       chunk_load<G>(C, segkv, R);
       tr(l, 22);
