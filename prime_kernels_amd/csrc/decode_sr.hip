@@ -100,8 +100,8 @@ struct SWS {
   static constexpr size_t XBYTES = size_t(REP) * LINES * SLOTS * 64;
   static constexpr size_t LMR = X0 + XBYTES;                  // per-workgroup end records: NWG units
   static constexpr size_t LOC = LMR + size_t(NWG) * 16;      // group-A records when they cannot stay in L2
-  // group-A records per layer, in units: statistics (2 per chunk), partials (3 heads x PU per chunk)
-  static constexpr size_t STAT_U = 0, PART_U = size_t(AG) * 2;
+  // group-A records per layer, in units: statistics (2 per wave of a chunk), partials (3 heads x PU per chunk)
+  static constexpr size_t STAT_U = 0, PART_U = size_t(AG) * NCW * 2;
   static constexpr size_t LOC_LAYER = (PART_U + size_t(AG) * 3 * S::PU) * 16;
   static constexpr size_t LOC_BYTES = LOC_LAYER * G::L;
   static constexpr size_t BYTES = LOC + LOC_BYTES;
@@ -247,7 +247,6 @@ struct SmemSR {
   };
   float keep[G::H];              // F: h1 (residual of down); A: x (residual of O, its own rows)
   float wo[NCW][3][64];          // per-wave P.V partials
-  float wml[NCW][2][3];          // per-wave softmax max / sum per head
   float red[NCW];
   LayerW lw[G::L];
   GUE gue[G::L];                 // group F: each layer's lossless gate/up stream of this workgroup
@@ -929,63 +928,59 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
     }
     m = ch == 0 ? mw[0] : ch == 1 ? mw[1] : mw[2];
   }
-  if (lane == 0)
-#pragma unroll
-    for (int h = 0; h < 3; ++h) {
-      sm.wml[w][0][h] = mw[h];
-      sm.wml[w][1][h] = lw[h];
-    }
   if (w == 0 && lane == 0) trace_at(p, l, 37, p.n_layers);
   if (has_new && lane == 0) trace_at(p, l, 39, p.n_layers);
-  C.cbar();
-  float mq = -INFINITY, lq = 0.f;
-  if (lane < 4 * 3) {
-    mq = sm.wml[lane & 3][0][lane >> 2];
-    lq = sm.wml[lane & 3][1][lane >> 2];
-  }
-  float mx = fmaxf(mq, dpp<0xb1>(mq, mq));
-  mx = fmaxf(mx, dpp<0x4e>(mx, mx));
-  float ex = mq == -INFINITY ? 0.f : lq * __expf(mq - mx);
-  ex += dpp<0xb1>(0.f, ex);
-  ex += dpp<0x4e>(0.f, ex);
-  float Mh[3], Lh[3];
-#pragma unroll
-  for (int h = 0; h < 3; ++h) {
-    Mh[h] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx), 4 * h));
-    Lh[h] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), 4 * h));
-  }
+  // exchange (max, sum) with every wave of the head's chunks, each wave publishing its own without
+  // waiting for the other waves of its chunk: wave v of chunk c' (group-A rank g + KVH c') has the
+  // record {max x3, tag}, {sum x3, tag} at units (rank NCW + v) 2 + {0, 1}
+  if (lane < 2)
+    C.put_loc(l, W::STAT_U + (size_t(P.rank) * NCW + w) * 2 + lane,
+              lane ? u32x4{__float_as_uint(lw[0]), __float_as_uint(lw[1]), __float_as_uint(lw[2]), C.tag}
+                   : u32x4{__float_as_uint(mw[0]), __float_as_uint(mw[1]), __float_as_uint(mw[2]), C.tag});
   if (w == 0 && lane == 0) trace_at(p, l, 17, p.n_layers);
-  // exchange (max, sum) with the other chunks of KV head g: chunk c' of head g is group-A rank
-  // g + KVH c'; its record is 2 units {max x3, tag}, {sum x3, tag}
-  if (w == 0 && lane < 2)
-    C.put_loc(l, W::STAT_U + size_t(P.rank) * 2 + lane,
-              lane ? u32x4{__float_as_uint(Lh[0]), __float_as_uint(Lh[1]), __float_as_uint(Lh[2]), C.tag}
-                   : u32x4{__float_as_uint(Mh[0]), __float_as_uint(Mh[1]), __float_as_uint(Mh[2]), C.tag});
+  float Mh[3], Lh[3];
   {
-    // lane 2k + s polls unit s of chunk k: lane 2k the maxima of chunk k, lane 2k+1 its sums
-    float st[3] = {(lane & 1) ? 0.f : -INFINITY, (lane & 1) ? 0.f : -INFINITY, (lane & 1) ? 0.f : -INFINITY};
-    C.template poll<1>(C.rl, 2 * S::C, lane, 64,
-                       [&](int i) { return W::loc(l, W::STAT_U + size_t(g + G::KVH * (i >> 1)) * 2 + (i & 1)); },
-                       [&](int, const u32x4& v) {
-                         st[0] = __uint_as_float(v.x);
-                         st[1] = __uint_as_float(v.y);
-                         st[2] = __uint_as_float(v.z);
-                       },
-                       31);
-    // combine in one pass: the odd lane of each pair takes its chunk's maxima from the even lane
-    float m[3], s[3];
+    // unit i = 2k + s (k = NCW c' + v) is polled by lane i % 64: an even lane the maxima of one
+    // (chunk, wave), the odd lane next to it the sums of the same one
+    constexpr int NU = 2 * NCW * S::C, MU = (NU + 63) / 64;
+    static_assert(MU <= 2, "two statistics units per lane at most");
+    float st[MU][3];
 #pragma unroll
-    for (int h = 0; h < 3; ++h) {
-      const float mo = __shfl_xor(st[h], 1);
-      m[h] = (lane & 1) ? mo : st[h];
-    }
-    float M[3] = {m[0], m[1], m[2]};
+    for (int k = 0; k < MU; ++k)
+#pragma unroll
+      for (int h = 0; h < 3; ++h) st[k][h] = (lane & 1) ? 0.f : -INFINITY;
+    C.template poll<MU>(C.rl, NU, lane, 64,
+                        [&](int i) {
+                          const int pr = i >> 1, c = pr / NCW, v = pr - c * NCW;
+                          return W::loc(l, W::STAT_U + (size_t(g + G::KVH * c) * NCW + v) * 2 + (i & 1));
+                        },
+                        [&](int i, const u32x4& v) {
+                          const float a = __uint_as_float(v.x), b = __uint_as_float(v.y), c = __uint_as_float(v.z);
+                          if (MU == 1 || i < 64) { st[0][0] = a; st[0][1] = b; st[0][2] = c; }
+                          else { st[MU - 1][0] = a; st[MU - 1][1] = b; st[MU - 1][2] = c; }
+                        },
+                        31);
+    // combine in one pass: the odd lane of each pair takes its (chunk, wave)'s maxima from the even lane
+    float m[MU][3], M[3] = {-INFINITY, -INFINITY, -INFINITY}, sum[3];
+#pragma unroll
+    for (int k = 0; k < MU; ++k)
+#pragma unroll
+      for (int h = 0; h < 3; ++h) {
+        const float mo = __shfl_xor(st[k][h], 1);
+        m[k][h] = (lane & 1) ? mo : st[k][h];
+        M[h] = fmaxf(M[h], m[k][h]);
+      }
     wave_max_n<3>(M);
 #pragma unroll
-    for (int h = 0; h < 3; ++h) s[h] = ((lane & 1) && lane < 2 * S::C && m[h] != -INFINITY) ? st[h] * __expf(m[h] - M[h]) : 0.f;
-    wave_sum_n<3>(s);
+    for (int h = 0; h < 3; ++h) {
+      sum[h] = 0.f;
 #pragma unroll
-    for (int h = 0; h < 3; ++h) { Mh[h] = M[h]; Lh[h] = s[h]; }
+      for (int k = 0; k < MU; ++k)
+        sum[h] += ((lane & 1) && lane + 64 * k < NU && m[k][h] != -INFINITY) ? st[k][h] * __expf(m[k][h] - M[h]) : 0.f;
+    }
+    wave_sum_n<3>(sum);
+#pragma unroll
+    for (int h = 0; h < 3; ++h) { Mh[h] = M[h]; Lh[h] = sum[h]; }
   }
   if (w == 0 && lane == 0) trace_at(p, l, 18, p.n_layers);
   // P.V on the matrix cores with the probabilities rounded to bf16 as HF does.  The scores'
