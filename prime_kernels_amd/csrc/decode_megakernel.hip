@@ -1,11 +1,19 @@
-// SmolLM2 single-token decode step as one persistent cooperative HIP kernel for gfx950 (MI355X).
+// SmolLM2 single-token decode step as one persistent HIP kernel per step for gfx950 (MI355X): the
+// general batch-1 kernel (decode_kernel) and the batched kernel (decode_kernel_b); the split-role
+// batch-1 kernel is in decode_sr.hip.  The launch is an ordinary hipLaunchKernel of one workgroup
+// per CU, which relies on all 256 workgroups being resident at once (true on an otherwise idle
+// device: a workgroup waiting for one that is not resident gives up after its bounded wait and the
+// step comes back poisoned and reported); PK_LAUNCH=cooperative or pk_set_option(PK_OPT_COOPERATIVE)
+// launches with hipLaunchCooperativeKernel instead, which guarantees co-residency for 18 us more per
+// step (measured at batch 1, context 1024; the same bits either way).
 //
-// One workgroup per CU (256), 5 wave64s each:
-//   wave 0      producer: streams this workgroup's share of every weight matrix (and its KV-cache
-//               chunk) from HBM into a 128 KB LDS ring with LDS-DMA loads
-//               (global_load_lds_dwordx4), up to DEPTH 1 KB packets in flight, running ahead of
-//               the dependency chain because weights and cached K/V do not depend on activations.
-//   waves 1..4  consumers: pull their rows from the ring into VGPRs, wait for the phase input,
+// One workgroup per CU (256), 8 wave64s each:
+//   waves 0..3  producers: stream this workgroup's share of every weight matrix (and its KV-cache
+//               chunk) from HBM into a 128 KB LDS ring (64 KB in the batched kernel) with LDS-DMA
+//               loads (global_load_lds_dwordx4), DEPTH (batched: DEPTH_B) 1 KB packets in flight
+//               per wave, running ahead of the dependency chain because weights and cached K/V do
+//               not depend on activations.
+//   waves 4..7  consumers: pull their rows from the ring into VGPRs, wait for the phase input,
 //               compute, publish the phase output.
 //
 // Phases per layer (the reference's eight grid barriers per layer, block360_kernel.inc:96-803,
@@ -19,12 +27,14 @@
 //   P5 down GEMV + residual               -> x (layer output)
 //   then final RMSNorm + tied LM head GEMV with per-workgroup argmax, and a 256-way argmax.
 //
-// Inter-workgroup exchange: no counters, no fences.  Every exchanged value is written as a
-// 64-bit word {bf16 or fp32 value, tag32} with device-scope relaxed atomic
-// stores, into a buffer owned by one (layer, phase, sequence).  Readers poll those words with
-// device-scope (sc1) loads until every tag equals this step's epoch, so the data arrives with
-// the "ready" signal in one round trip.  The epoch is a device counter bumped by workgroup 0 at
-// the end of every step.
+// Inter-workgroup exchange: no counters, no fences.  In the general kernel every exchanged value
+// is written as a 64-bit word {bf16 or fp32 value, tag32} with device-scope relaxed atomic stores,
+// into a buffer owned by one (layer, phase, sequence).  Readers poll those words with device-scope
+// (sc1) loads until every tag equals this step's epoch, so the data arrives with the "ready"
+// signal in one round trip.  The batched kernel instead writes each phase output as a plain
+// [B][K] bf16 array with sc1 2-byte stores, then each workgroup raises one tagged flag per
+// (phase, layer) after its stores have completed; readers poll the flags, then copy the array.
+// The epoch is a device counter bumped by workgroup 0 at the end of every step.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -3035,9 +3045,9 @@ struct LaunchCache {
 };
 
 // Library options (pk_set_option), initialised from the environment: PK_LAUNCH=cooperative makes
-// every decode launch cooperative (hipLaunchCooperativeKernel, which costs ~17 us more per launch
-// on this part than an ordinary launch of the same grid; the grid is one workgroup per CU either
-// way), PK_SPLIT_ROLE=0 keeps batch-1 steps on the general kernel.
+// every decode launch cooperative (hipLaunchCooperativeKernel, 18 us more per step than an ordinary
+// launch of the same grid at batch 1, context 1024; the grid is one workgroup per CU either way, and
+// the results are the same bits), PK_SPLIT_ROLE=0 keeps batch-1 steps on the general kernel.
 struct Options {
   int cooperative = -1;
   int split_role = -1;
