@@ -48,6 +48,8 @@ extern "C" {
                                     chunks share an XCD (the path a placement mismatch takes; default 1) */
 #define PK_OPT_SKEW 4            /* != 0: arrival-skew test, the seed of pseudo-random delays every workgroup
                                     takes before publishing exchange data (results must not change; default 0) */
+#define PK_OPT_SPLIT_WIDE 5      /* 0: batch-1 contexts beyond the narrow split-role limit go to the general
+                                    kernel instead of the wide split-role layout (default 1, or PK_SPLIT_WIDE=0) */
 
 /* Models. */
 #define PK_MODEL_SMOLLM2_360M 360
@@ -95,9 +97,10 @@ int pk_test_abort_next(void* stream);
 int pk_test_exchange_units(int mode, int rounds, int slot, unsigned* out);
 
 /* One greedy decode step for B = 1..16 sequences (vLLM FLASH_ATTN metadata, paged KV
- * [blocks, KVH, 16, 128]; contexts may differ per sequence).  B = 1 runs the split-role kernel
- * while max_seq_len is at most PK_NOALLOC_MAX_SEQ_360M / _135M (PK_OPT_SPLIT_ROLE 1, the default),
- * else the general GEMV kernel; B >= 2 runs the batched kernel, whose projections and LM head are
+ * [blocks, KVH, 16, 128]; contexts may differ per sequence).  B = 1 (bf16 or MXFP8 weights) runs the
+ * split-role kernel: its narrow layout for contexts up to PK_NOALLOC_MAX_SEQ_360M / _135M tokens, its
+ * wide layout (attention over KVH XCDs) up to PK_SR_WIDE_MAX_SEQ, the general GEMV kernel beyond
+ * (PK_OPT_SPLIT_ROLE / PK_OPT_SPLIT_WIDE switch the split-role layouts off); B >= 2 runs the batched kernel, whose projections and LM head are
  * MFMA tiles over all B tokens, so the weights are read once per step for the whole batch.  The
  * reference caps SmolLM2-360M at B <= 2 (decode_megakernel_360m/__init__.py:46).
  *   layers: device table [n_layers][6] of pointers (norm1, qkv, o, norm2, gate_up, down), bf16.
@@ -117,6 +120,8 @@ int pk_decode(void* stream, int model, int B, int n_layers, const void* input_id
 #define PK_NOALLOC_SCRATCH_BYTES 8388608
 #define PK_NOALLOC_MAX_SEQ_360M 1537
 #define PK_NOALLOC_MAX_SEQ_135M 2561
+/* Longest context (tokens attended) of the split-role kernel's wide layout, both models. */
+#define PK_SR_WIDE_MAX_SEQ 9729
 
 /* pk_decode that allocates nothing, for callers that cannot allocate device memory: code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc.  It has no counterpart in

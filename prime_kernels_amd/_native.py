@@ -22,6 +22,7 @@ PK_OPT_COOPERATIVE = 1
 PK_OPT_SPLIT_ROLE = 2
 PK_OPT_L2_RECORDS = 3
 PK_OPT_SKEW = 4
+PK_OPT_SPLIT_WIDE = 5
 
 _lib = None
 

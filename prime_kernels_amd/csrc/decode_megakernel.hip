@@ -648,11 +648,6 @@ __device__ __forceinline__ void dots_ring(const Consumer<G>& C, uint32_t seg, in
   for (int r = 0; r < MAXR; ++r) out[r] = wave_sum(out[r]);
 }
 
-// E8M0 scale code -> fp32 2^(s-127) (code 0 is the fp32 denormal 2^-127; 255 is NaN).
-__device__ __forceinline__ float e8m0_f32(uint32_t s) {
-  return __uint_as_float(s == 0 ? 0x00400000u : s == 255 ? 0x7fc00000u : s << 23);
-}
-
 // MXFP8 rows: out[r] = row (cw + NCW*r) . x with the row's e4m3 weights (K bytes in segment
 // `segq`) scaled by its e8m0 codes (scale_stride(K) bytes per row in segment `segs`).  Each 16-byte
 // chunk (16 weights, one scale block of 32 covers two chunks) becomes 8 bf16 pairs with
@@ -3047,10 +3042,12 @@ struct LaunchCache {
 // Library options (pk_set_option), initialised from the environment: PK_LAUNCH=cooperative makes
 // every decode launch cooperative (hipLaunchCooperativeKernel, 18 us more per step than an ordinary
 // launch of the same grid at batch 1, context 1024; the grid is one workgroup per CU either way, and
-// the results are the same bits), PK_SPLIT_ROLE=0 keeps batch-1 steps on the general kernel.
+// the results are the same bits), PK_SPLIT_ROLE=0 keeps batch-1 steps on the general kernel,
+// PK_SPLIT_WIDE=0 sends contexts beyond the narrow split-role limit to the general kernel.
 struct Options {
   int cooperative = -1;
   int split_role = -1;
+  int split_wide = -1;
   int l2_records = 1;
   uint32_t skew = 0;
 };
@@ -3068,6 +3065,13 @@ static int opt_split_role() {
     g_opt.split_role = (e && e[0] == '0') ? 0 : 1;
   }
   return g_opt.split_role;
+}
+static int opt_split_wide() {
+  if (g_opt.split_wide < 0) {
+    const char* e = getenv("PK_SPLIT_WIDE");
+    g_opt.split_wide = (e && e[0] == '0') ? 0 : 1;
+  }
+  return g_opt.split_wide;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -3100,8 +3104,11 @@ static constexpr size_t ws_general_bytes() {
 static constexpr size_t rec_general_bytes() {
   return round_up((WS<G360>::XREC_WORDS > WS<G135>::XREC_WORDS ? WS<G360>::XREC_WORDS : WS<G135>::XREC_WORDS) * 4, 4096);
 }
-static size_t ws_bytes() { return ws_general_bytes() + round_up(sr_region_bytes(), 4096); }
-static size_t rec_bytes() { return rec_general_bytes() + round_up(sr_local_bytes(), 4096); }
+static size_t ws_bytes() { return ws_general_bytes() + round_up(sr_region_bytes(1), 4096); }
+// the split-role group-A records: the narrow layout's, then the wide layout's (separate lines, so
+// that no XCD's L2 holds a line another layout writes from another XCD)
+static size_t rec_wide_off() { return rec_general_bytes() + round_up(sr_local_bytes(0), 4096); }
+static size_t rec_bytes() { return rec_wide_off() + round_up(sr_local_bytes(1), 4096); }
 
 __global__ void __launch_bounds__(256) zero_fill(uint4* p, size_t n) {
   for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
@@ -3168,8 +3175,8 @@ struct Dev {
 static std::mutex mu;
 static Dev devs[MAX_STATES];  // by device ordinal
 static size_t region_off() { return HDR_BYTES; }
-static size_t local_off() { return HDR_BYTES + round_up(sr_region_bytes(), 4096); }
-static size_t used_bytes() { return local_off() + round_up(sr_local_bytes(), 4096); }
+static size_t local_off() { return HDR_BYTES + round_up(sr_region_bytes(0), 4096); }
+static size_t used_bytes() { return local_off() + round_up(sr_local_bytes(0), 4096); }
 
 // The current device's array, cleared before its first use by a fill on `stream` (under capture
 // the fill is recorded, so every replay of the graph clears the array before its own step).  With
@@ -3328,7 +3335,7 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
   if (noalloc) {  // the split-role kernel on the fixed array; no library state is touched
     if constexpr (G::WF == 0) {
       const int model = G::H == 960 ? PK_MODEL_SMOLLM2_360M : PK_MODEL_SMOLLM2_135M;
-      const int lim = sr_max_seq(model);
+      const int lim = sr_max_seq(model, 0);
       if (B != 1 || debug || encoded_gu || input_hidden || max_seq_len > lim) return PK_ERR_NOALLOC;
       uint8_t* base = nullptr;
       const int rc = noalloc::base(s, false, &base);
@@ -3337,7 +3344,8 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
       p.xws = nullptr;
       p.host_status = nullptr;
       p.sr_max_s = lim;
-      return sr_launch(model, p, reinterpret_cast<uint32_t*>(base + noalloc::region_off()),
+      p.sr_min_s = 0;
+      return sr_launch(model, 0, 0, p, reinterpret_cast<uint32_t*>(base + noalloc::region_off()),
                        reinterpret_cast<uint32_t*>(base + noalloc::local_off()), s, opt_cooperative());
     } else {
       return PK_ERR_NOALLOC;
@@ -3356,18 +3364,27 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
   }
   if constexpr (G::WF == 0)
     if (B > 1) return launch<G, true>(p, s);
-  // Batch 1: the split-role kernel takes contexts up to its limit, the general kernel the rest.
-  // Both are launched; each reads the context length on the device and exactly one does the step,
-  // so the host never has to read it (no synchronisation, and the pair can be captured in a graph).
-  if constexpr (G::WF == 0) {
+  // Batch 1: the split-role kernel's narrow layout takes contexts up to its limit, the wide layout
+  // the next range, the general kernel the rest.  Each kernel that can get a context is launched;
+  // each reads the context length on the device and exactly one does the step, so the host never has
+  // to read it (no synchronisation, and the launches can be captured in a graph).
+  if (opt_split_role() && !input_hidden) {
     const int model = G::H == 960 ? PK_MODEL_SMOLLM2_360M : PK_MODEL_SMOLLM2_135M;
-    if (opt_split_role() && !input_hidden) {
-      p.sr_max_s = sr_max_seq(model);
-      const int e = sr_launch(model, p, reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(state->ws) + ws_general_bytes()),
-                              reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(state->rec) + rec_general_bytes()), s,
-                              opt_cooperative());
+    uint32_t* region = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(state->ws) + ws_general_bytes());
+    uint8_t* rec = reinterpret_cast<uint8_t*>(state->rec);
+    const int narrow = sr_max_seq(model, 0);
+    p.sr_min_s = 0;
+    p.sr_max_s = narrow;
+    int e = sr_launch(model, G::WF, 0, p, region, reinterpret_cast<uint32_t*>(rec + rec_general_bytes()), s,
+                      opt_cooperative());
+    if (e != PK_OK) return e;
+    if (max_seq_len <= p.sr_max_s) return PK_OK;  // no context can reach another kernel
+    if (opt_split_wide()) {
+      p.sr_min_s = narrow;
+      p.sr_max_s = sr_max_seq(model, 1);
+      e = sr_launch(model, G::WF, 1, p, region, reinterpret_cast<uint32_t*>(rec + rec_wide_off()), s, opt_cooperative());
       if (e != PK_OK) return e;
-      if (max_seq_len <= p.sr_max_s) return PK_OK;  // no context can reach the general kernel
+      if (max_seq_len <= p.sr_max_s) return PK_OK;
     }
   }
   return launch<G, false>(p, s);
@@ -3410,6 +3427,11 @@ extern "C" int pk_set_option(int option, int value) {
   if (option == PK_OPT_L2_RECORDS) {
     const int old = pk::g_opt.l2_records;
     pk::g_opt.l2_records = value ? 1 : 0;
+    return old;
+  }
+  if (option == PK_OPT_SPLIT_WIDE) {
+    const int old = pk::opt_split_wide();
+    pk::g_opt.split_wide = value ? 1 : 0;
     return old;
   }
   if (option == PK_OPT_SKEW) {

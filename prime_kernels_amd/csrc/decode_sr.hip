@@ -1,16 +1,23 @@
 // SmolLM2 batch-1 decode step, split-role persistent kernel for gfx950 (MI355X).
 //
 // The 256 workgroups (one per CU, dispatched to the 8 XCDs round-robin) take one of two roles:
-//   group A, the 32 workgroups wg % 8 == 0 (one XCD): attention over the KV cache (C chunks per
-//           KV head), the merge of the chunk partials and the O projection + residual -> h1;
-//   group F, the other 224 workgroups (seven XCDs): RMSNorm + gate/up + SwiGLU, down + residual
-//           -> x, RMSNorm + the QKV projection.
-// Per layer the data cross XCDs four times (h1 A->F, act F->F, x F->F, q/k/v F->A); the three
-// exchanges inside attention (softmax statistics, P.V partials, the merged attention vector) stay
-// inside group A's XCD and go through its L2.  The two groups alternate: while one works, the other
-// streams its next layer's weights (or KV chunk) into its LDS ring, so no workgroup has DMA in
-// flight when it polls for data (an exchange poll issued behind outstanding DMA on the same CU
-// waits for that DMA; measured, a hop costs 0.3-1.2 us more with the CU's own DMA in flight).
+//   group A, the workgroups on the first AX XCDs (wg % 8 < AX): attention over the KV cache (C
+//           chunks per KV head), the sum of the chunk partials and the O projection + residual -> h1;
+//   group F, the others: RMSNorm + gate/up + SwiGLU, down + residual -> x, RMSNorm + the QKV
+//           projection.
+// Two layouts of group A are compiled:
+//   narrow (AX = 1): the 32 workgroups of XCD 0, C = 32 / KVH chunks per KV head of at most 256
+//           cached tokens; the O workgroups read the chunks' partial sums from XCD 0's L2;
+//   wide (AX = KVH): KV head g on XCD g, 32 chunks per head of at most 304 cached tokens, for long
+//           contexts; chunk c of a head adds slice c of the head's partials over the 32 chunks and
+//           publishes that slice of the attention vector to every XCD.
+// Per layer the data cross XCDs four times (h1 A->F, act F->F, x F->F, q/k/v F->A), five in the
+// wide layout (also the attention vector); the exchanges among one KV head's chunks (softmax
+// statistics, P.V partials) stay inside its XCD and go through its L2.  The two groups alternate:
+// while one works, the other streams its next layer's weights (or KV chunk) into its LDS ring, so
+// no workgroup has DMA in flight when it polls for data (an exchange poll issued behind outstanding
+// DMA on the same CU waits for that DMA; measured, a hop costs 0.3-1.2 us more with the CU's own
+// DMA in flight).
 //
 // Exchange format: 16-byte units {three 32-bit payload words, 32-bit step tag}, written with one
 // 16-byte store and read with one 16-byte load (a payload of 6 bf16 or 3 fp32).  A reader polls a
@@ -20,9 +27,13 @@
 // Cross-XCD units live in uncached device memory (device-scope stores and loads) for pk_decode; for
 // pk_decode_noalloc they live in an ordinary (cached) device array, where the device-scope (sc1)
 // stores and loads alone keep them coherent across XCDs.  Group A's records live in ordinary device
-// memory written with plain stores into the XCD's L2 and read with device-scope loads.  At the start of a launch the
-// group-A workgroups check that they really share one XCC (hardware register XCC_ID); if not, the
-// records go through the uncached workspace instead.
+// memory written with plain stores into the XCD's L2 and read with device-scope loads.  At the start
+// of a launch the group-A workgroups check that the ones exchanging records really share one XCC
+// (hardware register XCC_ID); if not, the records go through the uncached workspace instead.
+//
+// Projection weights are bf16 or MXFP8 (G::WF): e4m3 rows plus one e8m0 scale per 32 weights,
+// dequantised to bf16(e4m3 * 2^(s-127)) as they are loaded into registers, so every dot product
+// runs the bf16 path's v_dot2_f32_bf16 sequence on the dequantised matrix.
 //
 // Rounding points are those of HF eager Llama (modeling_llama.py), as in the general kernel:
 // RMSNorm bf16(w * bf16(x * rsqrt(mean(x^2) + eps))), every projection bf16(W.x) with fp32
@@ -33,14 +44,13 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <type_traits>
 
 #include "pk_common.h"
 
 namespace pk {
 namespace sr {
 
-constexpr int AG = 32;                   // group A workgroups (wg % 8 == 0)
-constexpr int FG = NWG - AG;             // group F workgroups
 constexpr int VPU = 6;                   // bf16 values per 16-byte unit
 #ifndef PK_SR_REP
 #define PK_SR_REP 1
@@ -50,29 +60,53 @@ constexpr int VPU = 6;                   // bf16 values per 16-byte unit
 #endif
 constexpr int REP = PK_SR_REP;           // copies of each cross-XCD unit
 constexpr int UPL = PK_SR_UPL;           // cross-XCD units per 64-byte line (fewer: fewer polls per line)
-constexpr int TCS = 256;                 // max cached tokens per attention chunk
 #ifndef PK_SR_DEPTH
 #define PK_SR_DEPTH 8
 #endif
 constexpr int DEPTH_SR = PK_SR_DEPTH;    // DMA packets in flight per producer wave
 constexpr int LM_ROWS_SR = 24;           // LM-head rows per ring segment, 6 per consumer wave (16: -1.5%)
 
-__device__ __forceinline__ bool in_a(int wg) { return (wg & 7) == 0; }
+// 16-token tiles of a chunk per consumer wave (attention): at most MT
+constexpr int MT = 5;
+
+// The kernel's geometry: the model's (G0, with its weight format G0::WF) and group A's XCD count.
+template <class G0, int AX_>
+struct SrG : G0 {
+  static constexpr int AX = AX_;
+};
 
 template <class G>
 struct SG {
+  static constexpr int AX = G::AX;                      // XCDs of group A
+  static constexpr bool WIDE = AX > 1;
+  static constexpr int AG = 32 * AX;                    // group A workgroups
+  static constexpr int FG = NWG - AG;                   // group F workgroups
+  static constexpr int TCS = WIDE ? 304 : 256;          // max cached tokens per attention chunk
   static constexpr int HU = (G::H + VPU - 1) / VPU;     // units of an H-vector
   static constexpr int IU = (G::I + VPU - 1) / VPU;     // units of the act vector
   static constexpr int QU = (G::QKV + VPU - 1) / VPU;   // units of the qkv vector
   static constexpr int C = AG / G::KVH;                 // attention chunks per KV head
   static constexpr int NATT = C * G::KVH;
-  static constexpr int PU = 22;                         // units of one head's 64 fp32 partial sums
+  static constexpr int PU = 22;                         // narrow: units of one head's 64 fp32 partial sums
+  static constexpr int PUC = WIDE ? 64 : 3 * PU;        // partial-sum units per chunk record
   static constexpr int OU = (HU + AG - 1) / AG;         // most O units per group-A workgroup
+  static constexpr int NAU = (IU + FG - 1) / FG;        // most act units per group-F workgroup
+  static constexpr int NXU = (HU + FG - 1) / FG;        // most x (down) units per group-F workgroup
+  static constexpr int NQU = (QU + FG - 1) / FG;        // most qkv units per group-F workgroup
+  static constexpr int NIT = (2 * NAU + NCW - 1) / NCW; // gate/up 6-row items per wave
+  static constexpr int NPART = 2 * NAU > NCW * NXU ? 2 * NAU : NCW * NXU;  // rows of SmemSR::part
   // O rows loaded before the attention partials are polled (10 chunk records per thread leave no
-  // room for them in the SmolLM2-135M build without spills)
-  static constexpr bool O_EARLY = C <= 6;
+  // room for them in the narrow SmolLM2-135M build without spills)
+  static constexpr bool O_EARLY = WIDE || C <= 6;
+  static constexpr uint32_t WB = G::WF ? 1u : 2u;       // bytes per projection weight
+  __device__ static bool in_a(int wg) { return (wg & 7) < AX; }
   static_assert(G::GQA == 3 && (3 * 64) % VPU == 0 && G::H % VPU == 0, "head groups are whole units");
-  static_assert(C >= 1 && C <= 16, "chunks per KV head");
+  static_assert(!WIDE || AX == G::KVH, "the wide layout puts one KV head on each of its XCDs");
+  static_assert(C >= 1 && C <= 32 && (!WIDE || C == 32), "chunks per KV head");
+  static_assert(TCS + 1 <= MT * 16 * NCW, "a chunk's tiles (and the new token) fit MT tiles per wave");
+  static_assert(NQU <= NCW, "the QKV phase gives each wave at most one unit");
+  static_assert(NXU <= 2 && NIT <= 3, "down units and gate/up items per group-F workgroup");
+  static_assert(OU * VPU <= 8 * NCW, "the O rows fit 8 per wave");
 };
 
 // The qkv vector in slot order.  Its q and k parts are laid out by RoPE pair: slots 2p and 2p + 1
@@ -89,26 +123,28 @@ __device__ __forceinline__ int qkv_row(int s) {
 
 // Workspace (uncached, 32-bit words), placed after the general kernels' layout (base word SR0) so
 // that no word is ever read in a format it was not written in; the header (epoch, abort) is shared.
-enum SKind { K_H1, K_ACT, K_X, K_XQ, NK };
+enum SKind { K_H1, K_ACT, K_X, K_XQ, K_ATT, NK };
 template <class G>
 struct SWS {
   using S = SG<G>;
   static constexpr int LINES = (S::IU + UPL - 1) / UPL;
-  static constexpr int SLOTS = (G::L + 1) * NK;
-  static constexpr size_t XCC_TAB = 0;                        // 32 units: the group-A XCC ids
-  static constexpr size_t X0 = XCC_TAB + size_t(AG) * 16;     // cross-XCD vectors (bytes from the region base)
+  static constexpr int NKL = S::WIDE ? NK : K_ATT;            // vector kinds of the layout (narrow: no K_ATT)
+  static constexpr int SLOTS = (G::L + 1) * NKL;
+  static constexpr size_t XCC_TAB = 0;                        // the group-A XCC ids, one unit per rank
+  static constexpr size_t X0 = XCC_TAB + size_t(S::AG) * 16;  // cross-XCD vectors (bytes from the region base)
   static constexpr size_t XBYTES = size_t(REP) * LINES * SLOTS * 64;
   static constexpr size_t LMR = X0 + XBYTES;                  // per-workgroup end records: NWG units
   static constexpr size_t LOC = LMR + size_t(NWG) * 16;      // group-A records when they cannot stay in L2
-  // group-A records per layer, in units: statistics (2 per wave of a chunk), partials (3 heads x PU per chunk)
-  static constexpr size_t STAT_U = 0, PART_U = size_t(AG) * NCW * 2;
-  static constexpr size_t LOC_LAYER = (PART_U + size_t(AG) * 3 * S::PU) * 16;
+  // group-A records per layer, in units: statistics (2 per wave of a chunk), partials (PUC per chunk:
+  // narrow, 3 heads x PU units; wide, the chunk's 192 values in order, 3 per unit)
+  static constexpr size_t STAT_U = 0, PART_U = size_t(S::AG) * NCW * 2;
+  static constexpr size_t LOC_LAYER = (PART_U + size_t(S::AG) * S::PUC) * 16;
   static constexpr size_t LOC_BYTES = LOC_LAYER * G::L;
   static constexpr size_t BYTES = LOC + LOC_BYTES;
   // unit u of vector (kind, layer l, copy r): UPL units per line; consecutive lines of a vector are
   // SLOTS lines apart, so one vector's lines spread over the memory channels
   __device__ static uint32_t xoff(int kind, int l, int r, int u) {
-    return uint32_t(X0 + ((size_t(r) * LINES + size_t(u / UPL)) * SLOTS + size_t(l) * NK + kind) * 64 +
+    return uint32_t(X0 + ((size_t(r) * LINES + size_t(u / UPL)) * SLOTS + size_t(l) * NKL + kind) * 64 +
                     size_t(u % UPL) * 16);
   }
   __device__ static uint32_t loc(int l, size_t unit) { return uint32_t(size_t(l) * LOC_LAYER + unit * 16); }
@@ -135,11 +171,6 @@ __device__ __forceinline__ float rms_rsq(float sumsq) {
 // Per-workgroup plan
 // ------------------------------------------------------------------------------------------------
 
-static_assert((SG<G360>::IU + FG - 1) / FG <= 2 && (SG<G135>::IU + FG - 1) / FG <= 2,
-              "the gate/up phase gives each wave one 6-row item: at most 2 act units per F workgroup");
-static_assert((SG<G360>::QU + FG - 1) / FG <= NCW && (SG<G135>::QU + FG - 1) / FG <= NCW,
-              "the QKV phase gives each wave at most one unit");
-
 template <class G>
 struct PlanSR {
   using GG = SG<G>;
@@ -155,9 +186,11 @@ struct PlanSR {
   int v0, v1, n_lm, lm_pre;
 
   __device__ __forceinline__ void init(const Params& p, int wg_) {
+    constexpr int AX = GG::AX;
     wg = wg_;
-    a = in_a(wg);
-    rank = a ? wg >> 3 : (wg >> 3) * 7 + (wg & 7) - 1;
+    a = GG::in_a(wg);
+    // group A: rank c KVH + g is chunk c of KV head g (wide: head g on XCD g, chunk c = wg / 8)
+    rank = a ? (wg >> 3) * AX + (wg & 7) : (wg >> 3) * (8 - AX) + (wg & 7) - AX;
     au0 = au1 = xu0 = xu1 = qu0 = qu1 = a0 = a1 = d0 = d1 = q0 = q1 = 0;
     att = g = c = leader = t0 = t1 = ou0 = ou1 = o0 = o1 = 0;
     S = min(max(p.seq_lens[0], 1), p.max_seq);
@@ -172,14 +205,14 @@ struct PlanSR {
       const int tc = old <= 0 ? 16 : ((old + GG::C - 1) / GG::C + 15) / 16 * 16;
       t0 = att ? min(c * tc, old) : 0;
       t1 = att ? min((c + 1) * tc, old) : 0;
-      ou0 = split_lo(GG::HU, AG, rank);
-      ou1 = split_lo(GG::HU, AG, rank + 1);
+      ou0 = split_lo(GG::HU, GG::AG, rank);
+      ou1 = split_lo(GG::HU, GG::AG, rank + 1);
       o0 = ou0 * VPU;
       o1 = min(ou1 * VPU, G::H);
     } else {
-      au0 = split_lo(GG::IU, FG, rank); au1 = split_lo(GG::IU, FG, rank + 1);
-      xu0 = split_lo(GG::HU, FG, rank); xu1 = split_lo(GG::HU, FG, rank + 1);
-      qu0 = split_lo(GG::QU, FG, rank); qu1 = split_lo(GG::QU, FG, rank + 1);
+      au0 = split_lo(GG::IU, GG::FG, rank); au1 = split_lo(GG::IU, GG::FG, rank + 1);
+      xu0 = split_lo(GG::HU, GG::FG, rank); xu1 = split_lo(GG::HU, GG::FG, rank + 1);
+      qu0 = split_lo(GG::QU, GG::FG, rank); qu1 = split_lo(GG::QU, GG::FG, rank + 1);
       a0 = au0 * VPU; a1 = min(au1 * VPU, G::I);
       d0 = xu0 * VPU; d1 = min(xu1 * VPU, G::H);
       q0 = qu0 * VPU; q1 = min(qu1 * VPU, G::QKV);
@@ -191,12 +224,16 @@ struct PlanSR {
       v0 = v1 = 0;
     }
     n_lm = (v1 - v0 + LM_ROWS_SR - 1) / LM_ROWS_SR;
-    // the last bracket: what it streams before the LM-head segments (F: the last layer's MLP)
+    // the last bracket: what it streams before the LM-head segments (F: the last layer's MLP, an
+    // estimate for a lossless stream; a segment that does not fit waits for ring space in any case)
+    constexpr uint32_t WB = GG::WB;
+    constexpr uint32_t SH = G::WF ? uint32_t(scale_stride(G::H)) : 0u, SI = G::WF ? uint32_t(scale_stride(G::I)) : 0u;
     const uint32_t last = a ? pad_pkt(G::H * 2)
-                            : 2 * pad_pkt(G::H * 2) + 2 * pad_pkt(uint32_t(a1 - a0) * G::H * 2) +
-                                  pad_pkt(uint32_t(d1 - d0) * G::I * 2);
+                            : 2 * pad_pkt(G::H * 2) + 2 * pad_pkt(uint32_t(a1 - a0) * G::H * WB) +
+                                  2 * pad_pkt(uint32_t(a1 - a0) * SH) + pad_pkt(uint32_t(d1 - d0) * G::I * WB) +
+                                  pad_pkt(uint32_t(d1 - d0) * SI);
     const uint32_t lmseg = pad_pkt(uint32_t(LM_ROWS_SR) * G::H * 2);
-    lm_pre = min(n_lm, int((RING - last) / lmseg));
+    lm_pre = last >= RING ? 0 : min(n_lm, int((RING - last) / lmseg));
   }
 };
 
@@ -204,25 +241,35 @@ struct PlanSR {
 // rows, up rows, down rows; k >= 1) then norm1 and the QKV rows of layer k (k < L); bracket L ends
 // with the final-norm weights and the LM-head segments.  Group A, bracket k < L: the KV chunk and
 // the O rows of layer k; bracket L: the final-norm weights and the LM-head segments.
-enum SRSeg { R_NORM2, R_GATE, R_GATE_H, R_GATE_R, R_UP, R_UP_H, R_UP_R, R_DOWN, R_NORM1, R_QKV, R_KV, R_O, R_FNORM, R_LM };
+// MXFP8 weights: every weight segment (gate, up, down, QKV, O) is followed by its scale rows (the _S
+// segments, scale_stride(K) bytes per row; empty for bf16 weights).
+enum SRSeg { R_NORM2, R_GATE, R_GATE_S, R_GATE_H, R_GATE_R, R_UP, R_UP_S, R_UP_H, R_UP_R, R_DOWN, R_DOWN_S,
+             R_NORM1, R_QKV, R_QKV_S, R_KV, R_O, R_O_S, R_FNORM, R_LM };
 
 template <class G>
 __device__ __forceinline__ uint32_t sr_bytes(const PlanSR<G>& P, int kind, int lm_index, const GUE* e = nullptr) {
   const bool enc = e != nullptr && e->on != 0u;  // this layer's gate/up through the lossless codec
+  constexpr uint32_t WB = SG<G>::WB;
+  constexpr uint32_t SH = G::WF ? uint32_t(scale_stride(G::H)) : 0u, SI = G::WF ? uint32_t(scale_stride(G::I)) : 0u;
   switch (kind) {
     case R_NORM2:
     case R_NORM1:
     case R_FNORM: return G::H * 2;
+    case R_GATE_S:
+    case R_UP_S: return uint32_t(P.a1 - P.a0) * SH;
+    case R_DOWN_S: return uint32_t(P.d1 - P.d0) * SI;
+    case R_QKV_S: return uint32_t(P.q1 - P.q0) * SH;
+    case R_O_S: return uint32_t(P.o1 - P.o0) * SH;
     case R_GATE:
-    case R_UP: return uint32_t(P.a1 - P.a0) * G::H * (enc ? 1u : 2u);  // plane rows: 1 byte per weight
+    case R_UP: return uint32_t(P.a1 - P.a0) * G::H * (enc ? 1u : WB);  // plane rows: 1 byte per weight
     case R_GATE_H:
     case R_UP_H: return enc ? uint32_t(P.a1 - P.a0) * (G::H / 8) * 4u : 0u;  // one header per 8 weights
     case R_GATE_R: return enc ? e->cnt[0] * 16u : 0u;                      // the rows' escaped chunks
     case R_UP_R: return enc ? e->cnt[1] * 16u : 0u;
-    case R_DOWN: return uint32_t(P.d1 - P.d0) * G::I * 2;
-    case R_QKV: return uint32_t(P.q1 - P.q0) * G::H * 2;
+    case R_DOWN: return uint32_t(P.d1 - P.d0) * G::I * WB;
+    case R_QKV: return uint32_t(P.q1 - P.q0) * G::H * WB;
     case R_KV: return uint32_t(P.t1 - P.t0) * 256u;
-    case R_O: return uint32_t(P.o1 - P.o0) * G::H * 2;
+    case R_O: return uint32_t(P.o1 - P.o0) * G::H * WB;
     default: {
       const int r0 = P.v0 + lm_index * LM_ROWS_SR;
       return uint32_t(min(LM_ROWS_SR, P.v1 - r0)) * G::H * 2;
@@ -251,12 +298,12 @@ struct SmemSR {
   LayerW lw[G::L];
   GUE gue[G::L];                 // group F: each layer's lossless gate/up stream of this workgroup
   const void* kvp[G::L];
-  int32_t blk[TCS / 16 + 2];
+  int32_t blk[SG<G>::TCS / 16 + 2];
   float lm_val[NCW];
   int32_t lm_idx[NCW];
   alignas(16) uint32_t front[NPW];
   alignas(16) uint32_t zero16[4];  // a 16-byte zero line: what lanes past the end of a row read
-  float part[NCW][8];              // per-wave partial results combined across the waves
+  float part[SG<G>::NPART][8];     // per-wave (per-item) partial results combined across the waves
   uint32_t consumed[NCW];
   uint32_t cbar;
   uint32_t go;                   // brackets the consumers have finished
@@ -295,21 +342,28 @@ __device__ __forceinline__ void producer_sr(const Params& p, const PlanSR<G>& P,
     const uint8_t* cache = nullptr;
     auto u8 = [](const void* q) { return reinterpret_cast<const uint8_t*>(q); };
     const LayerW& Lw = sm.lw[layer];
+    constexpr size_t WB = SG<G>::WB;
+    constexpr size_t SH = scale_stride(G::H), SI = scale_stride(G::I);
     switch (kind) {
       case R_NORM2: base = u8(Lw.norm2); break;
-      case R_GATE: base = ge->on ? ge->plane + size_t(P.a0) * G::H : u8(Lw.gate_up) + size_t(P.a0) * G::H * 2; break;
+      case R_GATE: base = ge->on ? ge->plane + size_t(P.a0) * G::H : u8(Lw.gate_up) + size_t(P.a0) * G::H * WB; break;
+      case R_GATE_S: base = Lw.gate_up_s + size_t(P.a0) * SH; break;
       case R_GATE_H: base = u8(ge->hdr + size_t(P.a0) * (G::H / 8)); break;
       case R_GATE_R: base = u8(ge->raw + size_t(ge->first[0]) * 8); break;
       case R_UP:
-        base = ge->on ? ge->plane + size_t(G::I + P.a0) * G::H : u8(Lw.gate_up) + size_t(G::I + P.a0) * G::H * 2;
+        base = ge->on ? ge->plane + size_t(G::I + P.a0) * G::H : u8(Lw.gate_up) + size_t(G::I + P.a0) * G::H * WB;
         break;
+      case R_UP_S: base = Lw.gate_up_s + size_t(G::I + P.a0) * SH; break;
       case R_UP_H: base = u8(ge->hdr + size_t(G::I + P.a0) * (G::H / 8)); break;
       case R_UP_R: base = u8(ge->raw + size_t(ge->first[1]) * 8); break;
-      case R_DOWN: base = u8(Lw.down) + size_t(P.d0) * G::I * 2; break;
+      case R_DOWN: base = u8(Lw.down) + size_t(P.d0) * G::I * WB; break;
+      case R_DOWN_S: base = Lw.down_s + size_t(P.d0) * SI; break;
       case R_NORM1: base = u8(Lw.norm1); break;
-      case R_QKV: break;  // rows gathered in slot order below
+      case R_QKV:
+      case R_QKV_S: break;  // rows gathered in slot order below
       case R_KV: cache = u8(sm.kvp[layer]); break;
-      case R_O: base = u8(Lw.o) + size_t(P.o0) * G::H * 2; break;
+      case R_O: base = u8(Lw.o) + size_t(P.o0) * G::H * WB; break;
+      case R_O_S: base = Lw.o_s + size_t(P.o0) * SH; break;
       case R_FNORM: base = u8(p.final_norm); break;
       default: base = u8(p.embed) + size_t(P.v0 + lm_index * LM_ROWS_SR) * G::H * 2; break;
     }
@@ -340,10 +394,11 @@ __device__ __forceinline__ void producer_sr(const Params& p, const PlanSR<G>& P,
         const long long e = (long long)blk * p.block_stride + (long long)(t & 15) * p.token_stride +
                             (long long)P.g * p.head_stride + (piece ? p.v_off : p.k_off) + part * 8;
         src = cache + e * 2;
-      } else if (kind == R_QKV) {
-        // rows in slot order (qkv_row): byte `off` of the segment is in row q0 + off / (2 H)
-        const uint32_t ri = off / uint32_t(G::H * 2), cb = off - ri * uint32_t(G::H * 2);
-        src = u8(Lw.qkv) + size_t(qkv_row<G>(P.q0 + int(ri))) * G::H * 2 + cb;
+      } else if (kind == R_QKV || kind == R_QKV_S) {
+        // rows in slot order (qkv_row): byte `off` of the segment is in row q0 + off / (row bytes)
+        const uint32_t rb = kind == R_QKV ? uint32_t(G::H * WB) : uint32_t(SH);
+        const uint32_t ri = off / rb, cb = off - ri * rb;
+        src = (kind == R_QKV ? u8(Lw.qkv) : Lw.qkv_s) + size_t(qkv_row<G>(P.q0 + int(ri))) * rb + cb;
       } else {
         src = base + off;
       }
@@ -368,6 +423,7 @@ __device__ __forceinline__ void producer_sr(const Params& p, const PlanSR<G>& P,
       if (k < L) {
         issue(R_KV, k, 0);
         issue(R_O, k, 0);
+        issue(R_O_S, k, 0);
       } else {
         issue(R_FNORM, 0, 0);
       }
@@ -375,16 +431,20 @@ __device__ __forceinline__ void producer_sr(const Params& p, const PlanSR<G>& P,
       if (k > 0) {
         issue(R_NORM2, k - 1, 0);
         issue(R_GATE, k - 1, 0);
+        issue(R_GATE_S, k - 1, 0);
         issue(R_GATE_H, k - 1, 0);
         issue(R_GATE_R, k - 1, 0);
         issue(R_UP, k - 1, 0);
+        issue(R_UP_S, k - 1, 0);
         issue(R_UP_H, k - 1, 0);
         issue(R_UP_R, k - 1, 0);
         issue(R_DOWN, k - 1, 0);
+        issue(R_DOWN_S, k - 1, 0);
       }
       if (k < L) {
         issue(R_NORM1, k, 0);
         issue(R_QKV, k, 0);
+        issue(R_QKV_S, k, 0);
       } else {
         issue(R_FNORM, 0, 0);
       }
@@ -504,7 +564,8 @@ struct CSR {
   }
 
   // Poll n units, unit i at byte offset off(i) of resource r, spread over `nthr` threads starting
-  // at thread `tid` (at most MAXU per thread); use(i, unit) for each once its tag is current.
+  // at thread `tid` (at most MAXU per thread); use(i, unit) for each once its tag is current, or
+  // use(i, unit, k) with the thread's slot k (i = tid + k nthr) when `use` takes three arguments.
   template <int MAXU, class OFF, class USE>
   __device__ __forceinline__ void poll(__amdgpu_buffer_rsrc_t r, int n, int tid, int nthr, OFF off, USE use, int site) {
     u32x4 v[MAXU];
@@ -519,7 +580,8 @@ struct CSR {
 #pragma unroll
       for (int k = 0; k < MAXU; ++k)
         if (((pend >> k) & 1u) && v[k].w == tag) {
-          use(tid + k * nthr, v[k]);
+          if constexpr (std::is_invocable_v<USE, int, const u32x4&, int>) use(tid + k * nthr, v[k], k);
+          else use(tid + k * nthr, v[k]);
           pend &= ~(1u << k);
         }
       if (!pend) break;
@@ -568,6 +630,45 @@ __device__ __forceinline__ void ring_rows(const CT& C, uint32_t seg, int r0, uin
       const uint32_t at = seg + uint32_t(r0 + r) * uint32_t(K * 2) + uint32_t(C.lane + 64 * c) * 16u;
       w[r][c] = c == CPL - 1 ? C.ring16z(at, tail_ok) : C.ring16(at);
     }
+}
+
+// 8 e4m3 weights with their e8m0 scale code as the bf16 words of the dense path: bf16(e4m3 *
+// 2^(s-127)) per weight (v_cvt_scalef32_pk_bf16_fp8, two weights per conversion).
+__device__ __forceinline__ uint4 deq8(uint2 q, uint32_t s) {
+  const float f = e8m0_f32(s);
+  return make_uint4(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(int(q.x), f, false)),
+                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(int(q.x), f, true)),
+                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(int(q.y), f, false)),
+                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(int(q.y), f, true)));
+}
+
+// ring_rows for the model's weight format: MXFP8 rows (K e4m3 bytes per row in `seg`, scale_stride(K)
+// scale bytes per row in `segs`) become the bf16 words ring_rows would return for the dequantised
+// matrix; lanes past a row's last chunk get zeros (weights 0 with scale 2^0).
+template <class G, int K, int N, class CT>
+__device__ __forceinline__ void wrows(const CT& C, uint32_t seg, uint32_t segs, int r0, uint4 (&w)[N][Chunks<K>::CPL]) {
+  if constexpr (G::WF == 0) {
+    ring_rows<K, N>(C, seg, r0, w);
+  } else {
+    constexpr int CPL = Chunks<K>::CPL, CH = Chunks<K>::CH;
+    constexpr uint32_t SK = scale_stride(K);
+    const bool tail_ok = CH % 64 == 0 || C.lane + 64 * (CPL - 1) < CH;
+    uint2 q[N][CPL];
+    uint32_t sc[N][CPL];
+#pragma unroll
+    for (int r = 0; r < N; ++r)
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const uint32_t row = uint32_t(r0 + r), ch = uint32_t(C.lane + 64 * c);
+        const bool ok = c < CPL - 1 || tail_ok;
+        q[r][c] = ok ? C.ring8(seg + row * uint32_t(K) + ch * 8u) : make_uint2(0u, 0u);
+        sc[r][c] = ok ? uint32_t(C.sm.ring[(segs + row * SK + (ch >> 2)) & (RING - 1)]) : 127u;
+      }
+#pragma unroll
+    for (int r = 0; r < N; ++r)
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) w[r][c] = deq8(q[r][c], sc[r][c]);
+  }
 }
 
 // The same chunks rebuilt from a lossless segment set: plane rows (K bytes each) at segp, header rows
@@ -656,6 +757,32 @@ __device__ __forceinline__ void quarter_rows(const CT& C, uint32_t seg, int r0, 
       w[r][c] = c == Q::CPL - 1 ? C.ring16z(at, tail_ok) : C.ring16(at);
     }
 }
+// quarter_rows for the model's weight format (MXFP8 as in wrows).
+template <class G, int K, int N, class CT>
+__device__ __forceinline__ void wquarter(const CT& C, uint32_t seg, uint32_t segs, int r0, uint4 (&w)[N][Quarter<K>::CPL]) {
+  using Q = Quarter<K>;
+  if constexpr (G::WF == 0) {
+    quarter_rows<K, N>(C, seg, r0, w);
+  } else {
+    constexpr uint32_t SK = scale_stride(K);
+    const bool tail_ok = Q::CHW % 64 == 0 || C.lane + 64 * (Q::CPL - 1) < Q::CHW;
+    uint2 q[N][Q::CPL];
+    uint32_t sc[N][Q::CPL];
+#pragma unroll
+    for (int r = 0; r < N; ++r)
+#pragma unroll
+      for (int c = 0; c < Q::CPL; ++c) {
+        const uint32_t row = uint32_t(r0 + r), ch = uint32_t(C.cw * Q::CHW + C.lane + 64 * c);
+        const bool ok = c < Q::CPL - 1 || tail_ok;
+        q[r][c] = ok ? C.ring8(seg + row * uint32_t(K) + ch * 8u) : make_uint2(0u, 0u);
+        sc[r][c] = ok ? uint32_t(C.sm.ring[(segs + row * SK + (ch >> 2)) & (RING - 1)]) : 127u;
+      }
+#pragma unroll
+    for (int r = 0; r < N; ++r)
+#pragma unroll
+      for (int c = 0; c < Q::CPL; ++c) w[r][c] = deq8(q[r][c], sc[r][c]);
+  }
+}
 template <int K, int N>
 __device__ __forceinline__ void dots_quarter_w(const uint4 (&w)[N][Quarter<K>::CPL], const uint4 (&x)[Quarter<K>::CPL],
                                                float (&out)[N]) {
@@ -690,7 +817,6 @@ __device__ __forceinline__ void normw(const CT& C, XChunks<K, 8>& nw, uint32_t s
 // ------------------------------------------------------------------------------------------------
 
 // 16-token tiles of a chunk, tile t to wave t % NCW: at most MT per wave
-constexpr int MT = (TCS + 1 + 16 * NCW - 1) / (16 * NCW);
 struct ChunkRegs {
   uint32_t va[MT][4][2];    // V of the wave's tiles: A operands of the P.V tiles (bf16 pairs)
 };
@@ -943,7 +1069,7 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
     // unit i = 2k + s (k = NCW c' + v) is polled by lane i % 64: an even lane the maxima of one
     // (chunk, wave), the odd lane next to it the sums of the same one
     constexpr int NU = 2 * NCW * S::C, MU = (NU + 63) / 64;
-    static_assert(MU <= 2, "two statistics units per lane at most");
+    static_assert(MU <= 4, "four statistics units per lane at most");
     float st[MU][3];
 #pragma unroll
     for (int k = 0; k < MU; ++k)
@@ -954,31 +1080,58 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
                           const int pr = i >> 1, c = pr / NCW, v = pr - c * NCW;
                           return W::loc(l, W::STAT_U + (size_t(g + G::KVH * c) * NCW + v) * 2 + (i & 1));
                         },
-                        [&](int i, const u32x4& v) {
-                          const float a = __uint_as_float(v.x), b = __uint_as_float(v.y), c = __uint_as_float(v.z);
-                          if (MU == 1 || i < 64) { st[0][0] = a; st[0][1] = b; st[0][2] = c; }
-                          else { st[MU - 1][0] = a; st[MU - 1][1] = b; st[MU - 1][2] = c; }
+                        [&](int, const u32x4& v, int k) {
+                          st[k][0] = __uint_as_float(v.x);
+                          st[k][1] = __uint_as_float(v.y);
+                          st[k][2] = __uint_as_float(v.z);
                         },
                         31);
-    // combine in one pass: the odd lane of each pair takes its (chunk, wave)'s maxima from the even lane
-    float m[MU][3], M[3] = {-INFINITY, -INFINITY, -INFINITY}, sum[3];
+    // Merge with the association of a two-level merge (the waves of each chunk, then the chunks), so
+    // the sums round as they did when each chunk combined its waves before the exchange, all in DPP
+    // moves.  Lanes 8j .. 8j + 7 of slot k hold the four waves of chunk c = 8k + j (an even lane the
+    // maxima, the odd one the sums); chunk c: m_c = max_v m_cv, l_c = (e_c0 + e_c1) + (e_c2 + e_c3)
+    // with e_cv = l_cv exp(m_cv - m_c), in lane 8j + 1; then a_c = l_c exp(m_c - M) and per slot
+    // T_k = ((a7 + a6) + (a5 + a4)) + ((a3 + a2) + (a1 + a0)) over its eight chunks, L the T_k added
+    // pairwise.  With up to 8 chunks this is the sum a 64-lane scan gives with a_c in lane 2c + 1, and
+    // up to 16 chunks the same with the chunks past 8 added last.
+    float mc[MU][3], lc[MU][3], M[3] = {-INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
     for (int k = 0; k < MU; ++k)
 #pragma unroll
       for (int h = 0; h < 3; ++h) {
-        const float mo = __shfl_xor(st[k][h], 1);
-        m[k][h] = (lane & 1) ? mo : st[k][h];
-        M[h] = fmaxf(M[h], m[k][h]);
+        const float mo = dpp<0xb1>(0.f, st[k][h]);                 // quad_perm [1,0,3,2]: the pair's other lane
+        const float m = (lane & 1) ? mo : st[k][h];
+        float x = fmaxf(m, dpp<0x4e>(m, m));                      // quad_perm [2,3,0,1]: waves v, v ^ 1
+        x = fmaxf(x, dpp<0x141>(x, x));                            // row_half_mirror: the other quad
+        mc[k][h] = x;
+        M[h] = fmaxf(M[h], x);
+        float e = ((lane & 1) && lane + 64 * k < NU && m != -INFINITY) ? st[k][h] * __expf(m - x) : 0.f;
+        e += dpp<0x4e>(0.f, e);                                    // odd lanes: e_c0 + e_c1, e_c2 + e_c3
+        e += dpp<0xb1>(0.f, e);                                    // ... copied into the even lanes
+        e += dpp<0x141>(0.f, e);                                   // lane 8j + 1: (e_c0 + e_c1) + (e_c2 + e_c3)
+        lc[k][h] = e;
       }
     wave_max_n<3>(M);
+    float T[MU][3];
+#pragma unroll
+    for (int k = 0; k < MU; ++k)
+#pragma unroll
+      for (int h = 0; h < 3; ++h) {
+        float a = ((lane & 7) == 1 && mc[k][h] != -INFINITY) ? lc[k][h] * __expf(mc[k][h] - M[h]) : 0.f;
+        a += dpp<0x118>(0.f, a);                                   // row_shr:8: lane 16r + 9 = a_{2r+1} + a_{2r}
+        a = dpp<0x116>(0.f, a);                                    // row_shr:6: ... into lane 16r + 15
+        a += dpp<0x142, 0xa>(0.f, a);                              // row_bcast:15 into rows 1, 3
+        a += dpp<0x143, 0xc>(0.f, a);                              // row_bcast:31 into rows 2, 3
+        T[k][h] = lane63(a);
+      }
+    float sum[3];
 #pragma unroll
     for (int h = 0; h < 3; ++h) {
-      sum[h] = 0.f;
-#pragma unroll
-      for (int k = 0; k < MU; ++k)
-        sum[h] += ((lane & 1) && lane + 64 * k < NU && m[k][h] != -INFINITY) ? st[k][h] * __expf(m[k][h] - M[h]) : 0.f;
+      if constexpr (MU == 1) sum[h] = T[0][h];
+      else if constexpr (MU == 2) sum[h] = T[1][h] + T[0][h];
+      else if constexpr (MU == 3) sum[h] = T[2][h] + (T[1][h] + T[0][h]);
+      else sum[h] = (T[3][h] + T[2][h]) + (T[1][h] + T[0][h]);
     }
-    wave_sum_n<3>(sum);
 #pragma unroll
     for (int h = 0; h < 3; ++h) { Mh[h] = M[h]; Lh[h] = sum[h]; }
   }
@@ -1060,6 +1213,22 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
       *reinterpret_cast<float4*>(&sm.wo[w][hq][16 * mf + 4 * pq]) = make_float4(oacc[mf][0], oacc[mf][1], oacc[mf][2], oacc[mf][3]);
   C.cbar();
   if (w == 0 && lane == 0) trace_at(p, l, 19, p.n_layers);
+  if constexpr (S::WIDE) {
+    // the chunk's 192 partial sums (3 heads x 64 dims, each added over the waves in wave order, fp32),
+    // lane t of wave 0 publishing unit t = values 3t .. 3t + 2
+    if (w == 0) {
+      float f[3];
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        const int v = 3 * lane + k, h = v >> 6, d = v & 63;
+        f[k] = ((sm.wo[0][h][d] + sm.wo[1][h][d]) + sm.wo[2][h][d]) + sm.wo[3][h][d];
+      }
+      C.put_loc(l, W::PART_U + size_t(P.rank) * S::PUC + lane,
+                u32x4{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), C.tag});
+    }
+    if (w == 0 && lane == 0) trace_at(p, l, 20, p.n_layers);
+    return;
+  }
   // wave h < 3: head 3g + h.  The chunk's partial sum of p.v in fixed wave order, fp32.
   float O = 0.f;
   if (w < 3) {
@@ -1071,7 +1240,7 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
     // the O projection add the chunks' partials of each head in chunk order.
     const float f1 = __shfl_down(O, 1), f2 = __shfl_down(O, 2);
     if (lane % 3 == 0)
-      C.put_loc(l, W::PART_U + (size_t(P.rank) * 3 + w) * S::PU + lane / 3,
+      C.put_loc(l, W::PART_U + size_t(P.rank) * S::PUC + size_t(w) * S::PU + lane / 3,
                 u32x4{__float_as_uint(O), __float_as_uint(lane + 1 < 64 ? f1 : 0.f),
                       __float_as_uint(lane + 2 < 64 ? f2 : 0.f), C.tag});
   }
@@ -1130,6 +1299,43 @@ __device__ __forceinline__ void attention_vector(CSR<G>& C, int l) {
   };
   settle(v0, b0, hu0);
   if (R > 1) settle(v1, b1, hu1);
+}
+
+// Wide layout: slice c of KV head g's attention values (values 6c .. 6c + 5 of its 3 heads x 64
+// dims): the 32 chunks' partial sums added in chunk order in fp32 and rounded to bf16 once (HF's
+// bf16(p.v)), published as unit 32 g + c of the cross-XCD attention vector.  Wave 0: lane i polls
+// unit 2c + (i & 1) of chunk i >> 1's record, the sums run over LDS.
+template <class G>
+__device__ __forceinline__ void attention_slice(CSR<G>& C, int l) {
+  using S = SG<G>;
+  using W = SWS<G>;
+  static_assert(S::WIDE && 2 * S::C <= 64 && S::C * 6 <= NCW * 3 * 64, "one poll per lane; the slices fit sm.wo");
+  const PlanSR<G>& P = C.P;
+  if (C.cw != 0) return;
+  const int lane = C.lane;
+  float* flat = &C.sm.wo[0][0][0];  // [chunk][6]
+  C.template poll<1>(C.rl, 2 * S::C, lane, 64,
+                     [&](int i) {
+                       return W::loc(l, W::PART_U + size_t(P.g + G::KVH * (i >> 1)) * S::PUC + size_t(2 * P.c + (i & 1)));
+                     },
+                     [&](int i, const u32x4& v) {
+                       float* d = flat + (i >> 1) * 6 + (i & 1) * 3;
+                       d[0] = __uint_as_float(v.x);
+                       d[1] = __uint_as_float(v.y);
+                       d[2] = __uint_as_float(v.z);
+                     },
+                     37);
+  wait_lgkm0();
+  __builtin_amdgcn_wave_barrier();
+  float t = 0.f;
+  if (lane < VPU)
+#pragma unroll 8
+    for (int j = 0; j < S::C; ++j) t += flat[j * 6 + lane];
+  const float b = rnd(t);
+  float a[VPU];
+#pragma unroll
+  for (int k = 0; k < VPU; ++k) a[k] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, b), k));
+  if (lane == 0) C.put_x(K_ATT, l, S::C * P.g + P.c, C.unit6(a));
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1238,16 +1444,19 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
       const GUE& ge = sm.gue[l];
       const uint32_t segn = C.next_seg(sr_bytes(P, R_NORM2, 0));
       const uint32_t segg = C.next_seg(sr_bytes(P, R_GATE, 0, &ge));
+      const uint32_t segg_s = C.next_seg(sr_bytes(P, R_GATE_S, 0));
       const uint32_t segg_h = C.next_seg(sr_bytes(P, R_GATE_H, 0, &ge));
       const uint32_t segg_r = C.next_seg(sr_bytes(P, R_GATE_R, 0, &ge));
       const uint32_t segu = C.next_seg(sr_bytes(P, R_UP, 0, &ge));
+      const uint32_t segu_s = C.next_seg(sr_bytes(P, R_UP_S, 0));
       const uint32_t segu_h = C.next_seg(sr_bytes(P, R_UP_H, 0, &ge));
       const uint32_t segu_r = C.next_seg(sr_bytes(P, R_UP_R, 0, &ge));
       C.wait_filled(C.pos);
       XChunks<G::H, 8> nw;
       normw<G::H>(C, nw, segn);
-      // gate rows of units 0 .. n-1, then up rows of the same units: one 6-row item per wave.  The
-      // item's weights go from the ring into registers before h1 arrives.
+      // items: the gate rows of units 0 .. n-1, then the up rows of the same units, 6 rows each;
+      // wave w takes items w, w + NCW, ...  Its first item's weights go from the ring into registers
+      // before h1 arrives, the others (wide layout) are read after.
       const int nunits = P.au1 - P.au0;
       const bool item = C.cw < 2 * nunits;
       uint4 w[VPU][Chunks<G::H>::CPL];
@@ -1257,7 +1466,7 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
           lossless_rows<G::H, VPU>(C, m ? segu : segg, m ? segu_h : segg_h, m ? segu_r : segg_r, ge.first[m],
                                    j * VPU, w);
         else
-          ring_rows<G::H, VPU>(C, m ? segu : segg, j * VPU, w);
+          wrows<G, G::H, VPU>(C, m ? segu : segg, m ? segu_s : segg_s, j * VPU, w);
       }
       tr(l, 9);
       const float ss = C.template poll_vec<1>(K_H1, l, G::H, sm.xs, sm.keep, 40);
@@ -1274,20 +1483,42 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
 #pragma unroll
             for (int e = 0; e < VPU; ++e) sm.part[C.cw][e] = o[e];
         }
+        if constexpr (S::NIT > 1) {
+#pragma unroll
+          for (int k2 = 1; k2 < S::NIT; ++k2) {
+            const int it = C.cw + NCW * k2;
+            if (it < 2 * nunits) {
+              const int m = it < nunits ? 0 : 1, j = it - m * nunits;
+              if (ge.on)
+                lossless_rows<G::H, VPU>(C, m ? segu : segg, m ? segu_h : segg_h, m ? segu_r : segg_r, ge.first[m],
+                                         j * VPU, w);
+              else
+                wrows<G, G::H, VPU>(C, m ? segu : segg, m ? segu_s : segg_s, j * VPU, w);
+              float o[VPU];
+              dots_w<G::H, VPU>(w, x, o);
+              if (C.lane == 0)
+#pragma unroll
+                for (int e = 0; e < VPU; ++e) sm.part[it][e] = o[e];
+            }
+          }
+        }
         tr(l, 22);
         C.cbar();
         tr(l, 23);
-        if (C.cw < nunits) {
-          // lane e < 6 forms value e of unit cw, silu(bf16(gate)) * bf16(up); lane 0 stores the unit
+        // unit j (wave j % NCW): lane e < 6 forms value e, silu(bf16(gate)) * bf16(up); lane 0 stores it
+        auto swiglu = [&](int j) {
           const int e = min(C.lane, VPU - 1);
-          const float gv = rnd(sm.part[C.cw][e]), uv = rnd(sm.part[nunits + C.cw][e]);
+          const float gv = rnd(sm.part[j][e]), uv = rnd(sm.part[nunits + j][e]);
           const float act = rnd(gv / (1.0f + expf(-gv))) * uv;
           float a[VPU];
 #pragma unroll
           for (int k = 0; k < VPU; ++k)
             a[k] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, act), k));
-          if (C.lane == 0) C.put_x(K_ACT, l, P.au0 + C.cw, C.unit6(a));
-        }
+          if (C.lane == 0) C.put_x(K_ACT, l, P.au0 + j, C.unit6(a));
+        };
+        if (C.cw < nunits) swiglu(C.cw);
+        if constexpr (S::NAU > NCW)
+          if (C.cw + NCW < nunits) swiglu(C.cw + NCW);
         tr(l, 24);
       }
       C.release(C.pos);
@@ -1295,50 +1526,108 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
       // ---- down + residual of layer l -> x_{l+1} ----
       C.refresh();
       const uint32_t segd = C.next_seg(sr_bytes(P, R_DOWN, 0));
+      const uint32_t segd_s = C.next_seg(sr_bytes(P, R_DOWN_S, 0));
       C.wait_filled(C.pos);
-      const bool has_down = P.xu1 > P.xu0;  // workgroups without down rows do not need act
-      // each wave: its quarter of K for the unit's 6 rows, weights into registers before act arrives;
-      // the quarters are added in wave order
-      using Q = Quarter<G::I>;
-      uint4 wd[VPU][Q::CPL];
-      if (has_down) quarter_rows<G::I, VPU>(C, segd, 0, wd);
-      if (has_down) C.template poll_vec<2>(K_ACT, l, G::I, sm.xs, nullptr, 41);
-      C.cbar();
-      tr(l, 13);
-      if (has_down) {
-        uint4 xq[Q::CPL];
-#pragma unroll
-        for (int c = 0; c < Q::CPL; ++c) {
-          const int cq = C.lane + 64 * c;
-          const float* src = sm.xs + (C.cw * Q::CHW + min(cq, Q::CHW - 1)) * 8;
-          const float4 a = *reinterpret_cast<const float4*>(src);
-          const float4 b = *reinterpret_cast<const float4*>(src + 4);
-          const bool ok = cq < Q::CHW;
-          xq[c] = make_uint4(ok ? pack2(a.x, a.y) : 0u, ok ? pack2(a.z, a.w) : 0u, ok ? pack2(b.x, b.y) : 0u,
-                             ok ? pack2(b.z, b.w) : 0u);
-        }
-        tr(l, 28);
-        float od[VPU];
-        dots_quarter_w<G::I, VPU>(wd, xq, od);
-        if (C.lane == 0)
-#pragma unroll
-          for (int e = 0; e < VPU; ++e) sm.part[C.cw][e] = od[e];
+      if constexpr (S::NXU == 1) {
+        const bool has_down = P.xu1 > P.xu0;  // workgroups without down rows do not need act
+        // each wave: its quarter of K for the unit's 6 rows, weights into registers before act arrives;
+        // the quarters are added in wave order
+        using Q = Quarter<G::I>;
+        uint4 wd[VPU][Q::CPL];
+        if (has_down) wquarter<G, G::I, VPU>(C, segd, segd_s, 0, wd);
+        if (has_down) C.template poll_vec<2>(K_ACT, l, G::I, sm.xs, nullptr, 41);
         C.cbar();
-        tr(l, 29);
-        if (C.cw == 0) {
-          float y[VPU];
+        tr(l, 13);
+        if (has_down) {
+          uint4 xq[Q::CPL];
 #pragma unroll
-          for (int e = 0; e < VPU; ++e) {
-            const float d = ((sm.part[0][e] + sm.part[1][e]) + sm.part[2][e]) + sm.part[3][e];
-            const int r = min(P.d0 + e, G::H - 1);
-            y[e] = rnd(sm.keep[r] + rnd(d));
+          for (int c = 0; c < Q::CPL; ++c) {
+            const int cq = C.lane + 64 * c;
+            const float* src = sm.xs + (C.cw * Q::CHW + min(cq, Q::CHW - 1)) * 8;
+            const float4 a = *reinterpret_cast<const float4*>(src);
+            const float4 b = *reinterpret_cast<const float4*>(src + 4);
+            const bool ok = cq < Q::CHW;
+            xq[c] = make_uint4(ok ? pack2(a.x, a.y) : 0u, ok ? pack2(a.z, a.w) : 0u, ok ? pack2(b.x, b.y) : 0u,
+                               ok ? pack2(b.z, b.w) : 0u);
           }
-          if (C.lane == 0) C.put_x(K_X, l + 1, P.xu0, C.unit6(y));
-          if (p.layer_outputs && C.lane < VPU && P.d0 + C.lane < G::H) {
-            float yl = y[0];
+          tr(l, 28);
+          float od[VPU];
+          dots_quarter_w<G::I, VPU>(wd, xq, od);
+          if (C.lane == 0)
 #pragma unroll
-            for (int e = 1; e < VPU; ++e) yl = C.lane == e ? y[e] : yl;
-            p.layer_outputs[size_t(l) * G::H + P.d0 + C.lane] = uint16_t(f2bf(yl));
+            for (int e = 0; e < VPU; ++e) sm.part[C.cw][e] = od[e];
+          C.cbar();
+          tr(l, 29);
+          if (C.cw == 0) {
+            float y[VPU];
+#pragma unroll
+            for (int e = 0; e < VPU; ++e) {
+              const float d = ((sm.part[0][e] + sm.part[1][e]) + sm.part[2][e]) + sm.part[3][e];
+              const int r = min(P.d0 + e, G::H - 1);
+              y[e] = rnd(sm.keep[r] + rnd(d));
+            }
+            if (C.lane == 0) C.put_x(K_X, l + 1, P.xu0, C.unit6(y));
+            if (p.layer_outputs && C.lane < VPU && P.d0 + C.lane < G::H) {
+              float yl = y[0];
+#pragma unroll
+              for (int e = 1; e < VPU; ++e) yl = C.lane == e ? y[e] : yl;
+              p.layer_outputs[size_t(l) * G::H + P.d0 + C.lane] = uint16_t(f2bf(yl));
+            }
+          }
+        }
+      } else {
+        const int nx = P.xu1 - P.xu0;  // workgroups without down rows do not need act
+        // each wave: its quarter of K for every unit's 6 rows, the first unit's weights in registers
+        // before act arrives; the quarters are added in wave order
+        using Q = Quarter<G::I>;
+        uint4 wd[VPU][Q::CPL];
+        if (nx > 0) wquarter<G, G::I, VPU>(C, segd, segd_s, 0, wd);
+        if (nx > 0) C.template poll_vec<2>(K_ACT, l, G::I, sm.xs, nullptr, 41);
+        C.cbar();
+        tr(l, 13);
+        if (nx > 0) {
+          uint4 xq[Q::CPL];
+#pragma unroll
+          for (int c = 0; c < Q::CPL; ++c) {
+            const int cq = C.lane + 64 * c;
+            const float* src = sm.xs + (C.cw * Q::CHW + min(cq, Q::CHW - 1)) * 8;
+            const float4 a = *reinterpret_cast<const float4*>(src);
+            const float4 b = *reinterpret_cast<const float4*>(src + 4);
+            const bool ok = cq < Q::CHW;
+            xq[c] = make_uint4(ok ? pack2(a.x, a.y) : 0u, ok ? pack2(a.z, a.w) : 0u, ok ? pack2(b.x, b.y) : 0u,
+                               ok ? pack2(b.z, b.w) : 0u);
+          }
+          tr(l, 28);
+#pragma unroll
+          for (int u = 0; u < S::NXU; ++u) {
+            if (u >= nx) break;
+            if (u > 0) wquarter<G, G::I, VPU>(C, segd, segd_s, u * VPU, wd);
+            float od[VPU];
+            dots_quarter_w<G::I, VPU>(wd, xq, od);
+            if (C.lane == 0)
+#pragma unroll
+              for (int e = 0; e < VPU; ++e) sm.part[u * NCW + C.cw][e] = od[e];
+          }
+          C.cbar();
+          tr(l, 29);
+          if (C.cw < nx) {
+            const int u = C.cw;
+            float y[VPU];
+#pragma unroll
+            for (int e = 0; e < VPU; ++e) {
+              const float* q = &sm.part[u * NCW][e];
+              const float d = ((q[0] + q[8]) + q[16]) + q[24];  // the four waves' quarters, in wave order
+              const int r = min(P.d0 + u * VPU + e, G::H - 1);
+              y[e] = rnd(sm.keep[r] + rnd(d));
+            }
+            if (C.lane == 0) C.put_x(K_X, l + 1, P.xu0 + u, C.unit6(y));
+            const int r0 = P.d0 + u * VPU;
+            if (p.layer_outputs && C.lane < VPU && r0 + C.lane < G::H) {
+              float yl = y[0];
+#pragma unroll
+              for (int e = 1; e < VPU; ++e) yl = C.lane == e ? y[e] : yl;
+              p.layer_outputs[size_t(l) * G::H + r0 + C.lane] = uint16_t(f2bf(yl));
+            }
           }
         }
       }
@@ -1351,13 +1640,14 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
     C.refresh();
     const uint32_t segn = C.next_seg(sr_bytes(P, R_NORM1, 0));
     const uint32_t segq = C.next_seg(sr_bytes(P, R_QKV, 0));
+    const uint32_t segq_s = C.next_seg(sr_bytes(P, R_QKV_S, 0));
     C.wait_filled(C.pos);
     XChunks<G::H, 8> nw;
     normw<G::H>(C, nw, segn);
-    // the weights of the wave's first unit (a workgroup has at most NCW units), before x arrives
+    // the weights of the wave's unit (a workgroup has at most NCW units), before x arrives
     const int nq = P.qu1 - P.qu0;
     uint4 wq[VPU][Chunks<G::H>::CPL];
-    if (C.cw < nq) ring_rows<G::H, VPU>(C, segq, C.cw * VPU, wq);
+    if (C.cw < nq) wrows<G, G::H, VPU>(C, segq, segq_s, C.cw * VPU, wq);
     tr(l, 0);
     float ss;
     if (l == 0) {
@@ -1428,12 +1718,17 @@ __device__ __forceinline__ void consumer_a(CSR<G>& C) {
     id = min(max(id, 0LL), (long long)G::V - 1);
     for (int r = P.o0 + C.ct; r < P.o1; r += NCT) sm.keep[r] = bf2f(p.embed[size_t(id) * G::H + r]);
   }
-  // are the group-A workgroups on one XCC?  Each publishes its XCC_ID, each reads all 32.
+  // are the group-A workgroups that exchange records on one XCC (narrow: all of them, since the O
+  // workgroups read every chunk's partials; wide: the 32 chunks of each KV head)?  Each publishes its
+  // XCC_ID and reads those of its peers.
   {
     const uint32_t xcc = __builtin_amdgcn_s_getreg((15 << 11) | (0 << 6) | 20) & 15u;
     if (C.ct == 0) st_unit<16>(C.rx, uint32_t(W::XCC_TAB + size_t(P.rank) * 16), u32x4{xcc, 0u, 0u, C.tag});
     uint32_t mismatch = 0;
-    C.template poll<1>(C.rx, AG, C.lane, 64, [&](int i) { return uint32_t(W::XCC_TAB + size_t(i) * 16); },
+    constexpr int NP = S::WIDE ? S::C : S::AG;
+    static_assert(NP <= 64, "one peer per lane");
+    C.template poll<1>(C.rx, NP, C.lane, 64,
+                       [&](int i) { return uint32_t(W::XCC_TAB + size_t(S::WIDE ? P.g + G::KVH * i : i) * 16); },
                        [&](int, const u32x4& v) { mismatch |= v.x != xcc ? 1u : 0u; }, 34);
     mismatch = __builtin_amdgcn_ballot_w64(mismatch != 0u) != 0ull ? 1u : 0u;
     if (C.ct == 0) sm.loc_l2 = (mismatch == 0u && p.xws != nullptr && p.l2_records) ? 1u : 0u;
@@ -1445,6 +1740,7 @@ __device__ __forceinline__ void consumer_a(CSR<G>& C) {
     const uint32_t segkv = C.next_seg(sr_bytes(P, R_KV, 0));
     C.pos_kv_end = C.pos;
     const uint32_t sego = C.next_seg(sr_bytes(P, R_O, 0));
+    const uint32_t sego_s = C.next_seg(sr_bytes(P, R_O_S, 0));
     ChunkRegs R;
     tr(l, 0);
     if (P.att) {
@@ -1481,10 +1777,16 @@ __device__ __forceinline__ void consumer_a(CSR<G>& C) {
     constexpr int RW = (S::OU * VPU + NCW - 1) / NCW;
     static_assert(RW <= 8, "sm.part holds 8 values per wave");
     uint4 wo[RW][Chunks<G::H>::CPL];
-    if (S::O_EARLY) ring_rows<G::H, RW>(C, sego, C.cw * RW, wo);
+    if (S::O_EARLY) wrows<G, G::H, RW>(C, sego, sego_s, C.cw * RW, wo);
     C.refresh();  // the record loads below may not move up into the attention code
-    attention_vector<G>(C, l);
-    if (!S::O_EARLY) ring_rows<G::H, RW>(C, sego, C.cw * RW, wo);
+    if constexpr (S::WIDE) {
+      // this chunk's slice of the attention vector, then the whole vector from every XCD
+      attention_slice<G>(C, l);
+      C.template poll_vec<1>(K_ATT, l, G::H, sm.xs, nullptr, 38);
+    } else {
+      attention_vector<G>(C, l);
+    }
+    if (!S::O_EARLY) wrows<G, G::H, RW>(C, sego, sego_s, C.cw * RW, wo);
     tr(l, 30);
     C.cbar();
     tr(l, 7);
@@ -1588,8 +1890,12 @@ __device__ __forceinline__ void final_gather(CSR<G>& C) {
 
 template <class G>
 __global__ void __launch_bounds__(WG_THREADS, 1) decode_sr(Params p, uint32_t* region) {
-  // the general kernel takes contexts beyond this kernel's limit (both are launched, exactly one runs)
-  if (min(max(p.seq_lens[0], 1), p.max_seq) > p.sr_max_s) return;
+  // each launched kernel takes its own range of contexts (narrow, wide, then the general kernel
+  // beyond; all are launched and exactly one does the step)
+  {
+    const int S = min(max(p.seq_lens[0], 1), p.max_seq);
+    if (S <= p.sr_min_s || S > p.sr_max_s) return;
+  }
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
   SmemSR<G>& sm = *reinterpret_cast<SmemSR<G>*>(smem_raw);
   if (threadIdx.x == 0) {
@@ -1603,14 +1909,22 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_sr(Params p, uint32_t* r
   PlanSR<G> P;
   P.init(p, blockIdx.x);
   for (int i = threadIdx.x; i < p.n_layers; i += WG_THREADS) {
-    const void* const* t = p.layers + size_t(i) * 6;
     LayerW w{};
-    w.norm1 = t[0]; w.qkv = t[1]; w.o = t[2]; w.norm2 = t[3]; w.gate_up = t[4]; w.down = t[5];
+    if (G::WF) {
+      const void* const* t = p.layers + size_t(i) * 10;
+      w.norm1 = t[0]; w.qkv = t[1]; w.qkv_s = static_cast<const uint8_t*>(t[2]);
+      w.o = t[3]; w.o_s = static_cast<const uint8_t*>(t[4]); w.norm2 = t[5];
+      w.gate_up = t[6]; w.gate_up_s = static_cast<const uint8_t*>(t[7]);
+      w.down = t[8]; w.down_s = static_cast<const uint8_t*>(t[9]);
+    } else {
+      const void* const* t = p.layers + size_t(i) * 6;
+      w.norm1 = t[0]; w.qkv = t[1]; w.o = t[2]; w.norm2 = t[3]; w.gate_up = t[4]; w.down = t[5];
+    }
     sm.lw[i] = w;
     sm.kvp[i] = p.kv[i];
     // lossless gate/up (SmolLM2-360M): this workgroup's act rows [a0, a1) of each matrix and their escapes
     GUE e{};
-    if (p.encoded_gu != nullptr && !P.a && P.a1 > P.a0) {
+    if (G::WF == 0 && p.encoded_gu != nullptr && !P.a && P.a1 > P.a0) {
       const EncodedGULayer d = p.encoded_gu[i];
       if (*d.enabled != 0u) {
         e.plane = d.plane;
@@ -1672,8 +1986,8 @@ template <int AUX_ST>
 __global__ void __launch_bounds__(NCT, 1) unit_check(uint8_t* buf, uint32_t buf_bytes, uint32_t base, int rounds,
                                                      int upw, int slot, int one_xcd, uint32_t* out) {
   const int wg = blockIdx.x, t = threadIdx.x;
-  if (one_xcd && !in_a(wg)) return;
-  const int np = one_xcd ? AG : NWG;                     // participating workgroups
+  if (one_xcd && (wg & 7) != 0) return;
+  const int np = one_xcd ? NWG / 8 : NWG;                // participating workgroups
   const int rank = one_xcd ? wg >> 3 : wg;
   const int nu = np * upw;                               // units per round
   const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(buf, (short)0, int(buf_bytes), 0x00020000);
@@ -1766,28 +2080,43 @@ extern "C" int pk_test_exchange_units(int mode, int rounds, int slot, unsigned* 
 namespace pk {
 namespace sr {
 
+// The compiled kernels: narrow and wide layouts of SmolLM2-360M (bf16 and MXFP8 weights) and of
+// SmolLM2-135M.
+using N360 = SrG<G360, 1>;
+using N135 = SrG<G135, 1>;
+using N360Q = SrG<G360Q, 1>;
+using W360 = SrG<G360, G360::KVH>;
+using W135 = SrG<G135, G135::KVH>;
+using W360Q = SrG<G360Q, G360Q::KVH>;
+
 // Longest context (tokens attended, the new one included) the kernel takes: C chunks of at most TCS
 // cached tokens per KV head, and a chunk's K/V plus the workgroup's O rows within the LDS ring.
 template <class G>
 constexpr int max_seq() {
   using S = SG<G>;
-  constexpr uint32_t o_bytes = uint32_t(S::OU) * VPU * G::H * 2;
-  constexpr int tc_ring = int((RING - pad_pkt(o_bytes) - 2 * PKT) / 256u) / 16 * 16;
-  constexpr int tc = tc_ring < TCS ? tc_ring : TCS;
+  constexpr uint32_t o_bytes = pad_pkt(uint32_t(S::OU) * VPU * G::H * S::WB) +
+                               (G::WF ? pad_pkt(uint32_t(S::OU) * VPU * uint32_t(scale_stride(G::H))) : 0u);
+  constexpr int tc_ring = int((RING - o_bytes - 2 * PKT) / 256u) / 16 * 16;
+  constexpr int tc = tc_ring < S::TCS ? tc_ring : S::TCS;
   return S::C * tc + 1;
 }
-static_assert(max_seq<G360>() >= 1281 && max_seq<G135>() >= 769, "the split-role kernel covers configs 2 and 3");
-static_assert(max_seq<G360>() == PK_NOALLOC_MAX_SEQ_360M && max_seq<G135>() == PK_NOALLOC_MAX_SEQ_135M,
+static_assert(max_seq<N360>() >= 1281 && max_seq<N135>() >= 769, "the narrow layout covers configs 2 and 3");
+static_assert(max_seq<W360Q>() >= 8192 + 288 && max_seq<W360>() == max_seq<W360Q>() && max_seq<W135>() >= max_seq<W360>(),
+              "the wide layout covers config 5 (context 8192, then the benchmark's steps)");
+static_assert(max_seq<N360Q>() == max_seq<N360>(), "one narrow limit per model");
+static_assert(max_seq<N360>() == PK_NOALLOC_MAX_SEQ_360M && max_seq<N135>() == PK_NOALLOC_MAX_SEQ_135M,
               "the context limits pk_decode_noalloc documents");
 constexpr size_t pages(size_t n) { return (n + 4095) / 4096 * 4096; }
-static_assert(4096 + pages(SWS<G360>::BYTES) + pages(SWS<G360>::LOC_BYTES) <= PK_NOALLOC_SCRATCH_BYTES &&
-                  4096 + pages(SWS<G135>::BYTES) + pages(SWS<G135>::LOC_BYTES) <= PK_NOALLOC_SCRATCH_BYTES,
+static_assert(4096 + pages(SWS<N360>::BYTES) + pages(SWS<N360>::LOC_BYTES) <= PK_NOALLOC_SCRATCH_BYTES &&
+                  4096 + pages(SWS<N135>::BYTES) + pages(SWS<N135>::LOC_BYTES) <= PK_NOALLOC_SCRATCH_BYTES,
               "header, region and group-A records fit pk_decode_noalloc's array");
 
 template <class G>
 constexpr size_t lds_bytes() { return sizeof(SmemSR<G>); }
-static_assert((sizeof(SmemSR<G360>) + 15) / 16 * 16 + TRACE_LDS_BYTES <= 160 * 1024 &&
-                  (sizeof(SmemSR<G135>) + 15) / 16 * 16 + TRACE_LDS_BYTES <= 160 * 1024,
+template <class G>
+constexpr bool lds_fits() { return (sizeof(SmemSR<G>) + 15) / 16 * 16 + TRACE_LDS_BYTES <= 160 * 1024; }
+static_assert(lds_fits<N360>() && lds_fits<N135>() && lds_fits<N360Q>() && lds_fits<W360>() && lds_fits<W135>() &&
+                  lds_fits<W360Q>(),
               "LDS budget of one gfx950 workgroup, with the diagnostic timestamps");
 
 template <class G>
@@ -1830,18 +2159,36 @@ static int launch(const Params& p, uint32_t* region, uint32_t* local, hipStream_
 
 }  // namespace sr
 
-int sr_launch(int model, const Params& p, uint32_t* region, uint32_t* local, hipStream_t stream, int cooperative) {
-  if (model == PK_MODEL_SMOLLM2_360M) return sr::launch<G360>(p, region, local, stream, cooperative);
-  if (model == PK_MODEL_SMOLLM2_135M) return sr::launch<G135>(p, region, local, stream, cooperative);
+int sr_launch(int model, int wf, int wide, const Params& p, uint32_t* region, uint32_t* local, hipStream_t stream,
+              int cooperative) {
+  if (model == PK_MODEL_SMOLLM2_360M && wf)
+    return wide ? sr::launch<sr::W360Q>(p, region, local, stream, cooperative)
+                : sr::launch<sr::N360Q>(p, region, local, stream, cooperative);
+  if (model == PK_MODEL_SMOLLM2_360M)
+    return wide ? sr::launch<sr::W360>(p, region, local, stream, cooperative)
+                : sr::launch<sr::N360>(p, region, local, stream, cooperative);
+  if (model == PK_MODEL_SMOLLM2_135M && !wf)
+    return wide ? sr::launch<sr::W135>(p, region, local, stream, cooperative)
+                : sr::launch<sr::N135>(p, region, local, stream, cooperative);
   return PK_ERR_MODEL;
 }
-size_t sr_region_bytes() { return sr::SWS<G360>::BYTES > sr::SWS<G135>::BYTES ? sr::SWS<G360>::BYTES : sr::SWS<G135>::BYTES; }
-size_t sr_local_bytes() {
-  return sr::SWS<G360>::LOC_BYTES > sr::SWS<G135>::LOC_BYTES ? sr::SWS<G360>::LOC_BYTES : sr::SWS<G135>::LOC_BYTES;
+template <class A, class B>
+static constexpr size_t zmax(A a, B b) { return size_t(a) > size_t(b) ? size_t(a) : size_t(b); }
+size_t sr_region_bytes(int all) {
+  using namespace sr;
+  const size_t narrow = zmax(SWS<N360>::BYTES, SWS<N135>::BYTES);
+  return all ? zmax(zmax(narrow, SWS<N360Q>::BYTES), zmax(zmax(SWS<W360>::BYTES, SWS<W135>::BYTES), SWS<W360Q>::BYTES))
+             : narrow;
 }
-int sr_max_seq(int model) {
-  if (model == PK_MODEL_SMOLLM2_360M) return sr::max_seq<G360>();
-  if (model == PK_MODEL_SMOLLM2_135M) return sr::max_seq<G135>();
+size_t sr_local_bytes(int wide) {
+  using namespace sr;
+  return wide ? zmax(zmax(SWS<W360>::LOC_BYTES, SWS<W135>::LOC_BYTES), SWS<W360Q>::LOC_BYTES)
+              : zmax(zmax(SWS<N360>::LOC_BYTES, SWS<N135>::LOC_BYTES), SWS<N360Q>::LOC_BYTES);
+}
+int sr_max_seq(int model, int wide) {
+  using namespace sr;
+  if (model == PK_MODEL_SMOLLM2_360M) return wide ? max_seq<W360>() : max_seq<N360>();
+  if (model == PK_MODEL_SMOLLM2_135M) return wide ? max_seq<W135>() : max_seq<N135>();
   return 0;
 }
 

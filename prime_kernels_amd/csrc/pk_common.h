@@ -32,6 +32,11 @@ struct G360Q : G360 {
   static constexpr int WF = 1;
 };
 
+// E8M0 scale code -> fp32 2^(s-127) (code 0 is the fp32 denormal 2^-127; 255 is NaN).
+__device__ __forceinline__ float e8m0_f32(uint32_t s) {
+  return __uint_as_float(s == 0 ? 0x00400000u : s == 255 ? 0x7fc00000u : s << 23);
+}
+
 // MXFP8 scales are stored one byte per 32 weights, each row padded to a multiple of 16 bytes so
 // that every row segment a workgroup streams starts and ends on a 16-byte boundary.
 __host__ __device__ constexpr int scale_stride(int K) { return ((K / 32 + 15) / 16) * 16; }
@@ -136,17 +141,21 @@ struct Params {
   int h_dim;                   // hidden size of the model (for the poisoned hidden state)
   int l2_records;              // 0: batch-1 attention records stay in the uncached workspace
   uint32_t skew;               // != 0: seed of the arrival-skew test's delays before each publish
-  int sr_max_s;                // > 0: the split-role kernel was launched for this step and does contexts
-                               // up to sr_max_s tokens (the general batch-1 kernel then leaves them)
+  int sr_max_s;                // > 0: split-role kernels were launched for this step and do contexts up
+                               // to sr_max_s tokens (the general batch-1 kernel then leaves them)
+  int sr_min_s;                // a split-role kernel does contexts in (sr_min_s, sr_max_s] (its launch's
+                               // copy of the parameters; the narrow layout takes the short ones)
 };
 
 // Split-role batch-1 kernel (decode_sr.hip): launch, the sizes of its workspace regions (bytes), and
 // the longest context it takes (tokens attended, new one included; 0: not available for the model).
-__attribute__((visibility("hidden"))) int sr_launch(int model, const Params& p, uint32_t* region, uint32_t* local,
-                                                 hipStream_t stream, int cooperative);
-__attribute__((visibility("hidden"))) size_t sr_region_bytes();
-__attribute__((visibility("hidden"))) size_t sr_local_bytes();
-__attribute__((visibility("hidden"))) int sr_max_seq(int model);
+__attribute__((visibility("hidden"))) int sr_launch(int model, int wf, int wide, const Params& p, uint32_t* region,
+                                                 uint32_t* local, hipStream_t stream, int cooperative);
+// region: the largest over every compiled layout (all != 0) or over the narrow bf16 ones
+// (pk_decode_noalloc); local: the group-A records of the narrow (wide == 0) or the wide layouts.
+__attribute__((visibility("hidden"))) size_t sr_region_bytes(int all);
+__attribute__((visibility("hidden"))) size_t sr_local_bytes(int wide);
+__attribute__((visibility("hidden"))) int sr_max_seq(int model, int wide);
 
 // ------------------------------------------------------------------------------------------------
 // Scalar and cross-lane helpers

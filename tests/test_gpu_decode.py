@@ -345,13 +345,13 @@ def test_reference_abi_scratch_carries_nothing():
     assert rt.pending_failure() == (0, 0)
 
 
-@pytest.mark.parametrize("S", [300, 1100, 1537, 1538])
+@pytest.mark.parametrize("S", [300, 1100, 1537, 1538, 4097, 9729, 9730])
 def test_split_role_and_general_kernels_agree(S):
-    """Batch-1 steps run on the split-role kernel up to its context limit (1537 tokens for 360M) and
-    on the general kernel beyond; the general kernel also takes every context when the split-role
-    kernel is switched off.  Both reproduce HF's rounding points with different accumulation orders,
-    so both are held to the oracle, teacher-forced per layer (S = 1537 / 1538: either side of the
-    limit)."""
+    """Batch-1 steps run on the split-role kernel's narrow layout up to its context limit (1537 tokens
+    for 360M), on its wide layout up to PK_SR_WIDE_MAX_SEQ (9729) and on the general kernel beyond;
+    the general kernel also takes every context when the split-role kernel is switched off.  All
+    reproduce HF's rounding points with different accumulation orders, so all are held to the oracle,
+    teacher-forced per layer (S = 1537 / 1538 and 9729 / 9730: either side of each limit)."""
     _need_gpu()
     from prime_kernels_amd import _native
     lib = _native.library()

@@ -42,7 +42,7 @@ def test_quantizer_matches_oracle_bit_exact():
         assert np.array_equal(s.cpu().numpy(), s_ref), (rows, cols)
 
 
-@pytest.mark.parametrize("S", [1, 65, 1025])
+@pytest.mark.parametrize("S", [1, 65, 1025, 4097])
 def test_mxfp8_two_layers(S):
     """Twelve seeded 2-layer steps per context, held to the seed-set bar (gpu_cases), and at least
     half of them with both layer outputs at least half bit-identical to the oracle's (a bf16

@@ -55,16 +55,17 @@ def _step(mod, embed, final_norm, lw, kv, cos_sin, ids, positions):
 
 
 @pytest.mark.parametrize("report", ["next_call", "check_failures"])
-@pytest.mark.parametrize("path", ["split_role", "general", "batched"])
+@pytest.mark.parametrize("path", ["split_role", "split_wide", "general", "batched"])
 def test_abandoned_wait_poisons_outputs_and_is_reported(path, report):
     """The failed step is reported once: by the next decode call (which launches nothing), or by
-    check_failures, after which the next call runs normally."""
+    check_failures, after which the next call runs normally (split_wide: a context past the narrow
+    split-role limit, which the wide layout takes)."""
     _need_gpu()
     from prime_kernels_amd import _native
 
     lib = _native.library()
     batch = 3 if path == "batched" else 1
-    contexts = [300 + 41 * b for b in range(batch)]
+    contexts = [3000] if path == "split_wide" else [300 + 41 * b for b in range(batch)]
     mod, model, embed, final_norm, lw, kv, cos_sin = _setup(batch, contexts)
     rt = mod.workspace(embed.device)
     stream = torch.cuda.current_stream().cuda_stream
@@ -186,8 +187,8 @@ def test_embed_table_must_have_the_full_vocabulary():
     assert mod.workspace(dev).pending_failure() == (0, 0)
 
 
-@pytest.mark.parametrize("split_role", [1, 0], ids=["split_role", "general"])
-def test_attention_records_through_uncached_memory_give_the_same_bits(split_role):
+@pytest.mark.parametrize("split_role,S", [(1, 900), (1, 3000), (0, 900)], ids=["split_role", "split_wide", "general"])
+def test_attention_records_through_uncached_memory_give_the_same_bits(split_role, S):
     """A KV head's chunks exchange their softmax statistics and partials through their XCD's L2 when
     the run-time check finds them on one XCC, else through the uncached workspace.
     PK_OPT_L2_RECORDS=0 forces the second path, the one a placement mismatch takes: same bits."""
@@ -195,7 +196,7 @@ def test_attention_records_through_uncached_memory_give_the_same_bits(split_role
     from prime_kernels_amd import _native
 
     lib = _native.library()
-    mod, model, embed, final_norm, lw, kv, cos_sin = _setup(1, [900])
+    mod, model, embed, final_norm, lw, kv, cos_sin = _setup(1, [S])
     kv0 = [c.clone() for c in kv.caches]
     old_sr = lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, split_role)
     try:
@@ -205,7 +206,7 @@ def test_attention_records_through_uncached_memory_give_the_same_bits(split_role
             try:
                 for c, c0 in zip(kv.caches, kv0):
                     c.copy_(c0)
-                h, i, lg = _step(mod, embed, final_norm, lw, kv, cos_sin, [321], [900])
+                h, i, lg = _step(mod, embed, final_norm, lw, kv, cos_sin, [321], [S])
                 torch.cuda.synchronize()
                 outs.append((h, i, lg.clone(), [c.clone() for c in kv.caches]))
             finally:
@@ -220,7 +221,7 @@ def test_attention_records_through_uncached_memory_give_the_same_bits(split_role
         lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, old_sr)
 
 
-@pytest.mark.parametrize("case", ["b1_split_role", "b1_general", "b16_ragged"])
+@pytest.mark.parametrize("case", ["b1_split_role", "b1_split_wide", "b1_general", "b16_ragged"])
 def test_arrival_skew_leaves_every_bit_unchanged(case):
     """Arrival-skew test of the tagged exchange protocol: with PK_OPT_SKEW every workgroup sleeps a
     pseudo-random 0..23 x 512 cycles (from the seed, the workgroup, the layer and the site) before each
@@ -232,7 +233,7 @@ def test_arrival_skew_leaves_every_bit_unchanged(case):
 
     lib = _native.library()
     batch = 16 if case == "b16_ragged" else 1
-    contexts = [40 + 53 * b for b in range(batch)] if batch > 1 else [900]
+    contexts = [40 + 53 * b for b in range(batch)] if batch > 1 else [3000] if case == "b1_split_wide" else [900]
     mod, model, embed, final_norm, lw, kv, cos_sin = _setup(batch, contexts)
     kv0 = [c.clone() for c in kv.caches]
     ids = [(11 + 97 * b) % 49152 for b in range(batch)]
@@ -289,7 +290,7 @@ def test_exchange_units_are_never_torn(mode, slot):
     assert checked == rounds * participants * participants * 4, checked
 
 
-@pytest.mark.parametrize("path", ["split_role", "general", "batched", "mxfp8"])
+@pytest.mark.parametrize("path", ["split_role", "split_wide", "general", "batched", "mxfp8", "mxfp8_general"])
 def test_cooperative_launch_gives_the_same_bits(path):
     """The decode kernels run with the ordinary launch by default; PK_OPT_COOPERATIVE (or
     PK_LAUNCH=cooperative) launches them with hipLaunchCooperativeKernel as the reference does
@@ -299,16 +300,16 @@ def test_cooperative_launch_gives_the_same_bits(path):
 
     lib = _native.library()
     batch = 3 if path == "batched" else 1
-    contexts = [300 + 41 * b for b in range(batch)] if path != "mxfp8" else [2100]
+    contexts = [2100] if path.startswith("mxfp8") or path == "split_wide" else [300 + 41 * b for b in range(batch)]
     mod, model, embed, final_norm, lw, kv, cos_sin = _setup(batch, contexts)
-    if path == "mxfp8":
+    if path.startswith("mxfp8"):
         import prime_kernels_amd as pk
         from prime_kernels_amd import mxfp8
         mod = pk.load("decode_megakernel_360m_mxfp8")
         lw = mxfp8.quantize_layers(lw)
     kv0 = [c.clone() for c in kv.caches]
     ids = [(57 + 13 * b) % 49152 for b in range(batch)]
-    old_sr = lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, 0 if path == "general" else 1)
+    old_sr = lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, 0 if path.endswith("general") else 1)
     try:
         outs = []
         for coop in (0, 1):
