@@ -90,7 +90,11 @@ struct SG {
   static constexpr int PU = 22;                         // narrow: units of one head's 64 fp32 partial sums
   static constexpr int PUC = WIDE ? 64 : 3 * PU;        // partial-sum units per chunk record
   static constexpr int OU = (HU + AG - 1) / AG;         // most O units per group-A workgroup
-  static constexpr int NAU = (IU + FG - 1) / FG;        // most act units per group-F workgroup
+  // gate/up + SwiGLU: on group F in the narrow layout; on every workgroup in the wide one (group A,
+  // idle between its O projection and the next layer's q, takes its share after the O rows)
+  static constexpr bool GU_ALL = WIDE;
+  static constexpr int GUW = GU_ALL ? NWG : FG;         // workgroups sharing the act units
+  static constexpr int NAU = (IU + GUW - 1) / GUW;      // most act units per workgroup
   static constexpr int NXU = (HU + FG - 1) / FG;        // most x (down) units per group-F workgroup
   static constexpr int NQU = (QU + FG - 1) / FG;        // most qkv units per group-F workgroup
   static constexpr int NIT = (2 * NAU + NCW - 1) / NCW; // gate/up 6-row items per wave
@@ -105,7 +109,7 @@ struct SG {
   static_assert(C >= 1 && C <= 32 && (!WIDE || C == 32), "chunks per KV head");
   static_assert(TCS + 1 <= MT * 16 * NCW, "a chunk's tiles (and the new token) fit MT tiles per wave");
   static_assert(NQU <= NCW, "the QKV phase gives each wave at most one unit");
-  static_assert(NXU <= 2 && NIT <= 3, "down units and gate/up items per group-F workgroup");
+  static_assert(NXU <= 2 && NIT <= 3, "down units and gate/up items per workgroup");
   static_assert(OU * VPU <= 8 * NCW, "the O rows fit 8 per wave");
 };
 
@@ -213,10 +217,15 @@ struct PlanSR {
       au0 = split_lo(GG::IU, GG::FG, rank); au1 = split_lo(GG::IU, GG::FG, rank + 1);
       xu0 = split_lo(GG::HU, GG::FG, rank); xu1 = split_lo(GG::HU, GG::FG, rank + 1);
       qu0 = split_lo(GG::QU, GG::FG, rank); qu1 = split_lo(GG::QU, GG::FG, rank + 1);
-      a0 = au0 * VPU; a1 = min(au1 * VPU, G::I);
       d0 = xu0 * VPU; d1 = min(xu1 * VPU, G::H);
       q0 = qu0 * VPU; q1 = min(qu1 * VPU, G::QKV);
     }
+    if (GG::GU_ALL) {
+      au0 = split_lo(GG::IU, NWG, wg);
+      au1 = split_lo(GG::IU, NWG, wg + 1);
+    }
+    a0 = au0 * VPU;
+    a1 = min(au1 * VPU, G::I);
     if (p.lm_head) {
       v0 = split_lo(G::V, NWG, wg);
       v1 = split_lo(G::V, NWG, wg + 1);
@@ -228,10 +237,9 @@ struct PlanSR {
     // estimate for a lossless stream; a segment that does not fit waits for ring space in any case)
     constexpr uint32_t WB = GG::WB;
     constexpr uint32_t SH = G::WF ? uint32_t(scale_stride(G::H)) : 0u, SI = G::WF ? uint32_t(scale_stride(G::I)) : 0u;
+    const uint32_t gu = pad_pkt(G::H * 2) + 2 * pad_pkt(uint32_t(a1 - a0) * G::H * WB) + 2 * pad_pkt(uint32_t(a1 - a0) * SH);
     const uint32_t last = a ? pad_pkt(G::H * 2)
-                            : 2 * pad_pkt(G::H * 2) + 2 * pad_pkt(uint32_t(a1 - a0) * G::H * WB) +
-                                  2 * pad_pkt(uint32_t(a1 - a0) * SH) + pad_pkt(uint32_t(d1 - d0) * G::I * WB) +
-                                  pad_pkt(uint32_t(d1 - d0) * SI);
+                            : pad_pkt(G::H * 2) + gu + pad_pkt(uint32_t(d1 - d0) * G::I * WB) + pad_pkt(uint32_t(d1 - d0) * SI);
     const uint32_t lmseg = pad_pkt(uint32_t(LM_ROWS_SR) * G::H * 2);
     lm_pre = last >= RING ? 0 : min(n_lm, int((RING - last) / lmseg));
   }
@@ -239,8 +247,10 @@ struct PlanSR {
 
 // Segments in stream order.  Group F, bracket k (0 <= k <= L): the MLP of layer k-1 (norm2, gate
 // rows, up rows, down rows; k >= 1) then norm1 and the QKV rows of layer k (k < L); bracket L ends
-// with the final-norm weights and the LM-head segments.  Group A, bracket k < L: the KV chunk and
-// the O rows of layer k; bracket L: the final-norm weights and the LM-head segments.
+// with the final-norm weights and the LM-head segments (in the wide layout F's gate and up rows are
+// its share of the act units only).  Group A, bracket k < L: the KV chunk and the O rows of layer k,
+// in the wide layout then its gate/up share of layer k (norm2, gate rows, up rows); bracket L: the
+// final-norm weights and the LM-head segments.
 // MXFP8 weights: every weight segment (gate, up, down, QKV, O) is followed by its scale rows (the _S
 // segments, scale_stride(K) bytes per row; empty for bf16 weights).
 enum SRSeg { R_NORM2, R_GATE, R_GATE_S, R_GATE_H, R_GATE_R, R_UP, R_UP_S, R_UP_H, R_UP_R, R_DOWN, R_DOWN_S,
@@ -424,6 +434,17 @@ __device__ __forceinline__ void producer_sr(const Params& p, const PlanSR<G>& P,
         issue(R_KV, k, 0);
         issue(R_O, k, 0);
         issue(R_O_S, k, 0);
+        if (SG<G>::GU_ALL) {  // its gate/up share of the layer, needed after the O rows
+          issue(R_NORM2, k, 0);
+          issue(R_GATE, k, 0);
+          issue(R_GATE_S, k, 0);
+          issue(R_GATE_H, k, 0);
+          issue(R_GATE_R, k, 0);
+          issue(R_UP, k, 0);
+          issue(R_UP_S, k, 0);
+          issue(R_UP_H, k, 0);
+          issue(R_UP_R, k, 0);
+        }
       } else {
         issue(R_FNORM, 0, 0);
       }
@@ -1412,6 +1433,70 @@ __device__ __forceinline__ void lm_head_sr(CSR<G>& C) {
 // Consumer main loops
 // ------------------------------------------------------------------------------------------------
 
+// Wide layout: group A's share of RMSNorm(h1) + gate/up + SwiGLU of layer l, after its O rows (the
+// phase group F runs, without keeping h1 for the down residual): one 6-row gate or up item per wave,
+// its weights in registers before h1 arrives, act units published.
+template <class G>
+__device__ __forceinline__ void gate_up_a(CSR<G>& C, int l) {
+  static_assert(SG<G>::GU_ALL && SG<G>::NIT == 1, "one gate/up item per wave");
+  const Params& p = C.p;
+  const PlanSR<G>& P = C.P;
+  SmemSR<G>& sm = C.sm;
+  auto tr = [&](int ev) { if (C.ct == 0) trace_at(p, l, ev, p.n_layers); };
+  C.refresh();
+  const GUE& ge = sm.gue[l];
+  const uint32_t segn = C.next_seg(sr_bytes(P, R_NORM2, 0));
+  const uint32_t segg = C.next_seg(sr_bytes(P, R_GATE, 0, &ge));
+  const uint32_t segg_s = C.next_seg(sr_bytes(P, R_GATE_S, 0));
+  const uint32_t segg_h = C.next_seg(sr_bytes(P, R_GATE_H, 0, &ge));
+  const uint32_t segg_r = C.next_seg(sr_bytes(P, R_GATE_R, 0, &ge));
+  const uint32_t segu = C.next_seg(sr_bytes(P, R_UP, 0, &ge));
+  const uint32_t segu_s = C.next_seg(sr_bytes(P, R_UP_S, 0));
+  const uint32_t segu_h = C.next_seg(sr_bytes(P, R_UP_H, 0, &ge));
+  const uint32_t segu_r = C.next_seg(sr_bytes(P, R_UP_R, 0, &ge));
+  C.wait_filled(C.pos);
+  XChunks<G::H, 8> nw;
+  normw<G::H>(C, nw, segn);
+  const int nunits = P.au1 - P.au0;
+  const bool item = C.cw < 2 * nunits;
+  uint4 w[VPU][Chunks<G::H>::CPL];
+  if (item) {
+    const int j = C.cw % nunits, m = C.cw < nunits ? 0 : 1;
+    if (ge.on)
+      lossless_rows<G::H, VPU>(C, m ? segu : segg, m ? segu_h : segg_h, m ? segu_r : segg_r, ge.first[m], j * VPU, w);
+    else
+      wrows<G, G::H, VPU>(C, m ? segu : segg, m ? segu_s : segg_s, j * VPU, w);
+  }
+  tr(9);
+  const float ss = C.template poll_vec<1>(K_H1, l, G::H, sm.xs, nullptr, 43);
+  const float rs = rms_rsq<G::H>(C.block_total(ss));
+  tr(10);
+  {
+    XChunks<G::H, 8> x;
+    load_x<G::H, 8, true>(x, sm.xs, nw, rs, C.lane);
+    if (item) {
+      float o[VPU];
+      dots_w<G::H, VPU>(w, x, o);
+      if (C.lane == 0)
+#pragma unroll
+        for (int e = 0; e < VPU; ++e) sm.part[C.cw][e] = o[e];
+    }
+    C.cbar();
+    if (C.cw < nunits) {
+      const int e = min(C.lane, VPU - 1);
+      const float gv = rnd(sm.part[C.cw][e]), uv = rnd(sm.part[nunits + C.cw][e]);
+      const float act = rnd(gv / (1.0f + expf(-gv))) * uv;
+      float a[VPU];
+#pragma unroll
+      for (int k = 0; k < VPU; ++k)
+        a[k] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, act), k));
+      if (C.lane == 0) C.put_x(K_ACT, l, P.au0 + C.cw, C.unit6(a));
+    }
+  }
+  C.release(C.pos);
+  tr(11);
+}
+
 template <class G>
 __device__ __forceinline__ void consumer_f(CSR<G>& C) {
   using S = SG<G>;
@@ -1820,7 +1905,10 @@ __device__ __forceinline__ void consumer_a(CSR<G>& C) {
     }
     C.release(C.pos);
     tr(l, 8);
+    // the producers may stream the next bracket (wide: while this layer's gate/up share, streamed
+    // with this bracket, is computed)
     C.bracket_done(uint32_t(l + 1));
+    if constexpr (S::GU_ALL) gate_up_a<G>(C, l);
   }
   lm_head_sr<G>(C);
 }
@@ -1924,7 +2012,7 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_sr(Params p, uint32_t* r
     sm.kvp[i] = p.kv[i];
     // lossless gate/up (SmolLM2-360M): this workgroup's act rows [a0, a1) of each matrix and their escapes
     GUE e{};
-    if (G::WF == 0 && p.encoded_gu != nullptr && !P.a && P.a1 > P.a0) {
+    if (G::WF == 0 && p.encoded_gu != nullptr && (!P.a || SG<G>::GU_ALL) && P.a1 > P.a0) {
       const EncodedGULayer d = p.encoded_gu[i];
       if (*d.enabled != 0u) {
         e.plane = d.plane;
