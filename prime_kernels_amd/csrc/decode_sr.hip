@@ -63,7 +63,13 @@ constexpr int UPL = PK_SR_UPL;           // cross-XCD units per 64-byte line (fe
 #ifndef PK_SR_DEPTH
 #define PK_SR_DEPTH 8
 #endif
-constexpr int DEPTH_SR = PK_SR_DEPTH;    // DMA packets in flight per producer wave
+constexpr int DEPTH_SR = PK_SR_DEPTH;    // DMA packets in flight per producer wave (narrow layout)
+#ifndef PK_SR_DEPTH_W
+#define PK_SR_DEPTH_W 4   // wide layout (config 5: 2 / 3 / 4 / 6 / 8 / 16 = 1,691 / 1,698 / 1,701 / 1,663 / 1,642 / 1,584 tok/s)
+#endif
+#ifndef PK_SR_PRIO_W
+#define PK_SR_PRIO_W 1    // wide layout: consumer waves at issue priority 1 (0: -7% at config 5)
+#endif
 constexpr int LM_ROWS_SR = 24;           // LM-head rows per ring segment, 6 per consumer wave (16: -1.5%)
 
 // 16-token tiles of a chunk per consumer wave (attention): at most MT
@@ -103,6 +109,8 @@ struct SG {
   // room for them in the narrow SmolLM2-135M build without spills)
   static constexpr bool O_EARLY = WIDE || C <= 6;
   static constexpr uint32_t WB = G::WF ? 1u : 2u;       // bytes per projection weight
+  static constexpr int DEPTH = WIDE ? PK_SR_DEPTH_W : DEPTH_SR;  // DMA packets in flight per producer wave
+  static constexpr int PRIO = WIDE ? PK_SR_PRIO_W : 1;           // consumer waves' issue priority
   __device__ static bool in_a(int wg) { return (wg & 7) < AX; }
   static_assert(G::GQA == 3 && (3 * 64) % VPU == 0 && G::H % VPU == 0, "head groups are whole units");
   static_assert(!WIDE || AX == G::KVH, "the wide layout puts one KV head on each of its XCDs");
@@ -413,8 +421,8 @@ __device__ __forceinline__ void producer_sr(const Params& p, const PlanSR<G>& P,
         src = base + off;
       }
       if (off < bytes) dma16(src, __builtin_amdgcn_readfirstlane(ring_base + ((gn * PKT) & (RING - 1))));
-      wait_vmcnt<DEPTH_SR>();
-      if (gn >= uint32_t(DEPTH_SR - 1) * NPW) publish(gn - uint32_t(DEPTH_SR - 1) * NPW);
+      wait_vmcnt<SG<G>::DEPTH>();
+      if (gn >= uint32_t(SG<G>::DEPTH - 1) * NPW) publish(gn - uint32_t(SG<G>::DEPTH - 1) * NPW);
     }
     n += npk;
   };
@@ -2040,7 +2048,7 @@ __global__ void __launch_bounds__(WG_THREADS, 1) decode_sr(Params p, uint32_t* r
   } else {
     // the consumer waves are the step's critical path: their instructions win the SIMD's issue
     // over the producer waves' DMA issue and ring polling when both are ready (+3.4% at ctx 1024)
-    __builtin_amdgcn_s_setprio(1);
+    if constexpr (SG<G>::PRIO == 1) __builtin_amdgcn_s_setprio(1);
     CSR<G> C(p, P, sm, epoch, region);
     if (P.a) consumer_a<G>(C);
     else consumer_f<G>(C);
