@@ -67,6 +67,9 @@ constexpr int DEPTH_SR = PK_SR_DEPTH;    // DMA packets in flight per producer w
 #ifndef PK_SR_DEPTH_W
 #define PK_SR_DEPTH_W 4   // wide layout (config 5: 2 / 3 / 4 / 6 / 8 / 16 = 1,691 / 1,698 / 1,701 / 1,663 / 1,642 / 1,584 tok/s)
 #endif
+#ifndef PK_SR_STATS_CHUNK_W
+#define PK_SR_STATS_CHUNK_W 1
+#endif
 #ifndef PK_SR_PRIO_W
 #define PK_SR_PRIO_W 1    // wide layout: consumer waves at issue priority 1 (0: -7% at config 5)
 #endif
@@ -111,6 +114,9 @@ struct SG {
   static constexpr uint32_t WB = G::WF ? 1u : 2u;       // bytes per projection weight
   static constexpr int DEPTH = WIDE ? PK_SR_DEPTH_W : DEPTH_SR;  // DMA packets in flight per producer wave
   static constexpr int PRIO = WIDE ? PK_SR_PRIO_W : 1;           // consumer waves' issue priority
+  // softmax statistics: each wave publishes its own (narrow), or each chunk combines its waves first
+  // and publishes once (wide: 32 chunks x 4 waves would be 256 units for every wave to poll)
+  static constexpr bool STATS_CHUNK = WIDE && PK_SR_STATS_CHUNK_W;
   __device__ static bool in_a(int wg) { return (wg & 7) < AX; }
   static_assert(G::GQA == 3 && (3 * 64) % VPU == 0 && G::H % VPU == 0, "head groups are whole units");
   static_assert(!WIDE || AX == G::KVH, "the wide layout puts one KV head on each of its XCDs");
@@ -312,6 +318,7 @@ struct SmemSR {
   };
   float keep[G::H];              // F: h1 (residual of down); A: x (residual of O, its own rows)
   float wo[NCW][3][64];          // per-wave P.V partials
+  float wml[NCW][2][3];          // per-wave softmax max / sum per head (chunk-combined statistics)
   float red[NCW];
   LayerW lw[G::L];
   GUE gue[G::L];                 // group F: each layer's lossless gate/up stream of this workgroup
@@ -1085,6 +1092,74 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
   }
   if (w == 0 && lane == 0) trace_at(p, l, 37, p.n_layers);
   if (has_new && lane == 0) trace_at(p, l, 39, p.n_layers);
+  float Mh[3], Lh[3];
+  if constexpr (S::STATS_CHUNK) {
+    // the chunk's waves combined first, m_c = max_v m_v and l_c = (e_0 + e_1) + (e_2 + e_3) with
+    // e_v = l_v exp(m_v - m_c) (lanes 4h + v), then one record per chunk: chunk c' of head g
+    // (group-A rank g + KVH c') has {max x3, tag}, {sum x3, tag} at units 2 rank + {0, 1}
+    if (lane == 0)
+#pragma unroll
+      for (int h = 0; h < 3; ++h) {
+        sm.wml[w][0][h] = mw[h];
+        sm.wml[w][1][h] = lw[h];
+      }
+    C.cbar();
+    float mq = -INFINITY, lq = 0.f;
+    if (lane < 4 * 3) {
+      mq = sm.wml[lane & 3][0][lane >> 2];
+      lq = sm.wml[lane & 3][1][lane >> 2];
+    }
+    float mx = fmaxf(mq, dpp<0xb1>(mq, mq));
+    mx = fmaxf(mx, dpp<0x4e>(mx, mx));
+    float ex = mq == -INFINITY ? 0.f : lq * __expf(mq - mx);
+    ex += dpp<0xb1>(0.f, ex);
+    ex += dpp<0x4e>(0.f, ex);
+    if (w == 0) {
+      float v[3];
+#pragma unroll
+      for (int h = 0; h < 3; ++h) {
+        const float mc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx), 4 * h));
+        const float lc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), 4 * h));
+        v[h] = lane ? lc : mc;
+      }
+      if (lane < 2)
+        C.put_loc(l, W::STAT_U + size_t(P.rank) * 2 + lane,
+                  u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), C.tag});
+    }
+    if (w == 0 && lane == 0) trace_at(p, l, 17, p.n_layers);
+    // lane 2c polls the maxima of chunk c, lane 2c + 1 its sums; a_c = l_c exp(m_c - M) in lane 2c + 1;
+    // per row k (chunks 8k .. 8k + 7) T_k = ((a7 + a6) + (a5 + a4)) + ((a3 + a2) + (a1 + a0)), L =
+    // (T_3 + T_2) + (T_1 + T_0): the association of the per-wave merge, so the same bits
+    static_assert(2 * S::C == 64, "one statistics unit per lane, four rows of eight chunks");
+    float st[3] = {(lane & 1) ? 0.f : -INFINITY, (lane & 1) ? 0.f : -INFINITY, (lane & 1) ? 0.f : -INFINITY};
+    C.template poll<1>(C.rl, 2 * S::C, lane, 64,
+                       [&](int i) { return W::loc(l, W::STAT_U + size_t(g + G::KVH * (i >> 1)) * 2 + (i & 1)); },
+                       [&](int, const u32x4& v) {
+                         st[0] = __uint_as_float(v.x);
+                         st[1] = __uint_as_float(v.y);
+                         st[2] = __uint_as_float(v.z);
+                       },
+                       31);
+    float m[3], M[3];
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      const float mo = dpp<0xb1>(0.f, st[h]);
+      m[h] = (lane & 1) ? mo : st[h];
+      M[h] = m[h];
+    }
+    wave_max_n<3>(M);
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      float a = ((lane & 1) && m[h] != -INFINITY) ? st[h] * __expf(m[h] - M[h]) : 0.f;
+      a += dpp<0x4e>(0.f, a);  // quad_perm [2,3,0,1]: lane 4q + 3 = a_{2q+1} + a_{2q}
+      a += dpp<0x114>(0.f, a); // row_shr:4: lane 8p + 7 = (a_{4p+3} + a_{4p+2}) + (a_{4p+1} + a_{4p})
+      a += dpp<0x118>(0.f, a); // row_shr:8: lane 16k + 15 = T_k
+      a += dpp<0x142, 0xa>(0.f, a);  // row_bcast:15 into rows 1, 3: lane 31 = T_1 + T_0, lane 63 = T_3 + T_2
+      a += dpp<0x143, 0xc>(0.f, a);  // row_bcast:31 into rows 2, 3: lane 63 = (T_3 + T_2) + (T_1 + T_0)
+      Mh[h] = M[h];
+      Lh[h] = lane63(a);
+    }
+  } else {
   // exchange (max, sum) with every wave of the head's chunks, each wave publishing its own without
   // waiting for the other waves of its chunk: wave v of chunk c' (group-A rank g + KVH c') has the
   // record {max x3, tag}, {sum x3, tag} at units (rank NCW + v) 2 + {0, 1}
@@ -1093,7 +1168,6 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
               lane ? u32x4{__float_as_uint(lw[0]), __float_as_uint(lw[1]), __float_as_uint(lw[2]), C.tag}
                    : u32x4{__float_as_uint(mw[0]), __float_as_uint(mw[1]), __float_as_uint(mw[2]), C.tag});
   if (w == 0 && lane == 0) trace_at(p, l, 17, p.n_layers);
-  float Mh[3], Lh[3];
   {
     // unit i = 2k + s (k = NCW c' + v) is polled by lane i % 64: an even lane the maxima of one
     // (chunk, wave), the odd lane next to it the sums of the same one
@@ -1163,6 +1237,7 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
     }
 #pragma unroll
     for (int h = 0; h < 3; ++h) { Mh[h] = M[h]; Lh[h] = sum[h]; }
+  }
   }
   if (w == 0 && lane == 0) trace_at(p, l, 18, p.n_layers);
   // P.V on the matrix cores with the probabilities rounded to bf16 as HF does.  The scores'
