@@ -1745,11 +1745,13 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
         }
       } else {
         const int nx = P.xu1 - P.xu0;  // workgroups without down rows do not need act
-        // each wave: its quarter of K for every unit's 6 rows, the first unit's weights in registers
-        // before act arrives; the quarters are added in wave order
+        // each wave: its quarter of K for every unit's 6 rows, the weights in registers before act
+        // arrives; the quarters are added in wave order
         using Q = Quarter<G::I>;
-        uint4 wd[VPU][Q::CPL];
-        if (nx > 0) wquarter<G, G::I, VPU>(C, segd, segd_s, 0, wd);
+        uint4 wd[S::NXU][VPU][Q::CPL];
+#pragma unroll
+        for (int u = 0; u < S::NXU; ++u)
+          if (u < nx) wquarter<G, G::I, VPU>(C, segd, segd_s, u * VPU, wd[u]);
         if (nx > 0) C.template poll_vec<2>(K_ACT, l, G::I, sm.xs, nullptr, 41);
         C.cbar();
         tr(l, 13);
@@ -1769,9 +1771,8 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
 #pragma unroll
           for (int u = 0; u < S::NXU; ++u) {
             if (u >= nx) break;
-            if (u > 0) wquarter<G, G::I, VPU>(C, segd, segd_s, u * VPU, wd);
             float od[VPU];
-            dots_quarter_w<G::I, VPU>(wd, xq, od);
+            dots_quarter_w<G::I, VPU>(wd[u], xq, od);
             if (C.lane == 0)
 #pragma unroll
               for (int e = 0; e < VPU; ++e) sm.part[u * NCW + C.cw][e] = od[e];
@@ -1949,8 +1950,11 @@ __device__ __forceinline__ void consumer_a(CSR<G>& C) {
     C.refresh();  // the record loads below may not move up into the attention code
     if constexpr (S::WIDE) {
       // this chunk's slice of the attention vector, then the whole vector from every XCD
+      tr(l, 16);
       attention_slice<G>(C, l);
+      tr(l, 12);
       C.template poll_vec<1>(K_ATT, l, G::H, sm.xs, nullptr, 38);
+      tr(l, 15);
     } else {
       attention_vector<G>(C, l);
     }
