@@ -86,6 +86,9 @@ int pk_state_take(void* stream, unsigned* out);
  * state, or mark the next step as failed so that each of its bounded waits gives up at once. */
 int pk_test_set_epoch(void* stream, unsigned epoch);
 int pk_test_abort_next(void* stream);
+/* Test hook (synchronous; no reference counterpart): the next pk_decode_noalloc step on the current
+ * device gives up each of its bounded waits at once (the device's array must have been used). */
+int pk_test_abort_next_noalloc(void* stream);
 /* Test hook (synchronous; no reference counterpart): the exchange-unit integrity check.  Workgroups
  * publish 16-byte units {3 payload words, tag} with the decode kernels' stores, the payload a function
  * of (tag, unit), and read every unit back with the kernels' polling loads, comparing the payload of
@@ -116,6 +119,12 @@ int pk_decode(void* stream, int model, int B, int n_layers, const void* input_id
               int cs_fp32, void* out_hidden, void* layer_outputs, void* out_ids, void* out_logits,
               void* scratch, size_t scratch_bytes, int max_seq_len);
 
+/* pk_decode_noalloc's failure report, read from its fixed array on the current device (synchronises
+ * `stream`; allocates nothing): out[0] the epoch of the last step that gave up a bounded wait (0: none
+ * since the array was cleared or the report last cleared), out[1] its wait site, out[2] the epoch of
+ * the last step.  clear != 0 resets the report.  No reference counterpart. */
+int pk_noalloc_status(void* stream, int clear, unsigned* out);
+
 /* Limits of pk_decode_noalloc: its fixed per-device array, and the largest max_seq_len per model. */
 #define PK_NOALLOC_SCRATCH_BYTES 8388608
 #define PK_NOALLOC_MAX_SEQ_360M 1537
@@ -134,8 +143,9 @@ int pk_decode(void* stream, int model, int B, int n_layers, const void* input_id
  * on a device clears the array with a fill kernel on `stream` (pk_init also clears it; when the first
  * call is captured, every replay of the graph clears it).  All calls on one device share the array
  * and each leaves its contents for the next: calls that overlap on one device (from two streams, or
- * beside another decode step) race.  A step that gives up a bounded wait is reported through its
- * outputs only (token ids -1, NaN hidden state and logits); pk_state_status does not see it. */
+ * beside another decode step) race.  A step that gives up a bounded wait poisons its outputs (token
+ * ids -1, NaN hidden state and logits) and leaves its epoch and wait site in the array's header, which
+ * pk_noalloc_status reads; pk_state_status does not see it. */
 int pk_decode_noalloc(void* stream, int model, int B, int n_layers, const void* input_ids, int ids_i64,
                       const void* embed, const void* final_norm, const void* positions, const void* seq_lens,
                       const void* block_table, int bt_stride, const void* slot_mapping, const void* layers,

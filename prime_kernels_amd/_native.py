@@ -39,6 +39,8 @@ SIGNATURES = {
     "pk_test_exchange_units": (ci, [ci, ci, ci, ctypes.POINTER(ctypes.c_uint)]),
     "pk_test_set_epoch": (ci, [vp, ctypes.c_uint]),
     "pk_test_abort_next": (ci, [vp]),
+    "pk_test_abort_next_noalloc": (ci, [vp]),
+    "pk_noalloc_status": (ci, [vp, ci, ctypes.POINTER(ctypes.c_uint)]),
     "pk_decode": (ci, [vp, ci, ci, ci, vp, ci, vp, vp, vp, vp, vp, ci, vp, vp, vp,
                        ll, ll, ll, ll, ll, ci, vp, ci, vp, vp, vp, vp, vp, sz, ci]),
     "pk_decode_noalloc": (ci, [vp, ci, ci, ci, vp, ci, vp, vp, vp, vp, vp, ci, vp, vp, vp,

@@ -3488,6 +3488,58 @@ extern "C" int pk_test_set_epoch(void* stream, unsigned epoch) {
   if (e != hipSuccess) return e;
   return hipMemcpy(st->ws + pk::HDR_EPOCH, &epoch, 4, hipMemcpyHostToDevice);
 }
+// pk_decode_noalloc's failure report, read from the header of the current device's fixed array
+// (synchronises `stream`): out[0] the epoch of the last step that gave up a bounded wait (0: none
+// since the array was cleared or the report last cleared), out[1] its wait site, out[2] the epoch
+// of the last step.  With `clear`, the report is reset to none.  Allocates nothing.
+extern "C" int pk_noalloc_status(void* stream, int clear, unsigned* out) {
+  if (!out) return PK_ERR_NULL;
+  out[0] = out[1] = out[2] = 0u;
+  uint8_t* base = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(pk::noalloc::mu);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= pk::MAX_STATES) return PK_ERR_STATE;
+    base = pk::noalloc::devs[dev].ptr;
+  }
+  if (!base) return PK_OK;  // never used on this device: no step, no failure
+  hipError_t e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return e;
+  uint32_t h[3] = {0u, 0u, 0u};
+  if ((e = hipMemcpy(h, base, sizeof(h), hipMemcpyDeviceToHost)) != hipSuccess) return e;
+  out[0] = h[pk::HDR_ABORT];
+  out[1] = out[0] ? h[pk::HDR_ABORT_WHERE] : 0u;
+  out[2] = h[pk::HDR_EPOCH];
+  if (clear && out[0]) {
+    const uint32_t z = 0u;
+    if ((e = hipMemcpy(base + pk::HDR_ABORT * 4, &z, 4, hipMemcpyHostToDevice)) != hipSuccess) return e;
+  }
+  return PK_OK;
+}
+
+// Test hook (synchronous): the next pk_decode_noalloc step on the current device gives up each of its
+// bounded waits at once (the array must have been used).
+extern "C" int pk_test_abort_next_noalloc(void* stream) {
+  uint8_t* base = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(pk::noalloc::mu);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= pk::MAX_STATES) return PK_ERR_STATE;
+    base = pk::noalloc::devs[dev].ptr;
+  }
+  if (!base) return PK_ERR_STATE;
+  hipError_t e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return e;
+  uint32_t ep = 0;
+  if ((e = hipMemcpy(&ep, base + pk::HDR_EPOCH * 4, 4, hipMemcpyDeviceToHost)) != hipSuccess) return e;
+  ep = ep + 1u == 0u ? 1u : ep + 1u;
+  return hipMemcpy(base + pk::HDR_ABORT * 4, &ep, 4, hipMemcpyHostToDevice);
+}
+
 extern "C" int pk_test_abort_next(void* stream) {
   pk::DevState* st = nullptr;
   const int rc = pk::get_state(stream, &st);

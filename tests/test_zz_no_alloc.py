@@ -125,3 +125,50 @@ def _two_calls(lib, model, limit, first, second, seed):
     rc, h_ref, i_ref, _ = x.call(lib, lib.pk_decode, caches_ref, token=9, pos=second[0] + 1, cap=second[1],
                                  n_layers=second[2], scratch=scratch)
     assert rc == 0 and _same(h_na, h_ref) and torch.equal(i_na, i_ref)
+
+
+def test_noalloc_failure_is_reported_by_status():
+    """A pk_decode_noalloc step forced to give up its bounded waits (pk_test_abort_next_noalloc)
+    poisons its outputs; pk_noalloc_status reports that step's epoch until cleared; the next step is
+    bit-identical to pk_decode again."""
+    _need_gpu()
+    import ctypes
+
+    from prime_kernels_amd import _native
+    from prime_kernels_amd._decode import SMOLLM2_360M
+
+    lib = _native.library()
+    model = SMOLLM2_360M
+    x = _Inputs(model, 512, seed=21)
+    scratch = torch.empty((lib.pk_workspace_bytes(model.model_id),), dtype=torch.uint8, device="cuda:0")
+    caches_ref = x.kv.caches
+    caches_na = [c.clone() for c in caches_ref]
+    stream = torch.cuda.current_stream().cuda_stream
+    out = (ctypes.c_uint * 3)()
+    old_opt = lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, 1)
+    try:
+        rc, h_ok, i_ok, _ = x.call(lib, lib.pk_decode_noalloc, caches_na, token=3, pos=300, cap=512, n_layers=4)
+        assert rc == 0 and int(i_ok[0]) >= 0
+        assert lib.pk_noalloc_status(stream, 1, out) == 0  # clear whatever an earlier test left
+        assert lib.pk_noalloc_status(stream, 0, out) == 0 and out[0] == 0, list(out)
+        assert lib.pk_test_abort_next_noalloc(stream) == 0
+        rc, h_bad, i_bad, l_bad = x.call(lib, lib.pk_decode_noalloc, caches_na, token=4, pos=301, cap=512,
+                                         n_layers=4)
+        assert rc == 0  # the entry point itself cannot see the failure: it does not synchronise
+        assert torch.isnan(h_bad.float()).all() and (i_bad == -1).all() and torch.isnan(l_bad.float()).all()
+        assert lib.pk_noalloc_status(stream, 0, out) == 0
+        assert out[0] != 0 and out[0] == out[2], list(out)  # the failed step is the last one
+        assert lib.pk_noalloc_status(stream, 1, out) == 0 and out[0] != 0
+        assert lib.pk_noalloc_status(stream, 0, out) == 0 and out[0] == 0, list(out)
+        # the next step runs normally: the same bits as pk_decode on its own copy of the caches
+        for c_na, c_ref in zip(caches_na, caches_ref):
+            c_na.copy_(c_ref)
+        rc, h_na, i_na, l_na = x.call(lib, lib.pk_decode_noalloc, caches_na, token=5, pos=302, cap=512, n_layers=4)
+        assert rc == 0
+        rc, h_ref, i_ref, l_ref = x.call(lib, lib.pk_decode, caches_ref, token=5, pos=302, cap=512, n_layers=4,
+                                         scratch=scratch)
+        assert rc == 0
+        assert _same(h_na, h_ref) and torch.equal(i_na, i_ref) and _same(l_na, l_ref)
+        assert lib.pk_noalloc_status(stream, 0, out) == 0 and out[0] == 0, list(out)
+    finally:
+        lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, old_opt)
