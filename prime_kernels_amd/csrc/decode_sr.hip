@@ -200,8 +200,8 @@ struct PlanSR {
   int att, g, c, leader, t0, t1, S, pos;
   long long slot;
   int ou0, ou1, o0, o1;
-  // LM head rows [v0, v1) in n_lm segments, the first lm_pre of them streamed with the last bracket
-  int v0, v1, n_lm, lm_pre;
+  // LM head rows [v0, v1) in n_lm segments
+  int v0, v1, n_lm;
 
   __device__ __forceinline__ void init(const Params& p, int wg_) {
     constexpr int AX = GG::AX;
@@ -247,15 +247,6 @@ struct PlanSR {
       v0 = v1 = 0;
     }
     n_lm = (v1 - v0 + LM_ROWS_SR - 1) / LM_ROWS_SR;
-    // the last bracket: what it streams before the LM-head segments (F: the last layer's MLP, an
-    // estimate for a lossless stream; a segment that does not fit waits for ring space in any case)
-    constexpr uint32_t WB = GG::WB;
-    constexpr uint32_t SH = G::WF ? uint32_t(scale_stride(G::H)) : 0u, SI = G::WF ? uint32_t(scale_stride(G::I)) : 0u;
-    const uint32_t gu = pad_pkt(G::H * 2) + 2 * pad_pkt(uint32_t(a1 - a0) * G::H * WB) + 2 * pad_pkt(uint32_t(a1 - a0) * SH);
-    const uint32_t last = a ? pad_pkt(G::H * 2)
-                            : pad_pkt(G::H * 2) + gu + pad_pkt(uint32_t(d1 - d0) * G::I * WB) + pad_pkt(uint32_t(d1 - d0) * SI);
-    const uint32_t lmseg = pad_pkt(uint32_t(LM_ROWS_SR) * G::H * 2);
-    lm_pre = last >= RING ? 0 : min(n_lm, int((RING - last) / lmseg));
   }
 };
 
@@ -486,11 +477,9 @@ __device__ __forceinline__ void producer_sr(const Params& p, const PlanSR<G>& P,
       }
     }
   }
-  // LM head: the segments that fit with the last bracket now, the rest once the final hidden
-  // state has arrived (the consumers set go = L + 1)
-  for (int j = 0; j < P.lm_pre && !dead; ++j) issue(R_LM, 0, j);
-  if (P.lm_pre < P.n_lm) wait_go(uint32_t(L + 1));
-  for (int j = P.lm_pre; j < P.n_lm && !dead; ++j) issue(R_LM, 0, j);
+  // LM head: every segment right after the last bracket, each as ring space frees (not waiting for
+  // the consumers' final poll of x: +0.2% at config 3, +0.6% at config 5)
+  for (int j = 0; j < P.n_lm && !dead; ++j) issue(R_LM, 0, j);
   wait_vmcnt<0>();
   publish(dead ? 0x3fffffu : n);
 }
