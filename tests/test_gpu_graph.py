@@ -97,3 +97,39 @@ def _replay_check(batch):
         assert all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(kv.caches, kv_e)), step
         _ = (torch.randn(1024, device=hid_g.device) * 2).sum().item()   # unrelated eager work between replays
     assert mod.workspace(hid_g.device).pending_failure() == (0, 0)
+
+
+def test_one_graph_serves_every_context_range():
+    """The kernel choice is made on the device from the context length: one graph captured with a block
+    table that reaches 9,800 tokens replays steps at contexts in the split-role kernel's narrow range,
+    its wide range and the general kernel's, each bit-identical to the eager step on the same inputs."""
+    _need_gpu()
+    ranges = [1000, 3000, 9800]
+    mod, kv, st, logits, kw = _setup(1, [max(ranges)], layers=2)
+    kv0 = [c.clone() for c in kv.caches]
+    _fill(kv, st, [5], [ranges[0]])
+    mod.decode_step(**kw)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        hid_g, ids_g = mod.decode_step(**kw)
+    torch.cuda.synchronize()
+    for step, ctx in enumerate(ranges):
+        for c, c0 in zip(kv.caches, kv0):
+            c.copy_(c0)
+        _fill(kv, st, [7 + step], [ctx])
+        he, ie = mod.decode_step(**kw)
+        he, ie, le = he.clone(), ie.clone(), logits.clone()
+        kv_e = [c.clone() for c in kv.caches]
+        torch.cuda.synchronize()
+        for c, c0 in zip(kv.caches, kv0):
+            c.copy_(c0)
+        _fill(kv, st, [7 + step], [ctx])
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert not torch.isnan(he.float()).any(), ctx
+        assert torch.equal(hid_g.view(torch.int16), he.view(torch.int16)), ctx
+        assert torch.equal(ids_g, ie) and torch.equal(logits.view(torch.int16), le.view(torch.int16)), ctx
+        assert all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(kv.caches, kv_e)), ctx
+    assert mod.workspace(hid_g.device).pending_failure() == (0, 0)
