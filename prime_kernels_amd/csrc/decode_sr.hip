@@ -106,7 +106,7 @@ struct SG {
   static constexpr int NAU = (IU + GUW - 1) / GUW;      // most act units per workgroup
   static constexpr int NXU = (HU + FG - 1) / FG;        // most x (down) units per group-F workgroup
   static constexpr int NQU = (QU + FG - 1) / FG;        // most qkv units per group-F workgroup
-  static constexpr int NIT = (2 * NAU + NCW - 1) / NCW; // gate/up 6-row items per wave
+  static constexpr int NIT = (2 * NAU + NCW - 1) / NCW; // gate/up 6-row items per wave (one)
   static constexpr int NPART = 2 * NAU > NCW * NXU ? 2 * NAU : NCW * NXU;  // rows of SmemSR::part
   // O rows loaded before the attention partials are polled (10 chunk records per thread leave no
   // room for them in the narrow SmolLM2-135M build without spills)
@@ -123,7 +123,7 @@ struct SG {
   static_assert(C >= 1 && C <= 32 && (!WIDE || C == 32), "chunks per KV head");
   static_assert(TCS + 1 <= MT * 16 * NCW, "a chunk's tiles (and the new token) fit MT tiles per wave");
   static_assert(NQU <= NCW, "the QKV phase gives each wave at most one unit");
-  static_assert(NXU <= 2 && NIT <= 3, "down units and gate/up items per workgroup");
+  static_assert(NXU <= 2 && NIT == 1, "down units and gate/up items per workgroup");
   static_assert(OU * VPU <= 8 * NCW, "the O rows fit 8 per wave");
 };
 
@@ -1611,9 +1611,8 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
       C.wait_filled(C.pos);
       XChunks<G::H, 8> nw;
       normw<G::H>(C, nw, segn);
-      // items: the gate rows of units 0 .. n-1, then the up rows of the same units, 6 rows each;
-      // wave w takes items w, w + NCW, ...  Its first item's weights go from the ring into registers
-      // before h1 arrives, the others (wide layout) are read after.
+      // items: the gate rows of units 0 .. n-1, then the up rows of the same units, 6 rows each, item
+      // w on wave w; its weights go from the ring into registers before h1 arrives.
       const int nunits = P.au1 - P.au0;
       const bool item = C.cw < 2 * nunits;
       uint4 w[VPU][Chunks<G::H>::CPL];
@@ -1640,30 +1639,12 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
 #pragma unroll
             for (int e = 0; e < VPU; ++e) sm.part[C.cw][e] = o[e];
         }
-        if constexpr (S::NIT > 1) {
-#pragma unroll
-          for (int k2 = 1; k2 < S::NIT; ++k2) {
-            const int it = C.cw + NCW * k2;
-            if (it < 2 * nunits) {
-              const int m = it < nunits ? 0 : 1, j = it - m * nunits;
-              if (ge.on)
-                lossless_rows<G::H, VPU>(C, m ? segu : segg, m ? segu_h : segg_h, m ? segu_r : segg_r, ge.first[m],
-                                         j * VPU, w);
-              else
-                wrows<G, G::H, VPU>(C, m ? segu : segg, m ? segu_s : segg_s, j * VPU, w);
-              float o[VPU];
-              dots_w<G::H, VPU>(w, x, o);
-              if (C.lane == 0)
-#pragma unroll
-                for (int e = 0; e < VPU; ++e) sm.part[it][e] = o[e];
-            }
-          }
-        }
         tr(l, 22);
         C.cbar();
         tr(l, 23);
-        // unit j (wave j % NCW): lane e < 6 forms value e, silu(bf16(gate)) * bf16(up); lane 0 stores it
-        auto swiglu = [&](int j) {
+        // unit j (wave j): lane e < 6 forms value e, silu(bf16(gate)) * bf16(up); lane 0 stores it
+        if (C.cw < nunits) {
+          const int j = C.cw;
           const int e = min(C.lane, VPU - 1);
           const float gv = rnd(sm.part[j][e]), uv = rnd(sm.part[nunits + j][e]);
           const float act = rnd(gv / (1.0f + expf(-gv))) * uv;
@@ -1672,10 +1653,7 @@ __device__ __forceinline__ void consumer_f(CSR<G>& C) {
           for (int k = 0; k < VPU; ++k)
             a[k] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, act), k));
           if (C.lane == 0) C.put_x(K_ACT, l, P.au0 + j, C.unit6(a));
-        };
-        if (C.cw < nunits) swiglu(C.cw);
-        if constexpr (S::NAU > NCW)
-          if (C.cw + NCW < nunits) swiglu(C.cw + NCW);
+        }
         tr(l, 24);
       }
       C.release(C.pos);
