@@ -1271,9 +1271,13 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
     }
   }
   C.release(C.pos_kv_end);
-  if (has_new && P.slot >= 0 && hq < 2) {
-    // KV append at slot_mapping[0] (block360_kernel.inc:124-135; slot < 0 skips): lane 16 q (k) and
-    // lane 16 q + 1 (v) store pieces q and q + 4 of the new token, 16 bytes each
+  // KV append at slot_mapping[0] (block360_kernel.inc:124-135; slot < 0 skips): lane 16 q (k) and
+  // lane 16 q + 1 (v) store pieces q and q + 4 of the new token, 16 bytes each.  The wide layout
+  // stores here, the narrow one after the barrier below (the same code), since the barrier waits
+  // for the stores to complete: the narrow layout's last wave publishes no partials and its
+  // workgroups wait for the other chunks next, while the wide layout's next barrier gates its own
+  // slice of them.
+  if (S::WIDE && has_new && P.slot >= 0 && hq < 2) {
     uint16_t* cache = reinterpret_cast<uint16_t*>(const_cast<void*>(sm.kvp[l]));
     const long long e = (P.slot / 16) * p.block_stride + (P.slot % 16) * p.token_stride +
                         (long long)g * p.head_stride + (hq ? p.v_off : p.k_off);
@@ -1306,6 +1310,33 @@ __device__ __forceinline__ void attention_sr(CSR<G>& C, int l, uint32_t seg, Chu
       *reinterpret_cast<float4*>(&sm.wo[w][hq][16 * mf + 4 * pq]) = make_float4(oacc[mf][0], oacc[mf][1], oacc[mf][2], oacc[mf][3]);
   C.cbar();
   if (w == 0 && lane == 0) trace_at(p, l, 19, p.n_layers);
+  if (!S::WIDE && has_new && P.slot >= 0 && hq < 2) {
+    uint16_t* cache = reinterpret_cast<uint16_t*>(const_cast<void*>(sm.kvp[l]));
+    const long long e = (P.slot / 16) * p.block_stride + (P.slot % 16) * p.token_stride +
+                        (long long)g * p.head_stride + (hq ? p.v_off : p.k_off);
+#pragma unroll
+    for (int hv = 0; hv < 2; ++hv) {
+      const int piece = pq + 4 * hv;
+      uint32_t val[4];
+      if (hq == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) val[i] = hv ? khi[i] : klo[i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) val[i] = pack2(in[256 + piece * 8 + 2 * i], in[256 + piece * 8 + 2 * i + 1]);
+      }
+      uint16_t* dst = cache + e + piece * 8;
+      if ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+        st_global16(dst, val[0], val[1], val[2], val[3]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          st_global2(dst + 2 * i, uint16_t(val[i] & 0xffffu));
+          st_global2(dst + 2 * i + 1, uint16_t(val[i] >> 16));
+        }
+      }
+    }
+  }
   if constexpr (S::WIDE) {
     // the chunk's 192 partial sums (3 heads x 64 dims, each added over the waves in wave order, fp32),
     // lane t of wave 0 publishing unit t = values 3t .. 3t + 2
