@@ -2033,7 +2033,7 @@ __device__ __forceinline__ void put_bf16(const ConsumerB<G>& C, int kind, int l,
 // Wave w sums the squares of sequences w, w + 4, ... (lane l: 8-value chunks l and l + 64); the
 // normalisation then runs over 8-value chunks of all rows, 16-byte LDS reads and writes.
 template <class G>
-__device__ __forceinline__ void norm_staged(ConsumerB<G>& C, uint32_t segw) {
+__device__ __forceinline__ void norm_scales(ConsumerB<G>& C) {
   SmemB<G>& sm = C.sm;
   constexpr int CH = G::H / 8;
   constexpr int SPW = (BMAX + NCW - 1) / NCW;  // sequences per wave
@@ -2074,6 +2074,28 @@ __device__ __forceinline__ void norm_staged(ConsumerB<G>& C, uint32_t segw) {
     if (C.lane < SPW && b < C.P.B) sm.rsb[b] = rms_scale(mine, G::H);
   }
   C.cbar();
+}
+
+// 8 staged bf16 values of one row normalised: bf16(w * bf16(x * rs)) per value.
+__device__ __forceinline__ uint4 norm8(uint4 x, uint4 w, float rs) {
+  const uint32_t xv[4] = {x.x, x.y, x.z, x.w}, wu[4] = {w.x, w.y, w.z, w.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t t = pack2(bf_lo(xv[e]) * rs, bf_hi(xv[e]) * rs);
+    o[e] = pack2(bf_lo(wu[e]) * bf_lo(t), bf_hi(wu[e]) * bf_hi(t));
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// The scales, then the staged rows normalised in place (the final norm, whose rows are an output,
+// and the debug build, which captures them; the layers' norms are applied as the projections load
+// their operands).
+template <class G>
+__device__ __forceinline__ void norm_staged(ConsumerB<G>& C, uint32_t segw) {
+  SmemB<G>& sm = C.sm;
+  constexpr int CH = G::H / 8;
+  norm_scales<G>(C);
   // 8-value chunks of all rows, four per thread in flight: loads first, then the stores
   constexpr int U = 4;
   for (int i0 = C.ct; i0 < C.P.B * CH; i0 += U * NCT) {
@@ -2092,14 +2114,7 @@ __device__ __forceinline__ void norm_staged(ConsumerB<G>& C, uint32_t segw) {
       const int i = i0 + u * NCT;
       if (i >= C.P.B * CH) continue;
       const int b = i / CH, c = i - b * CH;
-      const uint32_t x[4] = {v[u].x, v[u].y, v[u].z, v[u].w}, wu[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
-      uint32_t o[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t t = pack2(bf_lo(x[e]) * rs[u], bf_hi(x[e]) * rs[u]);
-        o[e] = pack2(bf_lo(wu[e]) * bf_lo(t), bf_hi(wu[e]) * bf_hi(t));
-      }
-      *reinterpret_cast<uint4*>(sm.xs + b * G::H + c * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+      *reinterpret_cast<uint4*>(sm.xs + b * G::H + c * 8) = norm8(v[u], wv[u], rs[u]);
     }
   }
   C.cbar();
@@ -2108,17 +2123,22 @@ __device__ __forceinline__ void norm_staged(ConsumerB<G>& C, uint32_t segw) {
 // This wave's share of D[row][token] = sum_k W[row][k] * X[token][k] for rows 0..15 of ring segment
 // `seg` (K bf16 per row; rows past the segment read stale ring bytes and are discarded) and the
 // 16 staged token rows.  Lane l holds D[4*(l/16) + j][l % 16] (v_mfma_f32_16x16x32_bf16 layout).
-template <class G, int K>
-__device__ __forceinline__ floatx4 mfma_part(const ConsumerB<G>& C, uint32_t seg, int w, int nw) {
+// With NORM the staged rows are RMS-normalised as they load (norm8 with the scales sm.rsb and the
+// weights of ring segment segw), which is what norm_staged would have stored.
+template <class G, int K, bool NORM = false>
+__device__ __forceinline__ floatx4 mfma_part(const ConsumerB<G>& C, uint32_t seg, int w, int nw, uint32_t segw = 0) {
   constexpr int KS = K / 32;
   const int s0 = KS * w / nw, s1 = KS * (w + 1) / nw;
   const int row = C.lane & 15, kq = (C.lane >> 4) * 8;
+  static_assert(!NORM || BMAX == 16, "one token per MFMA column");
+  const float rs = NORM ? C.sm.rsb[row] : 0.f;
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
   for (int s = s0; s < s1; ++s) {
     const int k = s * 32 + kq;
     const uint4 a = C.ring16(seg + uint32_t(row * K + k) * 2u);
-    const uint4 x = *reinterpret_cast<const uint4*>(C.sm.xs + row * K + k);
+    uint4 x = *reinterpret_cast<const uint4*>(C.sm.xs + row * K + k);
+    if constexpr (NORM) x = norm8(x, C.ring16(segw + uint32_t(k) * 2u), rs);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, x), acc,
                                                  0, 0, 0);
   }
@@ -2127,10 +2147,10 @@ __device__ __forceinline__ floatx4 mfma_part(const ConsumerB<G>& C, uint32_t seg
 
 // Two tiles (gate and up rows of P4), each over the full K by two waves: waves 0-1 the first,
 // waves 2-3 the second; the pair sums are valid in wave 0.
-template <class G, int K>
+template <class G, int K, bool NORM = false>
 __device__ __forceinline__ void mfma_tile_pair(ConsumerB<G>& C, uint32_t seg0, uint32_t seg1, float (*tile)[256],
-                                               floatx4& t0, floatx4& t1) {
-  const floatx4 part = mfma_part<G, K>(C, C.cw < 2 ? seg0 : seg1, C.cw & 1, 2);
+                                               floatx4& t0, floatx4& t1, uint32_t segw = 0) {
+  const floatx4 part = mfma_part<G, K, NORM>(C, C.cw < 2 ? seg0 : seg1, C.cw & 1, 2, segw);
 #pragma unroll
   for (int j = 0; j < 4; ++j) tile[C.cw][C.lane * 4 + j] = part[j];
   C.cbar();
@@ -2144,9 +2164,9 @@ __device__ __forceinline__ void mfma_tile_pair(ConsumerB<G>& C, uint32_t seg0, u
 
 // Full tile, K split over the four waves; the partials are summed in wave order (deterministic)
 // and the result is valid in wave 0.
-template <class G, int K>
-__device__ __forceinline__ floatx4 mfma_tile(ConsumerB<G>& C, uint32_t seg, float (*tile)[256]) {
-  const floatx4 part = mfma_part<G, K>(C, seg, C.cw, NCW);
+template <class G, int K, bool NORM = false>
+__device__ __forceinline__ floatx4 mfma_tile(ConsumerB<G>& C, uint32_t seg, float (*tile)[256], uint32_t segw = 0) {
+  const floatx4 part = mfma_part<G, K, NORM>(C, seg, C.cw, NCW, segw);
 #pragma unroll
   for (int j = 0; j < 4; ++j) tile[C.cw][C.lane * 4 + j] = part[j];
   C.cbar();
@@ -2677,9 +2697,15 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
       }
       C.wait_filled(C.pos);
       tr(l, 2);
-      norm_staged<G>(C, segn);
-      if (DBG && p.debug) dbg_xs(dl(l) + Dbg<G>::NORM1);
-      const floatx4 acc = mfma_tile<G, G::H>(C, segq, sm.tile);
+      floatx4 acc;
+      if constexpr (DBG) {
+        norm_staged<G>(C, segn);
+        if (p.debug) dbg_xs(dl(l) + Dbg<G>::NORM1);
+        acc = mfma_tile<G, G::H>(C, segq, sm.tile);
+      } else {
+        norm_scales<G>(C);
+        acc = mfma_tile<G, G::H, true>(C, segq, sm.tile, segn);
+      }
       C.release(C.pos);
       skew_delay(p.skew, P.wg, l, 16);
       if (C.cw == 0 && tok < B)
@@ -2736,10 +2762,15 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
       }
       C.wait_filled(C.pos);
       tr(l, 13);
-      norm_staged<G>(C, segn);
-      if (DBG && p.debug) dbg_xs(dl(l) + Dbg<G>::NORM2);
       floatx4 gt = {0.f, 0.f, 0.f, 0.f}, up = {0.f, 0.f, 0.f, 0.f};
-      mfma_tile_pair<G, G::H>(C, segg, segu, sm.tile, gt, up);
+      if constexpr (DBG) {
+        norm_staged<G>(C, segn);
+        if (p.debug) dbg_xs(dl(l) + Dbg<G>::NORM2);
+        mfma_tile_pair<G, G::H>(C, segg, segu, sm.tile, gt, up);
+      } else {
+        norm_scales<G>(C);
+        mfma_tile_pair<G, G::H, true>(C, segg, segu, sm.tile, gt, up, segn);
+      }
       C.release(C.pos);
       if (C.cw == 0 && tok < B)
 #pragma unroll
