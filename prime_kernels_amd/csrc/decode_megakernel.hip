@@ -1721,7 +1721,6 @@ struct SmemB {
     float cst[IPW][2][3];             // chunk softmax max / sum per item and head
     float gml[IPW][2][3];             // global (all chunks) max / sum per item and head
     float wo[2][NCW][3][64];          // per-wave P.V partials, double-buffered over items
-    float csr[BMAX][64];              // rotary cos | sin of each sequence's position
   };
   uint8_t ring[RING_B];
   union {
@@ -1766,7 +1765,8 @@ struct PlanB {
   __device__ __forceinline__ void init(const Params& p, const int32_t* sS, int wg_) {
     wg = wg_;
     B = p.B;
-    q0 = split_lo(G::QKV, NWG, wg); q1 = split_lo(G::QKV, NWG, wg + 1);
+    // QKV slots (qkv_row order) in whole RoPE pairs: the QKV phase applies RoPE to its own rows
+    q0 = 2 * split_lo(G::QKV / 2, NWG, wg); q1 = 2 * split_lo(G::QKV / 2, NWG, wg + 1);
     o0 = split_lo(G::H, NWG, wg);   o1 = split_lo(G::H, NWG, wg + 1);
     a0 = split_lo(G::I, NWG, wg);   a1 = split_lo(G::I, NWG, wg + 1);
     d0 = split_lo(G::H, NWG, wg);   d1 = split_lo(G::H, NWG, wg + 1);
@@ -1841,14 +1841,13 @@ __device__ __forceinline__ uint32_t kvb_slot(int j, int part) {
 // Batched producer: per layer norm1, QKV rows, the B rotary rows, the K of every item, the V of
 // every item, O rows, norm2, gate rows, up rows, down rows; then the final norm and LM-head rows.
 // ------------------------------------------------------------------------------------------------
-enum SegB { B_NORM1, B_QKV, B_CS, B_K, B_V, B_O, B_NORM2, B_GATE, B_UP, B_DOWN, B_FNORM, B_LM };
+enum SegB { B_NORM1, B_QKV, B_K, B_V, B_O, B_NORM2, B_GATE, B_UP, B_DOWN, B_FNORM, B_LM };
 
 template <class G>
 __device__ __forceinline__ uint32_t segb_bytes(const PlanB<G>& P, const ItemB* it, int kind, int idx, int cs_fp32) {
   switch (kind) {
     case B_NORM1: case B_NORM2: case B_FNORM: return G::H * 2;
     case B_QKV: return uint32_t(P.q1 - P.q0) * G::H * 2;
-    case B_CS: return P.ni ? uint32_t(P.B) * (cs_fp32 ? 256u : 128u) : 0u;
     case B_K: case B_V: return uint32_t(it[idx].t1 - it[idx].t0) * 128u;
     case B_O: return uint32_t(P.o1 - P.o0) * G::H * 2;
     case B_GATE: case B_UP: return uint32_t(P.a1 - P.a0) * G::H * 2;
@@ -1907,7 +1906,7 @@ __device__ __forceinline__ void producer_b(const Params& p, const PlanB<G>& P, S
     int blkv = 0;  // K/V segments: lane i holds the block id of the item's i-th 16-token block
     switch (kind) {
       case B_NORM1: base = u8(Lw.norm1); break;
-      case B_QKV: base = u8(Lw.qkv) + size_t(P.q0) * G::H * 2; break;
+      case B_QKV: base = u8(Lw.qkv); break;
       case B_K: case B_V:
         ib = sm.it[idx].b;
         ig = sm.it[idx].g;
@@ -1924,7 +1923,6 @@ __device__ __forceinline__ void producer_b(const Params& p, const PlanB<G>& P, S
       case B_LM: base = u8(p.embed) + size_t(P.v0 + idx * LM_ROWS) * G::H * 2; break;
       default: break;
     }
-    const uint32_t cs_row = p.cs_fp32 ? 256u : 128u;
     for (uint32_t i = (uint32_t(pw) + NPW - n % NPW) % NPW; i < npk && !dead; i += NPW) {
       const uint32_t gn = n + i;
       if ((gn + 1) * PKT > avail && (gn + 1) * PKT > (avail = cmin() + RING_B)) {
@@ -1947,9 +1945,10 @@ __device__ __forceinline__ void producer_b(const Params& p, const PlanB<G>& P, S
           const long long e = (long long)blk * p.block_stride + (long long)(t & 15) * p.token_stride +
                               (long long)ig * p.head_stride + (kind == B_V ? p.v_off : p.k_off) + part * 8;
           src = cache + e * 2;
-        } else if (kind == B_CS) {
-          const int b = int(off / cs_row);
-          src = reinterpret_cast<const uint8_t*>(p.cos_sin) + size_t(sm.sPos[b]) * cs_row + (off % cs_row);
+        } else if (kind == B_QKV) {
+          // the workgroup's slots in order, slot s being projection row qkv_row(s)
+          const uint32_t r = off / uint32_t(G::H * 2);
+          src = base + size_t(qkv_row<G>(P.q0 + int(r))) * G::H * 2 + (off - r * uint32_t(G::H * 2));
         } else {
           src = base + off;
         }
@@ -1963,7 +1962,6 @@ __device__ __forceinline__ void producer_b(const Params& p, const PlanB<G>& P, S
   for (int l = 0; l < p.n_layers && !dead; ++l) {
     issue_segment(B_NORM1, l, 0);
     issue_segment(B_QKV, l, 0);
-    issue_segment(B_CS, l, 0);
     for (int k = 0; k < P.ni && !dead; ++k) issue_segment(B_K, l, k);
     for (int k = 0; k < P.ni && !dead; ++k) issue_segment(B_V, l, k);
     issue_segment(B_O, l, 0);
@@ -2195,7 +2193,7 @@ __device__ __forceinline__ floatx4 mfma_tile(ConsumerB<G>& C, uint32_t seg, floa
 // Records and statistics are reused by every layer, so their tags carry the layer as well.
 // ------------------------------------------------------------------------------------------------
 template <class G, bool DBG>
-__device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t segcs) {
+__device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l) {
   const Params& p = C.p;
   const PlanB<G>& P = C.P;
   SmemB<G>& sm = C.sm;
@@ -2237,7 +2235,11 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
       for (int gi = 0; gi < MAXG; ++gi)
         if (((pend >> gi) & 1u) && C.ok2(v[gi])) {
           const int gidx = C.ct + gi * NCT, k = gidx / GPI, e = (gidx - k * GPI) * 2;
-          *reinterpret_cast<float2*>(&sm.at.qb[k][e]) = make_float2(bf_lo(v[gi].x), bf_lo(v[gi].z));
+          // q heads and the new k (roped by their producers) as bf16 into qr, the new v into qb
+          if (e < 256)
+            *reinterpret_cast<uint32_t*>(&sm.at.qr[k][e >> 6][e & 63]) = (v[gi].x & 0xffffu) | (v[gi].z << 16);
+          else
+            *reinterpret_cast<float2*>(&sm.at.qb[k][e]) = make_float2(bf_lo(v[gi].x), bf_lo(v[gi].z));
           pend &= ~(1u << gi);
         }
       if (!pend) break;
@@ -2247,29 +2249,7 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l, uint32_t seg
         if ((pend >> gi) & 1u) v[gi] = ld_dev128(r, uint32_t(wd[gi]) * 4u);
     }
   }
-  if (P.ni) {  // every sequence's rotary row, out of the ring (its segment is released with item 0's K)
-    C.wait_filled(C.pos);
-    for (int i = C.ct; i < P.B * 64; i += NCT) {
-      const int b = i >> 6, f = i & 63;
-      sm.at.csr[b][f] = p.cs_fp32 ? __uint_as_float(C.ring4(segcs + uint32_t(b) * 256u + uint32_t(f) * 4u))
-                                  : bf2f(*reinterpret_cast<const uint16_t*>(
-                                        sm.ring + ((segcs + uint32_t(b) * 128u + uint32_t(f) * 2u) & (RING_B - 1))));
-    }
-  }
-  C.cbar();
-  // RoPE of every item's q heads (and the leaders' new k) once, all waves at once: pair (d, d + 32)
-  // of a head gives bf16(bf16(x cos) + bf16(-y sin)) and bf16(bf16(y cos) + bf16(x sin)), HF's
-  // rounding (modeling_llama.py:138-160); the items' score tiles read the bf16 pieces from qr
-  for (int i = C.ct; i < P.ni * 4 * 32; i += NCT) {
-    const int k = i >> 7, hv = (i >> 5) & 3, d = i & 31;
-    if (hv == 3 && sm.it[k].c != sm.it[k].C - 1) continue;
-    const float* head = sm.at.qb[k] + hv * 64;
-    const float* cs = sm.at.csr[sm.it[k].b];
-    const float x = head[d], y = head[d + 32], c = cs[d], s = cs[32 + d];
-    sm.at.qr[k][hv][d] = uint16_t(f2bf(rnd(rnd(x * c) + rnd((-y) * s))));
-    sm.at.qr[k][hv][d + 32] = uint16_t(f2bf(rnd(rnd(y * c) + rnd(x * s))));
-  }
-  C.cbar();
+  C.cbar();  // every item's q (and new k, v) in LDS for all waves
   tri(4);
   // ---- A: scores and per-wave statistics of every item ----
   // Scores on the matrix cores: D[token][head] = K[token][:] . q[head][:] as 16-token tiles,
@@ -2672,6 +2652,21 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
   // 4 attention start, 5-7 passes A-C done, 8 attn published, 9-11 P3, 12-14 P4, 15-17 P5).
   auto tr = [&](int l, int ev) { if (C.ct == 0) trace_at(p, l, ev, p.n_layers); };
   if (C.ct == 0) trace_tail(p, 0);
+  // cos and sin of sequence tok's position for the two RoPE pairs of this lane's QKV slots (the same
+  // in every layer; wave 0 applies them)
+  float rope_c[2] = {1.f, 1.f}, rope_s[2] = {0.f, 0.f};
+  if (C.cw == 0 && tok < B)
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int sl = P.q0 + orow + 2 * k;
+      if (sl < (G::NH + G::KVH) * 64) {
+        const size_t at = size_t(sm.sPos[tok]) * 64 + ((sl >> 1) & 31);
+        rope_c[k] = p.cs_fp32 ? reinterpret_cast<const float*>(p.cos_sin)[at]
+                              : bf2f(reinterpret_cast<const uint16_t*>(p.cos_sin)[at]);
+        rope_s[k] = p.cs_fp32 ? reinterpret_cast<const float*>(p.cos_sin)[at + 32]
+                              : bf2f(reinterpret_cast<const uint16_t*>(p.cos_sin)[at + 32]);
+      }
+    }
   for (int l = 0; l < p.n_layers; ++l) {
     // ---------------- P1: RMSNorm(x) + QKV ----------------
     C.refresh();
@@ -2708,20 +2703,33 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
       }
       C.release(C.pos);
       skew_delay(p.skew, P.wg, l, 16);
-      if (C.cw == 0 && tok < B)
+      if (C.cw == 0 && tok < B) {
+        // q = bf16(W x); slot pairs (orow, orow + 1), (orow + 2, orow + 3) of the q and k parts get
+        // HF's RoPE, bf16(bf16(x cos) + bf16(rotate_half(x) sin)) (modeling_llama.py:138-160)
+        float o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = rnd(acc[j]);
+#pragma unroll
+        for (int j = 0; j < 4; j += 2)
+          if (P.q0 + orow + j < (G::NH + G::KVH) * 64) {
+            const float x0 = o[j], x1 = o[j + 1], cs = rope_c[j / 2], sn = rope_s[j / 2];
+            o[j] = rnd(rnd(x0 * cs) + rnd((-x1) * sn));
+            o[j + 1] = rnd(rnd(x1 * cs) + rnd(x0 * sn));
+          }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           if (orow + j < nq) {
-            st_dev64(reinterpret_cast<uint64_t*>(p.ws + W::xw(X_QKV, l, tok, P.q0 + orow + j)), C.w64(acc[j]));
-            if (DBG && p.debug) dl(l)[Dbg<G>::QKV + size_t(tok) * G::QKV + P.q0 + orow + j] = uint16_t(f2bf(acc[j]));
+            const int row = qkv_row<G>(P.q0 + orow + j);
+            st_dev64(reinterpret_cast<uint64_t*>(p.ws + W::xw(X_QKV, l, tok, row)), C.w64(o[j]));
+            if (DBG && p.debug) dl(l)[Dbg<G>::QKV + size_t(tok) * G::QKV + row] = uint16_t(f2bf(acc[j]));
           }
+      }
       tr(l, 3);
     }
     // ---------------- P2: attention ----------------
     C.refresh();
     {
-      const uint32_t segcs = C.next_seg(P.ni ? uint32_t(B) * (p.cs_fp32 ? 256u : 128u) : 0u);
-      attention_b<G, DBG>(C, l, segcs);
+      attention_b<G, DBG>(C, l);
       tr(l, 8);
     }
     // ---------------- P3: O + residual ----------------

@@ -127,18 +127,6 @@ struct SG {
   static_assert(OU * VPU <= 8 * NCW, "the O rows fit 8 per wave");
 };
 
-// The qkv vector in slot order.  Its q and k parts are laid out by RoPE pair: slots 2p and 2p + 1
-// hold dims d and d + 32 (d = p % 32) of head p / 32 (the q heads, then the k heads), so that the
-// workgroup producing a 6-value unit holds both halves of its three pairs and applies RoPE itself;
-// the v part is in row order.  qkv_row(s) is the projection row of slot s.
-template <class G>
-__device__ __forceinline__ int qkv_row(int s) {
-  constexpr int ROPE = (G::NH + G::KVH) * 64;
-  if (s >= ROPE) return s;
-  const int pr = s >> 1;
-  return (pr >> 5) * 64 + (pr & 31) + 32 * (s & 1);
-}
-
 // Workspace (uncached, 32-bit words), placed after the general kernels' layout (base word SR0) so
 // that no word is ever read in a format it was not written in; the header (epoch, abort) is shared.
 enum SKind { K_H1, K_ACT, K_X, K_XQ, K_ATT, NK };

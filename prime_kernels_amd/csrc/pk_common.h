@@ -576,6 +576,18 @@ __device__ __forceinline__ uint32_t step_epoch(const uint32_t* ws) {
 
 // Balanced split of n items over `parts`: part i gets [split_lo(n, parts, i), split_lo(n, parts, i + 1)).
 __host__ __device__ constexpr int split_lo(int n, int parts, int i) { return int((long long)n * i / parts); }
+// The qkv vector in slot order.  Its q and k parts are laid out by RoPE pair: slots 2p and 2p + 1
+// hold dims d and d + 32 (d = p % 32) of head p / 32 (the q heads, then the k heads), so that the
+// workgroup producing a unit of slots holds both halves of its pairs and applies RoPE itself;
+// the v part is in row order.  qkv_row(s) is the projection row of slot s.
+template <class G>
+__device__ __forceinline__ int qkv_row(int s) {
+  constexpr int ROPE = (G::NH + G::KVH) * 64;
+  if (s >= ROPE) return s;
+  const int pr = s >> 1;
+  return (pr >> 5) * 64 + (pr & 31) + 32 * (s & 1);
+}
+
 // Bytes of a ring segment rounded up to whole LDS-DMA packets.
 __host__ __device__ constexpr uint32_t pad_pkt(uint32_t b) { return (b + PKT - 1) & ~(PKT - 1); }
 
