@@ -2643,7 +2643,13 @@ __device__ __forceinline__ void attention_b(ConsumerB<G>& C, int l) {
         if (kk < nc) O += __uint_as_float(uint32_t(ro[kk]));
     }
     O += sm.at.own[k][w * 64 + lane];
-    put_bf16<G>(C, X_ATTN, l, G::H, it.b, (it.g * 3 + w) * 64 + lane, O);
+    {  // lane pairs: the even lane stores both values in one 4-byte store
+      const float On = dpp<0xb1>(0.f, O);  // quad_perm [1,0,3,2]: the pair's other lane
+      if ((lane & 1) == 0) {
+        const __amdgpu_buffer_rsrc_t r = rsrc(p.ws + WSB<G>::data(X_ATTN, l));
+        __builtin_amdgcn_raw_buffer_store_b32(pack2(O, On), r, (it.b * G::H + (it.g * 3 + w) * 64 + lane) * 2, 0, 16);
+      }
+    }
     if (DBG && p.debug) {
       const size_t e = size_t(it.b) * G::H + (it.g * 3 + w) * 64 + lane;
       p.debug[size_t(l) * Dbg<G>::LAYER + Dbg<G>::ATTN + e] = uint16_t(f2bf(O));
