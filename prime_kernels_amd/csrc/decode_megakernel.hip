@@ -2744,13 +2744,30 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
             o[j] = rnd(rnd(x0 * cs) + rnd((-x1) * sn));
             o[j + 1] = rnd(rnd(x1 * cs) + rnd(x0 * sn));
           }
+        // slots j and j + 2 are projection rows r and r + 1 (within a head or in the v part): their
+        // two words {value, tag} in one 16-byte store when r is even
+        const __amdgpu_buffer_rsrc_t rq = rsrc(p.ws);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (orow + j < nq) {
-            const int row = qkv_row<G>(P.q0 + orow + j);
-            st_dev64(reinterpret_cast<uint64_t*>(p.ws + W::xw(X_QKV, l, tok, row)), C.w64(o[j]));
-            if (DBG && p.debug) dl(l)[Dbg<G>::QKV + size_t(tok) * G::QKV + row] = uint16_t(f2bf(acc[j]));
+        for (int j = 0; j < 2; ++j) {
+          const int s0 = P.q0 + orow + (P.q0 + orow >= (G::NH + G::KVH) * 64 ? 2 * j : j);
+          const int s1 = s0 + (P.q0 + orow >= (G::NH + G::KVH) * 64 ? 1 : 2);
+          const int j0 = s0 - P.q0 - orow, j1 = s1 - P.q0 - orow;
+          const bool ok0 = orow + j0 < nq, ok1 = orow + j1 < nq;
+          if (!ok0) continue;
+          const int r0 = qkv_row<G>(s0), r1 = qkv_row<G>(s1);
+          if (ok1 && r1 == r0 + 1 && (r0 & 1) == 0) {
+            const u32x4 v = {f2bf(o[j0]), C.tag32, f2bf(o[j1]), C.tag32};
+            __builtin_amdgcn_raw_buffer_store_b128(v, rq, int(W::xw(X_QKV, l, tok, r0) * 4u), 0, 16);
+          } else {
+            st_dev64(reinterpret_cast<uint64_t*>(p.ws + W::xw(X_QKV, l, tok, r0)), C.w64(o[j0]));
+            if (ok1) st_dev64(reinterpret_cast<uint64_t*>(p.ws + W::xw(X_QKV, l, tok, r1)), C.w64(o[j1]));
           }
+        }
+        if (DBG && p.debug)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (orow + j < nq)
+              dl(l)[Dbg<G>::QKV + size_t(tok) * G::QKV + qkv_row<G>(P.q0 + orow + j)] = uint16_t(f2bf(acc[j]));
       }
       tr(l, 3);
     }
