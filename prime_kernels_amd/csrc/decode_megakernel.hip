@@ -1754,6 +1754,7 @@ template <class G>
 struct PlanB {
   int wg, B;
   int q0, q1, o0, o1, a0, a1, d0, d1, v0, v1, n_lm;
+  int db0, db1;  // sequences of this workgroup's down rows
   int tc;      // cached tokens per attention chunk
   int nitems;  // attention items over all workgroups
   int ni;      // items of this workgroup: wg, wg + NWG, ...
@@ -1769,7 +1770,19 @@ struct PlanB {
     q0 = 2 * split_lo(G::QKV / 2, NWG, wg); q1 = 2 * split_lo(G::QKV / 2, NWG, wg + 1);
     o0 = split_lo(G::H, NWG, wg);   o1 = split_lo(G::H, NWG, wg + 1);
     a0 = split_lo(G::I, NWG, wg);   a1 = split_lo(G::I, NWG, wg + 1);
+#if PK_B_DOWN_SPLIT
+    // down: 128 row groups, each shared by workgroups wg and wg ^ 8 (one XCD, so the second read of
+    // the rows hits its L2), one taking the first half of the sequences and the other the rest, so
+    // that each stages half the act array
+    {
+      const int grp = (wg >> 4) * 8 + (wg & 7), half = (wg >> 3) & 1;
+      d0 = split_lo(G::H, NWG / 2, grp); d1 = split_lo(G::H, NWG / 2, grp + 1);
+      db0 = half ? (B + 1) / 2 : 0;      db1 = half ? B : (B + 1) / 2;
+    }
+#else
     d0 = split_lo(G::H, NWG, wg);   d1 = split_lo(G::H, NWG, wg + 1);
+    db0 = 0; db1 = B;
+#endif
     if (p.lm_head) { v0 = split_lo(G::V, NWG, wg); v1 = split_lo(G::V, NWG, wg + 1); }
     else { v0 = v1 = 0; }
     n_lm = (v1 - v0 + LM_ROWS - 1) / LM_ROWS;
@@ -1999,7 +2012,7 @@ __device__ __forceinline__ void publish_flag(ConsumerB<G>& C, int kind, int l) {
 
 // Wait until all workgroups have published (kind, l), then copy the [B][K] bf16 array into xs.
 template <class G>
-__device__ __forceinline__ void stage_flagged(ConsumerB<G>& C, int kind, int l, int K) {
+__device__ __forceinline__ void stage_flagged(ConsumerB<G>& C, int kind, int l, int K, int b0 = 0, int b1 = -1) {
   const uint32_t* flags = C.p.ws + WSB<G>::flag(kind, l, 0, C.P.wg % WSB<G>::FREP);
   {
     Spin spin(C.p.ws, C.tag32, 8);
@@ -2008,9 +2021,11 @@ __device__ __forceinline__ void stage_flagged(ConsumerB<G>& C, int kind, int l, 
         if (C.dead || !spin.again()) { C.dead = true; break; }
   }
   C.cbar();
-  const uint8_t* src = reinterpret_cast<const uint8_t*>(C.p.ws + WSB<G>::data(kind, l));
-  const uint32_t bytes = uint32_t(C.P.B) * uint32_t(K) * 2u;
-  const uint32_t lds = uint32_t(reinterpret_cast<uintptr_t>(C.sm.xs));
+  // rows [b0, b1) of the array (all by default), to the same rows of xs
+  if (b1 < 0) b1 = C.P.B;
+  const uint8_t* src = reinterpret_cast<const uint8_t*>(C.p.ws + WSB<G>::data(kind, l)) + size_t(b0) * K * 2;
+  const uint32_t bytes = uint32_t(b1 - b0) * uint32_t(K) * 2u;
+  const uint32_t lds = uint32_t(reinterpret_cast<uintptr_t>(C.sm.xs + size_t(b0) * K));
   for (uint32_t pk = uint32_t(C.cw); pk * PKT < bytes; pk += NCW) {
     const uint32_t off = pk * PKT + uint32_t(C.lane) * 16u;
     if (off < bytes) dma16_sc1(src + off, __builtin_amdgcn_readfirstlane(lds + pk * PKT));
@@ -2851,13 +2866,13 @@ __device__ __forceinline__ void consumer_b(const Params& p, const PlanB<G>& P, S
     C.refresh();
     {
       const uint32_t segd = C.next_seg(uint32_t(nd) * G::I * 2);
-      stage_flagged<G>(C, X_ACT, l, G::I);
+      stage_flagged<G>(C, X_ACT, l, G::I, P.db0, P.db1);
       tr(l, 15);
       C.wait_filled(C.pos);
       tr(l, 16);
       const floatx4 acc = mfma_tile<G, G::I>(C, segd, sm.tile);
       C.release(C.pos);
-      if (C.cw == 0 && tok < B) {
+      if (C.cw == 0 && tok >= P.db0 && tok < P.db1) {
         float yv[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {

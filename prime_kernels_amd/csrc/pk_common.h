@@ -62,6 +62,9 @@ constexpr int DEPTH = PK_DMA_DEPTH;      // packets in flight per producer wave 
 // are issued (or its queue drains), so a deep queue hides the end of each K or V segment from the
 // consumers until the next segment has streamed; at config 4 depth 32 / 16 / 8 / 4 / 3 / 2 gave
 // 7,695 / 7,709 / 7,892 / 8,362 / 8,409 / 8,401 tok/s.
+#ifndef PK_B_DOWN_SPLIT
+#define PK_B_DOWN_SPLIT 1                // batched down: two workgroups per row group, half the sequences each
+#endif
 #ifndef PK_DMA_DEPTH_B
 #define PK_DMA_DEPTH_B 3
 #endif
