@@ -61,9 +61,12 @@ constexpr int VPU = 6;                   // bf16 values per 16-byte unit
 constexpr int REP = PK_SR_REP;           // copies of each cross-XCD unit
 constexpr int UPL = PK_SR_UPL;           // cross-XCD units per 64-byte line (fewer: fewer polls per line)
 #ifndef PK_SR_DEPTH
-#define PK_SR_DEPTH 8
+#define PK_SR_DEPTH 4
 #endif
-constexpr int DEPTH_SR = PK_SR_DEPTH;    // DMA packets in flight per producer wave (narrow layout)
+// DMA packets in flight per producer wave (narrow layout; depth 2 / 3 / 4 / 6 / 8 / 12: config 3
+// 2,081 / 2,112 / 2,116 / 2,114 / 2,108 / 2,108 tok/s, config 2 2,447 / 2,450 / 2,450 / 2,441 /
+// 2,399 / 2,398)
+constexpr int DEPTH_SR = PK_SR_DEPTH;
 #ifndef PK_SR_DEPTH_W
 #define PK_SR_DEPTH_W 4   // wide layout (config 5: 2 / 3 / 4 / 6 / 8 / 16 = 1,691 / 1,698 / 1,701 / 1,663 / 1,642 / 1,584 tok/s)
 #endif
