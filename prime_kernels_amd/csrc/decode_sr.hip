@@ -76,7 +76,7 @@ constexpr int DEPTH_SR = PK_SR_DEPTH;
 #ifndef PK_SR_PRIO_W
 #define PK_SR_PRIO_W 1    // wide layout: consumer waves at issue priority 1 (0: -7% at config 5)
 #endif
-constexpr int LM_ROWS_SR = 24;           // LM-head rows per ring segment, 6 per consumer wave (16: -1.5%)
+
 
 // 16-token tiles of a chunk per consumer wave (attention): at most MT
 constexpr int MT = 5;
@@ -117,6 +117,9 @@ struct SG {
   static constexpr uint32_t WB = G::WF ? 1u : 2u;       // bytes per projection weight
   static constexpr int DEPTH = WIDE ? PK_SR_DEPTH_W : DEPTH_SR;  // DMA packets in flight per producer wave
   static constexpr int PRIO = WIDE ? PK_SR_PRIO_W : 1;           // consumer waves' issue priority
+  // LM-head rows per ring segment (narrow 32, 8 per consumer wave: config 3 +0.2%, config 2 +0.45%
+  // against 24; wide 24: 32 gave -0.3% at config 5, -0.8% at 4096 tokens; 16: -1.5%)
+  static constexpr int LMR = WIDE ? 24 : 32;
   // softmax statistics: each wave publishes its own (narrow), or each chunk combines its waves first
   // and publishes once (wide: 32 chunks x 4 waves would be 256 units for every wave to poll)
   static constexpr bool STATS_CHUNK = WIDE && PK_SR_STATS_CHUNK_W;
@@ -237,7 +240,7 @@ struct PlanSR {
     } else {
       v0 = v1 = 0;
     }
-    n_lm = (v1 - v0 + LM_ROWS_SR - 1) / LM_ROWS_SR;
+    n_lm = (v1 - v0 + GG::LMR - 1) / GG::LMR;
   }
 };
 
@@ -277,8 +280,8 @@ __device__ __forceinline__ uint32_t sr_bytes(const PlanSR<G>& P, int kind, int l
     case R_KV: return uint32_t(P.t1 - P.t0) * 256u;
     case R_O: return uint32_t(P.o1 - P.o0) * G::H * WB;
     default: {
-      const int r0 = P.v0 + lm_index * LM_ROWS_SR;
-      return uint32_t(min(LM_ROWS_SR, P.v1 - r0)) * G::H * 2;
+      const int r0 = P.v0 + lm_index * SG<G>::LMR;
+      return uint32_t(min(SG<G>::LMR, P.v1 - r0)) * G::H * 2;
     }
   }
 }
@@ -372,7 +375,7 @@ __device__ __forceinline__ void producer_sr(const Params& p, const PlanSR<G>& P,
       case R_O: base = u8(Lw.o) + size_t(P.o0) * G::H * WB; break;
       case R_O_S: base = Lw.o_s + size_t(P.o0) * SH; break;
       case R_FNORM: base = u8(p.final_norm); break;
-      default: base = u8(p.embed) + size_t(P.v0 + lm_index * LM_ROWS_SR) * G::H * 2; break;
+      default: base = u8(p.embed) + size_t(P.v0 + lm_index * SG<G>::LMR) * G::H * 2; break;
     }
     for (uint32_t i = (uint32_t(pw) + NPW - n % NPW) % NPW; i < npk && !dead; i += NPW) {
       const uint32_t gn = n + i;
@@ -1488,10 +1491,10 @@ __device__ __forceinline__ void lm_head_sr(CSR<G>& C) {
   int best_i = 0x7fffffff;
   for (int j = 0; j < P.n_lm; ++j) {
     const uint32_t seg = C.next_seg(sr_bytes(P, R_LM, j));
-    const int r0 = P.v0 + j * LM_ROWS_SR;
-    const int nrows = min(LM_ROWS_SR, P.v1 - r0);
+    const int r0 = P.v0 + j * S::LMR;
+    const int nrows = min(S::LMR, P.v1 - r0);
     C.wait_filled(C.pos);
-    constexpr int RW = LM_ROWS_SR / NCW;  // rows cw RW .. cw RW + RW - 1 of the segment
+    constexpr int RW = S::LMR / NCW;  // rows cw RW .. cw RW + RW - 1 of the segment
     float out[RW];
     dots_n<G::H, RW>(C, seg, C.cw * RW, x, out);
     C.release(C.pos);
