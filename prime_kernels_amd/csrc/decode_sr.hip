@@ -55,11 +55,13 @@ constexpr int VPU = 6;                   // bf16 values per 16-byte unit
 #ifndef PK_SR_REP
 #define PK_SR_REP 1
 #endif
-#ifndef PK_SR_UPL
-#define PK_SR_UPL 1
+#ifndef PK_SR_UPL_360
+#define PK_SR_UPL_360 2
+#endif
+#ifndef PK_SR_UPL_135
+#define PK_SR_UPL_135 1
 #endif
 constexpr int REP = PK_SR_REP;           // copies of each cross-XCD unit
-constexpr int UPL = PK_SR_UPL;           // cross-XCD units per 64-byte line (fewer: fewer polls per line)
 #ifndef PK_SR_DEPTH
 #define PK_SR_DEPTH 4
 #endif
@@ -139,6 +141,9 @@ enum SKind { K_H1, K_ACT, K_X, K_XQ, K_ATT, NK };
 template <class G>
 struct SWS {
   using S = SG<G>;
+  // cross-XCD units per 64-byte line (fewer: fewer polls per line).  360M, 2 against 1: config 3
+  // +0.8%, config 5 +1.0%, 4096 tokens +3.0%; 135M, 2 against 1: config 2 -1.5%
+  static constexpr int UPL = G::H == 960 ? PK_SR_UPL_360 : PK_SR_UPL_135;
   static constexpr int LINES = (S::IU + UPL - 1) / UPL;
   static constexpr int NKL = S::WIDE ? NK : K_ATT;            // vector kinds of the layout (narrow: no K_ATT)
   static constexpr int SLOTS = (G::L + 1) * NKL;
