@@ -3480,10 +3480,23 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
     uint32_t* region = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(state->ws) + ws_general_bytes());
     uint8_t* rec = reinterpret_cast<uint8_t*>(state->rec);
     const int narrow = sr_max_seq(model, 0);
+    int e = PK_OK;
     p.sr_min_s = 0;
-    p.sr_max_s = narrow;
-    int e = sr_launch(model, G::WF, 0, p, region, reinterpret_cast<uint32_t*>(rec + rec_general_bytes()), s,
+    if (G::WF == 0) {
+      // a narrow build with fewer attention chunks for the shortest contexts, where the model has one
+      const int small = sr_max_seq(model, 2);
+      if (small > 0) {
+        p.sr_max_s = small;
+        e = sr_launch(model, 0, 2, p, region, reinterpret_cast<uint32_t*>(rec + rec_general_bytes()), s,
                       opt_cooperative());
+        if (e != PK_OK) return e;
+        if (max_seq_len <= small) return PK_OK;  // no context can reach another kernel
+        p.sr_min_s = small;
+      }
+    }
+    p.sr_max_s = narrow;
+    e = sr_launch(model, G::WF, 0, p, region, reinterpret_cast<uint32_t*>(rec + rec_general_bytes()), s,
+                  opt_cooperative());
     if (e != PK_OK) return e;
     if (max_seq_len <= p.sr_max_s) return PK_OK;  // no context can reach another kernel
     if (opt_split_wide()) {

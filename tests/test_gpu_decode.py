@@ -374,6 +374,34 @@ def test_split_role_and_general_kernels_agree(S):
             assert lc["cos"] >= 0.9999, (split, S, li, lc)
 
 
+@pytest.mark.parametrize("S", [513, 1025, 1026, 2561, 2562])
+def test_split_role_135m_layouts_agree(S):
+    """SmolLM2-135M's batch-1 steps run on the split-role kernel's 4-chunk narrow build up to 1025
+    tokens, its 10-chunk narrow build up to 2561 and its wide layout beyond; each is held to the
+    oracle teacher-forced per layer, as is the general kernel with the split-role kernel switched off
+    (S = 1025 / 1026 and 2561 / 2562: either side of each limit)."""
+    _need_gpu()
+    from prime_kernels_amd import _native
+    lib = _native.library()
+    geom = O.with_layers(O.SMOLLM2_135M, 3)
+    case = GC.random_kv_case(geom, 43 + S, [S], capacity=S + 16)
+    r = case.oracle_step([91], [S - 1], layer_outputs=True)
+    f = case.eager_gpu_step([91], [S - 1])
+    outs = {}
+    for split in (1, 0):
+        old = lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, split)
+        try:
+            case.sync_kv_from_oracle()
+            outs[split] = case.kernel_step([91], [S - 1], layer_outputs=True)
+        finally:
+            lib.pk_set_option(_native.PK_OPT_SPLIT_ROLE, old)
+    for split, k in outs.items():
+        print(f"135M S={S} split-role={split}", GC.assert_within_floor(k, r, f, f"S={S} split={split}"))
+        for li in range(geom.layers):
+            lc = GC.compare_logits(k["layer_outputs"][li, 0], r["layer_outputs"][li, 0])
+            assert lc["cos"] >= 0.9999, (split, S, li, lc)
+
+
 def test_torch_op_matches_decode_step():
     """torch.ops.prime_decode.decode_step / decode_logits give the same hidden state, ids and
     logits as decode_step(**kw), as fresh tensors."""
