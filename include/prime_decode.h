@@ -102,8 +102,9 @@ int pk_test_exchange_units(int mode, int rounds, int slot, unsigned* out);
 /* One greedy decode step for B = 1..16 sequences (vLLM FLASH_ATTN metadata, paged KV
  * [blocks, KVH, 16, 128]; contexts may differ per sequence).  B = 1 (bf16 or MXFP8 weights) runs the
  * split-role kernel: its narrow layout for contexts up to PK_NOALLOC_MAX_SEQ_360M / _135M tokens (for
- * 135M a build with 4 attention chunks per KV head up to 1025 tokens, the 10-chunk build above), its
- * wide layout (attention over KVH XCDs) up to PK_SR_WIDE_MAX_SEQ, the general GEMV kernel beyond
+ * 135M builds with 4 and 6 attention chunks per KV head up to 1025 and 1537 tokens, the 10-chunk
+ * build above), its wide layout (attention over KVH XCDs) up to PK_SR_WIDE_MAX_SEQ, the general GEMV
+ * kernel beyond
  * (PK_OPT_SPLIT_ROLE / PK_OPT_SPLIT_WIDE switch the split-role layouts off); B >= 2 runs the batched kernel, whose projections and LM head are
  * MFMA tiles over all B tokens, so the weights are read once per step for the whole batch.  The
  * reference caps SmolLM2-360M at B <= 2 (decode_megakernel_360m/__init__.py:46).

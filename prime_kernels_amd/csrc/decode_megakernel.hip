@@ -3483,15 +3483,16 @@ static int decode_impl(void* stream, int B, int n_layers, const void* input_ids,
     int e = PK_OK;
     p.sr_min_s = 0;
     if (G::WF == 0) {
-      // a narrow build with fewer attention chunks for the shortest contexts, where the model has one
-      const int small = sr_max_seq(model, 2);
-      if (small > 0) {
-        p.sr_max_s = small;
-        e = sr_launch(model, 0, 2, p, region, reinterpret_cast<uint32_t*>(rec + rec_general_bytes()), s,
+      // narrow builds with fewer attention chunks for the shorter contexts, where the model has them
+      for (int build = 2; build <= 3; ++build) {
+        const int lim = sr_max_seq(model, build);
+        if (lim <= p.sr_min_s) continue;
+        p.sr_max_s = lim;
+        e = sr_launch(model, 0, build, p, region, reinterpret_cast<uint32_t*>(rec + rec_general_bytes()), s,
                       opt_cooperative());
         if (e != PK_OK) return e;
-        if (max_seq_len <= small) return PK_OK;  // no context can reach another kernel
-        p.sr_min_s = small;
+        if (max_seq_len <= lim) return PK_OK;  // no context can reach another kernel
+        p.sr_min_s = lim;
       }
     }
     p.sr_max_s = narrow;

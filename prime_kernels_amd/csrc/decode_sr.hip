@@ -2262,10 +2262,13 @@ using N360Q = SrG<G360Q, 1>;
 using W360 = SrG<G360, G360::KVH>;
 using W135 = SrG<G135, G135::KVH>;
 using W360Q = SrG<G360Q, G360Q::KVH>;
-// SmolLM2-135M's short contexts: 4 chunks per KV head instead of 10 (12 attending workgroups, the
-// other 20 of group A only project O): fewer records in both attention exchanges and the O rows
-// preloaded (config 2: 2,455 -> 2,624 tok/s); the 10-chunk build takes the contexts above its limit
+// SmolLM2-135M's shorter contexts: 4 chunks per KV head (12 attending workgroups, the other 20 of
+// group A only project O) up to 1,025 tokens, 6 up to 1,537, instead of 10: fewer records in both
+// attention exchanges and the O rows preloaded (config 2: 2,455 -> 2,624 tok/s; 1,200 tokens:
+// 2,438 -> 2,577; 3 or 6 chunks at config 2: -1.7%, -1.1%); the 10-chunk build takes the contexts
+// above 1,537
 using N135S = SrG<G135, 1, 4>;
+using N135M = SrG<G135, 1, 6>;
 
 // Longest context (tokens attended, the new one included) the kernel takes: C chunks of at most TCS
 // cached tokens per KV head, and a chunk's K/V plus the workgroup's O rows within the LDS ring.
@@ -2282,7 +2285,8 @@ static_assert(max_seq<N360>() >= 1281 && max_seq<N135>() >= 769, "the narrow lay
 static_assert(max_seq<W360Q>() >= 8192 + 288 && max_seq<W360>() == max_seq<W360Q>() && max_seq<W135>() >= max_seq<W360>(),
               "the wide layout covers config 5 (context 8192, then the benchmark's steps)");
 static_assert(max_seq<N360Q>() == max_seq<N360>(), "one narrow limit per model");
-static_assert(max_seq<N135S>() >= 769 && max_seq<N135S>() < max_seq<N135>(), "the 4-chunk 135M build covers config 2");
+static_assert(max_seq<N135S>() >= 769 && max_seq<N135S>() < max_seq<N135M>() && max_seq<N135M>() < max_seq<N135>(),
+              "the 4-chunk 135M build covers config 2; each shorter build ends below the next");
 static_assert(max_seq<N360>() == PK_NOALLOC_MAX_SEQ_360M && max_seq<N135>() == PK_NOALLOC_MAX_SEQ_135M,
               "the context limits pk_decode_noalloc documents");
 constexpr size_t pages(size_t n) { return (n + 4095) / 4096 * 4096; }
@@ -2295,7 +2299,7 @@ constexpr size_t lds_bytes() { return sizeof(SmemSR<G>); }
 template <class G>
 constexpr bool lds_fits() { return (sizeof(SmemSR<G>) + 15) / 16 * 16 + TRACE_LDS_BYTES <= 160 * 1024; }
 static_assert(lds_fits<N360>() && lds_fits<N135>() && lds_fits<N360Q>() && lds_fits<W360>() && lds_fits<W135>() &&
-                  lds_fits<W360Q>() && lds_fits<N135S>(),
+                  lds_fits<W360Q>() && lds_fits<N135S>() && lds_fits<N135M>(),
               "LDS budget of one gfx950 workgroup, with the diagnostic timestamps");
 
 template <class G>
@@ -2340,8 +2344,9 @@ static int launch(const Params& p, uint32_t* region, uint32_t* local, hipStream_
 
 int sr_launch(int model, int wf, int wide, const Params& p, uint32_t* region, uint32_t* local, hipStream_t stream,
               int cooperative) {
-  if (wide == 2) {  // the narrow layout with fewer chunks, for the short contexts (135M only)
-    if (model == PK_MODEL_SMOLLM2_135M && !wf) return sr::launch<sr::N135S>(p, region, local, stream, cooperative);
+  if (wide >= 2) {  // the narrow layout with fewer chunks, for the shorter contexts (135M only)
+    if (model == PK_MODEL_SMOLLM2_135M && !wf && wide == 2) return sr::launch<sr::N135S>(p, region, local, stream, cooperative);
+    if (model == PK_MODEL_SMOLLM2_135M && !wf && wide == 3) return sr::launch<sr::N135M>(p, region, local, stream, cooperative);
     return PK_ERR_MODEL;
   }
   if (model == PK_MODEL_SMOLLM2_360M && wf)
@@ -2360,7 +2365,7 @@ static constexpr size_t zmax(A a, B b) { return size_t(a) > size_t(b) ? size_t(a
 size_t sr_region_bytes(int all) {
   using namespace sr;
   const size_t narrow = zmax(SWS<N360>::BYTES, SWS<N135>::BYTES);
-  return all ? zmax(zmax(zmax(narrow, SWS<N360Q>::BYTES), SWS<N135S>::BYTES),
+  return all ? zmax(zmax(zmax(zmax(narrow, SWS<N360Q>::BYTES), SWS<N135S>::BYTES), SWS<N135M>::BYTES),
                    zmax(zmax(SWS<W360>::BYTES, SWS<W135>::BYTES), SWS<W360Q>::BYTES))
              : narrow;
 }
@@ -2368,12 +2373,13 @@ size_t sr_local_bytes(int wide) {
   using namespace sr;
   return wide ? zmax(zmax(SWS<W360>::LOC_BYTES, SWS<W135>::LOC_BYTES), SWS<W360Q>::LOC_BYTES)
               : zmax(zmax(zmax(SWS<N360>::LOC_BYTES, SWS<N135>::LOC_BYTES), SWS<N360Q>::LOC_BYTES),
-                     SWS<N135S>::LOC_BYTES);
+                     zmax(SWS<N135S>::LOC_BYTES, SWS<N135M>::LOC_BYTES));
 }
 int sr_max_seq(int model, int wide) {
   using namespace sr;
-  if (model == PK_MODEL_SMOLLM2_360M) return wide == 2 ? 0 : wide ? max_seq<W360>() : max_seq<N360>();
-  if (model == PK_MODEL_SMOLLM2_135M) return wide == 2 ? max_seq<N135S>() : wide ? max_seq<W135>() : max_seq<N135>();
+  if (model == PK_MODEL_SMOLLM2_360M) return wide >= 2 ? 0 : wide ? max_seq<W360>() : max_seq<N360>();
+  if (model == PK_MODEL_SMOLLM2_135M)
+    return wide == 3 ? max_seq<N135M>() : wide == 2 ? max_seq<N135S>() : wide ? max_seq<W135>() : max_seq<N135>();
   return 0;
 }
 

@@ -152,8 +152,8 @@ struct Params {
 
 // Split-role batch-1 kernel (decode_sr.hip): launch, the sizes of its workspace regions (bytes), and
 // the longest context it takes (tokens attended, new one included; 0: not available for the model).
-// `wide`: 0 the narrow layout, 1 the wide one, 2 the narrow layout with fewer attention chunks for
-// the shortest contexts (135M).
+// `wide`: 0 the narrow layout, 1 the wide one, 2 and 3 the narrow layout with fewer attention chunks
+// for the shorter contexts (135M: 4 chunks up to 1,025 tokens, 6 up to 1,537).
 __attribute__((visibility("hidden"))) int sr_launch(int model, int wf, int wide, const Params& p, uint32_t* region,
                                                  uint32_t* local, hipStream_t stream, int cooperative);
 // region: the largest over every compiled layout (all != 0) or over the narrow bf16 ones

@@ -374,12 +374,13 @@ def test_split_role_and_general_kernels_agree(S):
             assert lc["cos"] >= 0.9999, (split, S, li, lc)
 
 
-@pytest.mark.parametrize("S", [513, 1025, 1026, 2561, 2562])
+@pytest.mark.parametrize("S", [513, 1025, 1026, 1537, 1538, 2561, 2562])
 def test_split_role_135m_layouts_agree(S):
     """SmolLM2-135M's batch-1 steps run on the split-role kernel's 4-chunk narrow build up to 1025
-    tokens, its 10-chunk narrow build up to 2561 and its wide layout beyond; each is held to the
-    oracle teacher-forced per layer, as is the general kernel with the split-role kernel switched off
-    (S = 1025 / 1026 and 2561 / 2562: either side of each limit)."""
+    tokens, its 6-chunk narrow build up to 1537, its 10-chunk narrow build up to 2561 and its wide
+    layout beyond; each is held to the oracle teacher-forced per layer, as is the general kernel with
+    the split-role kernel switched off (S = 1025 / 1026, 1537 / 1538 and 2561 / 2562: either side of
+    each limit)."""
     _need_gpu()
     from prime_kernels_amd import _native
     lib = _native.library()
