@@ -11,6 +11,7 @@ import sys
 from pathlib import Path
 
 ORDER = [("stream_135m_ctx512", "config 2: SmolLM2-135M, 512-token prompt"),
+         ("stream_135m_ctx1200", "SmolLM2-135M, 1200-token prompt"),
          ("stream_360m_ctx1024", "config 3: SmolLM2-360M, 1024-token prompt"),
          ("stream_360m_mxfp8_ctx8192", "config 5: SmolLM2-360M MXFP8, 8192-token prompt")]
 

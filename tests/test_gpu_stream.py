@@ -182,6 +182,15 @@ def test_stream_config2_135m_ctx512():
     _run(case, ctx, 4321, "stream_135m_ctx512")
 
 
+def test_stream_135m_ctx1200():
+    """SmolLM2-135M past config 2's range: a 1200-token prompt and 256 generated tokens (contexts
+    1201..1456), the range of the split-role kernel's 6-chunk build."""
+    _need_gpu()
+    ctx = 1200
+    case = GC.random_kv_case(O.SMOLLM2_135M, 2012, [ctx], capacity=ctx + STEPS + 16, norm_jitter=0.0)
+    _run(case, ctx, 4321, "stream_135m_ctx1200")
+
+
 def test_stream_config3_360m_ctx1024():
     """SmolLM2-360M (32 layers), 1024-token prompt, 256 generated tokens."""
     _need_gpu()
