@@ -105,7 +105,9 @@ int pk_test_exchange_units(int mode, int rounds, int slot, unsigned* out);
  * 135M builds with 4 and 6 attention chunks per KV head up to 1025 and 1537 tokens, the 10-chunk
  * build above), its wide layout (attention over KVH XCDs) up to PK_SR_WIDE_MAX_SEQ, the general GEMV
  * kernel beyond
- * (PK_OPT_SPLIT_ROLE / PK_OPT_SPLIT_WIDE switch the split-role layouts off); B >= 2 runs the batched kernel, whose projections and LM head are
+ * (PK_OPT_SPLIT_ROLE / PK_OPT_SPLIT_WIDE switch the split-role layouts off).  B = 2 without
+ * layer_outputs runs as two batch-1 steps, one per sequence (faster than one batched step of two);
+ * B >= 2 otherwise runs the batched kernel, whose projections and LM head are
  * MFMA tiles over all B tokens, so the weights are read once per step for the whole batch.  The
  * reference caps SmolLM2-360M at B <= 2 (decode_megakernel_360m/__init__.py:46).
  *   layers: device table [n_layers][6] of pointers (norm1, qkv, o, norm2, gate_up, down), bf16.

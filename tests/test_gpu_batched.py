@@ -93,6 +93,31 @@ def test_batched_agrees_with_batch_one_kernel():
         assert c["max_abs"] <= GC.LOGIT_ATOL and c["cos"] >= GC.COS_MIN, (b, c)
 
 
+@pytest.mark.parametrize("ids_dtype", [torch.int64, torch.int32], ids=["i64", "i32"])
+def test_two_sequences_run_as_two_batch_one_steps(ids_dtype):
+    """Two sequences without layer_outputs run as two batch-1 steps on the split-role kernel (one
+    context on its narrow layout, one on its wide layout): within the eager floor of the oracle, the
+    appends where the oracle puts them, and every output bit equal to a batch-1 call per sequence."""
+    _need_gpu()
+    geom = O.with_layers(O.SMOLLM2_360M, 2)
+    contexts = [300, 1700]
+    case = GC.random_kv_case(geom, 97, contexts)
+    ids = [11, 12]
+    pos = [S - 1 for S in contexts]
+    k = case.kernel_step(ids, pos, ids_dtype=ids_dtype)
+    f = case.eager_gpu_step(ids, pos)
+    r = case.oracle_step(ids, pos)
+    GC.assert_within_floor(k, r, f, "two sequences")
+    _kv_appends_match(case, contexts, "two sequences")
+    for b in range(2):
+        case.sync_kv_from_oracle()
+        one = case.kernel_step([ids[b]], [pos[b]], seq_lens=[contexts[b]],
+                               slot_mapping=[case.kv.slot(b, contexts[b] - 1)], block_rows=[b], ids_dtype=ids_dtype)
+        assert torch.equal(k["logits"][b], one["logits"][0]), b
+        assert torch.equal(k["hidden"][b], one["hidden"][0]), b
+        assert int(k["ids"][b]) == int(one["ids"][0]), b
+
+
 def test_batched_deterministic():
     _need_gpu()
     geom = O.with_layers(O.SMOLLM2_360M, 2)
