@@ -93,13 +93,15 @@ def test_batched_agrees_with_batch_one_kernel():
         assert c["max_abs"] <= GC.LOGIT_ATOL and c["cos"] >= GC.COS_MIN, (b, c)
 
 
-@pytest.mark.parametrize("ids_dtype", [torch.int64, torch.int32], ids=["i64", "i32"])
-def test_two_sequences_run_as_two_batch_one_steps(ids_dtype):
-    """Two sequences without layer_outputs run as two batch-1 steps on the split-role kernel (one
-    context on its narrow layout, one on its wide layout): within the eager floor of the oracle, the
-    appends where the oracle puts them, and every output bit equal to a batch-1 call per sequence."""
+@pytest.mark.parametrize("base,ids_dtype", [(O.SMOLLM2_360M, torch.int64), (O.SMOLLM2_360M, torch.int32),
+                                             (O.SMOLLM2_135M, torch.int64)], ids=["360m-i64", "360m-i32", "135m-i64"])
+def test_two_sequences_run_as_two_batch_one_steps(base, ids_dtype):
+    """Two sequences without layer_outputs run as two batch-1 steps on the split-role kernel (360M:
+    one context on its narrow layout, one on its wide layout; 135M: its 4- and 10-chunk narrow
+    builds): within the eager floor of the oracle, the appends where the oracle puts them, and every
+    output bit equal to a batch-1 call per sequence."""
     _need_gpu()
-    geom = O.with_layers(O.SMOLLM2_360M, 2)
+    geom = O.with_layers(base, 2)
     contexts = [300, 1700]
     case = GC.random_kv_case(geom, 97, contexts)
     ids = [11, 12]
