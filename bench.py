@@ -235,9 +235,8 @@ def main() -> None:
                 if B == 1 else
                 f"{mname.lower()} greedy decode, batch {B}, contexts drawn uniformly from 128..4096 "
                 f"(seed {args.seed}, mean {sum(contexts) / B:.0f}), K steps per sequence")
-    kernel = ("split-role batch-1 kernel (contexts up to its limit; the general kernel beyond)"
-              if B == 1 and args.weights == "bf16" else
-              "batched MFMA kernel" if B > 1 else "general batch-1 kernel")
+    kernel = ("split-role batch-1 kernel (contexts up to its limit; the general kernel beyond)" if B == 1 else
+              "split-role batch-1 kernel, one step per sequence" if B == 2 else "batched MFMA kernel")
     line = {
         "metric": f"decode tok/s, {mname} {wname} bs={B} {ctx_name}; % of HBM roofline",
         "value": round(B * K / (ms * 1e-3), 2),
@@ -257,7 +256,7 @@ def main() -> None:
                    "batch": B, "context": context if B == 1 else contexts, "layers": layers_n, "weights": args.weights,
                    "gate_up": "lossless codec" if args.lossless else "dense",
                    "lm_head": "tied, fused argmax",
-                   "launch": f"one persistent launch per step, 256 workgroups (one per CU): {kernel}"},
+                   "launch": f"persistent launches of 256 workgroups (one per CU): {kernel}"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_source": f"profiles/{tname}_traffic.json" if traffic is not None else None,
