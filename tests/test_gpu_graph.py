@@ -46,7 +46,7 @@ def _fill(kv, st, ids, positions):
 
 
 @pytest.mark.parametrize("launch", ["ordinary", "cooperative"])
-@pytest.mark.parametrize("batch", [1, 3])
+@pytest.mark.parametrize("batch", [1, 2, 3])
 def test_decode_step_replays_from_a_graph(batch, launch):
     """Also with the kernels launched cooperatively (PK_OPT_COOPERATIVE), the captured launch
     replaying the eager step bit for bit."""
